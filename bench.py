@@ -1,0 +1,220 @@
+"""Batch-1 Q8 decode benchmark (Llama-3-8B shape) on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--config llama3-8b] [--prompt-len 1024]
+
+A step is one decode token: the whole per-token path (embedding gather, 32
+layers of RMSNorm / fused QKV / RoPE + int8 KV append / attention / O /
+RMSNorm / fused gate-up-SwiGLU / down, final norm, lm_head, greedy pick) as one
+HIP graph replay, with weights and KV cache resident in HBM.  The prompt runs
+first (untimed), then W untimed steps, then exactly K timed steps; the device is
+synchronised on both sides of the timed region.  Prints one JSON line.
+
+Extra fields: the achieved HBM rate of the whole step (algorithmic bytes per
+token / time), the dominant kernel's roofline (the fused gate/up matvec shape,
+timed with HIP events on its stream over copies that exceed the last-level
+cache), and a CPU baseline: jieyu's own decode path compiled from the reference
+sources (oracle/_ref) on this host, over a bounded sample of the same model,
+whose tokens are also compared with the GPU's.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "batch-1 decode tokens/s (Q8, 8B shape) + achieved HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def q8b(rows, cols):
+    return rows * (cols // 32) * 34
+
+
+def token_bytes(d, weight_bytes, p):
+    """Algorithmic HBM bytes of one decode step at position p (attends p+1 keys)."""
+    L, H, nkv, hd = d.num_layers, d.hidden, d.num_kv_heads, d.head_dim
+    embed_row = q8b(1, H) if d.embed.type == 3 else H * 4
+    return (weight_bytes + (2 * L + 1) * H * 4 + embed_row
+            + L * (p + 1) * nkv * (hd + 4) * 2      # int8 K,V + fp32 scales read
+            + L * nkv * (hd + 4) * 2)               # new K,V written
+
+
+def dominant_kernel_roofline(jy, olib, d, iters=60):
+    """The fused gate/up matvec (2F x hidden rows): its launch shape, timed in isolation
+    with HIP events over enough copies to defeat the 256 MiB infinity cache."""
+    rows, cols = 2 * d.intermediate, d.hidden
+    nbytes = q8b(rows, cols)
+    copies = max(2, int(np.ceil(1.2e9 / nbytes)))
+    x = np.zeros(rows * cols, np.float32)
+    olib.jysyn_normal_fill(11, 5, 0.02, ptr(x), x.size)
+    w = np.zeros(nbytes, np.uint8)
+    olib.jysyn_quantize_q8_0(ptr(x), ptr(w), x.size)
+    del x
+    xin = np.random.default_rng(0).standard_normal(cols).astype(np.float32)
+    m = jy.Q8Matrix(w, rows, cols, copies=copies)
+    us = m.time(xin, iters)
+    m.close()
+    algo = nbytes + cols * 4 + rows * 4
+    ach = algo / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "kernel": "matvec_q8_kernel (fused gate/up, %dx%d)" % (rows, cols),
+            "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+            "traffic": None, "bytes_per_launch": algo, "avg_launch_us": round(us, 3), "copies": copies}
+
+
+def cpu_baseline(desc, prompt, n_new, gpu_model):
+    """jieyu's decode loop built from the reference sources (or the C oracle where that
+    build is absent) on this host; rate as the reference's -tokenspeed report defines
+    it: (n-1) / (t_last - t_first) (libs/model_libs/pipeline.h:356-372)."""
+    import oracle
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    max_seq = len(prompt) + n_new + 1
+    olib = oracle.load_oracle()
+    half = desc.head_dim // 2
+    cos = np.zeros(max_seq * half, np.float32)
+    sin = np.zeros_like(cos)
+    olib.jyo_rope_table(max_seq, desc.head_dim, desc.rope_theta, ptr(cos), ptr(sin))
+    out = np.zeros(max_seq + 1, np.int32)
+    stamps = np.zeros(n_new + 1, np.float64)
+    t0 = time.monotonic()
+    if oracle.ref_available():
+        kind = "reference"
+        ref = oracle.load_ref()
+        n = ref.jyref_generate(C.byref(desc), ptr(prompt), len(prompt), None, 0, ptr(cos), ptr(sin), max_seq, n_new,
+                               0.0, 1.0, ptr(out), None, ptr(stamps), len(stamps))
+    else:
+        kind = "port"
+        n = olib.jyo_generate(C.byref(desc), ptr(prompt), len(prompt), None, 0, ptr(cos), ptr(sin), max_seq, n_new,
+                              0.0, 1.0, ptr(out), None, None)
+        stamps[:] = 0.0
+    wall = time.monotonic() - t0
+    made = n - len(prompt)
+    if kind == "reference" and made > 1:
+        rate = (made - 1) / (stamps[made - 1] - stamps[0])
+        prefill = len(prompt) / (stamps[0] - t0)
+    else:
+        rate = made / wall if wall > 0 else 0.0
+        prefill = None
+    gpu_ids, _ = gpu_model.generate(prompt, n_new, max_seq=max_seq)
+    same = bool(np.array_equal(gpu_ids, out[:n]))
+    return {"value": round(rate, 4), "unit": "tokens/s", "cores": threads, "kind": kind,
+            "sample": f"{len(prompt)}-token prompt then {made} greedy tokens on the same model "
+                      f"(decode rate = (n-1)/(t_last-t_first)); wall {wall:.1f} s",
+            "prefill_tokens_s": None if prefill is None else round(prefill, 3),
+            "gpu_tokens_identical": same}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=496)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--config", default="llama3-8b")
+    ap.add_argument("--prompt-len", type=int, default=1024)
+    ap.add_argument("--max-seq", type=int, default=4096)
+    ap.add_argument("--cpu-prompt", type=int, default=8)
+    ap.add_argument("--cpu-tokens", type=int, default=6)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-kernel", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this decode path is single-device (no sharding or collectives); "
+              "run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import jieyu_amd as jy
+    import oracle
+    from jieyu_amd.model import Synth, synth_config
+
+    if jy.device_count() < 1:
+        log("no HIP device visible")
+        sys.exit(1)
+    olib = oracle.load_oracle()
+    cfg = synth_config(args.config)
+    t = time.time()
+    log(f"generating the {args.config} model on the host (seed {cfg.seed}) ...")
+    syn = Synth(jy.lib(), cfg)
+    d = syn.desc
+    log(f"  {syn.weight_bytes / 1e9:.3f} GB of streamed weights in {time.time() - t:.1f} s; uploading ...")
+    g = jy.GpuModel(d, args.max_seq)
+    log(f"  uploaded + repacked in {g.upload_ms / 1e3:.1f} s")
+
+    prompt = np.zeros(args.prompt_len, np.int32)
+    olib.jysyn_uniform_int_fill(cfg.seed, 99, 0, d.vocab_size - 1, ptr(prompt), len(prompt))
+    K, W = args.steps, args.warmup
+    total_new = 1 + W + K
+    assert args.prompt_len + total_new <= args.max_seq
+    log(f"prefill {args.prompt_len} tokens ...")
+    sess = g.session(prompt, total_new, max_seq=args.max_seq)
+    st0 = sess.stats()
+    log(f"  prefill {st0.prefill_ms:.1f} ms; warmup {W} steps ...")
+    sess.step(W)
+    dec0 = sess.stats().decode_ms
+    t0 = time.perf_counter()
+    made = sess.step(K)
+    t1 = time.perf_counter()
+    st = sess.stats()
+    ids = sess.ids()
+    sess.close()
+    assert made == K, f"produced {made} of {K} steps"
+    wall_ms = (t1 - t0) * 1e3
+    dev_ms = st.decode_ms - dec0
+    ms_step = wall_ms / K
+    tok_s = K / (wall_ms / 1e3)
+    p0 = args.prompt_len + W  # position of the first timed step's token
+    bytes_total = sum(token_bytes(d, g.weight_bytes, p) for p in range(p0, p0 + K))
+    hbm_gbs = bytes_total / (wall_ms * 1e-3) / 1e9
+    log(f"  {K} steps: {wall_ms:.1f} ms wall ({dev_ms:.1f} ms device) -> {tok_s:.1f} tok/s, "
+        f"{hbm_gbs:.0f} GB/s = {100 * hbm_gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s")
+
+    roof = None
+    if not args.no_kernel:
+        log("dominant kernel in isolation ...")
+        roof = dominant_kernel_roofline(jy, olib, d)
+        log(f"  {roof['kernel']}: {roof['avg_launch_us']} us -> {roof['achieved']} GB/s")
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"CPU baseline: {args.cpu_prompt}-token prompt + {args.cpu_tokens} tokens ...")
+        cpu = cpu_baseline(d, prompt[:args.cpu_prompt].copy(), args.cpu_tokens, g)
+        log(f"  {cpu['kind']}: {cpu['value']} tok/s on {cpu['cores']} threads; GPU identical: "
+            f"{cpu['gpu_tokens_identical']}")
+    shape = {"num_layers": d.num_layers, "hidden": d.hidden, "heads": d.num_heads, "kv_heads": d.num_kv_heads,
+             "head_dim": d.head_dim, "ffn": d.intermediate, "vocab": d.vocab_size, "rope_theta": d.rope_theta}
+    g.close()
+    syn.close()
+
+    out = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: random-init N(0,0.02) weights quantized to Q8_0 (norms 1+N(0,0.02)), uniform random prompt ids",
+        "config": {"workload": f"{args.config} shape, Q8_0 weights, int8 KV cache, batch-1 greedy decode after a "
+                               f"{args.prompt_len}-token prompt (positions {p0}..{p0 + K - 1} timed)",
+                   **shape, "prompt_len": args.prompt_len, "max_seq": args.max_seq,
+                   "mode": "bit-exact (reference arithmetic order)"},
+        "hbm_gbs": round(hbm_gbs, 1), "hbm_frac": round(hbm_gbs / HBM_PEAK_GBS, 4),
+        "bytes_per_token_avg": int(bytes_total / K), "device_ms_per_step": round(dev_ms / K, 4),
+        "prefill_ms": round(st.prefill_ms, 2), "prefill_tokens_s": round(args.prompt_len / (st.prefill_ms / 1e3), 1),
+        "upload_s": round(st.upload_ms / 1e3, 2),
+        "last_ids": ids[-8:].tolist(),
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,122 @@
+/*
+ * jieyu_amd.h — C ABI of the MI355X (gfx950) decode path: HBM-resident
+ * weights and int8 KV cache, hand-written HIP kernels, one GPU.
+ *
+ * These entry points are the device-resident counterparts of jieyu's
+ * model_libs forward-step interface.  All take plain pointers and sizes, return
+ * an int status (0 / count on success, -1 on error) or a handle (NULL on
+ * error); jyhip_last_error() gives the calling thread's last error text.  No
+ * C++ exception crosses this boundary.
+ *
+ * Arithmetic: every kernel reproduces the reference CPU path's operation order
+ * and rounding, so outputs are bit-identical to jieyu's AVX2+FMA build on the
+ * same inputs (token ids, KV cache bytes, hidden states).
+ */
+#ifndef JIEYU_AMD_H
+#define JIEYU_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "jieyu_model.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define JYHIP_API __attribute__((visibility("default")))
+
+typedef struct jyhip_model jyhip_model;
+typedef struct jyhip_kv jyhip_kv;
+
+/* token_cb of libs/model_libs/generate.h:8 — return nonzero to stop */
+typedef int (*jyhip_token_cb)(int id, void* ud);
+
+typedef struct jyhip_stats {
+    double prefill_ms;      /* prompt forward + first token, device time */
+    double decode_ms;       /* every later token, device time             */
+    int prompt_len;
+    int decoded;            /* tokens produced after the first            */
+    double upload_ms;       /* host->device weight copy + repack (model)  */
+} jyhip_stats;
+
+/* Thread-local text of the last error ("" when none). */
+JYHIP_API const char* jyhip_last_error(void);
+/* Number of visible HIP devices (0 when none; never an error). */
+JYHIP_API int jyhip_device_count(void);
+/* Select the device used by subsequent calls of this thread. */
+JYHIP_API int jyhip_set_device(int device);
+
+/* Upload a model and precompute its RoPE table for positions [0, max_seq).
+ * Mirrors what jieyu's bind_model + RoPETable::init produce
+ * (libs/model_libs/pipeline.h:63-153, libs/date_libs/date.h:52-66); 2-D weights
+ * must all be JY_Q8_0 or all JY_F32. */
+JYHIP_API jyhip_model* jyhip_model_upload(const jy_model_desc* m, int max_seq);
+JYHIP_API void jyhip_model_free(jyhip_model* model);
+/* Bytes of 2-D weights (incl. lm_head) one decode step streams. */
+JYHIP_API size_t jyhip_model_weight_bytes(const jyhip_model* model);
+JYHIP_API double jyhip_model_upload_ms(const jyhip_model* model);
+
+/* __KVcache::init (libs/date_libs/date.h:99-111): zero-filled int8 K/V and fp32
+ * scales for num_layers x max_seq x num_kv_heads x head_dim. */
+JYHIP_API jyhip_kv* jyhip_kv_create(const jyhip_model* model, int max_seq);
+JYHIP_API void jyhip_kv_free(jyhip_kv* kv);
+JYHIP_API int jyhip_kv_len(const jyhip_kv* kv);
+JYHIP_API int jyhip_kv_set_len(jyhip_kv* kv, int current_len);
+/* Copy positions [pos0, pos0+npos) of one layer in jieyu's host layout:
+ * k, v int8 [npos][num_kv_heads][head_dim]; ks, vs float [npos][num_kv_heads]. */
+JYHIP_API int jyhip_kv_write(jyhip_kv* kv, int layer, int pos0, int npos, const int8_t* k, const float* ks,
+                             const int8_t* v, const float* vs);
+JYHIP_API int jyhip_kv_read(const jyhip_kv* kv, int layer, int pos0, int npos, int8_t* k, float* ks, int8_t* v,
+                            float* vs);
+
+/* forward_cached (libs/model_libs/forward.h:47-96).  X: host [seq][hidden], the
+ * embeddings of positions [start_pos, start_pos+seq) on entry, the final-normed
+ * hidden states on exit.  layer_out (optional, host [num_layers][seq][hidden])
+ * receives X after every layer.  Sets the cache length to start_pos+seq. */
+JYHIP_API int jyhip_forward_cached(jyhip_model* model, jyhip_kv* kv, float* X, int seq, int start_pos,
+                                   float* layer_out);
+
+/* generate / generate_cached (libs/model_libs/generate.h:9-112).  kv == NULL
+ * uses a private max_seq cache.  Returns the sequence length written to
+ * out_ids (prompt + generated), 0 for an empty / too long prompt, -1 on error.
+ * out_ids needs max_seq entries.  logits_out (optional, [vocab_size]) receives
+ * the logits of the last step. */
+JYHIP_API int jyhip_generate(jyhip_model* model, jyhip_kv* kv, const int* prompt_ids, int prompt_len,
+                             const int* eos_ids, int num_eos, int max_seq, int max_new, float temperature,
+                             float repetition_penalty, int* out_ids, jyhip_token_cb cb, void* cb_ud,
+                             float* logits_out, jyhip_stats* stats);
+
+/* The same generation driven step by step (no counterpart in the reference; the
+ * decode loop of generate_cached, generate.h:39-87, split so a caller can time
+ * or interleave steps).  begin runs the prompt and picks the first token;
+ * step produces up to n more (returns how many, 0 when finished); ids copies the
+ * sequence so far.  begin returns a finished session (len = what generate()
+ * would return) when the prompt is empty/too long or max_new <= 0. */
+typedef struct jyhip_session jyhip_session;
+JYHIP_API jyhip_session* jyhip_session_begin(jyhip_model* model, jyhip_kv* kv, const int* prompt_ids,
+                                             int prompt_len, const int* eos_ids, int num_eos, int max_seq,
+                                             int max_new, float temperature, float repetition_penalty);
+JYHIP_API int jyhip_session_step(jyhip_session* s, int n);
+JYHIP_API int jyhip_session_remaining(const jyhip_session* s);
+JYHIP_API int jyhip_session_len(const jyhip_session* s);
+JYHIP_API int jyhip_session_ids(const jyhip_session* s, int* out, int cap);
+JYHIP_API int jyhip_session_stats(jyhip_session* s, jyhip_stats* stats);
+JYHIP_API void jyhip_session_end(jyhip_session* s);
+
+/* Isolated Q8_0 matvec (decode kernel): y[n] = W[n][:] . x for a [rows][cols/32]x34
+ * jieyu matrix.  jyhip_q8_upload keeps `copies` identical device copies so timed
+ * runs can rotate through more bytes than the 256 MiB last-level cache. */
+typedef struct jyhip_q8mat jyhip_q8mat;
+JYHIP_API jyhip_q8mat* jyhip_q8_upload(const void* w, int rows, int cols, int copies);
+JYHIP_API void jyhip_q8_free(jyhip_q8mat* m);
+JYHIP_API int jyhip_q8_matvec(jyhip_q8mat* m, const float* x, float* y);
+/* Time `iters` launches (rotating copies) with HIP events on the launch stream:
+ * *avg_us = mean kernel-to-kernel time per launch. */
+JYHIP_API int jyhip_q8_matvec_time(jyhip_q8mat* m, const float* x, int iters, double* avg_us);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,71 @@
+"""Build libjieyu_amd.so in-tree (hipcc, gfx950) — the product library.
+
+    python -m jieyu_amd.build        # or: from jieyu_amd.build import build; build()
+
+Sources: csrc/*.hip and csrc/*.cpp through hipcc, csrc/*.c through gcc.  The
+library lands next to this file so it travels with the source tree.
+"""
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+LIB = os.path.join(HERE, "libjieyu_amd.so")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = os.environ.get("JIEYU_AMD_ARCH", "gfx950")
+
+# -ffp-contract=off: fused multiply-adds only where a kernel asks for one.
+# -packed-fp32-ops off: no v_pk_*_f32 generation.
+HIP_FLAGS = [
+    "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-fPIC", "-fvisibility=hidden",
+    "-ffp-contract=off", "-fno-fast-math",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument", "-I", INCLUDE, "-I", CSRC,
+]
+C_FLAGS = ["-std=c11", "-O2", "-ffp-contract=off", "-fno-fast-math", "-fopenmp", "-fPIC", "-I", INCLUDE]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout)
+        raise RuntimeError("build step failed: " + " ".join(cmd[:3]) + " ...")
+    return r.stdout
+
+
+def build(verbose=False):
+    srcs = sorted(os.listdir(CSRC))
+    tmp = tempfile.mkdtemp(prefix="jyamd_build_")
+    try:
+        objs = []
+        for s in srcs:
+            path = os.path.join(CSRC, s)
+            obj = os.path.join(tmp, s + ".o")
+            if s.endswith((".hip", ".cpp")):
+                cmd = [HIPCC, *HIP_FLAGS, "-c", path, "-o", obj]
+                if s.endswith(".cpp"):
+                    cmd[1:1] = ["-x", "hip"]
+            elif s.endswith(".c"):
+                cmd = ["gcc", *C_FLAGS, "-c", path, "-o", obj]
+            else:
+                continue
+            if verbose:
+                print(" ".join(cmd))
+            _run(cmd)
+            objs.append(obj)
+        out_tmp = LIB + ".tmp"
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out_tmp, *objs, "-lgomp", "-lm"])
+        os.replace(out_tmp, LIB)
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

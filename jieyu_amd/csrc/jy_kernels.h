@@ -1,0 +1,121 @@
+// jy_kernels.h — host-side launchers for the decode-path HIP kernels.
+//
+// Device data layouts (resident in HBM for the life of a model):
+//  Q8_0 weight matrices: row groups of 4 x chunks of 8 blocks (jy_layout.h).
+//  f32 weight matrices: [K][N] row-major (jieyu's [in][out], libs/matmul_libs/matmul.h:7).
+//  KV cache: K and V int8 [L][nkv][max_seq][hd], scales fp32 [L][nkv][max_seq]
+//    (head-major, so one head's keys are contiguous; jieyu keeps [L][pos][nkv][hd],
+//    libs/date_libs/date.h:89-147 — jyhip_kv_read/_write convert).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace jy {
+
+enum Epi { EPI_STORE = 0, EPI_BIAS = 1, EPI_RESID = 2, EPI_SWIGLU = 3, EPI_ROPE = 4, EPI_ARGMAX = 5 };
+
+struct Q8Dev {
+    uint8_t* qs = nullptr;
+    uint16_t* d = nullptr;
+    int rows = 0, cols = 0, nb = 0, nch = 0, nbp = 0, rows_pad = 0;
+};
+
+struct KVDev {
+    int8_t* k = nullptr;
+    int8_t* v = nullptr;
+    float* ks = nullptr;
+    float* vs = nullptr;
+    int num_layers = 0, max_seq = 0, nkv = 0, hd = 0;
+};
+
+// Epilogue arguments of the decode matvec.
+struct MvArgs {
+    const float* aux = nullptr;      // bias (EPI_BIAS / EPI_ROPE) or nothing
+    const int* state = nullptr;      // [0] = sequence length (position = state[0]-1), [1] = stop flag
+    int pos0 = 0;                    // EPI_ROPE position when state is null
+    const float* cos_t = nullptr;    // EPI_ROPE tables [max_seq][hd/2]
+    const float* sin_t = nullptr;
+    int nh = 0, nkv = 0, hd = 0;     // EPI_ROPE: rows [0, nh*hd) are q, then k, then v
+    int* ids = nullptr;              // EPI_ARGMAX: token ids (next id goes to ids[state[0]])
+    int* mstate = nullptr;           // EPI_ARGMAX: mutable state
+    const int* eos = nullptr;
+    int neos = 0;
+    float* part_val = nullptr;       // EPI_ARGMAX: per-workgroup partial maxima
+    int* part_idx = nullptr;
+    unsigned* counter = nullptr;     // EPI_ARGMAX: workgroups done (reset by the last)
+};
+
+size_t q8_qs_bytes(int rows, int cols);
+size_t q8_d_bytes(int rows, int cols);
+Q8Dev q8_shape(int rows, int cols);
+
+// Once per device, before any launch: raise the dynamic LDS limit of the kernels
+// that stage a full activation vector.
+hipError_t kernels_init();
+
+// src: jieyu Q8_0 rows [rows][cols/32] x 34 B (device copy).  Source row r lands
+// in destination row row_base + r*row_stride.
+void launch_repack_q8(const uint8_t* src, int rows, int cols, const Q8Dev& dst, int row_base, int row_stride,
+                      hipStream_t st);
+
+// Embedding rows.  ids_dev[id_index0 + i] (or, when state != null, ids_dev[state[0]-1])
+void launch_embed(const Q8Dev* q8, const float* f32, int hidden, const int* ids_dev, int id_index0,
+                  const int* state, int seq, float* X, hipStream_t st);
+
+void launch_rmsnorm(const float* X, float* Y, const float* w, int n, int rows, float eps, hipStream_t st);
+
+// y = W x for one token in the reference's 32-lane order; when norm_w != null the
+// kernel first applies RMSNorm (eps 1e-5) to x with those weights.
+void launch_matvec_q8(const Q8Dev& W, const float* x, const float* norm_w, float* out, Epi epi, const MvArgs& a,
+                      hipStream_t st);
+// f32 [K][N] matvec, fma chain over k; EPI_SWIGLU takes B2 as the up matrix.
+void launch_matvec_f32(const float* B, const float* B2, int K, int N, const float* x, float* out,
+                       const float* aux, Epi epi, hipStream_t st);
+// prefill GEMMs, C[m][N] (+ epilogue: EPI_STORE / EPI_BIAS / EPI_RESID)
+void launch_gemm_q8(const Q8Dev& W, int m, const float* A, float* C, const float* aux, Epi epi, hipStream_t st);
+void launch_gemm_f32(const float* B, int K, int N, int m, const float* A, float* C, const float* aux, Epi epi,
+                     hipStream_t st);
+// h[i][j] = silu(gu[i][2j]) * gu[i][2j+1]  (or silu(g) * u with separate buffers)
+void launch_silu_mul(const float* g, const float* u, int interleaved, int m, int F, float* h, hipStream_t st);
+
+// RoPE on q and k of every row, K/V int8 packing into the cache of `layer`, Q int8.
+// qkv: [seq][q_dim + 2*kv_dim].  Position start_pos + row, or state[0]-1 when
+// state != null (a one-row decode step).
+void launch_rope_pack(float* qkv, int seq, int start_pos, const int* state, int nh, int nkv, int hd,
+                      const float* cos_t, const float* sin_t, const KVDev& kv, int layer, int8_t* q8, float* qsc,
+                      hipStream_t st);
+
+struct AttnArgs {
+    // fused (decode): q, k, v rows of the token from qkv (already roped); the kernel
+    // quantizes them and appends K/V at position state[0]-1.  Otherwise q8/qsc come
+    // from launch_rope_pack and every key is already in the cache.
+    bool fused = false;
+    const float* qkv = nullptr;
+    const int8_t* q8 = nullptr;
+    const float* qsc = nullptr;
+    int row0 = 0, nrows = 1, start_pos = 0;
+    const int* state = nullptr;
+    int nh = 0, nkv = 0, hd = 0;
+    KVDev kv;
+    int layer = 0;
+    float* scratch = nullptr;        // nrows*nh*max_keys floats for contexts past the LDS budget
+    int max_keys = 0;
+    float* out = nullptr;            // [rows][nh*hd]
+};
+void launch_attention(const AttnArgs& a, hipStream_t st);
+
+// greedy next token (with repetition penalty): ids[state[0]] = argmax; state[0]++
+void launch_argmax(const float* logits, int V, int* ids, int* state, const int* eos, int neos, float rep_penalty,
+                   int prompt_len, hipStream_t st);
+
+// reference-layout <-> device-layout KV rows for one layer
+void launch_kv_import(const int8_t* k_ref, const float* ks_ref, const int8_t* v_ref, const float* vs_ref,
+                      int pos0, int npos, const KVDev& kv, int layer, hipStream_t st);
+void launch_kv_export(int8_t* k_ref, float* ks_ref, int8_t* v_ref, float* vs_ref, int pos0, int npos,
+                      const KVDev& kv, int layer, hipStream_t st);
+
+// argmax partials workspace for an EPI_ARGMAX matvec of `rows` rows
+int argmax_partials(int rows);
+
+}  // namespace jy

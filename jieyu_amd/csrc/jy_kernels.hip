@@ -1,0 +1,512 @@
+// jy_kernels.hip — CDNA4 (gfx950) kernels of jieyu's per-token decode loop.
+//
+// Every kernel reproduces the reference CPU arithmetic bit for bit (operation
+// order and rounding), so greedy token ids match the reference exactly:
+//   Q8_0 matvec        libs/matmul_libs/matmul_q.h:111-144     (32 FMA lanes, fixed tree)
+//   Q8_0 prefill GEMM  libs/matmul_libs/matmul_q.h:145-161     (sequential k, mul then add)
+//   f32 matvec/GEMM    libs/matmul_libs/x86/x86_classic.txt    (fma chain over k)
+//   RMSNorm            libs/model_libs/rmsnorm/x86/x86_classic.txt
+//   RoPE               libs/model_libs/rope/x86/x86_classic.txt
+//   int8 KV / Q        libs/model_libs/attention/attention_q8.h:20-37
+//   attention          libs/model_libs/attention/x86/x86_classic.txt
+//   SiLU               libs/model_libs/silu/x86/x86_classic.txt
+//   greedy             libs/model_libs/generate.h:57-60
+#include "jy_layout.h"
+
+namespace jy {
+
+Q8Dev q8_shape(int rows, int cols) {
+    Q8Dev q;
+    q.rows = rows;
+    q.cols = cols;
+    q.nb = cols / 32;
+    q.nch = (q.nb + 7) / 8;
+    q.nbp = q.nch * 8;
+    q.rows_pad = (rows + 3) / 4 * 4;
+    return q;
+}
+
+size_t q8_qs_bytes(int rows, int cols) {
+    const Q8Dev q = q8_shape(rows, cols);
+    return (size_t)(q.rows_pad / 4) * q.nch * 1024;
+}
+size_t q8_d_bytes(int rows, int cols) {
+    const Q8Dev q = q8_shape(rows, cols);
+    return (size_t)(q.rows_pad / 4) * q.nch * 64;
+}
+
+// ---------------------------------------------------------------- repack
+
+__global__ void repack_q8_kernel(const uint8_t* __restrict__ src, int rows, int nb, Q8Dev W, int row_base,
+                                 int row_stride) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)rows * nb) return;
+    const int r = (int)(i / nb), b = (int)(i % nb);
+    const uint8_t* s = src + i * 34;
+    const int R = row_base + r * row_stride;
+    const size_t chunk = q8_chunk(W, R, b >> 3);
+    const int ri = R & 3, j = b & 7;
+    uint8_t* q = W.qs + chunk * 1024 + (size_t)ri * 256 + j * 2;
+#pragma unroll
+    for (int g = 0; g < 16; g++)
+        *(uint16_t*)(q + g * 16) = (uint16_t)((uint32_t)s[2 + 2 * g] | ((uint32_t)s[3 + 2 * g] << 8));
+    W.d[chunk * 32 + ri * 8 + j] = (uint16_t)(s[0] | (s[1] << 8));
+}
+
+void launch_repack_q8(const uint8_t* src, int rows, int cols, const Q8Dev& dst, int row_base, int row_stride,
+                      hipStream_t st) {
+    const int nb = cols / 32;
+    const size_t n = (size_t)rows * nb;
+    hipLaunchKernelGGL(repack_q8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, src, rows, nb, dst,
+                       row_base, row_stride);
+}
+
+// ---------------------------------------------------------------- embedding (wmat_row, wmat_kernel.h:18-29)
+
+__global__ void embed_kernel(Q8Dev W, const float* __restrict__ f32, int hidden, const int* __restrict__ ids,
+                             int id0, const int* __restrict__ state, float* __restrict__ X) {
+    const int i = blockIdx.x;
+    const int id = state ? ids[state[0] - 1] : ids[id0 + i];
+    float* x = X + (size_t)i * hidden;
+    if (f32) {
+        const float* src = f32 + (size_t)id * hidden;
+        for (int c = threadIdx.x; c < hidden; c += blockDim.x) x[c] = src[c];
+    } else {
+        for (int c = threadIdx.x; c < hidden; c += blockDim.x) x[c] = q8_elem(W, id, c);
+    }
+}
+
+void launch_embed(const Q8Dev* q8, const float* f32, int hidden, const int* ids_dev, int id_index0,
+                  const int* state, int seq, float* X, hipStream_t st) {
+    Q8Dev w = q8 ? *q8 : Q8Dev{};
+    hipLaunchKernelGGL(embed_kernel, dim3(seq), dim3(256), 0, st, w, f32, hidden, ids_dev, id_index0, state, X);
+}
+
+// ---------------------------------------------------------------- RMSNorm
+
+// 16 FMA lanes over x^2 (lane l takes elements 16c+l; an 8-wide remainder pass
+// feeds lanes 0..7), then ((v0+v1) -> halves -> two hadds), scalar tail, then
+// y = (x*scale)*w with scale = 1/sqrtf(ss/n + eps).  The row is staged in LDS first.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ X, float* __restrict__ Y,
+                                                      const float* __restrict__ w, int n, float eps) {
+    extern __shared__ __align__(16) float xr[];
+    const float* x = X + (size_t)blockIdx.x * n;
+    float* y = Y + (size_t)blockIdx.x * n;
+    __shared__ float v[16];
+    __shared__ float sc;
+    __shared__ int zero;
+    const int t = threadIdx.x;
+    for (int i = t; i < n; i += blockDim.x) xr[i] = x[i];
+    __syncthreads();
+    const int n16 = n / 16 * 16;
+    const bool rem8 = n16 + 8 <= n;
+    if (t < 16) {
+        float a = 0.0f;
+#pragma unroll 8
+        for (int i = t; i < n16; i += 16) a = __builtin_fmaf(xr[i], xr[i], a);
+        if (t < 8 && rem8) a = __builtin_fmaf(xr[n16 + t], xr[n16 + t], a);
+        v[t] = a;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float s[8], q[4];
+#pragma unroll
+        for (int l = 0; l < 8; l++) s[l] = v[l] + v[8 + l];
+#pragma unroll
+        for (int l = 0; l < 4; l++) q[l] = s[l] + s[4 + l];
+        float ss = (q[0] + q[1]) + (q[2] + q[3]);
+        for (int i = n16 + (rem8 ? 8 : 0); i < n; i++) ss = __builtin_fmaf(xr[i], xr[i], ss);
+        const float den = ss / (float)n + eps;
+        zero = den <= 0.0f;
+        sc = zero ? 0.0f : 1.0f / sqrtf(den);
+    }
+    __syncthreads();
+    const float scale = sc;
+    const bool z = zero;
+    for (int i = t; i < n; i += blockDim.x) y[i] = z ? 0.0f : (xr[i] * scale) * w[i];
+}
+
+void launch_rmsnorm(const float* X, float* Y, const float* w, int n, int rows, float eps, hipStream_t st) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), (size_t)n * sizeof(float), st, X, Y, w, n, eps);
+}
+
+// ---------------------------------------------------------------- f32 matvec (decode, [K][N] weights)
+
+template <int EPI>
+__global__ __launch_bounds__(256) void matvec_f32_kernel(const float* __restrict__ B, const float* __restrict__ B2,
+                                                         int K, int N, const float* __restrict__ x,
+                                                         float* __restrict__ out, const float* __restrict__ aux) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= N) return;
+    float acc = 0.0f, acc2 = 0.0f;
+#pragma unroll 8
+    for (int p = 0; p < K; p++) {
+        const float xv = x[p];
+        acc = __builtin_fmaf(xv, B[(size_t)p * N + j], acc);
+        if (EPI == EPI_SWIGLU) acc2 = __builtin_fmaf(xv, B2[(size_t)p * N + j], acc2);
+    }
+    if (EPI == EPI_STORE) out[j] = acc;
+    if (EPI == EPI_BIAS) out[j] = acc + aux[j];
+    if (EPI == EPI_RESID) out[j] = out[j] + acc;
+    if (EPI == EPI_SWIGLU) out[j] = silu_ref(acc) * acc2;
+}
+
+void launch_matvec_f32(const float* B, const float* B2, int K, int N, const float* x, float* out, const float* aux,
+                       Epi epi, hipStream_t st) {
+    const dim3 grid((unsigned)((N + 255) / 256)), block(256);
+    switch (epi) {
+    case EPI_STORE:
+        hipLaunchKernelGGL(matvec_f32_kernel<EPI_STORE>, grid, block, 0, st, B, B2, K, N, x, out, aux);
+        break;
+    case EPI_BIAS:
+        hipLaunchKernelGGL(matvec_f32_kernel<EPI_BIAS>, grid, block, 0, st, B, B2, K, N, x, out, aux);
+        break;
+    case EPI_RESID:
+        hipLaunchKernelGGL(matvec_f32_kernel<EPI_RESID>, grid, block, 0, st, B, B2, K, N, x, out, aux);
+        break;
+    case EPI_SWIGLU:
+        hipLaunchKernelGGL(matvec_f32_kernel<EPI_SWIGLU>, grid, block, 0, st, B, B2, K, N, x, out, aux);
+        break;
+    }
+}
+
+// ---------------------------------------------------------------- prefill GEMMs (m > 1)
+
+// 64 tokens x 64 output rows per workgroup, 4x4 outputs per thread, k in order.
+// Q8: acc = acc + x*w, rounded separately (the generic path of matmul_q).
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_q8_kernel(Q8Dev W, int m, const float* __restrict__ A,
+                                                      float* __restrict__ Cm, const float* __restrict__ aux) {
+    __shared__ float xs[32][68];
+    __shared__ float ws[32][68];
+    const int t = threadIdx.x, ti = t & 15, tj = t >> 4;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const int K = W.cols, N = W.rows;
+    float acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[a][b] = 0.0f;
+    const int lt = t >> 2, lc = (t & 3) * 8;  // loader: token/row lt, k offset lc
+    for (int blk = 0; blk < W.nb; blk++) {
+        {
+            const int tok = m0 + lt;
+#pragma unroll
+            for (int c = 0; c < 8; c++) xs[lc + c][lt] = tok < m ? A[(size_t)tok * K + blk * 32 + lc + c] : 0.0f;
+            const int R = n0 + lt;
+#pragma unroll
+            for (int c = 0; c < 8; c++) ws[lc + c][lt] = R < N ? q8_elem(W, R, blk * 32 + lc + c) : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int kk = 0; kk < 32; kk++) {
+            const float4 xv = *reinterpret_cast<const float4*>(&xs[kk][ti * 4]);
+            const float4 wv = *reinterpret_cast<const float4*>(&ws[kk][tj * 4]);
+            const float xa[4] = {xv.x, xv.y, xv.z, xv.w}, wa[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) acc[a][b] = __fadd_rn(acc[a][b], __fmul_rn(xa[a], wa[b]));
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const int i = m0 + ti * 4 + a;
+        if (i >= m) continue;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int j = n0 + tj * 4 + b;
+            if (j >= N) continue;
+            float* c = Cm + (size_t)i * N + j;
+            if (EPI == EPI_STORE) *c = acc[a][b];
+            if (EPI == EPI_BIAS) *c = acc[a][b] + aux[j];
+            if (EPI == EPI_RESID) *c = *c + acc[a][b];
+        }
+    }
+}
+
+// f32 [K][N]: C = fma(A[i][p], B[p][j], C) in order of p.
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ B, int K, int N, int m,
+                                                       const float* __restrict__ A, float* __restrict__ Cm,
+                                                       const float* __restrict__ aux) {
+    __shared__ float xs[32][68];
+    __shared__ float ws[32][68];
+    const int t = threadIdx.x, ti = t & 15, tj = t >> 4;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    float acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[a][b] = 0.0f;
+    const int lt = t >> 2, lc = (t & 3) * 8;
+    for (int k0 = 0; k0 < K; k0 += 32) {
+        const int tok = m0 + lt;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const int k = k0 + lc + c;
+            xs[lc + c][lt] = (tok < m && k < K) ? A[(size_t)tok * K + k] : 0.0f;
+        }
+        // B rows k0..k0+31, columns n0..n0+63: thread loads 8 of them
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const int e = t * 8 + c, kk = e >> 6, col = e & 63;
+            const int k = k0 + kk, j = n0 + col;
+            ws[kk][col] = (k < K && j < N) ? B[(size_t)k * N + j] : 0.0f;
+        }
+        __syncthreads();
+        const int kmax = K - k0 < 32 ? K - k0 : 32;
+        for (int kk = 0; kk < kmax; kk++) {
+            const float4 xv = *reinterpret_cast<const float4*>(&xs[kk][ti * 4]);
+            const float4 wv = *reinterpret_cast<const float4*>(&ws[kk][tj * 4]);
+            const float xa[4] = {xv.x, xv.y, xv.z, xv.w}, wa[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) acc[a][b] = __builtin_fmaf(xa[a], wa[b], acc[a][b]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const int i = m0 + ti * 4 + a;
+        if (i >= m) continue;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int j = n0 + tj * 4 + b;
+            if (j >= N) continue;
+            float* c = Cm + (size_t)i * N + j;
+            if (EPI == EPI_STORE) *c = acc[a][b];
+            if (EPI == EPI_BIAS) *c = acc[a][b] + aux[j];
+            if (EPI == EPI_RESID) *c = *c + acc[a][b];
+        }
+    }
+}
+
+void launch_gemm_q8(const Q8Dev& W, int m, const float* A, float* C, const float* aux, Epi epi, hipStream_t st) {
+    const dim3 grid((unsigned)((W.rows + 63) / 64), (unsigned)((m + 63) / 64)), block(256);
+    if (epi == EPI_STORE) hipLaunchKernelGGL(gemm_q8_kernel<EPI_STORE>, grid, block, 0, st, W, m, A, C, aux);
+    if (epi == EPI_BIAS) hipLaunchKernelGGL(gemm_q8_kernel<EPI_BIAS>, grid, block, 0, st, W, m, A, C, aux);
+    if (epi == EPI_RESID) hipLaunchKernelGGL(gemm_q8_kernel<EPI_RESID>, grid, block, 0, st, W, m, A, C, aux);
+}
+
+void launch_gemm_f32(const float* B, int K, int N, int m, const float* A, float* C, const float* aux, Epi epi,
+                     hipStream_t st) {
+    const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((m + 63) / 64)), block(256);
+    if (epi == EPI_STORE) hipLaunchKernelGGL(gemm_f32_kernel<EPI_STORE>, grid, block, 0, st, B, K, N, m, A, C, aux);
+    if (epi == EPI_BIAS) hipLaunchKernelGGL(gemm_f32_kernel<EPI_BIAS>, grid, block, 0, st, B, K, N, m, A, C, aux);
+    if (epi == EPI_RESID) hipLaunchKernelGGL(gemm_f32_kernel<EPI_RESID>, grid, block, 0, st, B, K, N, m, A, C, aux);
+}
+
+__global__ void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u, int interleaved, int m,
+                                int F, float* __restrict__ h) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (size_t)m * F) return;
+    const size_t i = e / F, j = e % F;
+    const float gv = interleaved ? g[i * 2 * F + 2 * j] : g[e];
+    const float uv = interleaved ? g[i * 2 * F + 2 * j + 1] : u[e];
+    h[e] = silu_ref(gv) * uv;
+}
+
+void launch_silu_mul(const float* g, const float* u, int interleaved, int m, int F, float* h, hipStream_t st) {
+    const size_t n = (size_t)m * F;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, interleaved, m, F, h);
+}
+
+// ---------------------------------------------------------------- RoPE + int8 packing
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// One workgroup per token row.  Rotation of pair m of a head uses the table row of
+// position pos; within every full group of 8 pairs the reference's store order puts
+// rotated pairs (4,5) in slots (2,3) and pairs (2,3) in slots (4,5)
+// (rope/x86/x86_classic.txt:23-29); remainder pairs stay in place.  Then K (after
+// RoPE) and V are packed into the cache and Q is quantised per head.
+__global__ __launch_bounds__(256) void rope_pack_kernel(float* __restrict__ qkv, int start_pos,
+                                                        const int* __restrict__ state, int nh, int nkv, int hd,
+                                                        const float* __restrict__ cos_t,
+                                                        const float* __restrict__ sin_t, KVDev kv, int layer,
+                                                        int8_t* __restrict__ q8, float* __restrict__ qsc) {
+    extern __shared__ __align__(16) float sm[];
+    const int row = blockIdx.x;
+    const int pos = state ? state[0] - 1 : start_pos + row;
+    const int half = hd / 2, qd = nh * hd, kvd = nkv * hd;
+    float* base = qkv + (size_t)row * (qd + 2 * kvd);
+    const float* c = cos_t + (size_t)pos * half;
+    const float* s = sin_t + (size_t)pos * half;
+    const int npairs = (nh + nkv) * half;
+    const int full = half / 8 * 8;
+    for (int e = threadIdx.x; e < npairs; e += blockDim.x) {
+        const int hh = e / half, m = e - hh * half;
+        const float* xh = base + (size_t)hh * hd;
+        const float x0 = xh[2 * m], x1 = xh[2 * m + 1];
+        const float cm = c[m], sn = s[m];
+        const float y0 = __builtin_fmaf(x0, cm, -(x1 * sn));
+        const float y1 = __builtin_fmaf(x0, sn, x1 * cm);
+        int dst = m;
+        if (m < full) {
+            const int o = m & 7;
+            dst = m - o + ((o == 2 || o == 3) ? o + 2 : (o == 4 || o == 5) ? o - 2 : o);
+        }
+        sm[hh * hd + 2 * dst] = y0;
+        sm[hh * hd + 2 * dst + 1] = y1;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < (nh + nkv) * hd; e += blockDim.x) base[e] = sm[e];
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int hh = wave; hh < nh + 2 * nkv; hh += nw) {
+        const float* src = base + (size_t)hh * hd;
+        float amax = 0.0f;
+        for (int d = lane; d < hd; d += 64) amax = fmaxf(amax, fabsf(src[d]));
+        amax = wave_max(amax);
+        const float inv = quant_inv(amax), scl = quant_scale(amax);
+        int8_t* dst;
+        float* sdst;
+        if (hh < nh) {
+            dst = q8 + ((size_t)row * nh + hh) * hd;
+            sdst = qsc + (size_t)row * nh + hh;
+        } else {
+            const bool isv = hh >= nh + nkv;
+            const int kh = hh - nh - (isv ? nkv : 0);
+            const size_t slot = ((size_t)layer * nkv + kh) * kv.max_seq + pos;
+            dst = (isv ? kv.v : kv.k) + slot * hd;
+            sdst = (isv ? kv.vs : kv.ks) + slot;
+        }
+        for (int d = lane; d < hd; d += 64) dst[d] = quant_i8(src[d], inv);
+        if (lane == 0) *sdst = scl;
+    }
+}
+
+void launch_rope_pack(float* qkv, int seq, int start_pos, const int* state, int nh, int nkv, int hd,
+                      const float* cos_t, const float* sin_t, const KVDev& kv, int layer, int8_t* q8, float* qsc,
+                      hipStream_t st) {
+    const size_t lds = (size_t)(nh + nkv) * hd * sizeof(float);
+    hipLaunchKernelGGL(rope_pack_kernel, dim3(seq), dim3(256), lds, st, qkv, start_pos, state, nh, nkv, hd, cos_t,
+                       sin_t, kv, layer, q8, qsc);
+}
+
+// ---------------------------------------------------------------- greedy selection
+
+// next = first index of the strict maximum (generate.h:57-60); repetition penalty
+// first, applied once per occurrence in generation order (generate.h:50-56): ids
+// are split across threads by value, so each id's occurrences stay in order.
+__global__ __launch_bounds__(1024) void argmax_kernel(float* __restrict__ logits, int V, int* __restrict__ ids,
+                                                      int* __restrict__ state, const int* __restrict__ eos,
+                                                      int neos, float rp, int prompt_len) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    const int t = threadIdx.x;
+    const int len = state[0];
+    if (rp != 1.0f) {
+        for (int i = prompt_len; i < len; i++) {
+            const int id = ids[i];
+            if (id >= 0 && id < V && (id & 1023) == t) {
+                const float l = logits[id];
+                logits[id] = l > 0.0f ? l / rp : l * rp;
+            }
+        }
+        __syncthreads();
+    }
+    float best = -__builtin_inff();
+    int bidx = 0x7fffffff;
+    for (int v = t; v < V; v += blockDim.x) {
+        const float l = logits[v];
+        if (l > best || bidx == 0x7fffffff) {
+            if (!(l <= best)) {
+                best = l;
+                bidx = v;
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o);
+        const int oi = __shfl_xor(bidx, o);
+        if (ov > best || (ov == best && oi < bidx)) {
+            best = ov;
+            bidx = oi;
+        }
+    }
+    if ((t & 63) == 0) {
+        bv[t >> 6] = best;
+        bi[t >> 6] = bidx;
+    }
+    __syncthreads();
+    if (t == 0) {
+        best = bv[0];
+        bidx = bi[0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+            if (bv[w] > best || (bv[w] == best && bi[w] < bidx)) {
+                best = bv[w];
+                bidx = bi[w];
+            }
+        if (bidx == 0x7fffffff) bidx = 0;
+        if (!state[1]) {
+            ids[len] = bidx;
+            state[0] = len + 1;
+            for (int e = 0; e < neos; e++)
+                if (bidx == eos[e]) state[1] = 1;
+        }
+    }
+}
+
+void launch_argmax(const float* logits, int V, int* ids, int* state, const int* eos, int neos, float rep_penalty,
+                   int prompt_len, hipStream_t st) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, st, const_cast<float*>(logits), V, ids, state, eos, neos,
+                       rep_penalty, prompt_len);
+}
+
+// ---------------------------------------------------------------- KV layout conversion
+
+__global__ void kv_import_kernel(const int8_t* __restrict__ k_ref, const float* __restrict__ ks_ref,
+                                 const int8_t* __restrict__ v_ref, const float* __restrict__ vs_ref, int pos0,
+                                 int npos, KVDev kv, int layer) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t per = (size_t)kv.nkv * kv.hd;
+    if (e >= (size_t)npos * per) return;
+    const int p = (int)(e / per), rem = (int)(e % per), h = rem / kv.hd, d = rem % kv.hd;
+    const size_t slot = ((size_t)layer * kv.nkv + h) * kv.max_seq + pos0 + p;
+    kv.k[slot * kv.hd + d] = k_ref[e];
+    kv.v[slot * kv.hd + d] = v_ref[e];
+    if (d == 0) {
+        kv.ks[slot] = ks_ref[(size_t)p * kv.nkv + h];
+        kv.vs[slot] = vs_ref[(size_t)p * kv.nkv + h];
+    }
+}
+
+__global__ void kv_export_kernel(int8_t* __restrict__ k_ref, float* __restrict__ ks_ref, int8_t* __restrict__ v_ref,
+                                 float* __restrict__ vs_ref, int pos0, int npos, KVDev kv, int layer) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t per = (size_t)kv.nkv * kv.hd;
+    if (e >= (size_t)npos * per) return;
+    const int p = (int)(e / per), rem = (int)(e % per), h = rem / kv.hd, d = rem % kv.hd;
+    const size_t slot = ((size_t)layer * kv.nkv + h) * kv.max_seq + pos0 + p;
+    k_ref[e] = kv.k[slot * kv.hd + d];
+    v_ref[e] = kv.v[slot * kv.hd + d];
+    if (d == 0) {
+        ks_ref[(size_t)p * kv.nkv + h] = kv.ks[slot];
+        vs_ref[(size_t)p * kv.nkv + h] = kv.vs[slot];
+    }
+}
+
+void launch_kv_import(const int8_t* k_ref, const float* ks_ref, const int8_t* v_ref, const float* vs_ref, int pos0,
+                      int npos, const KVDev& kv, int layer, hipStream_t st) {
+    const size_t n = (size_t)npos * kv.nkv * kv.hd;
+    hipLaunchKernelGGL(kv_import_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, k_ref, ks_ref, v_ref,
+                       vs_ref, pos0, npos, kv, layer);
+}
+
+void launch_kv_export(int8_t* k_ref, float* ks_ref, int8_t* v_ref, float* vs_ref, int pos0, int npos,
+                      const KVDev& kv, int layer, hipStream_t st) {
+    const size_t n = (size_t)npos * kv.nkv * kv.hd;
+    hipLaunchKernelGGL(kv_export_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, k_ref, ks_ref, v_ref,
+                       vs_ref, pos0, npos, kv, layer);
+}
+
+}  // namespace jy

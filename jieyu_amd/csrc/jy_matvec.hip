@@ -1,0 +1,401 @@
+// jy_matvec.hip — the decode-step Q8_0 matvec (one token, batch 1).
+//
+// Arithmetic of dot_row_avx2 (libs/matmul_libs/matmul_q.h:111-132), bit for bit:
+// 32 virtual FMA lanes per row, lane L accumulates x[32b+L] * (q*d) over the
+// blocks b in order, then the fixed tree
+//   s[i] = (a[i]+a[8+i]) + (a[16+i]+a[24+i]),  r[i] = s[i]+s[4+i],  y = (r0+r1)+(r2+r3).
+// Each thread owns two lanes of one row (16 threads per row, 4 rows per wave),
+// so a row's 32 chains run in parallel and the tree is four butterflies plus an
+// in-lane add.  Weights stream from HBM as 16 B per lane (1 KiB per wave per
+// chunk of 8 blocks) with eight chunks in flight; the activation vector sits in
+// LDS, lane-pair major, and is optionally RMS-normalised there first (the
+// reference's rmsnorm, libs/model_libs/rmsnorm/x86/x86_classic.txt).
+// Dequantisation is one v_fma_mix (q * fp16 scale, exact) per weight.
+#include "jy_layout.h"
+
+namespace jy {
+
+static constexpr int MV_U = 4;  // chunks per register buffer (two buffers)
+
+__device__ __forceinline__ int xs_index(int k, int XS) {
+    return ((k & 31) >> 1) * XS + 2 * (k >> 5) + (k & 1);
+}
+
+__device__ __forceinline__ void mv_chunk(const uint4& w, const uint4& dd, const float* xrow, int cc, float& a0,
+                                         float& a1) {
+    const float4* xp = reinterpret_cast<const float4*>(xrow + cc * 16);
+    const float4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+    const float xv[16] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
+                          x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+    const uint32_t dv[4] = {dd.x, dd.y, dd.z, dd.w};
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t word = wv[j >> 1];
+        const int sh = (j & 1) * 16;
+        const float q0 = (float)(int8_t)(word >> sh);
+        const float q1 = (float)(int8_t)(word >> (sh + 8));
+        const float dh = (float)__builtin_bit_cast(_Float16, (uint16_t)(dv[j >> 1] >> sh));
+        const float w0 = __builtin_fmaf(q0, dh, 0.0f);  // exact q*d; +0 addend only affects the sign of 0
+        const float w1 = __builtin_fmaf(q1, dh, 0.0f);
+        a0 = __builtin_fmaf(xv[2 * j], w0, a0);
+        a1 = __builtin_fmaf(xv[2 * j + 1], w1, a1);
+    }
+}
+
+// one wave owns row groups wid, wid + TW, ... (TW = waves in the grid), `per` of
+// them; the chunk stream of consecutive row groups is pipelined without a gap.
+template <int EPI, bool NORM>
+__global__ __launch_bounds__(1024) void matvec_q8_kernel(Q8Dev W, const float* __restrict__ x,
+                                                         const float* __restrict__ nw, float* __restrict__ out,
+                                                         MvArgs a, int per) {
+    // [16][XS]: lane pair g, block b, lane c.  16-byte alignment keeps the ds_read_b128
+    // of the main loop aligned whatever static LDS the epilogue adds.
+    extern __shared__ __align__(16) float xs[];
+    __shared__ float red[18];
+    __shared__ float rowv[64];
+    __shared__ int rowi[64];
+    __shared__ int s_last;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwv = blockDim.x >> 6;
+    const int TW = gridDim.x * nwv, wid = blockIdx.x * nwv + wave;
+    const int r = lane >> 4, g = lane & 15;
+    const int K = W.cols, nch = W.nch, XS = 2 * W.nbp + 4;
+    const int nchp = (nch + 2 * MV_U - 1) / (2 * MV_U) * (2 * MV_U);
+    const int groups = (W.rows + 3) >> 2;
+
+    // chunk at loop position `p` of the wave's it-th row group (positions past the
+    // padded chunk count belong to the next row group).  Loads are unconditional
+    // (positions with no chunk re-read chunk 0, and are never computed), so the
+    // number of loads in flight is static and the waits stay partial.
+    const uint4* qs4 = reinterpret_cast<const uint4*>(W.qs);
+    const uint4* d4 = reinterpret_cast<const uint4*>(W.d);
+    auto load = [&](uint4* wb, uint4* db, int it, int p0) {
+#pragma unroll
+        for (int u = 0; u < MV_U; u++) {
+            int p = p0 + u, i2 = it;
+            if (p >= nchp) {
+                p -= nchp;
+                i2++;
+            }
+            const int rg = wid + i2 * TW;
+            const size_t c = (i2 < per && rg < groups && p < nch) ? (size_t)rg * nch + p : 0;
+            wb[u] = qs4[c * 64 + lane];
+            db[u] = d4[c * 4 + r];
+        }
+    };
+
+    // both register buffers are in flight before the prologue (staging, RMSNorm), and
+    // stay two buffers ahead of the compute afterwards
+    uint4 wA[MV_U], dA[MV_U], wB[MV_U], dB[MV_U];
+    load(wA, dA, 0, 0);
+    load(wB, dB, 0, MV_U);
+
+    // stage x, four floats per load, eight loads in flight per thread (zero past K:
+    // padding blocks then contribute exact zeros)
+    {
+        const int nv4 = W.nbp * 8;
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        for (int base = tid; base < nv4; base += 8 * blockDim.x) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = base + u * blockDim.x;
+                v[u] = (i < nv4 && 4 * i < K) ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = base + u * blockDim.x;
+                if (i < nv4) {
+                    const int k = 4 * i;
+                    xs[xs_index(k, XS)] = v[u].x;
+                    xs[xs_index(k + 1, XS)] = v[u].y;
+                    xs[xs_index(k + 2, XS)] = v[u].z;
+                    xs[xs_index(k + 3, XS)] = v[u].w;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (NORM) {
+        // rmsnorm: 16 FMA lanes over x^2 (lane l: elements 16c+l), 8-wide remainder,
+        // ((v0+v1) -> halves -> two hadds), den = ss/n + eps, scale = 1/sqrtf(den)
+        const int n16 = K / 16 * 16;
+        const bool rem8 = n16 + 8 <= K;
+        if (tid < 16) {
+            float v = 0.0f;
+#pragma unroll 8
+            for (int k = tid; k < n16; k += 16) {
+                const float e = xs[xs_index(k, XS)];
+                v = __builtin_fmaf(e, e, v);
+            }
+            if (tid < 8 && rem8) {
+                const float e = xs[xs_index(n16 + tid, XS)];
+                v = __builtin_fmaf(e, e, v);
+            }
+            red[tid] = v;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float s[8], q[4];
+#pragma unroll
+            for (int l = 0; l < 8; l++) s[l] = red[l] + red[8 + l];
+#pragma unroll
+            for (int l = 0; l < 4; l++) q[l] = s[l] + s[4 + l];
+            float ss = (q[0] + q[1]) + (q[2] + q[3]);
+            for (int k = n16 + (rem8 ? 8 : 0); k < K; k++) {
+                const float e = xs[xs_index(k, XS)];
+                ss = __builtin_fmaf(e, e, ss);
+            }
+            const float den = ss / (float)K + 1e-5f;
+            red[17] = den <= 0.0f ? 1.0f : 0.0f;
+            red[16] = den <= 0.0f ? 0.0f : 1.0f / sqrtf(den);
+        }
+        __syncthreads();
+        const float scale = red[16];
+        const bool zero = red[17] != 0.0f;
+        const float4* w4 = reinterpret_cast<const float4*>(nw);
+        const int nk4 = K / 4;
+        for (int base = tid; base < nk4; base += 8 * blockDim.x) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = base + u * blockDim.x;
+                if (i < nk4) v[u] = w4[i];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = base + u * blockDim.x;
+                if (i < nk4) {
+                    const float wv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        const int xi = xs_index(4 * i + c, XS);
+                        xs[xi] = zero ? 0.0f : (xs[xi] * scale) * wv[c];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    const float* xrow = xs + g * XS;
+    float best_v = -__builtin_inff();
+    int best_i = 0x7fffffff;
+    for (int it = 0; it < per; it++) {
+        const int rg = wid + it * TW;
+        const bool active = rg < groups;
+        float a0 = 0.0f, a1 = 0.0f;
+        for (int ch = 0; ch < nchp; ch += 2 * MV_U) {
+            if (active) {
+#pragma unroll
+                for (int u = 0; u < MV_U; u++)
+                    if (ch + u < nch) mv_chunk(wA[u], dA[u], xrow, ch + u, a0, a1);
+            }
+            load(wA, dA, it, ch + 2 * MV_U);
+            if (active) {
+#pragma unroll
+                for (int u = 0; u < MV_U; u++)
+                    if (ch + MV_U + u < nch) mv_chunk(wB[u], dB[u], xrow, ch + MV_U + u, a0, a1);
+            }
+            load(wB, dB, it, ch + 3 * MV_U);
+        }
+        // lanes 2g, 2g+1 -> the reference's reduction tree
+        a0 += __shfl_xor(a0, 4);
+        a1 += __shfl_xor(a1, 4);
+        a0 += __shfl_xor(a0, 8);
+        a1 += __shfl_xor(a1, 8);
+        a0 += __shfl_xor(a0, 2);
+        a1 += __shfl_xor(a1, 2);
+        const float t = a0 + a1;
+        const float y = t + __shfl_xor(t, 1);
+        const int row = rg * 4 + r;
+        const bool own = active && g == 0 && row < W.rows;
+
+        if (EPI == EPI_STORE) {
+            if (own) out[row] = y;
+        } else if (EPI == EPI_BIAS) {
+            if (own) out[row] = y + a.aux[row];
+        } else if (EPI == EPI_RESID) {
+            if (own) out[row] = out[row] + y;
+        } else if (EPI == EPI_SWIGLU) {
+            // rows are interleaved gate/up pairs: h = silu(gate) * up (libs/model_libs/ffn/ffn.h:13-17)
+            const float up = __shfl_xor(y, 16);
+            if (own && !(r & 1) && row + 1 < W.rows) out[row >> 1] = silu_ref(y) * up;
+        } else if (EPI == EPI_ROPE) {
+            // q/k rows: bias, then rope_at on the pair (2m, 2m+1) with the reference's
+            // store order inside each group of 8 pairs (libs/model_libs/rope/x86/x86_classic.txt:10-29)
+            const float yb = a.aux ? y + (own ? a.aux[row] : 0.0f) : y;
+            const float partner = __shfl_xor(yb, 16);
+            const int qk_rows = (a.nh + a.nkv) * a.hd;
+            if (own) {
+                if (row >= qk_rows) {
+                    out[row] = yb;
+                } else if (!(r & 1)) {
+                    const int hd = a.hd, half = hd >> 1;
+                    const int head = row / hd, m = (row - head * hd) >> 1;
+                    const int pos = a.state ? a.state[0] - 1 : a.pos0;
+                    const float c = a.cos_t[(size_t)pos * half + m], s = a.sin_t[(size_t)pos * half + m];
+                    const float y0 = __builtin_fmaf(yb, c, -(partner * s));
+                    const float y1 = __builtin_fmaf(yb, s, partner * c);
+                    int dst = m;
+                    if (m < half / 8 * 8) {
+                        const int o = m & 7;
+                        dst = m - o + ((o == 2 || o == 3) ? o + 2 : (o == 4 || o == 5) ? o - 2 : o);
+                    }
+                    out[head * hd + 2 * dst] = y0;
+                    out[head * hd + 2 * dst + 1] = y1;
+                }
+            }
+        } else if (EPI == EPI_ARGMAX) {
+            if (own) {
+                out[row] = y;
+                if (y > best_v || (y == best_v && row < best_i)) {
+                    best_v = y;
+                    best_i = row;
+                }
+            }
+        }
+    }
+
+    if (EPI == EPI_ARGMAX) {
+        // first index of the strict maximum (generate.h:57-60): per-workgroup first max,
+        // then the last workgroup to finish scans the partials
+        if (g == 0) {
+            rowv[wave * 4 + r] = best_v;
+            rowi[wave * 4 + r] = best_i;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float bv = rowv[0];
+            int bi = rowi[0];
+            for (int i = 1; i < nwv * 4; i++)
+                if (rowv[i] > bv || (rowv[i] == bv && rowi[i] < bi)) {
+                    bv = rowv[i];
+                    bi = rowi[i];
+                }
+            __hip_atomic_store(&a.part_val[blockIdx.x], bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&a.part_idx[blockIdx.x], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned done = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = done == gridDim.x - 1;
+        }
+        __syncthreads();
+        if (s_last) {
+            __atomic_thread_fence(__ATOMIC_ACQUIRE);
+            const int np = gridDim.x;
+            float bv = -__builtin_inff();
+            int bi = 0x7fffffff;
+            for (int i = tid; i < np; i += blockDim.x) {
+                const float v = __hip_atomic_load(&a.part_val[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const int ix = __hip_atomic_load(&a.part_idx[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (v > bv || (v == bv && ix < bi)) {
+                    bv = v;
+                    bi = ix;
+                }
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(bv, o);
+                const int oi = __shfl_xor(bi, o);
+                if (ov > bv || (ov == bv && oi < bi)) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+            if (lane == 0) {
+                rowv[wave] = bv;
+                rowi[wave] = bi;
+            }
+            __syncthreads();
+            if (tid == 0) {
+                bv = rowv[0];
+                bi = rowi[0];
+                for (int w = 1; w < nwv; w++)
+                    if (rowv[w] > bv || (rowv[w] == bv && rowi[w] < bi)) {
+                        bv = rowv[w];
+                        bi = rowi[w];
+                    }
+                if (bi == 0x7fffffff) bi = 0;
+                if (!a.mstate[1]) {
+                    const int len = a.mstate[0];
+                    a.ids[len] = bi;
+                    a.mstate[0] = len + 1;
+                    for (int e = 0; e < a.neos; e++)
+                        if (bi == a.eos[e]) a.mstate[1] = 1;
+                }
+                __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+}
+
+static int g_cus = 256;
+
+// launch shape: 4 waves per workgroup, at most 4 workgroups per CU; each wave owns
+// `per` row groups so the prologue (staging, RMSNorm) is paid once per workgroup
+static void mv_shape(const Q8Dev& W, int* grid, int* per) {
+    const int nwv = 4;
+    const int groups = (W.rows + 3) / 4;
+    const int max_waves = 4 * g_cus * nwv;
+    *per = (groups + max_waves - 1) / max_waves;
+    *grid = (groups + nwv * *per - 1) / (nwv * *per);
+}
+
+int argmax_partials(int rows) {
+    Q8Dev w;
+    w.rows = rows;
+    int grid, per;
+    mv_shape(w, &grid, &per);
+    return grid;
+}
+
+template <int EPI, bool NORM>
+static void mv_launch(const Q8Dev& W, const float* x, const float* nw, float* out, const MvArgs& a, hipStream_t st) {
+    int grid, per;
+    mv_shape(W, &grid, &per);
+    const size_t lds = (size_t)16 * (2 * W.nbp + 4) * sizeof(float);
+    hipLaunchKernelGGL((matvec_q8_kernel<EPI, NORM>), dim3(grid), dim3(256), lds, st, W, x, nw, out, a, per);
+}
+
+
+template <bool NORM>
+static void mv_dispatch(const Q8Dev& W, const float* x, const float* nw, float* out, Epi epi, const MvArgs& a,
+                        hipStream_t st) {
+    switch (epi) {
+    case EPI_STORE: mv_launch<EPI_STORE, NORM>(W, x, nw, out, a, st); break;
+    case EPI_BIAS: mv_launch<EPI_BIAS, NORM>(W, x, nw, out, a, st); break;
+    case EPI_RESID: mv_launch<EPI_RESID, NORM>(W, x, nw, out, a, st); break;
+    case EPI_SWIGLU: mv_launch<EPI_SWIGLU, NORM>(W, x, nw, out, a, st); break;
+    case EPI_ROPE: mv_launch<EPI_ROPE, NORM>(W, x, nw, out, a, st); break;
+    case EPI_ARGMAX: mv_launch<EPI_ARGMAX, NORM>(W, x, nw, out, a, st); break;
+    }
+}
+
+void launch_matvec_q8(const Q8Dev& W, const float* x, const float* norm_w, float* out, Epi epi, const MvArgs& a,
+                      hipStream_t st) {
+    if (norm_w)
+        mv_dispatch<true>(W, x, norm_w, out, epi, a, st);
+    else
+        mv_dispatch<false>(W, x, nullptr, out, epi, a, st);
+}
+
+template <int EPI, bool NORM>
+static hipError_t mv_attr() {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&matvec_q8_kernel<EPI, NORM>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 2048);
+}
+
+hipError_t matvec_init() {
+    int dev = 0, cus = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    if (cus > 0) g_cus = cus;
+    for (hipError_t r : {mv_attr<EPI_STORE, false>(), mv_attr<EPI_BIAS, false>(), mv_attr<EPI_RESID, false>(),
+                         mv_attr<EPI_SWIGLU, false>(), mv_attr<EPI_ROPE, false>(), mv_attr<EPI_ARGMAX, false>(),
+                         mv_attr<EPI_STORE, true>(), mv_attr<EPI_BIAS, true>(), mv_attr<EPI_RESID, true>(),
+                         mv_attr<EPI_SWIGLU, true>(), mv_attr<EPI_ROPE, true>(), mv_attr<EPI_ARGMAX, true>()})
+        if (r != hipSuccess && e == hipSuccess) e = r;
+    return e;
+}
+
+}  // namespace jy

@@ -1,0 +1,1117 @@
+// jy_runtime.cpp — host side of the MI355X decode path (C++17 over HIP).
+//
+// Owns device-resident models and KV caches and drives the per-token step:
+// prefill (the prompt, seq > 1) launches the GEMM kernels directly; every later
+// token replays one captured HIP graph whose kernels read the position from a
+// device-side state word, so no host round trip is needed between tokens.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "jieyu_amd.h"
+#include "jy_kernels.h"
+
+using namespace jy;
+
+namespace {
+
+thread_local std::string g_err;
+
+struct Error {
+    std::string msg;
+};
+
+void fail(const std::string& m) { throw Error{m}; }
+
+void ck(hipError_t e, const char* what) {
+    if (e != hipSuccess) fail(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define CK(x) ck((x), #x)
+
+template <class T>
+T* dalloc(size_t n, bool zero = true) {
+    void* p = nullptr;
+    if (n == 0) n = 1;
+    CK(hipMalloc(&p, n * sizeof(T)));
+    if (zero) CK(hipMemset(p, 0, n * sizeof(T)));
+    return (T*)p;
+}
+
+void dfree(void* p) {
+    if (p) (void)hipFree(p);
+}
+
+// RoPETable::init (libs/date_libs/date.h:52-66): float arithmetic with the host
+// libm, the same functions the reference calls, so the tables are identical.
+void rope_table(int max_seq, int head_dim, float theta, std::vector<float>& c, std::vector<float>& s) {
+    const int half = head_dim / 2;
+    c.resize((size_t)max_seq * half);
+    s.resize((size_t)max_seq * half);
+    for (int i = 0; i < max_seq; i++)
+        for (int j = 0; j < half; j++) {
+            const float freq = 1.0f / powf(theta, 2.0f * (float)j / (float)head_dim);
+            const float ang = (float)i * freq;
+            c[(size_t)i * half + j] = cosf(ang);
+            s[(size_t)i * half + j] = sinf(ang);
+        }
+}
+
+size_t q8_bytes(size_t rows, size_t cols) { return rows * (cols / 32) * 34; }
+
+// per-device kernel attributes (dynamic LDS limits), once per device and process
+void init_device_kernels(int device) {
+    static bool done[64] = {};
+    if (device < 0 || device >= 64) fail("device index out of range");
+    if (done[device]) return;
+    ck(kernels_init(), "kernel attributes");
+    done[device] = true;
+}
+
+}  // namespace
+
+struct DevLayer {
+    float* rms1 = nullptr;
+    float* rms2 = nullptr;
+    float* bqkv = nullptr;
+    Q8Dev qkv, o, gu, down;                        // JY_Q8_0
+    float *f_qkv = nullptr, *f_o = nullptr;        // JY_F32 [K][N]
+    float *f_w1 = nullptr, *f_w3 = nullptr, *f_w2 = nullptr;
+};
+
+struct Workspace {
+    int rows = 0;  // capacity in token rows
+    float *X = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *g = nullptr, *u = nullptr, *h = nullptr;
+    int8_t* q8 = nullptr;
+    float* qsc = nullptr;
+    float* scores = nullptr;
+    size_t scores_n = 0;
+};
+
+struct jyhip_model {
+    int device = 0;
+    int L = 0, H = 0, nh = 0, nkv = 0, hd = 0, F = 0, V = 0;
+    int qd = 0, kvd = 0;
+    int wtype = JY_Q8_0;
+    bool bias = false;
+    int max_seq = 0;
+    float theta = 0.0f;
+    float *cos_t = nullptr, *sin_t = nullptr;
+    Q8Dev embed_q8, lm_q8;
+    bool lm_shares_embed = false;
+    float *embed_f32 = nullptr, *lm_f32 = nullptr;
+    float* final_rms = nullptr;
+    std::vector<DevLayer> layers;
+    size_t weight_bytes = 0;
+    double upload_ms = 0.0;
+    hipStream_t stream = nullptr;
+    Workspace ws;
+    float* logits = nullptr;
+    int* ids = nullptr;      // [max_seq + 1]
+    int* state = nullptr;    // [0] = sequence length, [1] = stop flag
+    int* eos = nullptr;      // [eos_cap]
+    int eos_cap = 0;
+    float* part_val = nullptr;  // lm_head argmax partials
+    int* part_idx = nullptr;
+    unsigned* counter = nullptr;
+    std::vector<void*> owned;
+};
+
+struct jyhip_kv {
+    KVDev dev;
+    int current_len = 0;
+    int device = 0;
+};
+
+struct jyhip_q8mat {
+    std::vector<Q8Dev> copies;
+    float* x = nullptr;
+    float* y = nullptr;
+    hipStream_t stream = nullptr;
+    int next = 0;
+};
+
+namespace {
+
+void* own(jyhip_model* m, void* p) {
+    m->owned.push_back(p);
+    return p;
+}
+
+Q8Dev q8_alloc(jyhip_model* m, int rows, int cols) {
+    Q8Dev q = q8_shape(rows, cols);
+    q.qs = (uint8_t*)own(m, dalloc<uint8_t>(q8_qs_bytes(rows, cols)));
+    q.d = (uint16_t*)own(m, dalloc<uint8_t>(q8_d_bytes(rows, cols)));
+    return q;
+}
+
+// host jieyu Q8_0 rows -> staging -> tiled rows [row_base + r*row_stride]
+void q8_put(jyhip_model* m, uint8_t* staging, const void* src, int rows, int cols, const Q8Dev& dst, int row_base,
+            int row_stride) {
+    if (!src) fail("missing Q8_0 tensor");
+    CK(hipMemcpy(staging, src, q8_bytes(rows, cols), hipMemcpyHostToDevice));
+    launch_repack_q8(staging, rows, cols, dst, row_base, row_stride, m->stream);
+    CK(hipGetLastError());
+    CK(hipStreamSynchronize(m->stream));
+}
+
+float* f32_put(jyhip_model* m, const void* src, size_t n) {
+    if (!src) fail("missing f32 tensor");
+    float* d = (float*)own(m, dalloc<float>(n, false));
+    CK(hipMemcpy(d, src, n * sizeof(float), hipMemcpyHostToDevice));
+    return d;
+}
+
+void ensure_ws(jyhip_model* m, int rows) {
+    Workspace& w = m->ws;
+    if (w.rows >= rows) return;
+    for (void* p : {(void*)w.X, (void*)w.xn, (void*)w.qkv, (void*)w.att, (void*)w.g, (void*)w.u, (void*)w.h,
+                    (void*)w.q8, (void*)w.qsc})
+        dfree(p);
+    w = Workspace{};
+    const size_t r = (size_t)rows;
+    w.X = dalloc<float>(r * m->H);
+    w.xn = dalloc<float>(r * m->H);
+    w.qkv = dalloc<float>(r * (m->qd + 2 * m->kvd));
+    w.att = dalloc<float>(r * m->qd);
+    w.g = dalloc<float>(r * 2 * m->F);
+    w.u = dalloc<float>(r * m->F);
+    w.h = dalloc<float>(r * m->F);
+    w.q8 = dalloc<int8_t>(r * m->qd);
+    w.qsc = dalloc<float>(r * m->nh);
+    w.rows = rows;
+}
+
+void ensure_scores(jyhip_model* m, size_t n) {
+    Workspace& w = m->ws;
+    if (w.scores_n >= n) return;
+    dfree(w.scores);
+    w.scores = dalloc<float>(n, false);
+    w.scores_n = n;
+}
+
+void check_desc(const jy_model_desc* d) {
+    if (!d) fail("model description is NULL");
+    if (d->num_layers <= 0 || d->hidden <= 0 || d->num_heads <= 0 || d->num_kv_heads <= 0 || d->head_dim <= 0 ||
+        d->intermediate <= 0 || d->vocab_size <= 0)
+        fail("model hyper-parameters must be positive");
+    if (d->num_heads % d->num_kv_heads) fail("num_heads must be a multiple of num_kv_heads");
+    if (d->head_dim % 4 || d->head_dim > 256) fail("head_dim must be a multiple of 4 and at most 256");
+    if (!d->layers || !d->final_rms_weight) fail("layers / final norm missing");
+    const int t = d->layers[0].Wq.type;
+    if (t != JY_F32 && t != JY_Q8_0) fail("unsupported weight type");
+    for (int l = 0; l < d->num_layers; l++) {
+        const jy_layer_weights& w = d->layers[l];
+        for (const jy_wmat* x : {&w.Wq, &w.Wk, &w.Wv, &w.Wo, &w.W1, &w.W2, &w.W3})
+            if (!x->data || x->type != t) fail("2-D weights must all be present and of one type");
+        if (!w.rms1_weight || !w.rms2_weight) fail("norm weights missing");
+        if ((w.bq != nullptr) != (d->layers[0].bq != nullptr)) fail("q/k/v biases must be on every layer or none");
+        if ((w.bq == nullptr) != (w.bk == nullptr) || (w.bq == nullptr) != (w.bv == nullptr))
+            fail("q/k/v biases must come together");
+    }
+    if (!d->embed.data || !d->lm_head.data) fail("embedding / lm_head missing");
+    if (d->embed.type != t || d->lm_head.type != t) fail("embedding / lm_head type differs from the layers");
+    if (t == JY_Q8_0 && (d->hidden % 32 || d->intermediate % 32 || (d->num_heads * d->head_dim) % 32))
+        fail("Q8_0 needs hidden, intermediate and q_dim divisible by 32");
+}
+
+void upload(jyhip_model* m, const jy_model_desc* d, int max_seq) {
+    m->L = d->num_layers;
+    m->H = d->hidden;
+    m->nh = d->num_heads;
+    m->nkv = d->num_kv_heads;
+    m->hd = d->head_dim;
+    m->F = d->intermediate;
+    m->V = d->vocab_size;
+    m->qd = m->nh * m->hd;
+    m->kvd = m->nkv * m->hd;
+    m->wtype = d->layers[0].Wq.type;
+    m->bias = d->layers[0].bq != nullptr;
+    m->max_seq = max_seq;
+    m->theta = d->rope_theta;
+    CK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+
+    std::vector<float> c, s;
+    rope_table(max_seq, m->hd, m->theta, c, s);
+    m->cos_t = f32_put(m, c.data(), c.size());
+    m->sin_t = f32_put(m, s.data(), s.size());
+    m->final_rms = f32_put(m, d->final_rms_weight, m->H);
+
+    const int H = m->H, qd = m->qd, kvd = m->kvd, F = m->F, V = m->V;
+    m->layers.resize(m->L);
+    if (m->wtype == JY_Q8_0) {
+        size_t stage = q8_bytes(V, H);
+        stage = std::max(stage, q8_bytes(F, H));
+        stage = std::max(stage, q8_bytes(H, F));
+        stage = std::max(stage, q8_bytes(qd, H));
+        uint8_t* staging = dalloc<uint8_t>(stage, false);
+        try {
+            m->embed_q8 = q8_alloc(m, V, H);
+            q8_put(m, staging, d->embed.data, V, H, m->embed_q8, 0, 1);
+            m->lm_shares_embed = d->lm_head.data == d->embed.data;
+            if (m->lm_shares_embed) {
+                m->lm_q8 = m->embed_q8;
+            } else {
+                m->lm_q8 = q8_alloc(m, V, H);
+                q8_put(m, staging, d->lm_head.data, V, H, m->lm_q8, 0, 1);
+            }
+            for (int l = 0; l < m->L; l++) {
+                const jy_layer_weights& w = d->layers[l];
+                DevLayer& D = m->layers[l];
+                D.rms1 = f32_put(m, w.rms1_weight, H);
+                D.rms2 = f32_put(m, w.rms2_weight, H);
+                D.qkv = q8_alloc(m, qd + 2 * kvd, H);
+                q8_put(m, staging, w.Wq.data, qd, H, D.qkv, 0, 1);
+                q8_put(m, staging, w.Wk.data, kvd, H, D.qkv, qd, 1);
+                q8_put(m, staging, w.Wv.data, kvd, H, D.qkv, qd + kvd, 1);
+                D.o = q8_alloc(m, H, qd);
+                q8_put(m, staging, w.Wo.data, H, qd, D.o, 0, 1);
+                D.gu = q8_alloc(m, 2 * F, H);  // gate row i -> 2i, up row i -> 2i+1
+                q8_put(m, staging, w.W1.data, F, H, D.gu, 0, 2);
+                q8_put(m, staging, w.W3.data, F, H, D.gu, 1, 2);
+                D.down = q8_alloc(m, H, F);
+                q8_put(m, staging, w.W2.data, H, F, D.down, 0, 1);
+            }
+        } catch (...) {
+            dfree(staging);
+            throw;
+        }
+        dfree(staging);
+        m->weight_bytes = (size_t)m->L * (q8_bytes(qd + 2 * kvd, H) + q8_bytes(H, qd) + q8_bytes(2 * F, H) +
+                                          q8_bytes(H, F)) +
+                          q8_bytes(V, H);
+    } else {
+        m->embed_f32 = f32_put(m, d->embed.data, (size_t)V * H);
+        m->lm_f32 = f32_put(m, d->lm_head.data, (size_t)H * V);  // [hidden][vocab]
+        const size_t NQ = (size_t)qd + 2 * kvd;
+        for (int l = 0; l < m->L; l++) {
+            const jy_layer_weights& w = d->layers[l];
+            DevLayer& D = m->layers[l];
+            D.rms1 = f32_put(m, w.rms1_weight, H);
+            D.rms2 = f32_put(m, w.rms2_weight, H);
+            D.f_qkv = (float*)own(m, dalloc<float>((size_t)H * NQ, false));  // [H][qd | kvd | kvd]
+            CK(hipMemcpy2D(D.f_qkv, NQ * 4, w.Wq.data, (size_t)qd * 4, (size_t)qd * 4, H, hipMemcpyHostToDevice));
+            CK(hipMemcpy2D(D.f_qkv + qd, NQ * 4, w.Wk.data, (size_t)kvd * 4, (size_t)kvd * 4, H,
+                           hipMemcpyHostToDevice));
+            CK(hipMemcpy2D(D.f_qkv + qd + kvd, NQ * 4, w.Wv.data, (size_t)kvd * 4, (size_t)kvd * 4, H,
+                           hipMemcpyHostToDevice));
+            D.f_o = f32_put(m, w.Wo.data, (size_t)qd * H);
+            D.f_w1 = f32_put(m, w.W1.data, (size_t)H * F);
+            D.f_w3 = f32_put(m, w.W3.data, (size_t)H * F);
+            D.f_w2 = f32_put(m, w.W2.data, (size_t)F * H);
+        }
+        m->weight_bytes = ((size_t)m->L * ((size_t)H * NQ + (size_t)qd * H + 3 * (size_t)H * F) + (size_t)H * V) * 4;
+    }
+    if (m->bias)
+        for (int l = 0; l < m->L; l++) {
+            const jy_layer_weights& w = d->layers[l];
+            DevLayer& D = m->layers[l];
+            D.bqkv = (float*)own(m, dalloc<float>((size_t)qd + 2 * kvd, false));
+            CK(hipMemcpy(D.bqkv, w.bq, (size_t)qd * 4, hipMemcpyHostToDevice));
+            CK(hipMemcpy(D.bqkv + qd, w.bk, (size_t)kvd * 4, hipMemcpyHostToDevice));
+            CK(hipMemcpy(D.bqkv + qd + kvd, w.bv, (size_t)kvd * 4, hipMemcpyHostToDevice));
+        }
+    m->logits = (float*)own(m, dalloc<float>(V));
+    m->ids = (int*)own(m, dalloc<int>((size_t)max_seq + 1));
+    m->state = (int*)own(m, dalloc<int>(4));
+    m->eos_cap = 64;
+    m->eos = (int*)own(m, dalloc<int>(m->eos_cap));
+    const int np = argmax_partials(V);
+    m->part_val = (float*)own(m, dalloc<float>(np));
+    m->part_idx = (int*)own(m, dalloc<int>(np));
+    m->counter = (unsigned*)own(m, dalloc<unsigned>(4));
+}
+
+void release(jyhip_model* m) {
+    if (!m) return;
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    for (void* p : m->owned) dfree(p);
+    Workspace& w = m->ws;
+    for (void* p : {(void*)w.X, (void*)w.xn, (void*)w.qkv, (void*)w.att, (void*)w.g, (void*)w.u, (void*)w.h,
+                    (void*)w.q8, (void*)w.qsc, (void*)w.scores})
+        dfree(p);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
+    delete m;
+}
+
+// ---------------------------------------------------------------- the step
+
+// transformer_layer x L (libs/model_libs/transformer_layer.h:10-90) for one token
+// in ws.X at position state[0]-1 (state != null) or pos0: the m == 1 path of every
+// matmul (matmul_q.h:139-144).  Q8_0: five kernels per layer (RMSNorm fused into
+// the QKV and gate/up matvecs, RoPE into QKV, K/V packing into attention, SwiGLU
+// into gate/up, residual adds into O and down).
+void run_decode_layers(jyhip_model* m, const KVDev& kv, const int* state, int pos0, float* layer_out_host,
+                       int max_keys) {
+    Workspace& w = m->ws;
+    hipStream_t st = m->stream;
+    const int H = m->H, NQ = m->qd + 2 * m->kvd, F = m->F;
+    AttnArgs at;
+    at.nrows = 1;
+    at.start_pos = pos0;
+    at.state = state;
+    at.nh = m->nh;
+    at.nkv = m->nkv;
+    at.hd = m->hd;
+    at.kv = kv;
+    at.scratch = w.scores;
+    at.max_keys = max_keys;
+    at.out = w.att;
+    for (int l = 0; l < m->L; l++) {
+        const DevLayer& D = m->layers[l];
+        at.layer = l;
+        if (m->wtype == JY_Q8_0) {
+            MvArgs qa;
+            qa.aux = D.bqkv;
+            qa.state = state;
+            qa.pos0 = pos0;
+            qa.cos_t = m->cos_t;
+            qa.sin_t = m->sin_t;
+            qa.nh = m->nh;
+            qa.nkv = m->nkv;
+            qa.hd = m->hd;
+            launch_matvec_q8(D.qkv, w.X, D.rms1, w.qkv, EPI_ROPE, qa, st);
+            at.fused = true;
+            at.qkv = w.qkv;
+            launch_attention(at, st);
+            const MvArgs none;
+            launch_matvec_q8(D.o, w.att, nullptr, w.X, EPI_RESID, none, st);
+            launch_matvec_q8(D.gu, w.X, D.rms2, w.h, EPI_SWIGLU, none, st);
+            launch_matvec_q8(D.down, w.h, nullptr, w.X, EPI_RESID, none, st);
+        } else {
+            launch_rmsnorm(w.X, w.xn, D.rms1, H, 1, 1e-5f, st);
+            launch_matvec_f32(D.f_qkv, nullptr, H, NQ, w.xn, w.qkv, D.bqkv, D.bqkv ? EPI_BIAS : EPI_STORE, st);
+            launch_rope_pack(w.qkv, 1, pos0, state, m->nh, m->nkv, m->hd, m->cos_t, m->sin_t, kv, l, w.q8, w.qsc, st);
+            at.fused = false;
+            at.q8 = w.q8;
+            at.qsc = w.qsc;
+            at.row0 = 0;
+            launch_attention(at, st);
+            launch_matvec_f32(D.f_o, nullptr, m->qd, H, w.att, w.X, nullptr, EPI_RESID, st);
+            launch_rmsnorm(w.X, w.xn, D.rms2, H, 1, 1e-5f, st);
+            launch_matvec_f32(D.f_w1, D.f_w3, H, F, w.xn, w.h, nullptr, EPI_SWIGLU, st);
+            launch_matvec_f32(D.f_w2, nullptr, F, H, w.h, w.X, nullptr, EPI_RESID, st);
+        }
+        if (layer_out_host) {
+            CK(hipMemcpyAsync(layer_out_host + (size_t)l * H, w.X, sizeof(float) * H, hipMemcpyDeviceToHost, st));
+            CK(hipStreamSynchronize(st));
+        }
+    }
+    CK(hipGetLastError());
+}
+
+// the prompt (seq > 1): the generic m > 1 matmul path (matmul_q.h:145-161) as tiled
+// GEMMs, RoPE + K/V packing of every row before attention.
+void run_prefill_layers(jyhip_model* m, const KVDev& kv, int seq, int start_pos, float* layer_out_host,
+                        int max_keys) {
+    Workspace& w = m->ws;
+    hipStream_t st = m->stream;
+    const bool q8 = m->wtype == JY_Q8_0;
+    const int H = m->H, NQ = m->qd + 2 * m->kvd, F = m->F;
+    // attention rows per launch keep the HBM score scratch within its allocation
+    const size_t per_row = (size_t)m->nh * max_keys;
+    const int chunk = (int)std::max<size_t>(1, std::min<size_t>(seq, w.scores_n / per_row));
+    AttnArgs at;
+    at.fused = false;
+    at.q8 = w.q8;
+    at.qsc = w.qsc;
+    at.start_pos = start_pos;
+    at.nh = m->nh;
+    at.nkv = m->nkv;
+    at.hd = m->hd;
+    at.kv = kv;
+    at.scratch = w.scores;
+    at.max_keys = max_keys;
+    at.out = w.att;
+    for (int l = 0; l < m->L; l++) {
+        const DevLayer& D = m->layers[l];
+        launch_rmsnorm(w.X, w.xn, D.rms1, H, seq, 1e-5f, st);
+        const Epi qkv_epi = D.bqkv ? EPI_BIAS : EPI_STORE;
+        if (q8)
+            launch_gemm_q8(D.qkv, seq, w.xn, w.qkv, D.bqkv, qkv_epi, st);
+        else
+            launch_gemm_f32(D.f_qkv, H, NQ, seq, w.xn, w.qkv, D.bqkv, qkv_epi, st);
+        launch_rope_pack(w.qkv, seq, start_pos, nullptr, m->nh, m->nkv, m->hd, m->cos_t, m->sin_t, kv, l, w.q8,
+                         w.qsc, st);
+        at.layer = l;
+        for (int r0 = 0; r0 < seq; r0 += chunk) {
+            at.row0 = r0;
+            at.nrows = std::min(chunk, seq - r0);
+            launch_attention(at, st);
+        }
+        if (q8)
+            launch_gemm_q8(D.o, seq, w.att, w.X, nullptr, EPI_RESID, st);
+        else
+            launch_gemm_f32(D.f_o, m->qd, H, seq, w.att, w.X, nullptr, EPI_RESID, st);
+        launch_rmsnorm(w.X, w.xn, D.rms2, H, seq, 1e-5f, st);
+        if (q8) {
+            launch_gemm_q8(D.gu, seq, w.xn, w.g, nullptr, EPI_STORE, st);
+            launch_silu_mul(w.g, nullptr, 1, seq, F, w.h, st);
+            launch_gemm_q8(D.down, seq, w.h, w.X, nullptr, EPI_RESID, st);
+        } else {
+            launch_gemm_f32(D.f_w1, H, F, seq, w.xn, w.g, nullptr, EPI_STORE, st);
+            launch_gemm_f32(D.f_w3, H, F, seq, w.xn, w.u, nullptr, EPI_STORE, st);
+            launch_silu_mul(w.g, w.u, 0, seq, F, w.h, st);
+            launch_gemm_f32(D.f_w2, F, H, seq, w.h, w.X, nullptr, EPI_RESID, st);
+        }
+        if (layer_out_host) {
+            CK(hipMemcpyAsync(layer_out_host + (size_t)l * seq * H, w.X, sizeof(float) * seq * H,
+                              hipMemcpyDeviceToHost, st));
+            CK(hipStreamSynchronize(st));
+        }
+    }
+    CK(hipGetLastError());
+}
+
+void run_layers(jyhip_model* m, const KVDev& kv, int seq, int start_pos, const int* state, float* layer_out_host,
+                int max_keys) {
+    ensure_scores(m, (size_t)m->nh * max_keys * (size_t)std::max(1, std::min(seq, 64)));
+    if (seq == 1)
+        run_decode_layers(m, kv, state, start_pos, layer_out_host, max_keys);
+    else
+        run_prefill_layers(m, kv, seq, start_pos, layer_out_host, max_keys);
+}
+
+// final RMSNorm of the last row + lm_head (+ greedy pick when fused) -> m->logits
+void final_and_head(jyhip_model* m, const float* xlast, bool argmax, int neos) {
+    if (m->wtype == JY_Q8_0) {
+        MvArgs a;
+        if (argmax) {
+            a.ids = m->ids;
+            a.mstate = m->state;
+            a.eos = m->eos;
+            a.neos = neos;
+            a.part_val = m->part_val;
+            a.part_idx = m->part_idx;
+            a.counter = m->counter;
+        }
+        launch_matvec_q8(m->lm_q8, xlast, m->final_rms, m->logits, argmax ? EPI_ARGMAX : EPI_STORE, a, m->stream);
+    } else {
+        launch_rmsnorm(xlast, m->ws.xn, m->final_rms, m->H, 1, 1e-5f, m->stream);
+        launch_matvec_f32(m->lm_f32, nullptr, m->H, m->V, m->ws.xn, m->logits, nullptr, EPI_STORE, m->stream);
+    }
+}
+
+// greedy pick: fused into lm_head when possible, else the standalone kernel
+// (repetition penalty, f32 models)
+void head_and_pick(jyhip_model* m, const float* xlast, bool greedy, float rp, int prompt_len, int neos) {
+    const bool fused = greedy && rp == 1.0f && m->wtype == JY_Q8_0;
+    final_and_head(m, xlast, fused, neos);
+    if (greedy && !fused) launch_argmax(m->logits, m->V, m->ids, m->state, m->eos, neos, rp, prompt_len, m->stream);
+}
+
+// one decode step: embed ids[len-1], layers, final norm, lm_head, greedy pick
+void decode_step(jyhip_model* m, const KVDev& kv, int max_keys, bool greedy, float rp, int prompt_len, int neos) {
+    Workspace& w = m->ws;
+    launch_embed(m->wtype == JY_Q8_0 ? &m->embed_q8 : nullptr, m->embed_f32, m->H, m->ids, 0, m->state, 1, w.X,
+                 m->stream);
+    run_decode_layers(m, kv, m->state, 0, nullptr, max_keys);
+    head_and_pick(m, w.X, greedy, rp, prompt_len, neos);
+}
+
+// temperature sampling and the repetition penalty on the host, as generate.h:50-77
+int host_pick(jyhip_model* m, std::vector<float>& logits, const std::vector<int>& ids, int len, int prompt_len,
+              float temperature, float rp, unsigned& rng) {
+    const int V = m->V;
+    if (rp != 1.0f)
+        for (int i = prompt_len; i < len; i++) {
+            const int id = ids[i];
+            if (id >= 0 && id < V) logits[id] = logits[id] > 0.0f ? logits[id] / rp : logits[id] * rp;
+        }
+    int next = 0;
+    if (temperature <= 0.0f) {
+        for (int v = 1; v < V; v++)
+            if (logits[v] > logits[next]) next = v;
+        return next;
+    }
+    float mx = logits[0];
+    for (int v = 1; v < V; v++)
+        if (logits[v] > mx) mx = logits[v];
+    double sum = 0.0;
+    for (int v = 0; v < V; v++) {
+        logits[v] = expf((logits[v] - mx) / temperature);
+        sum += logits[v];
+    }
+    rng = rng * 1664525u + 1013904223u;
+    double r = (double)(rng >> 8) / 16777216.0 * sum;
+    next = V - 1;
+    for (int v = 0; v < V; v++) {
+        r -= logits[v];
+        if (r <= 0.0) {
+            next = v;
+            break;
+        }
+    }
+    return next;
+}
+// One generation (generate_cached, libs/model_libs/generate.h:9-89) driven step by
+// step: begin() runs the prompt and picks the first token, step(n) produces up to
+// n more.  Greedy decoding stays on the device (ids and the sequence length live
+// in device memory), so a run of steps is a run of graph launches with no host
+// round trip unless eos ids, a callback or sampling need one.
+struct Session {
+    jyhip_model* m = nullptr;
+    jyhip_kv* kv = nullptr;
+    bool kv_owned = false;
+    int plen = 0, max_seq = 0, total = 0, len = 0, max_keys = 0, neos = 0;
+    float temperature = 0.0f, rp = 1.0f;
+    bool greedy = true, stopped = false, done_early = false;
+    std::vector<int> ids, eos;
+    unsigned rng = 12345u;
+    jyhip_token_cb cb = nullptr;
+    void* ud = nullptr;
+    hipGraphExec_t exec = nullptr;
+    hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+    double decode_ms = 0.0;
+    int decoded = 0;
+    std::vector<float> hlog;
+    float* logits_out = nullptr;
+
+    ~Session() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        for (hipEvent_t e : ev)
+            if (e) (void)hipEventDestroy(e);
+        if (kv_owned && kv) jyhip_kv_free(kv);
+    }
+
+    bool is_eos(int id) const {
+        for (int e : eos)
+            if (id == e) return true;
+        return false;
+    }
+
+    // sampling / penalty on the host (generate.h:50-77); writes the pick back
+    int pick_host() {
+        hipStream_t st = m->stream;
+        hlog.resize(m->V);
+        CK(hipMemcpyAsync(hlog.data(), m->logits, sizeof(float) * m->V, hipMemcpyDeviceToHost, st));
+        CK(hipStreamSynchronize(st));
+        if (logits_out) memcpy(logits_out, hlog.data(), sizeof(float) * m->V);
+        const int next = host_pick(m, hlog, ids, len, plen, temperature, rp, rng);
+        const int s2[2] = {len + 1, 0};
+        CK(hipMemcpyAsync(m->ids + len, &next, sizeof(int), hipMemcpyHostToDevice, st));
+        CK(hipMemcpyAsync(m->state, s2, sizeof(s2), hipMemcpyHostToDevice, st));
+        CK(hipStreamSynchronize(st));
+        return next;
+    }
+
+    int fetch_last() {
+        int v[2];
+        CK(hipMemcpyAsync(v, m->state, sizeof(v), hipMemcpyDeviceToHost, m->stream));
+        CK(hipStreamSynchronize(m->stream));
+        int id = 0;
+        CK(hipMemcpy(&id, m->ids + v[0] - 1, sizeof(int), hipMemcpyDeviceToHost));
+        return id;
+    }
+
+    void accept(int next) {
+        ids[len++] = next;
+        if (cb && cb(next, ud)) stopped = true;
+        if (is_eos(next)) stopped = true;
+    }
+
+    // returns false when generate() would return before the loop (generate.h:25-32)
+    bool begin(jyhip_model* model, jyhip_kv* kv_in, const int* prompt, int plen_, const int* eos_ids, int neos_,
+               int max_seq_, int max_new, float temperature_, float rp_, jyhip_token_cb cb_, void* ud_,
+               int* prompt_out) {
+        m = model;
+        plen = plen_;
+        max_seq = max_seq_;
+        temperature = temperature_;
+        rp = rp_;
+        cb = cb_;
+        ud = ud_;
+        if (!prompt) fail("prompt_ids is NULL");
+        if (plen <= 0 || plen > max_seq) return false;  // generate.h:25
+        if (max_seq > m->max_seq) fail("max_seq exceeds the model's RoPE table (jyhip_model_upload max_seq)");
+        if (neos_ < 0 || (neos_ > 0 && !eos_ids)) fail("bad eos list");
+        if (neos_ > m->eos_cap) fail("too many eos ids");
+        for (int i = 0; i < plen; i++)
+            if (prompt[i] < 0 || prompt[i] >= m->V) fail("prompt id out of vocabulary");
+        if (kv_in) {
+            kv = kv_in;
+            if (kv->dev.num_layers < m->L || kv->dev.max_seq < max_seq || kv->dev.nkv != m->nkv || kv->dev.hd != m->hd)
+                fail("generate: KV cache shape does not match the model");
+        } else {
+            kv = jyhip_kv_create(m, max_seq);
+            if (!kv) fail(g_err);
+            kv_owned = true;
+        }
+        neos = neos_;
+        eos.assign(eos_ids, eos_ids + neos);
+        ids.assign(prompt, prompt + plen);
+        ids.resize((size_t)max_seq + 1);
+        if (prompt_out)
+            for (int i = 0; i < plen; i++) prompt_out[i] = prompt[i];
+        len = plen;
+        kv->current_len = 0;
+        if (max_new <= 0) return false;                  // generate.h:32
+        total = std::min(max_new, max_seq - plen);        // tokens this generation may produce
+        if (total <= 0) return false;                     // generate.h:39: len < max_seq fails at once
+        greedy = temperature <= 0.0f;
+        max_keys = (max_seq + 3) / 4 * 4;
+        for (hipEvent_t& e : ev) CK(hipEventCreate(&e));
+
+        hipStream_t st = m->stream;
+        ensure_ws(m, plen);
+        CK(hipMemcpyAsync(m->ids, prompt, sizeof(int) * plen, hipMemcpyHostToDevice, st));
+        const int st0[4] = {plen, 0, 0, 0};
+        CK(hipMemcpyAsync(m->state, st0, sizeof(st0), hipMemcpyHostToDevice, st));
+        if (neos) CK(hipMemcpyAsync(m->eos, eos_ids, sizeof(int) * neos, hipMemcpyHostToDevice, st));
+        // step 0: the prompt (generate.h:43-49 with seq = prompt_len)
+        CK(hipEventRecord(ev[0], st));
+        Workspace& w = m->ws;
+        launch_embed(m->wtype == JY_Q8_0 ? &m->embed_q8 : nullptr, m->embed_f32, m->H, m->ids, 0, nullptr, plen, w.X,
+                     st);
+        run_layers(m, kv->dev, plen, 0, nullptr, nullptr, max_keys);
+        head_and_pick(m, w.X + (size_t)(plen - 1) * m->H, greedy, rp, plen, neos);
+        CK(hipEventRecord(ev[1], st));
+        CK(hipGetLastError());
+        accept(greedy ? fetch_last() : pick_host());
+        return true;
+    }
+
+    int remaining() const { return stopped ? 0 : plen + total - len; }
+
+    void capture() {
+        hipStream_t st = m->stream;
+        hipGraph_t graph = nullptr;
+        CK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        try {
+            decode_step(m, kv->dev, max_keys, greedy, rp, plen, neos);
+        } catch (...) {
+            (void)hipStreamEndCapture(st, &graph);
+            if (graph) (void)hipGraphDestroy(graph);
+            throw;
+        }
+        CK(hipStreamEndCapture(st, &graph));
+        const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        ck(ie, "hipGraphInstantiate");
+    }
+
+    // up to n more tokens; returns how many were produced
+    int step(int n) {
+        n = std::min(n, remaining());
+        if (n <= 0) return 0;
+        if (!exec) capture();
+        hipStream_t st = m->stream;
+        CK(hipEventRecord(ev[2], st));
+        int made = 0;
+        if (!greedy || cb || neos > 0) {
+            for (; made < n && !stopped; made++) {
+                CK(hipGraphLaunch(exec, st));
+                accept(greedy ? fetch_last() : pick_host());
+            }
+        } else {
+            for (int s = 0; s < n; s++) CK(hipGraphLaunch(exec, st));
+            CK(hipMemcpyAsync(ids.data() + len, m->ids + len, sizeof(int) * n, hipMemcpyDeviceToHost, st));
+            made = n;
+            len += n;
+        }
+        CK(hipEventRecord(ev[3], st));
+        CK(hipStreamSynchronize(st));
+        float ms = 0.0f;
+        CK(hipEventElapsedTime(&ms, ev[2], ev[3]));
+        decode_ms += ms;
+        decoded += made;
+        return made;
+    }
+
+    double prefill_ms() {
+        float ms = 0.0f;
+        CK(hipEventElapsedTime(&ms, ev[0], ev[1]));
+        return ms;
+    }
+
+    void finish() { kv->current_len = len - 1; }  // K/V of the last token is never computed
+};
+
+int generate_impl(jyhip_model* m, jyhip_kv* kv_in, const int* prompt, int plen, const int* eos, int neos,
+                  int max_seq, int max_new, float temperature, float rp, int* out_ids, jyhip_token_cb cb, void* ud,
+                  float* logits_out, jyhip_stats* stats) {
+    if (stats) *stats = jyhip_stats{};
+    if (!out_ids) fail("out_ids is NULL");
+    Session s;
+    s.logits_out = logits_out;
+    if (!s.begin(m, kv_in, prompt, plen, eos, neos, max_seq, max_new, temperature, rp, cb, ud, out_ids))
+        return (plen <= 0 || plen > max_seq) ? 0 : plen;
+    while (s.remaining() > 0) s.step(s.remaining());
+    s.finish();
+    if (logits_out && s.greedy)
+        CK(hipMemcpy(logits_out, m->logits, sizeof(float) * m->V, hipMemcpyDeviceToHost));
+    for (int i = plen; i < s.len; i++) out_ids[i] = s.ids[i];
+    if (stats) {
+        stats->prefill_ms = s.prefill_ms();
+        stats->decode_ms = s.decode_ms;
+        stats->prompt_len = plen;
+        stats->decoded = s.decoded;
+        stats->upload_ms = m->upload_ms;
+    }
+    return s.len;
+}
+
+
+int forward_impl(jyhip_model* m, jyhip_kv* kv, float* X, int seq, int start_pos, float* layer_out) {
+    if (!kv || !X) fail("forward: NULL kv or X");
+    if (kv->dev.num_layers < m->L || kv->dev.nkv != m->nkv || kv->dev.hd != m->hd)
+        fail("forward: KV cache shape does not match the model");  // forward.h:60-61
+    if (start_pos < 0) fail("forward: start_pos must not be negative");
+    if (seq <= 0) fail("forward: seq must be positive");
+    if ((size_t)start_pos + seq > (size_t)kv->dev.max_seq) fail("forward: KV cache capacity exceeded");
+    if (start_pos + seq > m->max_seq) fail("forward: position beyond the RoPE table");
+    hipStream_t st = m->stream;
+    ensure_ws(m, seq);
+    Workspace& w = m->ws;
+    CK(hipMemcpyAsync(w.X, X, sizeof(float) * seq * m->H, hipMemcpyHostToDevice, st));
+    const int max_keys = (start_pos + seq + 3) / 4 * 4;
+    run_layers(m, kv->dev, seq, start_pos, nullptr, layer_out, max_keys);
+    launch_rmsnorm(w.X, w.xn, m->final_rms, m->H, seq, 1e-5f, st);  // forward.h:86-94
+    CK(hipGetLastError());
+    CK(hipMemcpyAsync(X, w.xn, sizeof(float) * seq * m->H, hipMemcpyDeviceToHost, st));
+    CK(hipStreamSynchronize(st));
+    kv->current_len = start_pos + seq;
+    return 0;
+}
+
+template <class F>
+auto guarded(F&& f, decltype(f()) bad) -> decltype(f()) {
+    try {
+        g_err.clear();
+        return f();
+    } catch (const Error& e) {
+        g_err = e.msg;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+    } catch (...) {
+        g_err = "unknown error";
+    }
+    return bad;
+}
+
+}  // namespace
+
+extern "C" {
+
+JYHIP_API const char* jyhip_last_error(void) { return g_err.c_str(); }
+
+JYHIP_API int jyhip_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+JYHIP_API int jyhip_set_device(int device) {
+    return guarded([&]() {
+        CK(hipSetDevice(device));
+        return 0;
+    }, -1);
+}
+
+JYHIP_API jyhip_model* jyhip_model_upload(const jy_model_desc* d, int max_seq) {
+    return guarded([&]() -> jyhip_model* {
+        check_desc(d);
+        if (max_seq <= 0) fail("max_seq must be positive");
+        jyhip_model* m = new jyhip_model();
+        try {
+            CK(hipGetDevice(&m->device));
+            init_device_kernels(m->device);
+            const auto t0 = std::chrono::steady_clock::now();
+            upload(m, d, max_seq);
+            CK(hipDeviceSynchronize());
+            m->upload_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        } catch (...) {
+            release(m);
+            throw;
+        }
+        return m;
+    }, nullptr);
+}
+
+JYHIP_API void jyhip_model_free(jyhip_model* m) { release(m); }
+
+JYHIP_API size_t jyhip_model_weight_bytes(const jyhip_model* m) { return m ? m->weight_bytes : 0; }
+
+JYHIP_API double jyhip_model_upload_ms(const jyhip_model* m) { return m ? m->upload_ms : 0.0; }
+
+JYHIP_API jyhip_kv* jyhip_kv_create(const jyhip_model* m, int max_seq) {
+    return guarded([&]() -> jyhip_kv* {
+        if (!m) fail("model is NULL");
+        if (max_seq <= 0) fail("max_seq must be positive");
+        jyhip_kv* kv = new jyhip_kv();
+        KVDev& k = kv->dev;
+        k.num_layers = m->L;
+        k.max_seq = max_seq;
+        k.nkv = m->nkv;
+        k.hd = m->hd;
+        const size_t n = (size_t)m->L * m->nkv * max_seq * m->hd, rows = (size_t)m->L * m->nkv * max_seq;
+        try {
+            k.k = dalloc<int8_t>(n);
+            k.v = dalloc<int8_t>(n);
+            k.ks = dalloc<float>(rows);
+            k.vs = dalloc<float>(rows);
+        } catch (...) {
+            dfree(k.k);
+            dfree(k.v);
+            dfree(k.ks);
+            dfree(k.vs);
+            delete kv;
+            throw;
+        }
+        kv->device = m->device;
+        return kv;
+    }, nullptr);
+}
+
+JYHIP_API void jyhip_kv_free(jyhip_kv* kv) {
+    if (!kv) return;
+    (void)hipDeviceSynchronize();
+    dfree(kv->dev.k);
+    dfree(kv->dev.v);
+    dfree(kv->dev.ks);
+    dfree(kv->dev.vs);
+    delete kv;
+}
+
+JYHIP_API int jyhip_kv_len(const jyhip_kv* kv) { return kv ? kv->current_len : -1; }
+
+JYHIP_API int jyhip_kv_set_len(jyhip_kv* kv, int n) {
+    return guarded([&]() {
+        if (!kv) fail("kv is NULL");
+        if (n < 0 || n > kv->dev.max_seq) fail("length outside the cache");
+        kv->current_len = n;
+        return 0;
+    }, -1);
+}
+
+static void kv_range(const jyhip_kv* kv, int layer, int pos0, int npos) {
+    if (!kv) fail("kv is NULL");
+    if (layer < 0 || layer >= kv->dev.num_layers) fail("layer out of range");
+    if (pos0 < 0 || npos < 0 || (size_t)pos0 + npos > (size_t)kv->dev.max_seq) fail("positions out of range");
+}
+
+JYHIP_API int jyhip_kv_write(jyhip_kv* kv, int layer, int pos0, int npos, const int8_t* k, const float* ks,
+                             const int8_t* v, const float* vs) {
+    return guarded([&]() {
+        kv_range(kv, layer, pos0, npos);
+        if (npos == 0) return 0;
+        if (!k || !ks || !v || !vs) fail("NULL buffer");
+        const size_t n = (size_t)npos * kv->dev.nkv * kv->dev.hd, r = (size_t)npos * kv->dev.nkv;
+        int8_t *dk = dalloc<int8_t>(n, false), *dv = dalloc<int8_t>(n, false);
+        float *dks = dalloc<float>(r, false), *dvs = dalloc<float>(r, false);
+        hipError_t e = hipMemcpy(dk, k, n, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(dv, v, n, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(dks, ks, r * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(dvs, vs, r * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess) {
+            launch_kv_import(dk, dks, dv, dvs, pos0, npos, kv->dev, layer, nullptr);
+            e = hipGetLastError();
+        }
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        dfree(dk);
+        dfree(dv);
+        dfree(dks);
+        dfree(dvs);
+        ck(e, "kv_write");
+        return 0;
+    }, -1);
+}
+
+JYHIP_API int jyhip_kv_read(const jyhip_kv* kv, int layer, int pos0, int npos, int8_t* k, float* ks, int8_t* v,
+                            float* vs) {
+    return guarded([&]() {
+        kv_range(kv, layer, pos0, npos);
+        if (npos == 0) return 0;
+        if (!k || !ks || !v || !vs) fail("NULL buffer");
+        const size_t n = (size_t)npos * kv->dev.nkv * kv->dev.hd, r = (size_t)npos * kv->dev.nkv;
+        int8_t *dk = dalloc<int8_t>(n, false), *dv = dalloc<int8_t>(n, false);
+        float *dks = dalloc<float>(r, false), *dvs = dalloc<float>(r, false);
+        launch_kv_export(dk, dks, dv, dvs, pos0, npos, kv->dev, layer, nullptr);
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e == hipSuccess) e = hipMemcpy(k, dk, n, hipMemcpyDeviceToHost);
+        if (e == hipSuccess) e = hipMemcpy(v, dv, n, hipMemcpyDeviceToHost);
+        if (e == hipSuccess) e = hipMemcpy(ks, dks, r * 4, hipMemcpyDeviceToHost);
+        if (e == hipSuccess) e = hipMemcpy(vs, dvs, r * 4, hipMemcpyDeviceToHost);
+        dfree(dk);
+        dfree(dv);
+        dfree(dks);
+        dfree(dvs);
+        ck(e, "kv_read");
+        return 0;
+    }, -1);
+}
+
+JYHIP_API int jyhip_forward_cached(jyhip_model* m, jyhip_kv* kv, float* X, int seq, int start_pos, float* layer_out) {
+    return guarded([&]() {
+        if (!m) fail("model is NULL");
+        return forward_impl(m, kv, X, seq, start_pos, layer_out);
+    }, -1);
+}
+
+JYHIP_API int jyhip_generate(jyhip_model* m, jyhip_kv* kv, const int* prompt_ids, int prompt_len, const int* eos_ids,
+                             int num_eos, int max_seq, int max_new, float temperature, float repetition_penalty,
+                             int* out_ids, jyhip_token_cb cb, void* cb_ud, float* logits_out, jyhip_stats* stats) {
+    return guarded([&]() {
+        if (!m) fail("model is NULL");
+        return generate_impl(m, kv, prompt_ids, prompt_len, eos_ids, num_eos, max_seq, max_new, temperature,
+                             repetition_penalty, out_ids, cb, cb_ud, logits_out, stats);
+    }, -1);
+}
+
+struct jyhip_session {
+    Session s;
+    bool active = false;  // false: generate() would have returned before its loop
+    int result = 0;       // what generate() returns in that case
+};
+
+JYHIP_API jyhip_session* jyhip_session_begin(jyhip_model* m, jyhip_kv* kv, const int* prompt_ids, int prompt_len,
+                                             const int* eos_ids, int num_eos, int max_seq, int max_new,
+                                             float temperature, float repetition_penalty) {
+    return guarded([&]() -> jyhip_session* {
+        if (!m) fail("model is NULL");
+        jyhip_session* h = new jyhip_session();
+        try {
+            h->active = h->s.begin(m, kv, prompt_ids, prompt_len, eos_ids, num_eos, max_seq, max_new, temperature,
+                                   repetition_penalty, nullptr, nullptr, nullptr);
+            h->result = h->active ? h->s.len : ((prompt_len <= 0 || prompt_len > max_seq) ? 0 : prompt_len);
+        } catch (...) {
+            delete h;
+            throw;
+        }
+        return h;
+    }, nullptr);
+}
+
+JYHIP_API int jyhip_session_step(jyhip_session* h, int n) {
+    return guarded([&]() {
+        if (!h) fail("session is NULL");
+        if (!h->active || n <= 0) return 0;
+        const int made = h->s.step(n);
+        h->s.finish();
+        return made;
+    }, -1);
+}
+
+JYHIP_API int jyhip_session_remaining(const jyhip_session* h) { return h && h->active ? h->s.remaining() : 0; }
+
+JYHIP_API int jyhip_session_len(const jyhip_session* h) { return !h ? -1 : h->active ? h->s.len : h->result; }
+
+JYHIP_API int jyhip_session_ids(const jyhip_session* h, int* out, int cap) {
+    return guarded([&]() {
+        if (!h || !out) fail("NULL argument");
+        const int n = h->active ? h->s.len : std::min(h->result, (int)h->s.ids.size());
+        if (cap < n) fail("output buffer too small");
+        for (int i = 0; i < n; i++) out[i] = h->s.ids[i];
+        return n;
+    }, -1);
+}
+
+JYHIP_API int jyhip_session_stats(jyhip_session* h, jyhip_stats* st) {
+    return guarded([&]() {
+        if (!h || !st) fail("NULL argument");
+        *st = jyhip_stats{};
+        if (!h->active) return 0;
+        st->prefill_ms = h->s.prefill_ms();
+        st->decode_ms = h->s.decode_ms;
+        st->prompt_len = h->s.plen;
+        st->decoded = h->s.decoded;
+        st->upload_ms = h->s.m->upload_ms;
+        return 0;
+    }, -1);
+}
+
+JYHIP_API void jyhip_session_end(jyhip_session* h) { delete h; }
+
+JYHIP_API jyhip_q8mat* jyhip_q8_upload(const void* w, int rows, int cols, int copies) {
+    return guarded([&]() -> jyhip_q8mat* {
+        if (!w || rows <= 0 || cols <= 0 || cols % 32) fail("bad Q8_0 matrix");
+        if (copies <= 0) copies = 1;
+        jyhip_q8mat* q = new jyhip_q8mat();
+        jyhip_model holder;  // borrow q8_alloc's bookkeeping
+        try {
+            int dev = 0;
+            CK(hipGetDevice(&dev));
+            init_device_kernels(dev);
+            CK(hipStreamCreateWithFlags(&q->stream, hipStreamNonBlocking));
+            holder.stream = q->stream;
+            uint8_t* staging = dalloc<uint8_t>(q8_bytes(rows, cols), false);
+            for (int c = 0; c < copies; c++) {
+                Q8Dev d = q8_alloc(&holder, rows, cols);
+                q8_put(&holder, staging, w, rows, cols, d, 0, 1);
+                q->copies.push_back(d);
+            }
+            dfree(staging);
+            q->x = dalloc<float>(cols);
+            q->y = dalloc<float>(rows);
+        } catch (...) {
+            for (void* p : holder.owned) dfree(p);
+            if (q->stream) (void)hipStreamDestroy(q->stream);
+            delete q;
+            throw;
+        }
+        holder.owned.clear();
+        holder.stream = nullptr;
+        return q;
+    }, nullptr);
+}
+
+JYHIP_API void jyhip_q8_free(jyhip_q8mat* q) {
+    if (!q) return;
+    (void)hipStreamSynchronize(q->stream);
+    for (Q8Dev& d : q->copies) {
+        dfree(d.qs);
+        dfree(d.d);
+    }
+    dfree(q->x);
+    dfree(q->y);
+    (void)hipStreamDestroy(q->stream);
+    delete q;
+}
+
+JYHIP_API int jyhip_q8_matvec(jyhip_q8mat* q, const float* x, float* y) {
+    return guarded([&]() {
+        if (!q || !x || !y) fail("NULL argument");
+        const Q8Dev& d = q->copies[0];
+        CK(hipMemcpyAsync(q->x, x, sizeof(float) * d.cols, hipMemcpyHostToDevice, q->stream));
+        launch_matvec_q8(d, q->x, nullptr, q->y, EPI_STORE, MvArgs(), q->stream);
+        CK(hipGetLastError());
+        CK(hipMemcpyAsync(y, q->y, sizeof(float) * d.rows, hipMemcpyDeviceToHost, q->stream));
+        CK(hipStreamSynchronize(q->stream));
+        return 0;
+    }, -1);
+}
+
+JYHIP_API int jyhip_q8_matvec_time(jyhip_q8mat* q, const float* x, int iters, double* avg_us) {
+    return guarded([&]() {
+        if (!q || !x || !avg_us || iters <= 0) fail("bad argument");
+        const Q8Dev& d0 = q->copies[0];
+        CK(hipMemcpyAsync(q->x, x, sizeof(float) * d0.cols, hipMemcpyHostToDevice, q->stream));
+        for (size_t c = 0; c < q->copies.size(); c++)  // warm: one pass over every copy
+            launch_matvec_q8(q->copies[c], q->x, nullptr, q->y, EPI_STORE, MvArgs(), q->stream);
+        hipEvent_t a, b;
+        CK(hipEventCreate(&a));
+        CK(hipEventCreate(&b));
+        CK(hipEventRecord(a, q->stream));
+        for (int i = 0; i < iters; i++)
+            launch_matvec_q8(q->copies[(size_t)i % q->copies.size()], q->x, nullptr, q->y, EPI_STORE, MvArgs(),
+                             q->stream);
+        CK(hipEventRecord(b, q->stream));
+        CK(hipEventSynchronize(b));
+        float ms = 0.0f;
+        CK(hipEventElapsedTime(&ms, a, b));
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        CK(hipGetLastError());
+        *avg_us = 1000.0 * ms / iters;
+        return 0;
+    }, -1);
+}
+
+}  // extern "C"

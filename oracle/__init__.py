@@ -50,7 +50,7 @@ def load_oracle():
     _proto(lib, "jyo_kv_init", I, C.POINTER(JyoKV), I, I, I, I)
     _proto(lib, "jyo_kv_free", None, C.POINTER(JyoKV))
     _proto(lib, "jyo_attention", I, P, P, P, P, I, I, I, I, I, P, P, P, P, I)
-    _proto(lib, "jyo_forward_cached", I, C.POINTER(ModelDesc), P, P, I, I, C.POINTER(JyoKV), P)
+    _proto(lib, "jyo_forward_cached", I, C.POINTER(ModelDesc), P, P, P, I, I, C.POINTER(JyoKV), P)
     _proto(lib, "jyo_generate", I, C.POINTER(ModelDesc), P, I, P, I, P, P, I, I, F, F, P,
            C.POINTER(JyoKV), P)
     return lib

@@ -404,7 +404,7 @@ done:
 }
 
 /* libs/model_libs/forward.h:47-96 */
-int jyo_forward_cached(float* X, const jy_model_desc* m, const float* cos_t, const float* sin_t, int seq,
+int jyo_forward_cached(const jy_model_desc* m, float* X, const float* cos_t, const float* sin_t, int seq,
                        int start_pos, jyo_kv* kv, float* layer_out) {
     if (kv->num_layers < m->num_layers || kv->num_kv_heads != m->num_kv_heads || kv->head_dim != m->head_dim)
         return -1;
@@ -457,7 +457,7 @@ int jyo_generate(const jy_model_desc* m, const int* prompt_ids, int prompt_len, 
     for (int step = 0; step < max_new && len < max_seq; step++) {
         const int start_pos = len - seq;
         for (int i = 0; i < seq; i++) jyo_embed_row(&m->embed, out_ids[start_pos + i], H, X + (size_t)i * H);
-        if (jyo_forward_cached(X, m, cos_t, sin_t, seq, start_pos, kv, NULL)) {
+        if (jyo_forward_cached(m, X, cos_t, sin_t, seq, start_pos, kv, NULL)) {
             len = -1;
             break;
         }

@@ -75,7 +75,7 @@ int jyo_transformer_layer(float* X, const jy_layer_weights* w, const float* cos_
 
 /* forward_cached (libs/model_libs/forward.h:47-96).  If layer_out != NULL it receives X after
  * every layer, [num_layers][seq][hidden].  Returns 0 / -1 (bad shape / capacity). */
-int jyo_forward_cached(float* X, const jy_model_desc* m, const float* cos_t, const float* sin_t, int seq,
+int jyo_forward_cached(const jy_model_desc* m, float* X, const float* cos_t, const float* sin_t, int seq,
                        int start_pos, jyo_kv* kv, float* layer_out);
 
 /* generate_cached / generate (libs/model_libs/generate.h:9-112).  kv == NULL: a private cache of

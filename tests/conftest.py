@@ -1,0 +1,64 @@
+"""Shared fixtures.  GPU tests are marked `gpu`; everything else runs on the CPU."""
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP library)")
+
+
+def ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+@pytest.fixture(scope="session")
+def oracle_lib():
+    import oracle
+    return oracle.load_oracle()
+
+
+@pytest.fixture(scope="session")
+def ref_lib():
+    import oracle
+    if not oracle.ref_available():
+        pytest.skip("oracle/_ref/libjyref.so not built (needs the reference tree)")
+    return oracle.load_ref()
+
+
+def rope_tables(olib, max_seq, head_dim, theta):
+    half = head_dim // 2
+    c = np.zeros(max_seq * half, np.float32)
+    s = np.zeros_like(c)
+    olib.jyo_rope_table(max_seq, head_dim, theta, ptr(c), ptr(s))
+    return c, s
+
+
+def q8_random_normal(olib, rows, cols, seed, std=0.02):
+    """Q8_0 rows [rows][cols/32]x34 from N(0, std) (the synthetic-model quantizer)."""
+    x = np.zeros(rows * cols, np.float32)
+    olib.jysyn_normal_fill(seed, 7, std, ptr(x), x.size)
+    out = np.zeros(rows * (cols // 32) * 34, np.uint8)
+    olib.jysyn_quantize_q8_0(ptr(x), ptr(out), x.size)
+    return out
+
+
+def q8_random_uniform(olib, rows, cols, seed):
+    """Isolated-matvec inputs: int8 ~ U[-127, 127], per-block scale ~ U(0.001, 0.01) as fp16."""
+    nb = rows * (cols // 32)
+    q = np.zeros(nb * 32, np.int32)
+    olib.jysyn_uniform_int_fill(seed, 11, -127, 127, ptr(q), q.size)
+    d = np.zeros(nb, np.float32)
+    olib.jysyn_uniform_fill(seed, 12, 0.001, 0.01, ptr(d), d.size)
+    dh = d.astype(np.float16).view(np.uint16)  # round to nearest even, as jysyn_f32_to_f16
+    blk = np.zeros((nb, 34), np.uint8)
+    blk[:, 0:2] = dh.view(np.uint8).reshape(nb, 2)
+    blk[:, 2:] = q.astype(np.int8).view(np.uint8).reshape(nb, 32)
+    return blk.reshape(-1)
