@@ -13,31 +13,30 @@ namespace jy {
 
 // IEEE half -> float.  Every half, subnormals included, is exact in float, which
 // is the value libs/date_libs/wmat.h:8-24 builds bit by bit.
-__device__ __forceinline__ float half_to_float(uint16_t h) {
+__host__ __device__ __forceinline__ float half_to_float(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
-
-// 2^(i/32) as double bits minus i<<47: the table of the exp2f-family reduction
-// (exp(x) = 2^(k/32) * 2^(r/32)); entry i is the correctly rounded double of
-// 2^(i/32) with the exponent contribution of i/32 taken out.
-__constant__ uint64_t kExp2Tab[32] = {
-    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
-    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
-    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
-    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
-    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
-    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
-    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
-    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
-};
 
 // expf with the results of the host libm the reference links (glibc 2.35,
 // x86-64 FMA variant): the published exp2f-table algorithm of ARM's
 // optimized-routines (32-entry table, cubic in double), with the contractions
 // GCC forms when that C is built with FMA.  Checked bit-exact against glibc's
 // expf on all 2^32 inputs on the host; the softmax only feeds it x <= 0.
-__device__ __forceinline__ float expf_libm(float x) {
-    const uint32_t ux = __float_as_uint(x);
+__host__ __device__ __forceinline__ float expf_libm(float x) {
+    // 2^(i/32) as double bits minus i<<47: the table of the exp2f-family reduction
+    // (exp(x) = 2^(k/32) * 2^(r/32)); entry i is the correctly rounded double of
+    // 2^(i/32) with the exponent contribution of i/32 taken out.
+    static constexpr uint64_t kExp2Tab[32] = {
+        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+    };
+    const uint32_t ux = __builtin_bit_cast(uint32_t, x);
     const uint32_t abstop = (ux >> 20) & 0x7ffu;
     if (abstop >= 0x42bu) {                      // |x| >= 88 or non-finite
         if (ux == 0xff800000u) return 0.0f;      // -inf
@@ -52,12 +51,12 @@ __device__ __forceinline__ float expf_libm(float x) {
     const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
     const double xd = (double)x;
     double kd = __builtin_fma(inv_ln2_n, xd, shift);
-    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd -= shift;
     const double r = __builtin_fma(inv_ln2_n, xd, -kd);
     uint64_t t = kExp2Tab[ki & 31u];
     t += ki << 47;
-    const double s = __longlong_as_double((long long)t);
+    const double s = __builtin_bit_cast(double, t);
     const double z = __builtin_fma(c0, r, c1);
     const double r2 = r * r;
     double y = __builtin_fma(c2, r, 1.0);
@@ -69,7 +68,7 @@ __device__ __forceinline__ float expf_libm(float x) {
 // SiLU of libs/model_libs/silu/x86/x86_classic.txt:2-28 as GCC -O3 builds it with
 // FMA: Cody-Waite reduction and the denominator contracted, explicit polynomial
 // FMAs, 2^n by exponent bits, one correctly rounded division.
-__device__ __forceinline__ float silu_ref(float vx) {
+__host__ __device__ __forceinline__ float silu_ref(float vx) {
     float xa = 0.0f - vx;
     xa = xa > -87.0f ? xa : -87.0f;
     xa = xa < 88.0f ? xa : 88.0f;
@@ -81,19 +80,19 @@ __device__ __forceinline__ float silu_ref(float vx) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    const float two_n = __uint_as_float((uint32_t)((int)nf + 127) << 23);
+    const float two_n = __builtin_bit_cast(float, (uint32_t)((int)nf + 127) << 23);
     return vx / __builtin_fmaf(p, two_n, 1.0f);
 }
 
 // int8 absmax quantisation step of kv_pack_q8 / the Q quantisation in attention
 // (libs/model_libs/attention/attention_q8.h:29-35): clamp to +-127, lrintf.
-__device__ __forceinline__ int8_t quant_i8(float v, float inv) {
+__host__ __device__ __forceinline__ int8_t quant_i8(float v, float inv) {
     float x = v * inv;
     x = x > 127.0f ? 127.0f : (x < -127.0f ? -127.0f : x);
     return (int8_t)(int)__builtin_rintf(x);
 }
 
-__device__ __forceinline__ float quant_inv(float amax) { return amax > 1e-8f ? 127.0f / amax : 0.0f; }
-__device__ __forceinline__ float quant_scale(float amax) { return amax > 1e-8f ? amax / 127.0f : 0.0f; }
+__host__ __device__ __forceinline__ float quant_inv(float amax) { return amax > 1e-8f ? 127.0f / amax : 0.0f; }
+__host__ __device__ __forceinline__ float quant_scale(float amax) { return amax > 1e-8f ? amax / 127.0f : 0.0f; }
 
 }  // namespace jy

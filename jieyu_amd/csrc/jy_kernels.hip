@@ -86,7 +86,8 @@ void launch_embed(const Q8Dev* q8, const float* f32, int hidden, const int* ids_
 
 // 16 FMA lanes over x^2 (lane l takes elements 16c+l; an 8-wide remainder pass
 // feeds lanes 0..7), then ((v0+v1) -> halves -> two hadds), scalar tail, then
-// y = (x*scale)*w with scale = 1/sqrtf(ss/n + eps).  The row is staged in LDS first.
+// y = (x*scale)*w with scale = 1/sqrtf(ss/n + eps)
+// (libs/model_libs/rmsnorm/x86/x86_classic.txt:2-26).  The row is staged in LDS first.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ X, float* __restrict__ Y,
                                                       const float* __restrict__ w, int n, float eps) {
     extern __shared__ __align__(16) float xr[];
@@ -115,7 +116,13 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
 #pragma unroll
         for (int l = 0; l < 4; l++) q[l] = s[l] + s[4 + l];
         float ss = (q[0] + q[1]) + (q[2] + q[3]);
-        for (int i = n16 + (rem8 ? 8 : 0); i < n; i++) ss = __builtin_fmaf(xr[i], xr[i], ss);
+        // tail of t < 8 elements: with t >= 4 the first four squares are rounded
+        // products added in order (the host compiler's in-order vector reduction),
+        // the rest fused
+        int i = n16 + (rem8 ? 8 : 0);
+        if (n - i >= 4)
+            for (const int e = i + 4; i < e; i++) ss = ss + xr[i] * xr[i];
+        for (; i < n; i++) ss = __builtin_fmaf(xr[i], xr[i], ss);
         const float den = ss / (float)n + eps;
         zero = den <= 0.0f;
         sc = zero ? 0.0f : 1.0f / sqrtf(den);

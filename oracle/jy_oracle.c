@@ -133,8 +133,10 @@ void jyo_embed_row(const jy_wmat* w, int id, int width, float* dst) {
 }
 
 /* rmsnorm/x86/x86_classic.txt:2-26: 16 FMA lanes over x^2 (an 8-wide remainder pass
- * feeds lanes 0..7), reduction ((v0+v1) -> halves -> two hadds), scalar tail
- * contracted, then y = (x*scale)*w. */
+ * feeds lanes 0..7), reduction ((v0+v1) -> halves -> two hadds), then the scalar
+ * tail of t < 8 elements (:15), then y = (x*scale)*w.  GCC 11 -O3 builds that
+ * tail loop as an in-order vector reduction: when t >= 4 the first four squares
+ * are rounded products added in order, the rest are contracted to FMAs. */
 void jyo_rmsnorm(const float* x, float* y, const float* w, int n, float eps) {
     float v[16];
     for (int l = 0; l < 16; l++) v[l] = 0.0f;
@@ -147,6 +149,8 @@ void jyo_rmsnorm(const float* x, float* y, const float* w, int n, float eps) {
     for (int l = 0; l < 8; l++) s[l] = v[l] + v[8 + l];
     for (int l = 0; l < 4; l++) t[l] = s[l] + s[4 + l];
     float ss = (t[0] + t[1]) + (t[2] + t[3]);
+    if (n - i >= 4)
+        for (const int e = i + 4; i < e; i++) ss = ss + x[i] * x[i];
     for (; i < n; i++) ss = fmaf(x[i], x[i], ss);
     const float den = ss / (float)n + eps;
     if (den <= 0.0f) {
