@@ -53,9 +53,24 @@ def token_bytes(d, weight_bytes, p):
             + L * nkv * (hd + 4) * 2)               # new K,V written
 
 
-def dominant_kernel_roofline(jy, olib, d, iters=60):
-    """The fused gate/up matvec (2F x hidden rows): its launch shape, timed in isolation
-    with HIP events over enough copies to defeat the 256 MiB infinity cache."""
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "matvec_q8_gateup_llama3-8b_pmc.md")
+
+
+def pmc_traffic(path=PMC_SUMMARY):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE runs, each scaled by a copy kernel of known size), or None."""
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def dominant_kernel_roofline(jy, olib, d, iters=64):
+    """The decode step's gate/up launch (2F x hidden interleaved rows, RMSNorm prologue,
+    SwiGLU epilogue), timed in isolation with HIP events on its stream over enough
+    copies to defeat the 256 MiB infinity cache."""
     rows, cols = 2 * d.intermediate, d.hidden
     nbytes = q8b(rows, cols)
     copies = max(2, int(np.ceil(1.2e9 / nbytes)))
@@ -66,13 +81,50 @@ def dominant_kernel_roofline(jy, olib, d, iters=60):
     del x
     xin = np.random.default_rng(0).standard_normal(cols).astype(np.float32)
     m = jy.Q8Matrix(w, rows, cols, copies=copies)
-    us = m.time(xin, iters)
+    us = m.time(xin, iters, variant=1)
     m.close()
-    algo = nbytes + cols * 4 + rows * 4
+    algo = nbytes + 2 * cols * 4 + (rows // 2) * 4  # weights, x, norm weights, SwiGLU output
     ach = algo / (us * 1e-6) / 1e9
-    return {"bound": "hbm", "kernel": "matvec_q8_kernel (fused gate/up, %dx%d)" % (rows, cols),
-            "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-            "traffic": None, "bytes_per_launch": algo, "avg_launch_us": round(us, 3), "copies": copies}
+    return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(),
+            "kernel": "matvec_q8_kernel<EPI_SWIGLU, NORM> (gate/up, %d x %d)" % (rows, cols),
+            "bytes_per_launch": algo, "avg_launch_us": round(us, 3), "launches": iters, "copies": copies}
+
+
+def isolated_matvecs(jy, olib, iters=64):
+    """The plain Q8 matvec at the isolated-kernel shapes (int8 ~ U[-127,127], scales
+    U(0.001,0.01), x ~ N(0,1), seed 1), rotating >1 GB of copies."""
+    res = {}
+    for rows, cols in ((4096, 4096), (14336, 4096), (4096, 14336)):
+        nb = rows * (cols // 32)
+        q = np.zeros(nb * 32, np.int32)
+        olib.jysyn_uniform_int_fill(1, 11, -127, 127, ptr(q), q.size)
+        dsc = np.zeros(nb, np.float32)
+        olib.jysyn_uniform_fill(1, 12, 0.001, 0.01, ptr(dsc), dsc.size)
+        blk = np.zeros((nb, 34), np.uint8)
+        blk[:, 0:2] = dsc.astype(np.float16).view(np.uint8).reshape(nb, 2)
+        blk[:, 2:] = q.astype(np.int8).view(np.uint8).reshape(nb, 32)
+        x = np.zeros(cols, np.float32)
+        olib.jysyn_normal_fill(1, 13, 1.0, ptr(x), cols)
+        copies = max(2, int(np.ceil(1.2e9 / blk.size)))
+        m = jy.Q8Matrix(blk.reshape(-1), rows, cols, copies=copies)
+        us = m.time(x, iters)
+        m.close()
+        algo = blk.size + cols * 4 + rows * 4
+        res[f"{rows}x{cols}"] = {"us": round(us, 3), "GB/s": round(algo / (us * 1e-6) / 1e9, 1)}
+    return res
+
+
+def copy_calibration(mb):
+    """A plain device copy of known size for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    n = mb * (1 << 20) // 4
+    a = torch.ones(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(8):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "launches": 8}), flush=True)
 
 
 def cpu_baseline(desc, prompt, n_new, gpu_model):
@@ -129,11 +181,17 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=6)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernel", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
+                    help="only run a plain device copy of MB MiB (rocprofv3 counter scaling) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this decode path is single-device (no sharding or collectives); "
               "run it with --gpus 1", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
 
     import jieyu_amd as jy
     import oracle
@@ -180,11 +238,13 @@ def main():
     log(f"  {K} steps: {wall_ms:.1f} ms wall ({dev_ms:.1f} ms device) -> {tok_s:.1f} tok/s, "
         f"{hbm_gbs:.0f} GB/s = {100 * hbm_gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s")
 
-    roof = None
+    roof = iso = None
     if not args.no_kernel:
         log("dominant kernel in isolation ...")
         roof = dominant_kernel_roofline(jy, olib, d)
         log(f"  {roof['kernel']}: {roof['avg_launch_us']} us -> {roof['achieved']} GB/s")
+        iso = isolated_matvecs(jy, olib)
+        log(f"  isolated matvec shapes: {iso}")
 
     cpu = None
     if not args.no_cpu:
@@ -211,7 +271,7 @@ def main():
         "prefill_ms": round(st.prefill_ms, 2), "prefill_tokens_s": round(args.prompt_len / (st.prefill_ms / 1e3), 1),
         "upload_s": round(st.upload_ms / 1e3, 2),
         "last_ids": ids[-8:].tolist(),
-        "roofline": roof, "cpu_baseline": cpu,
+        "roofline": roof, "cpu_baseline": cpu, "isolated_q8_matvec": iso,
     }
     print(json.dumps(out), flush=True)
 

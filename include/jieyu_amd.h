@@ -112,8 +112,10 @@ JYHIP_API jyhip_q8mat* jyhip_q8_upload(const void* w, int rows, int cols, int co
 JYHIP_API void jyhip_q8_free(jyhip_q8mat* m);
 JYHIP_API int jyhip_q8_matvec(jyhip_q8mat* m, const float* x, float* y);
 /* Time `iters` launches (rotating copies) with HIP events on the launch stream:
- * *avg_us = mean kernel-to-kernel time per launch. */
-JYHIP_API int jyhip_q8_matvec_time(jyhip_q8mat* m, const float* x, int iters, double* avg_us);
+ * *avg_us = mean kernel-to-kernel time per launch.  variant 0 is the plain
+ * matvec; variant 1 is the decode step's gate/up launch of the same kernel
+ * (RMSNorm prologue over x, SwiGLU epilogue over interleaved row pairs). */
+JYHIP_API int jyhip_q8_matvec_time(jyhip_q8mat* m, const float* x, int variant, int iters, double* avg_us);
 
 #ifdef __cplusplus
 }

@@ -74,7 +74,7 @@ def lib():
     _proto(L, "jyhip_q8_upload", P, P, I, I, I)
     _proto(L, "jyhip_q8_free", None, P)
     _proto(L, "jyhip_q8_matvec", I, P, P, P)
-    _proto(L, "jyhip_q8_matvec_time", I, P, P, I, C.POINTER(C.c_double))
+    _proto(L, "jyhip_q8_matvec_time", I, P, P, I, I, C.POINTER(C.c_double))
     _lib = L
     return L
 
@@ -277,10 +277,11 @@ class Q8Matrix:
         _check(self._lib.jyhip_q8_matvec(self.h, _ptr(x), _ptr(y)))
         return y
 
-    def time(self, x, iters):
+    def time(self, x, iters, variant=0):
+        """Mean µs per launch over `iters` launches; variant 1 = the decode gate/up launch."""
         x = np.ascontiguousarray(x, np.float32)
         us = C.c_double()
-        _check(self._lib.jyhip_q8_matvec_time(self.h, _ptr(x), iters, C.byref(us)))
+        _check(self._lib.jyhip_q8_matvec_time(self.h, _ptr(x), variant, iters, C.byref(us)))
         return us.value
 
     def close(self):

@@ -6,20 +6,597 @@
 //   e_j = expf(score_j - max); sum += e_j in ascending j; p_j = e_j * (1/sum);
 //   o[d] = fma(p_j * vs_j, (float)v8[j][d], o[d]) in ascending j.
 //
-// One workgroup per (query head, token row, slice of 32 output dims).  The scores
-// are parallel; the softmax sum and the output components are the reference's
-// ascending chains, run from LDS: the sum on one lane while the other waves stage
-// this slice of V (as fp16, exact for int8, so each chain step is one v_fma_mix),
-// then one lane per output dim.  In the fused decode form the kernel also quantises
-// the token's q, k and v itself and the first head of each GQA group appends k/v to
-// the cache (kv_pack_q8 of the new position).
+// Two kernels per attention call.
+//  1. attn_scores_kernel: one workgroup per (kv head, run of keys, token row)
+//     computes the scores of every query head of the GQA group against its keys,
+//     so each key is read once per group.  A key's bytes are spread over adjacent
+//     lanes (16 B each: 8 lanes per 128-byte key), the loads are coalesced and the
+//     lanes combine their partial int32 dots with butterflies.  In the fused decode
+//     form it also quantises the token's q, k and v, and one workgroup per kv head
+//     appends k/v to the cache (kv_pack_q8 of the new position).
+//  2. attn_softmax_pv_kernel: one workgroup per (query head, token row, slice of
+//     output dims) runs the reference's two ascending chains: the softmax sum on
+//     one lane while the other waves stage this slice of V in LDS (fp16, exact for
+//     int8, rows padded so the chain's 16-byte reads do not collide in a bank),
+//     then one lane per output dim.
+// Scores travel between the two through a per-row [nh][max_keys] float array.
 #include "jy_layout.h"
 
 namespace jy {
 
 static constexpr int ATT_THREADS = 256;
-static constexpr int ATT_ECAP = 4096;   // scores kept in LDS up to this many keys
-static constexpr int ATT_WIN = 2048;    // window of the sum chain beyond that
+static constexpr int ATT_ECAP = 4096;  // scores kept in LDS up to this many keys
+static constexpr int ATT_GB = 8;       // query heads per scores workgroup
+static constexpr int ATT_U = 2;        // key loads per lane in the scores kernel
+
+// ------------------------------------------------------------------ scores
+
+__global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a, int kc) {
+    __shared__ __align__(16) int8_t qv8[ATT_GB][256];
+    __shared__ __align__(16) int8_t kloc[256];
+    __shared__ __align__(16) int8_t vloc[256];
+    __shared__ float qsc[ATT_GB];
+    __shared__ float kvsc[2];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int hd = a.hd, nh = a.nh, nkv = a.nkv, group = nh / nkv;
+    const int nb = (group + ATT_GB - 1) / ATT_GB;
+    const int kvh = blockIdx.x / nb, hb = blockIdx.x - kvh * nb;
+    const int h0 = kvh * group + hb * ATT_GB;
+    const int gh = min(ATT_GB, group - hb * ATT_GB);
+    const int rr = blockIdx.z, r = a.row0 + rr;
+    const int pos = a.state ? a.state[0] - 1 : a.start_pos + r;
+    const int nk = pos + 1;
+    const int j0 = blockIdx.y * kc;
+    const bool fused = a.fused;
+    const bool appender = fused && blockIdx.y == 0 && hb == 0;
+    if (j0 >= nk) return;  // whole workgroup: no key of this run is attended (run 0 always is)
+    const int jend = min(j0 + kc, nk);
+    const size_t head = (size_t)a.layer * nkv + kvh;
+    const int8_t* K = a.kv.k + head * a.kv.max_seq * hd;
+    const float* KS = a.kv.ks + head * a.kv.max_seq;
+
+    // ---- the keys first: their loads depend only on the position, so they are in
+    // flight while the token's vectors are quantised.  One key's 16-byte pieces sit
+    // on LP adjacent lanes (the pieces of hd rounded up to a power of two); a wave
+    // covers KW = 64/LP keys per load and each lane ATT_U loads (kc = 4*KW*ATT_U).
+    const bool vec = (hd & 15) == 0;
+    const int P = hd >> 4;
+    int LP = 1;
+    while (LP < P) LP <<= 1;
+    const int KW = 64 / LP, piece = lane & (LP - 1), kl = lane / LP;
+    const bool live = vec && piece < P;
+    int4 k4[ATT_U];
+    float ksv[ATT_U];
+#pragma unroll
+    for (int u = 0; u < ATT_U; u++) {
+        const int j = j0 + (u * (ATT_THREADS / 64) + wave) * KW + kl;
+        const int jc = min(j, jend - 1);
+        k4[u] = live ? *reinterpret_cast<const int4*>(K + (size_t)jc * hd + piece * 16) : make_int4(0, 0, 0, 0);
+        ksv[u] = vec ? KS[jc] : 0.0f;
+    }
+
+    // ---- this token's q (and, fused, k and v) as int8: absmax, lrintf (kv_pack_q8,
+    // attention_q8.h:29-35); wave w takes items w, w+4, w+8 with all their loads
+    // issued before the reductions
+    if (fused) {
+        const float* row = a.qkv + (size_t)rr * (nh + 2 * nkv) * hd;
+        const int nitems = gh + 2;  // query heads, then k, then v
+        float vals[3][4];
+#pragma unroll
+        for (int t = 0; t < 3; t++) {
+            const int i = wave + 4 * t;
+            if (i < nitems) {
+                const float* src = i < gh ? row + (size_t)(h0 + i) * hd
+                                          : row + (size_t)((i == gh ? nh : nh + nkv) + kvh) * hd;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const int d = lane + 64 * c;
+                    vals[t][c] = d < hd ? src[d] : 0.0f;
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 3; t++) {
+            const int i = wave + 4 * t;
+            if (i < nitems) {
+                float amax = 0.0f;
+#pragma unroll
+                for (int c = 0; c < 4; c++) amax = fmaxf(amax, fabsf(vals[t][c]));
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+                const float inv = quant_inv(amax);
+                int8_t* dst = i < gh ? qv8[i] : (i == gh ? kloc : vloc);
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const int d = lane + 64 * c;
+                    if (d < hd) dst[d] = quant_i8(vals[t][c], inv);
+                }
+                if (lane == 0) {
+                    if (i < gh)
+                        qsc[i] = quant_scale(amax);
+                    else
+                        kvsc[i - gh] = quant_scale(amax);
+                }
+            }
+        }
+    } else {
+        for (int i = tid; i < gh * hd; i += blockDim.x) {
+            const int hh = i / hd, d = i - hh * hd;
+            qv8[hh][d] = a.q8[((size_t)r * nh + h0 + hh) * hd + d];
+        }
+        if (tid < gh) qsc[tid] = a.qsc[(size_t)r * nh + h0 + tid];
+    }
+    __syncthreads();
+    if (appender) {  // kv_pack_q8 of the new position, once per kv head
+        const size_t slot = head * a.kv.max_seq + pos;
+        for (int d = tid; d < hd; d += blockDim.x) {
+            a.kv.k[slot * hd + d] = kloc[d];
+            a.kv.v[slot * hd + d] = vloc[d];
+        }
+        if (tid == 0) {
+            a.kv.ks[slot] = kvsc[0];
+            a.kv.vs[slot] = kvsc[1];
+        }
+    }
+
+    float* S = a.scratch + ((size_t)rr * nh + h0) * a.max_keys;
+    const float scale = 1.0f / sqrtf((float)hd);
+    if (vec) {
+        int4 qw[ATT_GB];  // this lane's piece of every query head (pieces < P only: no read past hd)
+#pragma unroll
+        for (int hh = 0; hh < ATT_GB; hh++)
+            qw[hh] = (live && hh < gh) ? *reinterpret_cast<const int4*>(&qv8[hh][piece * 16]) : make_int4(0, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < ATT_U; u++) {
+            const int j = j0 + (u * (ATT_THREADS / 64) + wave) * KW + kl;
+            if (fused && j == pos) {  // the new key is not in the cache yet
+                k4[u] = live ? *reinterpret_cast<const int4*>(&kloc[piece * 16]) : make_int4(0, 0, 0, 0);
+                ksv[u] = kvsc[0];
+            }
+            int dot[ATT_GB];
+#pragma unroll
+            for (int hh = 0; hh < ATT_GB; hh++) {
+                int d = __builtin_amdgcn_sdot4(qw[hh].x, k4[u].x, 0, false);
+                d = __builtin_amdgcn_sdot4(qw[hh].y, k4[u].y, d, false);
+                d = __builtin_amdgcn_sdot4(qw[hh].z, k4[u].z, d, false);
+                d = __builtin_amdgcn_sdot4(qw[hh].w, k4[u].w, d, false);
+                for (int o = 1; o < LP; o <<= 1) d += __shfl_xor(d, o);
+                dot[hh] = d;
+            }
+            if (piece == 0 && j < jend) {
+#pragma unroll
+                for (int hh = 0; hh < ATT_GB; hh++)
+                    if (hh < gh) S[(size_t)hh * a.max_keys + j] = (float)dot[hh] * ((ksv[u] * qsc[hh]) * scale);
+            }
+        }
+    } else {
+        // head dims that are not a multiple of 16: one lane per key, 4-byte words
+        for (int j = j0 + tid; j < jend; j += blockDim.x) {
+            const bool here = fused && j == pos;
+            const int32_t* k32 = here ? reinterpret_cast<const int32_t*>(kloc)
+                                      : reinterpret_cast<const int32_t*>(K + (size_t)j * hd);
+            const float ksj = here ? kvsc[0] : KS[j];
+            for (int hh = 0; hh < gh; hh++) {
+                const int32_t* q32 = reinterpret_cast<const int32_t*>(qv8[hh]);
+                int dot = 0;
+                for (int i = 0; i < (hd >> 2); i++) dot = __builtin_amdgcn_sdot4(q32[i], k32[i], dot, false);
+                S[(size_t)hh * a.max_keys + j] = (float)dot * ((ksj * qsc[hh]) * scale);
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ softmax + PV
+
+// byte address of an LDS object for ds_* instructions (the local-address-space view
+// of a generic pointer into __shared__ memory)
+__device__ __forceinline__ uint32_t lds_off(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+__device__ __forceinline__ float hx(uint32_t w, int hi) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? (w >> 16) : w));
+}
+
+// The two sequential chains of the reference softmax/PV, one dependent VALU op per
+// step.  Their LDS operands stream through two register sets of 32 steps each: the
+// loads of one set are in flight while the chain runs through the other.  Written
+// as GCN assembly because the compiler turns a C ping-pong of register arrays into
+// one register copy per step; the loops are short, fixed and wait on lgkmcnt only
+// for the set they are about to read (LDS returns in order).  Batches of 64 steps;
+// the tail is C.
+//
+// sum += e[j], j ascending (libs/model_libs/attention/x86/x86_classic.txt:55-58)
+__device__ __forceinline__ float chain_sum(const float* e, int n, float sum) {
+    int nb = n >> 6;
+    if (nb > 0) {
+        uint32_t pa = lds_off(e);
+        asm volatile(
+        "s_waitcnt lgkmcnt(0)\n"
+        "ds_read_b128 v[100:103], %[pa]\n"
+        "ds_read_b128 v[104:107], %[pa] offset:16\n"
+        "ds_read_b128 v[108:111], %[pa] offset:32\n"
+        "ds_read_b128 v[112:115], %[pa] offset:48\n"
+        "ds_read_b128 v[116:119], %[pa] offset:64\n"
+        "ds_read_b128 v[120:123], %[pa] offset:80\n"
+        "ds_read_b128 v[124:127], %[pa] offset:96\n"
+        "ds_read_b128 v[128:131], %[pa] offset:112\n"
+        "ds_read_b128 v[132:135], %[pa] offset:128\n"
+        "ds_read_b128 v[136:139], %[pa] offset:144\n"
+        "ds_read_b128 v[140:143], %[pa] offset:160\n"
+        "ds_read_b128 v[144:147], %[pa] offset:176\n"
+        "ds_read_b128 v[148:151], %[pa] offset:192\n"
+        "ds_read_b128 v[152:155], %[pa] offset:208\n"
+        "ds_read_b128 v[156:159], %[pa] offset:224\n"
+        "ds_read_b128 v[160:163], %[pa] offset:240\n"
+        "s_sub_u32 %[nb], %[nb], 1\n"
+        "L_sum_loop_%=:\n"
+        "s_cmp_eq_u32 %[nb], 0\n"
+        "s_cbranch_scc1 L_sum_last_%=\n"
+        "s_waitcnt lgkmcnt(8)\n"
+        "v_add_f32 %[s], %[s], v100\n"
+        "v_add_f32 %[s], %[s], v101\n"
+        "v_add_f32 %[s], %[s], v102\n"
+        "v_add_f32 %[s], %[s], v103\n"
+        "v_add_f32 %[s], %[s], v104\n"
+        "v_add_f32 %[s], %[s], v105\n"
+        "v_add_f32 %[s], %[s], v106\n"
+        "v_add_f32 %[s], %[s], v107\n"
+        "v_add_f32 %[s], %[s], v108\n"
+        "v_add_f32 %[s], %[s], v109\n"
+        "v_add_f32 %[s], %[s], v110\n"
+        "v_add_f32 %[s], %[s], v111\n"
+        "v_add_f32 %[s], %[s], v112\n"
+        "v_add_f32 %[s], %[s], v113\n"
+        "v_add_f32 %[s], %[s], v114\n"
+        "v_add_f32 %[s], %[s], v115\n"
+        "v_add_f32 %[s], %[s], v116\n"
+        "v_add_f32 %[s], %[s], v117\n"
+        "v_add_f32 %[s], %[s], v118\n"
+        "v_add_f32 %[s], %[s], v119\n"
+        "v_add_f32 %[s], %[s], v120\n"
+        "v_add_f32 %[s], %[s], v121\n"
+        "v_add_f32 %[s], %[s], v122\n"
+        "v_add_f32 %[s], %[s], v123\n"
+        "v_add_f32 %[s], %[s], v124\n"
+        "v_add_f32 %[s], %[s], v125\n"
+        "v_add_f32 %[s], %[s], v126\n"
+        "v_add_f32 %[s], %[s], v127\n"
+        "v_add_f32 %[s], %[s], v128\n"
+        "v_add_f32 %[s], %[s], v129\n"
+        "v_add_f32 %[s], %[s], v130\n"
+        "v_add_f32 %[s], %[s], v131\n"
+        "v_add_u32_e32 %[pa], 0x100, %[pa]\n"
+        "ds_read_b128 v[100:103], %[pa]\n"
+        "ds_read_b128 v[104:107], %[pa] offset:16\n"
+        "ds_read_b128 v[108:111], %[pa] offset:32\n"
+        "ds_read_b128 v[112:115], %[pa] offset:48\n"
+        "ds_read_b128 v[116:119], %[pa] offset:64\n"
+        "ds_read_b128 v[120:123], %[pa] offset:80\n"
+        "ds_read_b128 v[124:127], %[pa] offset:96\n"
+        "ds_read_b128 v[128:131], %[pa] offset:112\n"
+        "s_waitcnt lgkmcnt(8)\n"
+        "v_add_f32 %[s], %[s], v132\n"
+        "v_add_f32 %[s], %[s], v133\n"
+        "v_add_f32 %[s], %[s], v134\n"
+        "v_add_f32 %[s], %[s], v135\n"
+        "v_add_f32 %[s], %[s], v136\n"
+        "v_add_f32 %[s], %[s], v137\n"
+        "v_add_f32 %[s], %[s], v138\n"
+        "v_add_f32 %[s], %[s], v139\n"
+        "v_add_f32 %[s], %[s], v140\n"
+        "v_add_f32 %[s], %[s], v141\n"
+        "v_add_f32 %[s], %[s], v142\n"
+        "v_add_f32 %[s], %[s], v143\n"
+        "v_add_f32 %[s], %[s], v144\n"
+        "v_add_f32 %[s], %[s], v145\n"
+        "v_add_f32 %[s], %[s], v146\n"
+        "v_add_f32 %[s], %[s], v147\n"
+        "v_add_f32 %[s], %[s], v148\n"
+        "v_add_f32 %[s], %[s], v149\n"
+        "v_add_f32 %[s], %[s], v150\n"
+        "v_add_f32 %[s], %[s], v151\n"
+        "v_add_f32 %[s], %[s], v152\n"
+        "v_add_f32 %[s], %[s], v153\n"
+        "v_add_f32 %[s], %[s], v154\n"
+        "v_add_f32 %[s], %[s], v155\n"
+        "v_add_f32 %[s], %[s], v156\n"
+        "v_add_f32 %[s], %[s], v157\n"
+        "v_add_f32 %[s], %[s], v158\n"
+        "v_add_f32 %[s], %[s], v159\n"
+        "v_add_f32 %[s], %[s], v160\n"
+        "v_add_f32 %[s], %[s], v161\n"
+        "v_add_f32 %[s], %[s], v162\n"
+        "v_add_f32 %[s], %[s], v163\n"
+        "ds_read_b128 v[132:135], %[pa] offset:128\n"
+        "ds_read_b128 v[136:139], %[pa] offset:144\n"
+        "ds_read_b128 v[140:143], %[pa] offset:160\n"
+        "ds_read_b128 v[144:147], %[pa] offset:176\n"
+        "ds_read_b128 v[148:151], %[pa] offset:192\n"
+        "ds_read_b128 v[152:155], %[pa] offset:208\n"
+        "ds_read_b128 v[156:159], %[pa] offset:224\n"
+        "ds_read_b128 v[160:163], %[pa] offset:240\n"
+        "s_sub_u32 %[nb], %[nb], 1\n"
+        "s_branch L_sum_loop_%=\n"
+        "L_sum_last_%=:\n"
+        "s_waitcnt lgkmcnt(8)\n"
+        "v_add_f32 %[s], %[s], v100\n"
+        "v_add_f32 %[s], %[s], v101\n"
+        "v_add_f32 %[s], %[s], v102\n"
+        "v_add_f32 %[s], %[s], v103\n"
+        "v_add_f32 %[s], %[s], v104\n"
+        "v_add_f32 %[s], %[s], v105\n"
+        "v_add_f32 %[s], %[s], v106\n"
+        "v_add_f32 %[s], %[s], v107\n"
+        "v_add_f32 %[s], %[s], v108\n"
+        "v_add_f32 %[s], %[s], v109\n"
+        "v_add_f32 %[s], %[s], v110\n"
+        "v_add_f32 %[s], %[s], v111\n"
+        "v_add_f32 %[s], %[s], v112\n"
+        "v_add_f32 %[s], %[s], v113\n"
+        "v_add_f32 %[s], %[s], v114\n"
+        "v_add_f32 %[s], %[s], v115\n"
+        "v_add_f32 %[s], %[s], v116\n"
+        "v_add_f32 %[s], %[s], v117\n"
+        "v_add_f32 %[s], %[s], v118\n"
+        "v_add_f32 %[s], %[s], v119\n"
+        "v_add_f32 %[s], %[s], v120\n"
+        "v_add_f32 %[s], %[s], v121\n"
+        "v_add_f32 %[s], %[s], v122\n"
+        "v_add_f32 %[s], %[s], v123\n"
+        "v_add_f32 %[s], %[s], v124\n"
+        "v_add_f32 %[s], %[s], v125\n"
+        "v_add_f32 %[s], %[s], v126\n"
+        "v_add_f32 %[s], %[s], v127\n"
+        "v_add_f32 %[s], %[s], v128\n"
+        "v_add_f32 %[s], %[s], v129\n"
+        "v_add_f32 %[s], %[s], v130\n"
+        "v_add_f32 %[s], %[s], v131\n"
+        "s_waitcnt lgkmcnt(0)\n"
+        "v_add_f32 %[s], %[s], v132\n"
+        "v_add_f32 %[s], %[s], v133\n"
+        "v_add_f32 %[s], %[s], v134\n"
+        "v_add_f32 %[s], %[s], v135\n"
+        "v_add_f32 %[s], %[s], v136\n"
+        "v_add_f32 %[s], %[s], v137\n"
+        "v_add_f32 %[s], %[s], v138\n"
+        "v_add_f32 %[s], %[s], v139\n"
+        "v_add_f32 %[s], %[s], v140\n"
+        "v_add_f32 %[s], %[s], v141\n"
+        "v_add_f32 %[s], %[s], v142\n"
+        "v_add_f32 %[s], %[s], v143\n"
+        "v_add_f32 %[s], %[s], v144\n"
+        "v_add_f32 %[s], %[s], v145\n"
+        "v_add_f32 %[s], %[s], v146\n"
+        "v_add_f32 %[s], %[s], v147\n"
+        "v_add_f32 %[s], %[s], v148\n"
+        "v_add_f32 %[s], %[s], v149\n"
+        "v_add_f32 %[s], %[s], v150\n"
+        "v_add_f32 %[s], %[s], v151\n"
+        "v_add_f32 %[s], %[s], v152\n"
+        "v_add_f32 %[s], %[s], v153\n"
+        "v_add_f32 %[s], %[s], v154\n"
+        "v_add_f32 %[s], %[s], v155\n"
+        "v_add_f32 %[s], %[s], v156\n"
+        "v_add_f32 %[s], %[s], v157\n"
+        "v_add_f32 %[s], %[s], v158\n"
+        "v_add_f32 %[s], %[s], v159\n"
+        "v_add_f32 %[s], %[s], v160\n"
+        "v_add_f32 %[s], %[s], v161\n"
+        "v_add_f32 %[s], %[s], v162\n"
+        "v_add_f32 %[s], %[s], v163\n"
+        : [s] "+v"(sum), [pa] "+v"(pa), [nb] "+s"(nb)
+        :
+        : "v100", "v101", "v102", "v103", "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111", "v112", "v113", "v114", "v115", "v116", "v117", "v118", "v119", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "v128", "v129", "v130", "v131", "v132", "v133", "v134", "v135", "v136", "v137", "v138", "v139", "v140", "v141", "v142", "v143", "v144", "v145", "v146", "v147", "v148", "v149", "v150", "v151", "v152", "v153", "v154", "v155", "v156", "v157", "v158", "v159", "v160", "v161", "v162", "v163", "scc", "memory");
+    }
+    for (int j = n & ~63; j < n; j++) sum += e[j];
+    return sum;
+}
+
+// o = fma(p_j, v_j, o), j ascending; v as fp16 (exact for int8), so each step is one
+// v_fma_mix (libs/model_libs/attention/x86/x86_classic.txt:63-70)
+__device__ __forceinline__ float chain_pv(const float* P, const _Float16* vr, float o, int n) {
+    int nb = n >> 6;
+    if (nb > 0) {
+        uint32_t pa = lds_off(P), va = lds_off(vr);
+        asm volatile(
+        "s_waitcnt lgkmcnt(0)\n"
+        "ds_read_b128 v[100:103], %[pa]\n"
+        "ds_read_b128 v[104:107], %[pa] offset:16\n"
+        "ds_read_b128 v[108:111], %[pa] offset:32\n"
+        "ds_read_b128 v[112:115], %[pa] offset:48\n"
+        "ds_read_b128 v[116:119], %[pa] offset:64\n"
+        "ds_read_b128 v[120:123], %[pa] offset:80\n"
+        "ds_read_b128 v[124:127], %[pa] offset:96\n"
+        "ds_read_b128 v[128:131], %[pa] offset:112\n"
+        "ds_read_b128 v[132:135], %[va]\n"
+        "ds_read_b128 v[136:139], %[va] offset:16\n"
+        "ds_read_b128 v[140:143], %[va] offset:32\n"
+        "ds_read_b128 v[144:147], %[va] offset:48\n"
+        "ds_read_b128 v[148:151], %[pa] offset:128\n"
+        "ds_read_b128 v[152:155], %[pa] offset:144\n"
+        "ds_read_b128 v[156:159], %[pa] offset:160\n"
+        "ds_read_b128 v[160:163], %[pa] offset:176\n"
+        "ds_read_b128 v[164:167], %[pa] offset:192\n"
+        "ds_read_b128 v[168:171], %[pa] offset:208\n"
+        "ds_read_b128 v[172:175], %[pa] offset:224\n"
+        "ds_read_b128 v[176:179], %[pa] offset:240\n"
+        "ds_read_b128 v[180:183], %[va] offset:64\n"
+        "ds_read_b128 v[184:187], %[va] offset:80\n"
+        "ds_read_b128 v[188:191], %[va] offset:96\n"
+        "ds_read_b128 v[192:195], %[va] offset:112\n"
+        "s_sub_u32 %[nb], %[nb], 1\n"
+        "L_pv_loop_%=:\n"
+        "s_cmp_eq_u32 %[nb], 0\n"
+        "s_cbranch_scc1 L_pv_last_%=\n"
+        "s_waitcnt lgkmcnt(12)\n"
+        "v_fma_mix_f32 %[o], v100, v132, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v101, v132, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v102, v133, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v103, v133, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v104, v134, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v105, v134, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v106, v135, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v107, v135, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v108, v136, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v109, v136, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v110, v137, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v111, v137, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v112, v138, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v113, v138, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v114, v139, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v115, v139, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v116, v140, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v117, v140, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v118, v141, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v119, v141, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v120, v142, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v121, v142, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v122, v143, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v123, v143, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v124, v144, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v125, v144, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v126, v145, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v127, v145, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v128, v146, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v129, v146, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v130, v147, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v131, v147, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_add_u32_e32 %[pa], 0x100, %[pa]\n"
+        "v_add_u32_e32 %[va], 0x80, %[va]\n"
+        "ds_read_b128 v[100:103], %[pa]\n"
+        "ds_read_b128 v[104:107], %[pa] offset:16\n"
+        "ds_read_b128 v[108:111], %[pa] offset:32\n"
+        "ds_read_b128 v[112:115], %[pa] offset:48\n"
+        "ds_read_b128 v[116:119], %[pa] offset:64\n"
+        "ds_read_b128 v[120:123], %[pa] offset:80\n"
+        "ds_read_b128 v[124:127], %[pa] offset:96\n"
+        "ds_read_b128 v[128:131], %[pa] offset:112\n"
+        "ds_read_b128 v[132:135], %[va]\n"
+        "ds_read_b128 v[136:139], %[va] offset:16\n"
+        "ds_read_b128 v[140:143], %[va] offset:32\n"
+        "ds_read_b128 v[144:147], %[va] offset:48\n"
+        "s_waitcnt lgkmcnt(12)\n"
+        "v_fma_mix_f32 %[o], v148, v180, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v149, v180, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v150, v181, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v151, v181, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v152, v182, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v153, v182, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v154, v183, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v155, v183, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v156, v184, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v157, v184, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v158, v185, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v159, v185, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v160, v186, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v161, v186, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v162, v187, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v163, v187, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v164, v188, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v165, v188, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v166, v189, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v167, v189, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v168, v190, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v169, v190, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v170, v191, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v171, v191, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v172, v192, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v173, v192, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v174, v193, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v175, v193, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v176, v194, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v177, v194, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v178, v195, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v179, v195, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "ds_read_b128 v[148:151], %[pa] offset:128\n"
+        "ds_read_b128 v[152:155], %[pa] offset:144\n"
+        "ds_read_b128 v[156:159], %[pa] offset:160\n"
+        "ds_read_b128 v[160:163], %[pa] offset:176\n"
+        "ds_read_b128 v[164:167], %[pa] offset:192\n"
+        "ds_read_b128 v[168:171], %[pa] offset:208\n"
+        "ds_read_b128 v[172:175], %[pa] offset:224\n"
+        "ds_read_b128 v[176:179], %[pa] offset:240\n"
+        "ds_read_b128 v[180:183], %[va] offset:64\n"
+        "ds_read_b128 v[184:187], %[va] offset:80\n"
+        "ds_read_b128 v[188:191], %[va] offset:96\n"
+        "ds_read_b128 v[192:195], %[va] offset:112\n"
+        "s_sub_u32 %[nb], %[nb], 1\n"
+        "s_branch L_pv_loop_%=\n"
+        "L_pv_last_%=:\n"
+        "s_waitcnt lgkmcnt(12)\n"
+        "v_fma_mix_f32 %[o], v100, v132, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v101, v132, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v102, v133, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v103, v133, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v104, v134, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v105, v134, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v106, v135, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v107, v135, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v108, v136, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v109, v136, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v110, v137, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v111, v137, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v112, v138, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v113, v138, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v114, v139, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v115, v139, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v116, v140, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v117, v140, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v118, v141, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v119, v141, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v120, v142, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v121, v142, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v122, v143, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v123, v143, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v124, v144, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v125, v144, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v126, v145, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v127, v145, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v128, v146, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v129, v146, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v130, v147, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v131, v147, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "s_waitcnt lgkmcnt(0)\n"
+        "v_fma_mix_f32 %[o], v148, v180, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v149, v180, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v150, v181, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v151, v181, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v152, v182, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v153, v182, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v154, v183, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v155, v183, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v156, v184, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v157, v184, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v158, v185, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v159, v185, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v160, v186, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v161, v186, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v162, v187, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v163, v187, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v164, v188, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v165, v188, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v166, v189, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v167, v189, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v168, v190, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v169, v190, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v170, v191, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v171, v191, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v172, v192, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v173, v192, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v174, v193, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v175, v193, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v176, v194, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v177, v194, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v178, v195, %[o] op_sel_hi:[0,1,0]\n"
+        "v_fma_mix_f32 %[o], v179, v195, %[o] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+        : [o] "+v"(o), [pa] "+v"(pa), [va] "+v"(va), [nb] "+s"(nb)
+        :
+        : "v100", "v101", "v102", "v103", "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111", "v112", "v113", "v114", "v115", "v116", "v117", "v118", "v119", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "v128", "v129", "v130", "v131", "v132", "v133", "v134", "v135", "v136", "v137", "v138", "v139", "v140", "v141", "v142", "v143", "v144", "v145", "v146", "v147", "v148", "v149", "v150", "v151", "v152", "v153", "v154", "v155", "v156", "v157", "v158", "v159", "v160", "v161", "v162", "v163", "v164", "v165", "v166", "v167", "v168", "v169", "v170", "v171", "v172", "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183", "v184", "v185", "v186", "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195", "scc", "memory");
+    }
+    for (int j = n & ~63; j < n; j++) o = __builtin_fmaf(P[j], (float)vr[j], o);
+    return o;
+}
 
 __device__ __forceinline__ float att_block_max(float v, float* red) {
 #pragma unroll
@@ -33,91 +610,68 @@ __device__ __forceinline__ float att_block_max(float v, float* red) {
     return r;
 }
 
-// absmax int8 quantisation of one head vector by one wave (kv_pack_q8)
-__device__ __forceinline__ void att_quant(const float* src, int hd, int8_t* dst, float* scale_out) {
-    const int lane = threadIdx.x & 63;
-    float amax = 0.0f;
-    for (int d = lane; d < hd; d += 64) amax = fmaxf(amax, fabsf(src[d]));
+// V[j0 .. j0+cnt)[d0 .. d0+ds) -> VH (fp16, [d][j] with row stride vstr halves), by
+// the threads t0.. of the workgroup; each takes two adjacent keys so its stores are
+// whole 32-bit words (adjacent lanes -> adjacent words)
+__device__ __forceinline__ void att_stage_v(const int8_t* V, int hd, int d0, int ds, int j0, int cnt, _Float16* VH,
+                                            int vstr, int t0) {
+    const int nthr = (int)blockDim.x - t0, t = (int)threadIdx.x - t0;
+    if (t < 0) return;
+    uint32_t* VW = reinterpret_cast<uint32_t*>(VH);
+    const int wstr = vstr >> 1, pairs = (cnt + 1) >> 1;
+    if ((ds & 15) == 0 && ds <= 64) {
+        const int pieces = ds >> 4;
+        for (int kp = t; kp < pairs; kp += nthr) {
+            const int ja = j0 + 2 * kp;
+            const bool hasb = 2 * kp + 1 < cnt;
+            uint4 wa[4], wb[4];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-    const float inv = quant_inv(amax);
-    for (int d = lane; d < hd; d += 64) dst[d] = quant_i8(src[d], inv);
-    if (lane == 0) *scale_out = quant_scale(amax);
-}
-
-// The two sequential chains of the reference softmax/PV, with their LDS operands
-// fetched 16 steps ahead into registers so each step is one dependent VALU op.
-__device__ __forceinline__ float chain_sum(const float* e, int n, float sum) {
-    int j = 0;
-    if (n >= 16) {
-        const float4* e4 = reinterpret_cast<const float4*>(e);
-        float4 c0 = e4[0], c1 = e4[1], c2 = e4[2], c3 = e4[3];
-        for (; j + 32 <= n; j += 16) {
-            const float4 n0 = e4[(j >> 2) + 4], n1 = e4[(j >> 2) + 5], n2 = e4[(j >> 2) + 6], n3 = e4[(j >> 2) + 7];
-            sum += c0.x; sum += c0.y; sum += c0.z; sum += c0.w;
-            sum += c1.x; sum += c1.y; sum += c1.z; sum += c1.w;
-            sum += c2.x; sum += c2.y; sum += c2.z; sum += c2.w;
-            sum += c3.x; sum += c3.y; sum += c3.z; sum += c3.w;
-            c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+            for (int pc = 0; pc < 4; pc++)
+                if (pc < pieces) {
+                    wa[pc] = *reinterpret_cast<const uint4*>(V + (size_t)ja * hd + d0 + pc * 16);
+                    wb[pc] = hasb ? *reinterpret_cast<const uint4*>(V + (size_t)(ja + 1) * hd + d0 + pc * 16)
+                                  : make_uint4(0, 0, 0, 0);
+                }
+#pragma unroll
+            for (int pc = 0; pc < 4; pc++)
+                if (pc < pieces) {
+                    const uint32_t xa[4] = {wa[pc].x, wa[pc].y, wa[pc].z, wa[pc].w};
+                    const uint32_t xb[4] = {wb[pc].x, wb[pc].y, wb[pc].z, wb[pc].w};
+#pragma unroll
+                    for (int b = 0; b < 16; b++) {
+                        const _Float16 lo = (_Float16)(int8_t)(xa[b >> 2] >> (8 * (b & 3)));
+                        const _Float16 hi = (_Float16)(int8_t)(xb[b >> 2] >> (8 * (b & 3)));
+                        VW[(size_t)(pc * 16 + b) * wstr + kp] =
+                            (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+                    }
+                }
         }
-        sum += c0.x; sum += c0.y; sum += c0.z; sum += c0.w;
-        sum += c1.x; sum += c1.y; sum += c1.z; sum += c1.w;
-        sum += c2.x; sum += c2.y; sum += c2.z; sum += c2.w;
-        sum += c3.x; sum += c3.y; sum += c3.z; sum += c3.w;
-        j += 16;
-    }
-    for (; j < n; j++) sum += e[j];
-    return sum;
-}
-
-__device__ __forceinline__ float hx(uint32_t w, int hi) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? (w >> 16) : w));
-}
-
-// o = fma(p_j, v_j, o) for j ascending; v as fp16 (exact int8), one v_fma_mix per step
-__device__ __forceinline__ float chain_pv(const float* P, const _Float16* vr, float o, int n) {
-    int j = 0;
-    if (n >= 16) {
-        const float4* p4 = reinterpret_cast<const float4*>(P);
-        const uint4* v4 = reinterpret_cast<const uint4*>(vr);
-        float4 a0 = p4[0], a1 = p4[1], a2 = p4[2], a3 = p4[3];
-        uint4 b0 = v4[0], b1 = v4[1];
-        auto steps = [&](const float4& q0, const float4& q1, const float4& q2, const float4& q3, const uint4& u0,
-                         const uint4& u1) {
-            o = __builtin_fmaf(q0.x, hx(u0.x, 0), o); o = __builtin_fmaf(q0.y, hx(u0.x, 1), o);
-            o = __builtin_fmaf(q0.z, hx(u0.y, 0), o); o = __builtin_fmaf(q0.w, hx(u0.y, 1), o);
-            o = __builtin_fmaf(q1.x, hx(u0.z, 0), o); o = __builtin_fmaf(q1.y, hx(u0.z, 1), o);
-            o = __builtin_fmaf(q1.z, hx(u0.w, 0), o); o = __builtin_fmaf(q1.w, hx(u0.w, 1), o);
-            o = __builtin_fmaf(q2.x, hx(u1.x, 0), o); o = __builtin_fmaf(q2.y, hx(u1.x, 1), o);
-            o = __builtin_fmaf(q2.z, hx(u1.y, 0), o); o = __builtin_fmaf(q2.w, hx(u1.y, 1), o);
-            o = __builtin_fmaf(q3.x, hx(u1.z, 0), o); o = __builtin_fmaf(q3.y, hx(u1.z, 1), o);
-            o = __builtin_fmaf(q3.z, hx(u1.w, 0), o); o = __builtin_fmaf(q3.w, hx(u1.w, 1), o);
-        };
-        for (; j + 32 <= n; j += 16) {
-            const float4 n0 = p4[(j >> 2) + 4], n1 = p4[(j >> 2) + 5], n2 = p4[(j >> 2) + 6], n3 = p4[(j >> 2) + 7];
-            const uint4 m0 = v4[(j >> 3) + 2], m1 = v4[(j >> 3) + 3];
-            steps(a0, a1, a2, a3, b0, b1);
-            a0 = n0; a1 = n1; a2 = n2; a3 = n3; b0 = m0; b1 = m1;
+    } else {  // any ds that is a multiple of 4: 4-byte words
+        const int words = ds >> 2;
+        for (int e = t; e < pairs * words; e += nthr) {
+            const int kp = e / words, wd = e - kp * words, ja = j0 + 2 * kp;
+            const uint32_t xa = *reinterpret_cast<const uint32_t*>(V + (size_t)ja * hd + d0 + wd * 4);
+            const uint32_t xb =
+                2 * kp + 1 < cnt ? *reinterpret_cast<const uint32_t*>(V + (size_t)(ja + 1) * hd + d0 + wd * 4) : 0u;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const _Float16 lo = (_Float16)(int8_t)(xa >> (8 * b));
+                const _Float16 hi = (_Float16)(int8_t)(xb >> (8 * b));
+                VW[(size_t)(wd * 4 + b) * wstr + kp] =
+                    (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+            }
         }
-        steps(a0, a1, a2, a3, b0, b1);
-        j += 16;
     }
-    for (; j < n; j++) o = __builtin_fmaf(P[j], (float)vr[j], o);
-    return o;
 }
 
-__global__ __launch_bounds__(ATT_THREADS) void attention_kernel(AttnArgs a, int ds, int vcap) {
+__global__ __launch_bounds__(ATT_THREADS) void attn_softmax_pv_kernel(AttnArgs a, int ds, int vcap, int vstr) {
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ __align__(16) int8_t qv8[256];
-    __shared__ __align__(16) int8_t kloc[256];
-    __shared__ __align__(16) int8_t vloc[256];
-    __shared__ float sc3[3];  // qsc, kscale, vscale
     __shared__ float red[8];
     __shared__ float s_inv;
     float* E = reinterpret_cast<float*>(smem);                                   // [ATT_ECAP]
-    _Float16* VH = reinterpret_cast<_Float16*>(smem + ATT_ECAP * sizeof(float));  // [ds][vcap]
+    _Float16* VH = reinterpret_cast<_Float16*>(smem + ATT_ECAP * sizeof(float));  // [ds][vstr]
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = tid >> 6;
     const int h = blockIdx.x, rr = blockIdx.y, slice = blockIdx.z;
     const int r = a.row0 + rr;
     const int hd = a.hd, nh = a.nh, nkv = a.nkv, group = nh / nkv, kvh = h / group;
@@ -125,229 +679,117 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(AttnArgs a, int 
     const int nk = pos + 1;
     const int d0 = slice * ds;
     const size_t head = (size_t)a.layer * nkv + kvh;
-    const int8_t* K = a.kv.k + head * a.kv.max_seq * hd;
     const int8_t* V = a.kv.v + head * a.kv.max_seq * hd;
-    const float* KS = a.kv.ks + head * a.kv.max_seq;
     const float* VS = a.kv.vs + head * a.kv.max_seq;
-    const bool fused = a.fused;
-    const bool long_ctx = nk > ATT_ECAP;
-    float* G = a.scratch + ((size_t)rr * nh + h) * a.max_keys;  // long contexts: scores in HBM
+    const float* S = a.scratch + ((size_t)rr * nh + h) * a.max_keys;
 
-    // ---- this token's q (and, fused, k and v) as int8
-    if (fused) {
-        const float* row = a.qkv + (size_t)rr * (nh + 2 * nkv) * hd;
-        if (wave == 0) att_quant(row + (size_t)h * hd, hd, qv8, &sc3[0]);
-        if (wave == 1) att_quant(row + (size_t)(nh + kvh) * hd, hd, kloc, &sc3[1]);
-        if (wave == 2) att_quant(row + (size_t)(nh + nkv + kvh) * hd, hd, vloc, &sc3[2]);
-    } else if (wave == 0) {
-        const int8_t* q = a.q8 + ((size_t)r * nh + h) * hd;
-        for (int d = lane; d < hd; d += 64) qv8[d] = q[d];
-        if (lane == 0) sc3[0] = a.qsc[(size_t)r * nh + h];
-    }
-    __syncthreads();
-    if (fused && slice == 0 && h % group == 0) {  // the group's first head appends k/v
-        const size_t slot = head * a.kv.max_seq + pos;
-        for (int d = tid; d < hd; d += blockDim.x) {
-            a.kv.k[slot * hd + d] = kloc[d];
-            a.kv.v[slot * hd + d] = vloc[d];
+    float o = 0.0f;
+    if (nk <= ATT_ECAP) {
+        // scores -> LDS, max, e_j in place
+        float lmax = -1e30f;
+        for (int j = tid; j < nk; j += blockDim.x) {
+            const float s = S[j];
+            E[j] = s;
+            lmax = fmaxf(lmax, s);
         }
-        if (tid == 0) {
-            a.kv.ks[slot] = sc3[1];
-            a.kv.vs[slot] = sc3[2];
-        }
-    }
-
-    // ---- scores
-    const float qs = sc3[0];
-    const float scale = 1.0f / sqrtf((float)hd);
-    const int nwords = hd >> 2;
-    const int32_t* q32 = reinterpret_cast<const int32_t*>(qv8);
-    const bool vec = (hd & 15) == 0;
-    int4 qw4[16];  // the int8 query as 16-byte words (hd <= 256), loop-invariant
-#pragma unroll
-    for (int i = 0; i < 16; i++)
-        if (vec && i < (hd >> 4)) qw4[i] = reinterpret_cast<const int4*>(qv8)[i];
-    float lmax = -1e30f;
-    auto score_of = [&](int j, int dot) {
-        const bool here = fused && j == pos;
-        const float ksj = here ? sc3[1] : KS[j];
-        const float sv = (float)dot * ((ksj * qs) * scale);
-        if (long_ctx)
-            G[j] = sv;
-        else
-            E[j] = sv;
-        lmax = fmaxf(lmax, sv);
-    };
-    // exact int32 q.k (|q|,|k| <= 127); two keys per thread per pass keep 32 loads in flight
-    for (int j = tid; j < nk; j += 2 * blockDim.x) {
-        const int j2 = j + blockDim.x;
-        const bool here = fused && j == pos, here2 = fused && j2 == pos;
-        if (vec && !here && !here2 && j2 < nk) {
-            const int4* k4a = reinterpret_cast<const int4*>(K + (size_t)j * hd);
-            const int4* k4b = reinterpret_cast<const int4*>(K + (size_t)j2 * hd);
-            int4 ka[16], kb[16];
-#pragma unroll
-            for (int i = 0; i < 16; i++)
-                if (i < (hd >> 4)) {
-                    ka[i] = k4a[i];
-                    kb[i] = k4b[i];
-                }
-            int da = 0, db = 0;
-#pragma unroll
-            for (int i = 0; i < 16; i++)
-                if (i < (hd >> 4)) {
-                    da = __builtin_amdgcn_sdot4(qw4[i].x, ka[i].x, da, false);
-                    da = __builtin_amdgcn_sdot4(qw4[i].y, ka[i].y, da, false);
-                    da = __builtin_amdgcn_sdot4(qw4[i].z, ka[i].z, da, false);
-                    da = __builtin_amdgcn_sdot4(qw4[i].w, ka[i].w, da, false);
-                    db = __builtin_amdgcn_sdot4(qw4[i].x, kb[i].x, db, false);
-                    db = __builtin_amdgcn_sdot4(qw4[i].y, kb[i].y, db, false);
-                    db = __builtin_amdgcn_sdot4(qw4[i].z, kb[i].z, db, false);
-                    db = __builtin_amdgcn_sdot4(qw4[i].w, kb[i].w, db, false);
-                }
-            score_of(j, da);
-            score_of(j2, db);
-            continue;
-        }
-        for (int jj = j; jj <= j2 && jj < nk; jj += blockDim.x) {
-            const bool h1 = fused && jj == pos;
-            const int32_t* k32 = h1 ? reinterpret_cast<const int32_t*>(kloc)
-                                    : reinterpret_cast<const int32_t*>(K + (size_t)jj * hd);
-            int dot = 0;
-            for (int i = 0; i < nwords; i++) dot = __builtin_amdgcn_sdot4(q32[i], k32[i], dot, false);
-            score_of(jj, dot);
-        }
-    }
-    const float mx = att_block_max(lmax, red);
-    for (int j = tid; j < nk; j += blockDim.x) {
-        if (long_ctx)
-            G[j] = expf_libm(G[j] - mx);
-        else
-            E[j] = expf_libm(E[j] - mx);
-    }
-    __syncthreads();
-
-    // ---- sum chain (wave 0, lane 0) while waves 1.. stage V chunk 0
-    const int nstage_thr = blockDim.x - 64;
-    auto stage_v = [&](int j0, int cnt) {  // V[j0 .. j0+cnt)[d0 .. d0+ds) -> VH (fp16, [d][j])
-        const int t = tid - 64;
-        if ((ds & 15) == 0) {  // 16-byte pieces, eight in flight per thread
-            const int pieces = ds >> 4, total = cnt * pieces;
-            for (int base = t; base < total; base += 8 * nstage_thr) {
-                uint4 w[8];
-#pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const int e = base + u * nstage_thr;
-                    if (e < total) {
-                        const int jj = e / pieces, pc = e - jj * pieces, j = j0 + jj;
-                        w[u] = (fused && j == pos) ? *reinterpret_cast<const uint4*>(vloc + d0 + pc * 16)
-                                                   : *reinterpret_cast<const uint4*>(V + (size_t)j * hd + d0 + pc * 16);
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const int e = base + u * nstage_thr;
-                    if (e < total) {
-                        const int jj = e / pieces, pc = e - jj * pieces;
-                        const uint32_t wv[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-#pragma unroll
-                        for (int b = 0; b < 16; b++)
-                            VH[(size_t)(pc * 16 + b) * vcap + jj] = (_Float16)(int8_t)(wv[b >> 2] >> (8 * (b & 3)));
-                    }
-                }
-            }
-        } else {  // 4-byte pieces (head dims that are not a multiple of 16)
-            const int pieces = ds >> 2, total = cnt * pieces;
-            for (int e = t; e < total; e += nstage_thr) {
-                const int jj = e / pieces, pc = e - jj * pieces, j = j0 + jj;
-                const uint32_t w = (fused && j == pos) ? *reinterpret_cast<const uint32_t*>(vloc + d0 + pc * 4)
-                                                       : *reinterpret_cast<const uint32_t*>(V + (size_t)j * hd + d0 + pc * 4);
-#pragma unroll
-                for (int b = 0; b < 4; b++) VH[(size_t)(pc * 4 + b) * vcap + jj] = (_Float16)(int8_t)(w >> (8 * b));
-            }
-        }
-    };
-    const int c0 = nk < vcap ? nk : vcap;
-    if (!long_ctx) {
-        if (tid == 0) s_inv = 1.0f / chain_sum(E, nk, 0.0f);
-        if (wave > 0) stage_v(0, c0);
+        const float mx = att_block_max(lmax, red);
+        for (int j = tid; j < nk; j += blockDim.x) E[j] = expf_libm(E[j] - mx);
         __syncthreads();
+        // the sum chain on one lane while the other waves stage the first run of V
+        const int c0 = min(nk, vcap);
+        if (tid == 0) s_inv = 1.0f / chain_sum(E, nk, 0.0f);
+        if (wave > 0) att_stage_v(V, hd, d0, ds, 0, c0, VH, vstr, 64);
+        __syncthreads();
+        const float inv = s_inv;
+        for (int base = tid; base < nk; base += 8 * blockDim.x) {  // p_j * vs_j
+            float vsv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int j = base + u * blockDim.x;
+                if (j < nk) vsv[u] = VS[j];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int j = base + u * blockDim.x;
+                if (j < nk) E[j] = (E[j] * inv) * vsv[u];
+            }
+        }
+        __syncthreads();
+        for (int cs = 0; cs < nk; cs += vcap) {
+            const int cnt = min(vcap, nk - cs);
+            if (cs > 0) {
+                __syncthreads();
+                att_stage_v(V, hd, d0, ds, cs, cnt, VH, vstr, 0);
+                __syncthreads();
+            }
+            if (tid < ds) o = chain_pv(E + cs, VH + (size_t)tid * vstr, o, cnt);
+        }
     } else {
-        // windows of the HBM score array through LDS (E doubles as two windows)
+        // long contexts: scores stay in the global array; e_j is recomputed from them
+        // (expf is deterministic) window by window instead of being written back
+        float lmax = -1e30f;
+        for (int j = tid; j < nk; j += blockDim.x) lmax = fmaxf(lmax, S[j]);
+        const float mx = att_block_max(lmax, red);
         float sum = 0.0f;
-        for (int w0 = 0; w0 < nk; w0 += 2 * ATT_WIN) {
-            for (int b = 0; b < 2; b++) {
-                const int ws = w0 + b * ATT_WIN;
-                for (int j = tid; j < ATT_WIN && ws + j < nk; j += blockDim.x) E[b * ATT_WIN + j] = G[ws + j];
-            }
+        for (int w0 = 0; w0 < nk; w0 += ATT_ECAP) {
+            const int cnt = min(ATT_ECAP, nk - w0);
+            for (int j = tid; j < cnt; j += blockDim.x) E[j] = expf_libm(S[w0 + j] - mx);
             __syncthreads();
-            if (tid == 0) {
-                const int cnt = min(2 * ATT_WIN, nk - w0);
-                sum = chain_sum(E, cnt, sum);
-            }
+            if (tid == 0) sum = chain_sum(E, cnt, sum);
             __syncthreads();
         }
         if (tid == 0) s_inv = 1.0f / sum;
-        if (wave > 0) stage_v(0, c0);
         __syncthreads();
-    }
-    const float inv = s_inv;
-    // p_j * vs_j (the reference scales by 1/sum in place, then multiplies by vs_j)
-    for (int base = tid; base < nk; base += 8 * blockDim.x) {
-        float vsv[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int j = base + u * blockDim.x;
-            if (j < nk) vsv[u] = (fused && j == pos) ? sc3[2] : VS[j];
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int j = base + u * blockDim.x;
-            if (j < nk) {
-                if (long_ctx)
-                    G[j] = (G[j] * inv) * vsv[u];
-                else
-                    E[j] = (E[j] * inv) * vsv[u];
-            }
-        }
-    }
-    __syncthreads();
-
-    // ---- output chains, one lane per dim of this slice
-    float o = 0.0f;
-    for (int cstart = 0; cstart < nk; cstart += vcap) {
-        const int cnt = min(vcap, nk - cstart);
-        if (cstart > 0) {
+        const float inv = s_inv;
+        for (int cs = 0; cs < nk; cs += vcap) {
+            const int cnt = min(vcap, nk - cs);
+            for (int j = tid; j < cnt; j += blockDim.x) E[j] = (expf_libm(S[cs + j] - mx) * inv) * VS[cs + j];
+            att_stage_v(V, hd, d0, ds, cs, cnt, VH, vstr, 0);
             __syncthreads();
-            if (wave > 0) stage_v(cstart, cnt);
-            if (long_ctx)
-                for (int j = tid; j < cnt && j < ATT_ECAP; j += blockDim.x) E[j] = G[cstart + j];
-            __syncthreads();
-        } else if (long_ctx) {
-            for (int j = tid; j < cnt && j < ATT_ECAP; j += blockDim.x) E[j] = G[j];
+            if (tid < ds) o = chain_pv(E, VH + (size_t)tid * vstr, o, cnt);
             __syncthreads();
         }
-        if (tid < ds) o = chain_pv(long_ctx ? E : E + cstart, VH + (size_t)tid * vcap, o, cnt);
     }
     if (tid < ds) a.out[((size_t)r * nh + h) * hd + d0 + tid] = o;
 }
 
+// ------------------------------------------------------------------ launch
+
 static int g_att_lds_max = 0;
 
-static void att_shape(int hd, int* ds, int* vcap) {
+// output dims per softmax/PV workgroup and the V run it stages (fp16 rows of
+// vstr = vcap + 8 halves: 16 bytes of padding per row)
+static void att_shape(int hd, int* ds, int* vcap, int* vstr) {
     *ds = (hd % 32 == 0) ? 32 : hd;
-    // fp16 V slice: ds * vcap * 2 bytes next to the ATT_ECAP score floats
     const int budget = (g_att_lds_max > 0 ? g_att_lds_max : 65536) - ATT_ECAP * 4 - 2048;
-    int v = 2048;
-    while (v > 64 && (size_t)(*ds) * v * 2 > (size_t)budget) v >>= 1;
+    int v = ATT_ECAP;
+    while (v > 64 && (size_t)(*ds) * (v + 8) * 2 > (size_t)budget) v >>= 1;
+    if (v > ATT_ECAP) v = ATT_ECAP;
     *vcap = v;
+    *vstr = v + 8;
+}
+
+static int att_keys_per_wg(int hd) {
+    if (hd & 15) return ATT_THREADS;
+    int lp = 1;
+    while (lp < (hd >> 4)) lp <<= 1;
+    return (ATT_THREADS / 64) * (64 / lp) * ATT_U;
 }
 
 void launch_attention(const AttnArgs& a, hipStream_t st) {
-    int ds, vcap;
-    att_shape(a.hd, &ds, &vcap);
-    const size_t lds = (size_t)ATT_ECAP * 4 + (size_t)ds * vcap * 2;
-    hipLaunchKernelGGL(attention_kernel, dim3(a.nh, a.nrows, a.hd / ds), dim3(ATT_THREADS), lds, st, a, ds, vcap);
+    const int kc = att_keys_per_wg(a.hd);
+    // with the position on the device (graph replays) every run up to max_keys is launched
+    // and the runs past the current length return at once
+    const int keys = a.state ? a.max_keys : a.start_pos + a.row0 + a.nrows;
+    const int group = a.nh / a.nkv;
+    const int nb = (group + ATT_GB - 1) / ATT_GB;
+    hipLaunchKernelGGL(attn_scores_kernel, dim3(a.nkv * nb, (keys + kc - 1) / kc, a.nrows), dim3(ATT_THREADS), 0, st,
+                       a, kc);
+    int ds, vcap, vstr;
+    att_shape(a.hd, &ds, &vcap, &vstr);
+    const size_t lds = (size_t)ATT_ECAP * 4 + (size_t)ds * vstr * 2;
+    hipLaunchKernelGGL(attn_softmax_pv_kernel, dim3(a.nh, a.nrows, a.hd / ds), dim3(ATT_THREADS), lds, st, a, ds,
+                       vcap, vstr);
 }
 
 hipError_t matvec_init();
@@ -358,7 +800,7 @@ hipError_t kernels_init() {
     if (e == hipSuccess) e = hipDeviceGetAttribute(&mx, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
     if (e != hipSuccess) return e;
     g_att_lds_max = mx;
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel),
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_softmax_pv_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, mx - 2048);
     if (e != hipSuccess) return e;
     return matvec_init();

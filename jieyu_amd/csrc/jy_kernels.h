@@ -41,9 +41,8 @@ struct MvArgs {
     int* mstate = nullptr;           // EPI_ARGMAX: mutable state
     const int* eos = nullptr;
     int neos = 0;
-    float* part_val = nullptr;       // EPI_ARGMAX: per-workgroup partial maxima
+    float* part_val = nullptr;       // EPI_ARGMAX: per-workgroup partial maxima (argmax_partials(rows) each)
     int* part_idx = nullptr;
-    unsigned* counter = nullptr;     // EPI_ARGMAX: workgroups done (reset by the last)
 };
 
 size_t q8_qs_bytes(int rows, int cols);
@@ -63,10 +62,12 @@ void launch_repack_q8(const uint8_t* src, int rows, int cols, const Q8Dev& dst, 
 void launch_embed(const Q8Dev* q8, const float* f32, int hidden, const int* ids_dev, int id_index0,
                   const int* state, int seq, float* X, hipStream_t st);
 
-void launch_rmsnorm(const float* X, float* Y, const float* w, int n, int rows, float eps, hipStream_t st);
+// RMSNorm (eps 1e-5) of `rows` rows of n floats
+void launch_rmsnorm(const float* X, float* Y, const float* w, int n, int rows, hipStream_t st);
 
 // y = W x for one token in the reference's 32-lane order; when norm_w != null the
-// kernel first applies RMSNorm (eps 1e-5) to x with those weights.
+// kernel first applies RMSNorm (eps 1e-5) to x with those weights.  EPI_ARGMAX also
+// launches the one-workgroup pick over the per-workgroup maxima.
 void launch_matvec_q8(const Q8Dev& W, const float* x, const float* norm_w, float* out, Epi epi, const MvArgs& a,
                       hipStream_t st);
 // f32 [K][N] matvec, fma chain over k; EPI_SWIGLU takes B2 as the up matrix.
@@ -99,7 +100,7 @@ struct AttnArgs {
     int nh = 0, nkv = 0, hd = 0;
     KVDev kv;
     int layer = 0;
-    float* scratch = nullptr;        // nrows*nh*max_keys floats for contexts past the LDS budget
+    float* scratch = nullptr;        // scores between the two attention kernels: nrows*nh*max_keys floats
     int max_keys = 0;
     float* out = nullptr;            // [rows][nh*hd]
 };

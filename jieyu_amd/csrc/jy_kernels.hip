@@ -61,19 +61,16 @@ void launch_repack_q8(const uint8_t* src, int rows, int cols, const Q8Dev& dst, 
                        row_base, row_stride);
 }
 
-// ---------------------------------------------------------------- embedding (wmat_row, wmat_kernel.h:18-29)
+// ---------------------------------------------------------------- embedding
 
+// embedding rows (libs/model_libs/wmat_kernel.h:18-29)
 __global__ void embed_kernel(Q8Dev W, const float* __restrict__ f32, int hidden, const int* __restrict__ ids,
                              int id0, const int* __restrict__ state, float* __restrict__ X) {
     const int i = blockIdx.x;
     const int id = state ? ids[state[0] - 1] : ids[id0 + i];
     float* x = X + (size_t)i * hidden;
-    if (f32) {
-        const float* src = f32 + (size_t)id * hidden;
-        for (int c = threadIdx.x; c < hidden; c += blockDim.x) x[c] = src[c];
-    } else {
-        for (int c = threadIdx.x; c < hidden; c += blockDim.x) x[c] = q8_elem(W, id, c);
-    }
+    for (int c = threadIdx.x; c < hidden; c += blockDim.x)
+        x[c] = f32 ? f32[(size_t)id * hidden + c] : q8_elem(W, id, c);
 }
 
 void launch_embed(const Q8Dev* q8, const float* f32, int hidden, const int* ids_dev, int id_index0,
@@ -84,57 +81,19 @@ void launch_embed(const Q8Dev* q8, const float* f32, int hidden, const int* ids_
 
 // ---------------------------------------------------------------- RMSNorm
 
-// 16 FMA lanes over x^2 (lane l takes elements 16c+l; an 8-wide remainder pass
-// feeds lanes 0..7), then ((v0+v1) -> halves -> two hadds), scalar tail, then
-// y = (x*scale)*w with scale = 1/sqrtf(ss/n + eps)
-// (libs/model_libs/rmsnorm/x86/x86_classic.txt:2-26).  The row is staged in LDS first.
+// one row per workgroup, staged in LDS, then block_rmsnorm
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ X, float* __restrict__ Y,
-                                                      const float* __restrict__ w, int n, float eps) {
+                                                      const float* __restrict__ w, int n) {
     extern __shared__ __align__(16) float xr[];
+    __shared__ float red[18];
     const float* x = X + (size_t)blockIdx.x * n;
-    float* y = Y + (size_t)blockIdx.x * n;
-    __shared__ float v[16];
-    __shared__ float sc;
-    __shared__ int zero;
-    const int t = threadIdx.x;
-    for (int i = t; i < n; i += blockDim.x) xr[i] = x[i];
+    for (int i = threadIdx.x; i < n; i += blockDim.x) xr[i] = x[i];
     __syncthreads();
-    const int n16 = n / 16 * 16;
-    const bool rem8 = n16 + 8 <= n;
-    if (t < 16) {
-        float a = 0.0f;
-#pragma unroll 8
-        for (int i = t; i < n16; i += 16) a = __builtin_fmaf(xr[i], xr[i], a);
-        if (t < 8 && rem8) a = __builtin_fmaf(xr[n16 + t], xr[n16 + t], a);
-        v[t] = a;
-    }
-    __syncthreads();
-    if (t == 0) {
-        float s[8], q[4];
-#pragma unroll
-        for (int l = 0; l < 8; l++) s[l] = v[l] + v[8 + l];
-#pragma unroll
-        for (int l = 0; l < 4; l++) q[l] = s[l] + s[4 + l];
-        float ss = (q[0] + q[1]) + (q[2] + q[3]);
-        // tail of t < 8 elements: with t >= 4 the first four squares are rounded
-        // products added in order (the host compiler's in-order vector reduction),
-        // the rest fused
-        int i = n16 + (rem8 ? 8 : 0);
-        if (n - i >= 4)
-            for (const int e = i + 4; i < e; i++) ss = ss + xr[i] * xr[i];
-        for (; i < n; i++) ss = __builtin_fmaf(xr[i], xr[i], ss);
-        const float den = ss / (float)n + eps;
-        zero = den <= 0.0f;
-        sc = zero ? 0.0f : 1.0f / sqrtf(den);
-    }
-    __syncthreads();
-    const float scale = sc;
-    const bool z = zero;
-    for (int i = t; i < n; i += blockDim.x) y[i] = z ? 0.0f : (xr[i] * scale) * w[i];
+    block_rmsnorm(xr, n, w, Y + (size_t)blockIdx.x * n, red);
 }
 
-void launch_rmsnorm(const float* X, float* Y, const float* w, int n, int rows, float eps, hipStream_t st) {
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), (size_t)n * sizeof(float), st, X, Y, w, n, eps);
+void launch_rmsnorm(const float* X, float* Y, const float* w, int n, int rows, hipStream_t st) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), (size_t)n * sizeof(float), st, X, Y, w, n);
 }
 
 // ---------------------------------------------------------------- f32 matvec (decode, [K][N] weights)

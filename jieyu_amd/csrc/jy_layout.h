@@ -34,4 +34,45 @@ __device__ __forceinline__ float q8_elem(const Q8Dev& W, int R, int k) {
     return (float)q * half_to_float(W.d[chunk * 32 + ri * 8 + j]);
 }
 
+// RMSNorm of one row already staged in LDS, by the whole workgroup, written to y
+// (libs/model_libs/rmsnorm/x86/x86_classic.txt:2-26; eps 1e-5): 16 FMA lanes over
+// x^2 (lane l takes elements 16c+l; an 8-wide remainder pass feeds lanes 0..7),
+// ((v0+v1) -> halves -> two hadds), then the scalar tail of t < 8 elements as GCC
+// builds it (with t >= 4 the first four squares are rounded products added in
+// order, the rest fused), den = ss/n + eps, scale = 1/sqrtf(den),
+// y = (x*scale)*w.  red: 18 floats of shared memory.
+__device__ __forceinline__ void block_rmsnorm(const float* x, int n, const float* __restrict__ w,
+                                              float* __restrict__ y, float* red) {
+    const int t = threadIdx.x;
+    const int n16 = n / 16 * 16;
+    const bool rem8 = n16 + 8 <= n;
+    if (t < 16) {
+        float a = 0.0f;
+#pragma unroll 8
+        for (int i = t; i < n16; i += 16) a = __builtin_fmaf(x[i], x[i], a);
+        if (t < 8 && rem8) a = __builtin_fmaf(x[n16 + t], x[n16 + t], a);
+        red[t] = a;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float s[8], q[4];
+#pragma unroll
+        for (int l = 0; l < 8; l++) s[l] = red[l] + red[8 + l];
+#pragma unroll
+        for (int l = 0; l < 4; l++) q[l] = s[l] + s[4 + l];
+        float ss = (q[0] + q[1]) + (q[2] + q[3]);
+        int i = n16 + (rem8 ? 8 : 0);
+        if (n - i >= 4)
+            for (const int e = i + 4; i < e; i++) ss = ss + x[i] * x[i];
+        for (; i < n; i++) ss = __builtin_fmaf(x[i], x[i], ss);
+        const float den = ss / (float)n + 1e-5f;
+        red[17] = den <= 0.0f ? 1.0f : 0.0f;
+        red[16] = den <= 0.0f ? 0.0f : 1.0f / sqrtf(den);
+    }
+    __syncthreads();
+    const float scale = red[16];
+    const bool zero = red[17] != 0.0f;
+    for (int i = t; i < n; i += blockDim.x) y[i] = zero ? 0.0f : (x[i] * scale) * w[i];
+}
+
 }  // namespace jy

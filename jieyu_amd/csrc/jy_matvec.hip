@@ -8,9 +8,11 @@
 // so a row's 32 chains run in parallel and the tree is four butterflies plus an
 // in-lane add.  Weights stream from HBM as 16 B per lane (1 KiB per wave per
 // chunk of 8 blocks) with eight chunks in flight; the activation vector sits in
-// LDS, lane-pair major, and is optionally RMS-normalised there first (the
-// reference's rmsnorm, libs/model_libs/rmsnorm/x86/x86_classic.txt).
-// Dequantisation is one v_fma_mix (q * fp16 scale, exact) per weight.
+// LDS, lane-pair major.  Dequantisation is one v_fma_mix (q * fp16 scale, exact)
+// per weight.  With NORM the staged vector is RMS-normalised in LDS first (the
+// reference's rmsnorm), its weights prefetched while x is staged.
+#include <algorithm>
+
 #include "jy_layout.h"
 
 namespace jy {
@@ -46,16 +48,15 @@ __device__ __forceinline__ void mv_chunk(const uint4& w, const uint4& dd, const 
 // one wave owns row groups wid, wid + TW, ... (TW = waves in the grid), `per` of
 // them; the chunk stream of consecutive row groups is pipelined without a gap.
 template <int EPI, bool NORM>
-__global__ __launch_bounds__(1024) void matvec_q8_kernel(Q8Dev W, const float* __restrict__ x,
-                                                         const float* __restrict__ nw, float* __restrict__ out,
-                                                         MvArgs a, int per) {
+__global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __restrict__ x,
+                                                        const float* __restrict__ nw, float* __restrict__ out,
+                                                        MvArgs a, int per) {
     // [16][XS]: lane pair g, block b, lane c.  16-byte alignment keeps the ds_read_b128
     // of the main loop aligned whatever static LDS the epilogue adds.
     extern __shared__ __align__(16) float xs[];
     __shared__ float red[18];
     __shared__ float rowv[64];
     __shared__ int rowi[64];
-    __shared__ int s_last;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwv = blockDim.x >> 6;
     const int TW = gridDim.x * nwv, wid = blockIdx.x * nwv + wave;
     const int r = lane >> 4, g = lane & 15;
@@ -89,21 +90,26 @@ __global__ __launch_bounds__(1024) void matvec_q8_kernel(Q8Dev W, const float* _
     uint4 wA[MV_U], dA[MV_U], wB[MV_U], dB[MV_U];
     load(wA, dA, 0, 0);
     load(wB, dB, 0, MV_U);
-
-    // stage x, four floats per load, eight loads in flight per thread (zero past K:
-    // padding blocks then contribute exact zeros)
+    // stage x, four floats per load, several loads in flight per thread (zero past K:
+    // padding blocks then contribute exact zeros); with NORM the RMSNorm weights come
+    // in the same batches, into nws behind the staged vector
+    float* nws = xs + 16 * XS;
+    const int nk4 = K / 4;
     {
         const int nv4 = W.nbp * 8;
         const float4* x4 = reinterpret_cast<const float4*>(x);
-        for (int base = tid; base < nv4; base += 8 * blockDim.x) {
-            float4 v[8];
+        const float4* w4 = reinterpret_cast<const float4*>(nw);
+        constexpr int SU = NORM ? 4 : 8;  // loads per thread per batch (x and w with NORM)
+        for (int base = tid; base < nv4; base += SU * blockDim.x) {
+            float4 v[SU], wv[SU];
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
+            for (int u = 0; u < SU; u++) {
                 const int i = base + u * blockDim.x;
-                v[u] = (i < nv4 && 4 * i < K) ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                v[u] = (i < nv4 && i < nk4) ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (NORM) wv[u] = i < nk4 ? w4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
+            for (int u = 0; u < SU; u++) {
                 const int i = base + u * blockDim.x;
                 if (i < nv4) {
                     const int k = 4 * i;
@@ -111,69 +117,63 @@ __global__ __launch_bounds__(1024) void matvec_q8_kernel(Q8Dev W, const float* _
                     xs[xs_index(k + 1, XS)] = v[u].y;
                     xs[xs_index(k + 2, XS)] = v[u].z;
                     xs[xs_index(k + 3, XS)] = v[u].w;
+                    if (NORM && i < nk4) reinterpret_cast<float4*>(nws)[i] = wv[u];
                 }
             }
         }
     }
     __syncthreads();
     if (NORM) {
-        // rmsnorm: 16 FMA lanes over x^2 (lane l: elements 16c+l), 8-wide remainder,
-        // ((v0+v1) -> halves -> two hadds), den = ss/n + eps, scale = 1/sqrtf(den)
-        const int n16 = K / 16 * 16;
-        const bool rem8 = n16 + 8 <= K;
-        if (tid < 16) {
+        // RMSNorm of the staged vector (libs/model_libs/rmsnorm/x86/x86_classic.txt:2-26):
+        // lanes 0..15 of wave 0 run the 16 FMA chains (lane l: elements 16c+l, an 8-wide
+        // remainder pass feeds lanes 0..7), lane 0 folds them ((v0+v1) -> halves -> two
+        // hadds) and the tail, then x = (x*scale)*w with the staged weights
+        if (wave == 0) {
+            const int n16 = K / 16 * 16;
+            const bool rem8 = n16 + 8 <= K;
             float v = 0.0f;
+            if (lane < 16) {
 #pragma unroll 8
-            for (int k = tid; k < n16; k += 16) {
-                const float e = xs[xs_index(k, XS)];
-                v = __builtin_fmaf(e, e, v);
+                for (int k = lane; k < n16; k += 16) {
+                    const float e = xs[xs_index(k, XS)];
+                    v = __builtin_fmaf(e, e, v);
+                }
+                if (lane < 8 && rem8) {
+                    const float e = xs[xs_index(n16 + lane, XS)];
+                    v = __builtin_fmaf(e, e, v);
+                }
             }
-            if (tid < 8 && rem8) {
-                const float e = xs[xs_index(n16 + tid, XS)];
-                v = __builtin_fmaf(e, e, v);
-            }
-            red[tid] = v;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            float s[8], q[4];
+            float vv[16];
 #pragma unroll
-            for (int l = 0; l < 8; l++) s[l] = red[l] + red[8 + l];
+            for (int l = 0; l < 16; l++) vv[l] = __shfl(v, l);
+            if (lane == 0) {
+                float s8[8], q4[4];
 #pragma unroll
-            for (int l = 0; l < 4; l++) q[l] = s[l] + s[4 + l];
-            float ss = (q[0] + q[1]) + (q[2] + q[3]);
-            for (int k = n16 + (rem8 ? 8 : 0); k < K; k++) {
-                const float e = xs[xs_index(k, XS)];
-                ss = __builtin_fmaf(e, e, ss);
+                for (int l = 0; l < 8; l++) s8[l] = vv[l] + vv[8 + l];
+#pragma unroll
+                for (int l = 0; l < 4; l++) q4[l] = s8[l] + s8[4 + l];
+                float ss = (q4[0] + q4[1]) + (q4[2] + q4[3]);
+                int k = n16 + (rem8 ? 8 : 0);
+                if (K - k >= 4)
+                    for (const int e = k + 4; k < e; k++) {
+                        const float t = xs[xs_index(k, XS)];
+                        ss = ss + t * t;
+                    }
+                for (; k < K; k++) {
+                    const float t = xs[xs_index(k, XS)];
+                    ss = __builtin_fmaf(t, t, ss);
+                }
+                const float den = ss / (float)K + 1e-5f;
+                red[17] = den <= 0.0f ? 1.0f : 0.0f;
+                red[16] = den <= 0.0f ? 0.0f : 1.0f / sqrtf(den);
             }
-            const float den = ss / (float)K + 1e-5f;
-            red[17] = den <= 0.0f ? 1.0f : 0.0f;
-            red[16] = den <= 0.0f ? 0.0f : 1.0f / sqrtf(den);
         }
         __syncthreads();
         const float scale = red[16];
         const bool zero = red[17] != 0.0f;
-        const float4* w4 = reinterpret_cast<const float4*>(nw);
-        const int nk4 = K / 4;
-        for (int base = tid; base < nk4; base += 8 * blockDim.x) {
-            float4 v[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int i = base + u * blockDim.x;
-                if (i < nk4) v[u] = w4[i];
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int i = base + u * blockDim.x;
-                if (i < nk4) {
-                    const float wv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        const int xi = xs_index(4 * i + c, XS);
-                        xs[xi] = zero ? 0.0f : (xs[xi] * scale) * wv[c];
-                    }
-                }
-            }
+        for (int k = tid; k < K; k += blockDim.x) {
+            const int xi = xs_index(k, XS);
+            xs[xi] = zero ? 0.0f : (xs[xi] * scale) * nws[k];
         }
         __syncthreads();
     }
@@ -258,8 +258,9 @@ __global__ __launch_bounds__(1024) void matvec_q8_kernel(Q8Dev W, const float* _
     }
 
     if (EPI == EPI_ARGMAX) {
-        // first index of the strict maximum (generate.h:57-60): per-workgroup first max,
-        // then the last workgroup to finish scans the partials
+        // first index of the strict maximum (generate.h:57-60): the workgroup's first
+        // maximum goes to the partials; argmax_finish_kernel scans them after this
+        // kernel (the kernel boundary makes them visible device-wide)
         if (g == 0) {
             rowv[wave * 4 + r] = best_v;
             rowi[wave * 4 + r] = best_i;
@@ -273,57 +274,60 @@ __global__ __launch_bounds__(1024) void matvec_q8_kernel(Q8Dev W, const float* _
                     bv = rowv[i];
                     bi = rowi[i];
                 }
-            __hip_atomic_store(&a.part_val[blockIdx.x], bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&a.part_idx[blockIdx.x], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const unsigned done = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            s_last = done == gridDim.x - 1;
+            a.part_val[blockIdx.x] = bv;
+            a.part_idx[blockIdx.x] = bi;
         }
-        __syncthreads();
-        if (s_last) {
-            __atomic_thread_fence(__ATOMIC_ACQUIRE);
-            const int np = gridDim.x;
-            float bv = -__builtin_inff();
-            int bi = 0x7fffffff;
-            for (int i = tid; i < np; i += blockDim.x) {
-                const float v = __hip_atomic_load(&a.part_val[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const int ix = __hip_atomic_load(&a.part_idx[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (v > bv || (v == bv && ix < bi)) {
-                    bv = v;
-                    bi = ix;
-                }
-            }
+    }
+}
+
+// the greedy pick over the lm_head workgroups' partial maxima: lowest index among
+// equal values (the reference's first strict maximum), then ids[len] = pick, len++,
+// and the stop flag on an EOS id (generate.h:57-60, :78-83)
+__global__ __launch_bounds__(256) void argmax_finish_kernel(const float* __restrict__ part_val,
+                                                            const int* __restrict__ part_idx, int np, int* ids,
+                                                            int* mstate, const int* eos, int neos) {
+    __shared__ float wv[4];
+    __shared__ int wi[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float bv = -__builtin_inff();
+    int bi = 0x7fffffff;
+    for (int i = tid; i < np; i += blockDim.x) {
+        const float v = part_val[i];
+        const int ix = part_idx[i];
+        if (v > bv || (v == bv && ix < bi)) {
+            bv = v;
+            bi = ix;
+        }
+    }
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(bv, o);
-                const int oi = __shfl_xor(bi, o);
-                if (ov > bv || (ov == bv && oi < bi)) {
-                    bv = ov;
-                    bi = oi;
-                }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (ov > bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) {
+        wv[wave] = bv;
+        wi[wave] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        bv = wv[0];
+        bi = wi[0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+            if (wv[w] > bv || (wv[w] == bv && wi[w] < bi)) {
+                bv = wv[w];
+                bi = wi[w];
             }
-            if (lane == 0) {
-                rowv[wave] = bv;
-                rowi[wave] = bi;
-            }
-            __syncthreads();
-            if (tid == 0) {
-                bv = rowv[0];
-                bi = rowi[0];
-                for (int w = 1; w < nwv; w++)
-                    if (rowv[w] > bv || (rowv[w] == bv && rowi[w] < bi)) {
-                        bv = rowv[w];
-                        bi = rowi[w];
-                    }
-                if (bi == 0x7fffffff) bi = 0;
-                if (!a.mstate[1]) {
-                    const int len = a.mstate[0];
-                    a.ids[len] = bi;
-                    a.mstate[0] = len + 1;
-                    for (int e = 0; e < a.neos; e++)
-                        if (bi == a.eos[e]) a.mstate[1] = 1;
-                }
-                __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+        if (bi == 0x7fffffff) bi = 0;
+        if (!mstate[1]) {
+            const int len = mstate[0];
+            ids[len] = bi;
+            mstate[0] = len + 1;
+            for (int e = 0; e < neos; e++)
+                if (bi == eos[e]) mstate[1] = 1;
         }
     }
 }
@@ -331,7 +335,7 @@ __global__ __launch_bounds__(1024) void matvec_q8_kernel(Q8Dev W, const float* _
 static int g_cus = 256;
 
 // launch shape: 4 waves per workgroup, at most 4 workgroups per CU; each wave owns
-// `per` row groups so the prologue (staging, RMSNorm) is paid once per workgroup
+// `per` row groups so the prologue (staging x) is paid once per workgroup
 static void mv_shape(const Q8Dev& W, int* grid, int* per) {
     const int nwv = 4;
     const int groups = (W.rows + 3) / 4;
@@ -352,10 +356,12 @@ template <int EPI, bool NORM>
 static void mv_launch(const Q8Dev& W, const float* x, const float* nw, float* out, const MvArgs& a, hipStream_t st) {
     int grid, per;
     mv_shape(W, &grid, &per);
-    const size_t lds = (size_t)16 * (2 * W.nbp + 4) * sizeof(float);
+    const size_t lds = ((size_t)16 * (2 * W.nbp + 4) + (NORM ? (size_t)W.cols : 0)) * sizeof(float);
     hipLaunchKernelGGL((matvec_q8_kernel<EPI, NORM>), dim3(grid), dim3(256), lds, st, W, x, nw, out, a, per);
+    if (EPI == EPI_ARGMAX)
+        hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(256), 0, st, a.part_val, a.part_idx, grid, a.ids,
+                           a.mstate, a.eos, a.neos);
 }
-
 
 template <bool NORM>
 static void mv_dispatch(const Q8Dev& W, const float* x, const float* nw, float* out, Epi epi, const MvArgs& a,

@@ -119,7 +119,6 @@ struct jyhip_model {
     int eos_cap = 0;
     float* part_val = nullptr;  // lm_head argmax partials
     int* part_idx = nullptr;
-    unsigned* counter = nullptr;
     std::vector<void*> owned;
 };
 
@@ -133,6 +132,7 @@ struct jyhip_q8mat {
     std::vector<Q8Dev> copies;
     float* x = nullptr;
     float* y = nullptr;
+    float* nw = nullptr;  // unit RMSNorm weights for the gate/up timing variant
     hipStream_t stream = nullptr;
     int next = 0;
 };
@@ -325,7 +325,6 @@ void upload(jyhip_model* m, const jy_model_desc* d, int max_seq) {
     const int np = argmax_partials(V);
     m->part_val = (float*)own(m, dalloc<float>(np));
     m->part_idx = (int*)own(m, dalloc<int>(np));
-    m->counter = (unsigned*)own(m, dalloc<unsigned>(4));
 }
 
 void release(jyhip_model* m) {
@@ -344,9 +343,9 @@ void release(jyhip_model* m) {
 
 // transformer_layer x L (libs/model_libs/transformer_layer.h:10-90) for one token
 // in ws.X at position state[0]-1 (state != null) or pos0: the m == 1 path of every
-// matmul (matmul_q.h:139-144).  Q8_0: five kernels per layer (RMSNorm fused into
-// the QKV and gate/up matvecs, RoPE into QKV, K/V packing into attention, SwiGLU
-// into gate/up, residual adds into O and down).
+// matmul (matmul_q.h:139-144).  Q8_0: six kernels per layer (RMSNorm + QKV + RoPE,
+// the two attention kernels with K/V packing, O + residual, RMSNorm + gate/up +
+// SwiGLU, down + residual).
 void run_decode_layers(jyhip_model* m, const KVDev& kv, const int* state, int pos0, float* layer_out_host,
                        int max_keys) {
     Workspace& w = m->ws;
@@ -385,7 +384,7 @@ void run_decode_layers(jyhip_model* m, const KVDev& kv, const int* state, int po
             launch_matvec_q8(D.gu, w.X, D.rms2, w.h, EPI_SWIGLU, none, st);
             launch_matvec_q8(D.down, w.h, nullptr, w.X, EPI_RESID, none, st);
         } else {
-            launch_rmsnorm(w.X, w.xn, D.rms1, H, 1, 1e-5f, st);
+            launch_rmsnorm(w.X, w.xn, D.rms1, H, 1, st);
             launch_matvec_f32(D.f_qkv, nullptr, H, NQ, w.xn, w.qkv, D.bqkv, D.bqkv ? EPI_BIAS : EPI_STORE, st);
             launch_rope_pack(w.qkv, 1, pos0, state, m->nh, m->nkv, m->hd, m->cos_t, m->sin_t, kv, l, w.q8, w.qsc, st);
             at.fused = false;
@@ -394,7 +393,7 @@ void run_decode_layers(jyhip_model* m, const KVDev& kv, const int* state, int po
             at.row0 = 0;
             launch_attention(at, st);
             launch_matvec_f32(D.f_o, nullptr, m->qd, H, w.att, w.X, nullptr, EPI_RESID, st);
-            launch_rmsnorm(w.X, w.xn, D.rms2, H, 1, 1e-5f, st);
+            launch_rmsnorm(w.X, w.xn, D.rms2, H, 1, st);
             launch_matvec_f32(D.f_w1, D.f_w3, H, F, w.xn, w.h, nullptr, EPI_SWIGLU, st);
             launch_matvec_f32(D.f_w2, nullptr, F, H, w.h, w.X, nullptr, EPI_RESID, st);
         }
@@ -431,7 +430,7 @@ void run_prefill_layers(jyhip_model* m, const KVDev& kv, int seq, int start_pos,
     at.out = w.att;
     for (int l = 0; l < m->L; l++) {
         const DevLayer& D = m->layers[l];
-        launch_rmsnorm(w.X, w.xn, D.rms1, H, seq, 1e-5f, st);
+        launch_rmsnorm(w.X, w.xn, D.rms1, H, seq, st);
         const Epi qkv_epi = D.bqkv ? EPI_BIAS : EPI_STORE;
         if (q8)
             launch_gemm_q8(D.qkv, seq, w.xn, w.qkv, D.bqkv, qkv_epi, st);
@@ -449,7 +448,7 @@ void run_prefill_layers(jyhip_model* m, const KVDev& kv, int seq, int start_pos,
             launch_gemm_q8(D.o, seq, w.att, w.X, nullptr, EPI_RESID, st);
         else
             launch_gemm_f32(D.f_o, m->qd, H, seq, w.att, w.X, nullptr, EPI_RESID, st);
-        launch_rmsnorm(w.X, w.xn, D.rms2, H, seq, 1e-5f, st);
+        launch_rmsnorm(w.X, w.xn, D.rms2, H, seq, st);
         if (q8) {
             launch_gemm_q8(D.gu, seq, w.xn, w.g, nullptr, EPI_STORE, st);
             launch_silu_mul(w.g, nullptr, 1, seq, F, w.h, st);
@@ -479,6 +478,7 @@ void run_layers(jyhip_model* m, const KVDev& kv, int seq, int start_pos, const i
 }
 
 // final RMSNorm of the last row + lm_head (+ greedy pick when fused) -> m->logits
+// final norm + lm_head (generate.h:48-49): fused into the Q8 matvec's prologue
 void final_and_head(jyhip_model* m, const float* xlast, bool argmax, int neos) {
     if (m->wtype == JY_Q8_0) {
         MvArgs a;
@@ -489,11 +489,10 @@ void final_and_head(jyhip_model* m, const float* xlast, bool argmax, int neos) {
             a.neos = neos;
             a.part_val = m->part_val;
             a.part_idx = m->part_idx;
-            a.counter = m->counter;
         }
         launch_matvec_q8(m->lm_q8, xlast, m->final_rms, m->logits, argmax ? EPI_ARGMAX : EPI_STORE, a, m->stream);
     } else {
-        launch_rmsnorm(xlast, m->ws.xn, m->final_rms, m->H, 1, 1e-5f, m->stream);
+        launch_rmsnorm(xlast, m->ws.xn, m->final_rms, m->H, 1, m->stream);
         launch_matvec_f32(m->lm_f32, nullptr, m->H, m->V, m->ws.xn, m->logits, nullptr, EPI_STORE, m->stream);
     }
 }
@@ -772,7 +771,7 @@ int forward_impl(jyhip_model* m, jyhip_kv* kv, float* X, int seq, int start_pos,
     CK(hipMemcpyAsync(w.X, X, sizeof(float) * seq * m->H, hipMemcpyHostToDevice, st));
     const int max_keys = (start_pos + seq + 3) / 4 * 4;
     run_layers(m, kv->dev, seq, start_pos, nullptr, layer_out, max_keys);
-    launch_rmsnorm(w.X, w.xn, m->final_rms, m->H, seq, 1e-5f, st);  // forward.h:86-94
+    launch_rmsnorm(w.X, w.xn, m->final_rms, m->H, seq, st);  // forward.h:86-94
     CK(hipGetLastError());
     CK(hipMemcpyAsync(X, w.xn, sizeof(float) * seq * m->H, hipMemcpyDeviceToHost, st));
     CK(hipStreamSynchronize(st));
@@ -1071,6 +1070,7 @@ JYHIP_API void jyhip_q8_free(jyhip_q8mat* q) {
     }
     dfree(q->x);
     dfree(q->y);
+    dfree(q->nw);
     (void)hipStreamDestroy(q->stream);
     delete q;
 }
@@ -1088,20 +1088,31 @@ JYHIP_API int jyhip_q8_matvec(jyhip_q8mat* q, const float* x, float* y) {
     }, -1);
 }
 
-JYHIP_API int jyhip_q8_matvec_time(jyhip_q8mat* q, const float* x, int iters, double* avg_us) {
+JYHIP_API int jyhip_q8_matvec_time(jyhip_q8mat* q, const float* x, int variant, int iters, double* avg_us) {
     return guarded([&]() {
-        if (!q || !x || !avg_us || iters <= 0) fail("bad argument");
+        if (!q || !x || !avg_us || iters <= 0 || variant < 0 || variant > 1) fail("bad argument");
         const Q8Dev& d0 = q->copies[0];
+        if (variant == 1 && d0.rows % 2) fail("the gate/up variant needs interleaved row pairs");
         CK(hipMemcpyAsync(q->x, x, sizeof(float) * d0.cols, hipMemcpyHostToDevice, q->stream));
+        const float* nw = nullptr;
+        Epi epi = EPI_STORE;
+        if (variant == 1) {  // decode's gate/up launch: RMSNorm prologue (unit weights), SwiGLU epilogue
+            if (!q->nw) {
+                std::vector<float> ones(d0.cols, 1.0f);
+                q->nw = dalloc<float>(d0.cols);
+                CK(hipMemcpy(q->nw, ones.data(), sizeof(float) * d0.cols, hipMemcpyHostToDevice));
+            }
+            nw = q->nw;
+            epi = EPI_SWIGLU;
+        }
         for (size_t c = 0; c < q->copies.size(); c++)  // warm: one pass over every copy
-            launch_matvec_q8(q->copies[c], q->x, nullptr, q->y, EPI_STORE, MvArgs(), q->stream);
+            launch_matvec_q8(q->copies[c], q->x, nw, q->y, epi, MvArgs(), q->stream);
         hipEvent_t a, b;
         CK(hipEventCreate(&a));
         CK(hipEventCreate(&b));
         CK(hipEventRecord(a, q->stream));
         for (int i = 0; i < iters; i++)
-            launch_matvec_q8(q->copies[(size_t)i % q->copies.size()], q->x, nullptr, q->y, EPI_STORE, MvArgs(),
-                             q->stream);
+            launch_matvec_q8(q->copies[(size_t)i % q->copies.size()], q->x, nw, q->y, epi, MvArgs(), q->stream);
         CK(hipEventRecord(b, q->stream));
         CK(hipEventSynchronize(b));
         float ms = 0.0f;
