@@ -19,6 +19,8 @@ struct Q8Dev {
     uint8_t* qs = nullptr;
     uint16_t* d = nullptr;
     int rows = 0, cols = 0, nb = 0, nch = 0, nbp = 0, rows_pad = 0;
+    int nchp = 0;  // chunks stored per row group: nch rounded up to a multiple of 2*U
+    int U = 0;     // decode matvec register-buffer depth (chunks per buffer, two buffers)
 };
 
 struct KVDev {
@@ -70,6 +72,10 @@ void launch_rmsnorm(const float* X, float* Y, const float* w, int n, int rows, h
 // launches the one-workgroup pick over the per-workgroup maxima.
 void launch_matvec_q8(const Q8Dev& W, const float* x, const float* norm_w, float* out, Epi epi, const MvArgs& a,
                       hipStream_t st);
+// LDS the Q8 matvec takes for rows of `cols` (staged x, and the norm weights with
+// NORM), and what one workgroup may take (valid after kernels_init)
+size_t matvec_lds_bytes(int cols, bool norm);
+size_t matvec_lds_limit();
 // f32 [K][N] matvec, fma chain over k; EPI_SWIGLU takes B2 as the up matrix.
 void launch_matvec_f32(const float* B, const float* B2, int K, int N, const float* x, float* out,
                        const float* aux, Epi epi, hipStream_t st);

@@ -15,6 +15,9 @@
 
 namespace jy {
 
+// Chunks per row group are padded to a multiple of the matvec's two register
+// buffers (2*U chunks), so a wave's weight stream is one linear run; U is the
+// deepest of 4, 2, 1 whose padding stays within 1/16 of the row.
 Q8Dev q8_shape(int rows, int cols) {
     Q8Dev q;
     q.rows = rows;
@@ -23,16 +26,27 @@ Q8Dev q8_shape(int rows, int cols) {
     q.nch = (q.nb + 7) / 8;
     q.nbp = q.nch * 8;
     q.rows_pad = (rows + 3) / 4 * 4;
+    q.U = 1;
+    for (int u : {4, 2}) {
+        const int padded = (q.nch + 2 * u - 1) / (2 * u) * (2 * u);
+        if ((padded - q.nch) * 16 <= q.nch) {
+            q.U = u;
+            break;
+        }
+    }
+    q.nchp = (q.nch + 2 * q.U - 1) / (2 * q.U) * (2 * q.U);
     return q;
 }
 
+// + 8 chunks of zeros after the last row group: the matvec's prefetch runs up to
+// 2*U chunks past the end of a wave's run
 size_t q8_qs_bytes(int rows, int cols) {
     const Q8Dev q = q8_shape(rows, cols);
-    return (size_t)(q.rows_pad / 4) * q.nch * 1024;
+    return ((size_t)(q.rows_pad / 4) * q.nchp + 8) * 1024;
 }
 size_t q8_d_bytes(int rows, int cols) {
     const Q8Dev q = q8_shape(rows, cols);
-    return (size_t)(q.rows_pad / 4) * q.nch * 64;
+    return ((size_t)(q.rows_pad / 4) * q.nchp + 8) * 64;
 }
 
 // ---------------------------------------------------------------- repack

@@ -17,7 +17,6 @@
 
 namespace jy {
 
-static constexpr int MV_U = 4;  // chunks per register buffer (two buffers)
 
 __device__ __forceinline__ int xs_index(int k, int XS) {
     return ((k & 31) >> 1) * XS + 2 * (k >> 5) + (k & 1);
@@ -47,7 +46,7 @@ __device__ __forceinline__ void mv_chunk(const uint4& w, const uint4& dd, const 
 
 // one wave owns row groups wid, wid + TW, ... (TW = waves in the grid), `per` of
 // them; the chunk stream of consecutive row groups is pipelined without a gap.
-template <int EPI, bool NORM>
+template <int EPI, bool NORM, int MV_U>
 __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __restrict__ x,
                                                         const float* __restrict__ nw, float* __restrict__ out,
                                                         MvArgs a, int per) {
@@ -58,38 +57,45 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
     __shared__ float rowv[64];
     __shared__ int rowi[64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwv = blockDim.x >> 6;
-    const int TW = gridDim.x * nwv, wid = blockIdx.x * nwv + wave;
+    // the wave index is uniform: computed from readfirstlane, every chunk address is
+    // scalar (a scalar base plus the lane's fixed offset)
+    const int wid = blockIdx.x * nwv + __builtin_amdgcn_readfirstlane(wave);
     const int r = lane >> 4, g = lane & 15;
-    const int K = W.cols, nch = W.nch, XS = 2 * W.nbp + 4;
-    const int nchp = (nch + 2 * MV_U - 1) / (2 * MV_U) * (2 * MV_U);
+    const int K = W.cols, nch = W.nch, nchp = W.nchp, XS = 2 * W.nbp + 4;
     const int groups = (W.rows + 3) >> 2;
 
-    // chunk at loop position `p` of the wave's it-th row group (positions past the
-    // padded chunk count belong to the next row group).  Loads are unconditional
-    // (positions with no chunk re-read chunk 0, and are never computed), so the
-    // number of loads in flight is static and the waits stay partial.
-    const uint4* qs4 = reinterpret_cast<const uint4*>(W.qs);
-    const uint4* d4 = reinterpret_cast<const uint4*>(W.d);
-    auto load = [&](uint4* wb, uint4* db, int it, int p0) {
+    // this wave's row groups are wid, wid+TW, ... (TW = waves in the grid), so the waves
+    // in flight read neighbouring row groups.  The wave's weight stream runs through
+    // each row group's nchp stored chunks (those past nch are zero and never computed)
+    // and jumps to its next row group; nchp is a multiple of the batch size, so a batch
+    // never straddles two.  Chunk offsets are scalar (buffer loads with the lane's fixed
+    // offset in a register), clamped so loads past the matrix stay in its zero tail.
+    const int TW = gridDim.x * nwv;
+    const int cmax = groups * nchp + 8 - MV_U;
+    int lrg = wid, lp = 0;  // row group and chunk of the next load
+    const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(W.qs, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t drs = __builtin_amdgcn_make_buffer_rsrc(W.d, (short)0, 0x7fffffff, 0x00020000);
+    const int qoff = lane * 16, doff = r * 16;
+    auto load = [&](uint4* wb, uint4* db) {
+        const int c = min(lrg * nchp + lp, cmax);
 #pragma unroll
         for (int u = 0; u < MV_U; u++) {
-            int p = p0 + u, i2 = it;
-            if (p >= nchp) {
-                p -= nchp;
-                i2++;
-            }
-            const int rg = wid + i2 * TW;
-            const size_t c = (i2 < per && rg < groups && p < nch) ? (size_t)rg * nch + p : 0;
-            wb[u] = qs4[c * 64 + lane];
-            db[u] = d4[c * 4 + r];
+            wb[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(qrs, qoff, (c + u) * 1024, 0));
+            db[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(drs, doff, (c + u) * 64, 0));
+        }
+        lp += MV_U;
+        if (lp == nchp) {
+            lp = 0;
+            lrg = min(lrg + TW, groups);
         }
     };
 
     // both register buffers are in flight before the prologue (staging, RMSNorm), and
     // stay two buffers ahead of the compute afterwards
     uint4 wA[MV_U], dA[MV_U], wB[MV_U], dB[MV_U];
-    load(wA, dA, 0, 0);
-    load(wB, dB, 0, MV_U);
+    load(wA, dA);
+    load(wB, dB);
+
     // stage x, four floats per load, several loads in flight per thread (zero past K:
     // padding blocks then contribute exact zeros); with NORM the RMSNorm weights come
     // in the same batches, into nws behind the staged vector
@@ -126,16 +132,25 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
     if (NORM) {
         // RMSNorm of the staged vector (libs/model_libs/rmsnorm/x86/x86_classic.txt:2-26):
         // lanes 0..15 of wave 0 run the 16 FMA chains (lane l: elements 16c+l, an 8-wide
-        // remainder pass feeds lanes 0..7), lane 0 folds them ((v0+v1) -> halves -> two
-        // hadds) and the tail, then x = (x*scale)*w with the staged weights
+        // remainder pass feeds lanes 0..7), the fold ((v0+v1) -> halves -> two hadds) is
+        // four butterflies, lane 0 adds the tail, then x = (x*scale)*w with the staged weights
         if (wave == 0) {
             const int n16 = K / 16 * 16;
             const bool rem8 = n16 + 8 <= K;
+            // element 16c + l sits at xs_index = (8(c&1) + l/2)*XS + 2(c/2) + (l&1): two
+            // running addresses per lane, one for even c and one for odd c
             float v = 0.0f;
             if (lane < 16) {
+                const float* pe = xs + (lane >> 1) * XS + (lane & 1);
+                const float* po = pe + 8 * XS;
+                const int npairs = n16 >> 5;
 #pragma unroll 8
-                for (int k = lane; k < n16; k += 16) {
-                    const float e = xs[xs_index(k, XS)];
+                for (int m = 0; m < npairs; m++) {
+                    v = __builtin_fmaf(pe[2 * m], pe[2 * m], v);
+                    v = __builtin_fmaf(po[2 * m], po[2 * m], v);
+                }
+                if (n16 & 16) {  // an odd number of 16-element groups ends on an even c
+                    const float e = pe[2 * npairs];
                     v = __builtin_fmaf(e, e, v);
                 }
                 if (lane < 8 && rem8) {
@@ -143,25 +158,24 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
                     v = __builtin_fmaf(e, e, v);
                 }
             }
-            float vv[16];
-#pragma unroll
-            for (int l = 0; l < 16; l++) vv[l] = __shfl(v, l);
+            // fold ((v0+v1) -> halves -> two hadds) as butterflies; every add of the tree
+            // is commutative, so lane 0 ends with the reference's value bit for bit
+            float t = v + __shfl_xor(v, 8);   // s[i] = v[i] + v[8+i]
+            t = t + __shfl_xor(t, 4);         // q[i] = s[i] + s[4+i]
+            t = t + __shfl_xor(t, 1);         // q0+q1 (lane 0), q2+q3 (lane 2)
+            float ss = t + __shfl_xor(t, 2);  // (q0+q1) + (q2+q3)
             if (lane == 0) {
-                float s8[8], q4[4];
-#pragma unroll
-                for (int l = 0; l < 8; l++) s8[l] = vv[l] + vv[8 + l];
-#pragma unroll
-                for (int l = 0; l < 4; l++) q4[l] = s8[l] + s8[4 + l];
-                float ss = (q4[0] + q4[1]) + (q4[2] + q4[3]);
+                // the scalar tail as GCC builds it: with four or more left, the first four
+                // squares are rounded products added in order, the rest fused
                 int k = n16 + (rem8 ? 8 : 0);
                 if (K - k >= 4)
                     for (const int e = k + 4; k < e; k++) {
-                        const float t = xs[xs_index(k, XS)];
-                        ss = ss + t * t;
+                        const float q = xs[xs_index(k, XS)];
+                        ss = ss + q * q;
                     }
                 for (; k < K; k++) {
-                    const float t = xs[xs_index(k, XS)];
-                    ss = __builtin_fmaf(t, t, ss);
+                    const float q = xs[xs_index(k, XS)];
+                    ss = __builtin_fmaf(q, q, ss);
                 }
                 const float den = ss / (float)K + 1e-5f;
                 red[17] = den <= 0.0f ? 1.0f : 0.0f;
@@ -191,13 +205,13 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
                 for (int u = 0; u < MV_U; u++)
                     if (ch + u < nch) mv_chunk(wA[u], dA[u], xrow, ch + u, a0, a1);
             }
-            load(wA, dA, it, ch + 2 * MV_U);
+            load(wA, dA);
             if (active) {
 #pragma unroll
                 for (int u = 0; u < MV_U; u++)
                     if (ch + MV_U + u < nch) mv_chunk(wB[u], dB[u], xrow, ch + MV_U + u, a0, a1);
             }
-            load(wB, dB, it, ch + 3 * MV_U);
+            load(wB, dB);
         }
         // lanes 2g, 2g+1 -> the reference's reduction tree
         a0 += __shfl_xor(a0, 4);
@@ -357,7 +371,12 @@ static void mv_launch(const Q8Dev& W, const float* x, const float* nw, float* ou
     int grid, per;
     mv_shape(W, &grid, &per);
     const size_t lds = ((size_t)16 * (2 * W.nbp + 4) + (NORM ? (size_t)W.cols : 0)) * sizeof(float);
-    hipLaunchKernelGGL((matvec_q8_kernel<EPI, NORM>), dim3(grid), dim3(256), lds, st, W, x, nw, out, a, per);
+    if (W.U == 4)
+        hipLaunchKernelGGL((matvec_q8_kernel<EPI, NORM, 4>), dim3(grid), dim3(256), lds, st, W, x, nw, out, a, per);
+    else if (W.U == 2)
+        hipLaunchKernelGGL((matvec_q8_kernel<EPI, NORM, 2>), dim3(grid), dim3(256), lds, st, W, x, nw, out, a, per);
+    else
+        hipLaunchKernelGGL((matvec_q8_kernel<EPI, NORM, 1>), dim3(grid), dim3(256), lds, st, W, x, nw, out, a, per);
     if (EPI == EPI_ARGMAX)
         hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(256), 0, st, a.part_val, a.part_idx, grid, a.ids,
                            a.mstate, a.eos, a.neos);
@@ -384,10 +403,20 @@ void launch_matvec_q8(const Q8Dev& W, const float* x, const float* norm_w, float
         mv_dispatch<false>(W, x, nullptr, out, epi, a, st);
 }
 
+size_t matvec_lds_bytes(int cols, bool norm) {
+    const Q8Dev w = q8_shape(1, cols);
+    return ((size_t)16 * (2 * w.nbp + 4) + (norm ? (size_t)cols : 0)) * sizeof(float);
+}
+size_t matvec_lds_limit() { return 160 * 1024 - 2048; }
+
 template <int EPI, bool NORM>
 static hipError_t mv_attr() {
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&matvec_q8_kernel<EPI, NORM>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 2048);
+    hipError_t e = hipSuccess;
+    for (const void* f : {reinterpret_cast<const void*>(&matvec_q8_kernel<EPI, NORM, 4>),
+                          reinterpret_cast<const void*>(&matvec_q8_kernel<EPI, NORM, 2>),
+                          reinterpret_cast<const void*>(&matvec_q8_kernel<EPI, NORM, 1>)})
+        if (e == hipSuccess) e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 2048);
+    return e;
 }
 
 hipError_t matvec_init() {

@@ -246,6 +246,11 @@ void upload(jyhip_model* m, const jy_model_desc* d, int max_seq) {
     const int H = m->H, qd = m->qd, kvd = m->kvd, F = m->F, V = m->V;
     m->layers.resize(m->L);
     if (m->wtype == JY_Q8_0) {
+        // the decode matvec stages its whole input vector in LDS (with the norm weights
+        // where it normalises): hidden for QKV / gate-up / lm_head, q_dim for O, F for down
+        if (matvec_lds_bytes(H, true) > matvec_lds_limit() || matvec_lds_bytes(qd, false) > matvec_lds_limit() ||
+            matvec_lds_bytes(F, false) > matvec_lds_limit())
+            fail("hidden / q_dim / intermediate too large for the decode matvec's LDS staging");
         size_t stage = q8_bytes(V, H);
         stage = std::max(stage, q8_bytes(F, H));
         stage = std::max(stage, q8_bytes(H, F));
