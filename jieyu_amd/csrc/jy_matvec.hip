@@ -44,6 +44,90 @@ __device__ __forceinline__ void mv_chunk(const uint4& w, const uint4& dd, const 
     }
 }
 
+// The sum of squares of one RMSNorm lane: v = fma(e, e, v) over pe[0], po[0], pe[2],
+// po[2], ... (npairs of each), two LDS rows walked in step.  The LDS operands stream
+// through two register sets of 4 pairs each (GCN assembly, as for the attention
+// chains: in C the compiler waits on every batch's own loads); the tail is C.  The
+// sets are small so the normalising matvec keeps its register budget.
+__device__ __forceinline__ float norm_chain(const float* pe, const float* po, int npairs, float v) {
+    int nb = npairs >> 3;
+    if (nb > 0) {
+        uint32_t ae = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float*)pe;
+        uint32_t ao = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float*)po;
+        asm volatile(
+        "s_waitcnt lgkmcnt(0)\n"
+        "ds_read2_b32 v[112:113], %[pe] offset0:0 offset1:2\n"
+        "ds_read2_b32 v[114:115], %[pe] offset0:4 offset1:6\n"
+        "ds_read2_b32 v[116:117], %[po] offset0:0 offset1:2\n"
+        "ds_read2_b32 v[118:119], %[po] offset0:4 offset1:6\n"
+        "ds_read2_b32 v[120:121], %[pe] offset0:8 offset1:10\n"
+        "ds_read2_b32 v[122:123], %[pe] offset0:12 offset1:14\n"
+        "ds_read2_b32 v[124:125], %[po] offset0:8 offset1:10\n"
+        "ds_read2_b32 v[126:127], %[po] offset0:12 offset1:14\n"
+        "s_sub_u32 %[nb], %[nb], 1\n"
+        "L_ss_loop_%=:\n"
+        "s_cmp_eq_u32 %[nb], 0\n"
+        "s_cbranch_scc1 L_ss_last_%=\n"
+        "s_waitcnt lgkmcnt(4)\n"
+        "v_fmac_f32_e32 %[v], v112, v112\n"
+        "v_fmac_f32_e32 %[v], v116, v116\n"
+        "v_fmac_f32_e32 %[v], v113, v113\n"
+        "v_fmac_f32_e32 %[v], v117, v117\n"
+        "v_fmac_f32_e32 %[v], v114, v114\n"
+        "v_fmac_f32_e32 %[v], v118, v118\n"
+        "v_fmac_f32_e32 %[v], v115, v115\n"
+        "v_fmac_f32_e32 %[v], v119, v119\n"
+        "v_add_u32_e32 %[pe], 64, %[pe]\n"
+        "v_add_u32_e32 %[po], 64, %[po]\n"
+        "ds_read2_b32 v[112:113], %[pe] offset0:0 offset1:2\n"
+        "ds_read2_b32 v[114:115], %[pe] offset0:4 offset1:6\n"
+        "ds_read2_b32 v[116:117], %[po] offset0:0 offset1:2\n"
+        "ds_read2_b32 v[118:119], %[po] offset0:4 offset1:6\n"
+        "s_waitcnt lgkmcnt(4)\n"
+        "v_fmac_f32_e32 %[v], v120, v120\n"
+        "v_fmac_f32_e32 %[v], v124, v124\n"
+        "v_fmac_f32_e32 %[v], v121, v121\n"
+        "v_fmac_f32_e32 %[v], v125, v125\n"
+        "v_fmac_f32_e32 %[v], v122, v122\n"
+        "v_fmac_f32_e32 %[v], v126, v126\n"
+        "v_fmac_f32_e32 %[v], v123, v123\n"
+        "v_fmac_f32_e32 %[v], v127, v127\n"
+        "ds_read2_b32 v[120:121], %[pe] offset0:8 offset1:10\n"
+        "ds_read2_b32 v[122:123], %[pe] offset0:12 offset1:14\n"
+        "ds_read2_b32 v[124:125], %[po] offset0:8 offset1:10\n"
+        "ds_read2_b32 v[126:127], %[po] offset0:12 offset1:14\n"
+        "s_sub_u32 %[nb], %[nb], 1\n"
+        "s_branch L_ss_loop_%=\n"
+        "L_ss_last_%=:\n"
+        "s_waitcnt lgkmcnt(4)\n"
+        "v_fmac_f32_e32 %[v], v112, v112\n"
+        "v_fmac_f32_e32 %[v], v116, v116\n"
+        "v_fmac_f32_e32 %[v], v113, v113\n"
+        "v_fmac_f32_e32 %[v], v117, v117\n"
+        "v_fmac_f32_e32 %[v], v114, v114\n"
+        "v_fmac_f32_e32 %[v], v118, v118\n"
+        "v_fmac_f32_e32 %[v], v115, v115\n"
+        "v_fmac_f32_e32 %[v], v119, v119\n"
+        "s_waitcnt lgkmcnt(0)\n"
+        "v_fmac_f32_e32 %[v], v120, v120\n"
+        "v_fmac_f32_e32 %[v], v124, v124\n"
+        "v_fmac_f32_e32 %[v], v121, v121\n"
+        "v_fmac_f32_e32 %[v], v125, v125\n"
+        "v_fmac_f32_e32 %[v], v122, v122\n"
+        "v_fmac_f32_e32 %[v], v126, v126\n"
+        "v_fmac_f32_e32 %[v], v123, v123\n"
+        "v_fmac_f32_e32 %[v], v127, v127\n"
+        : [v] "+v"(v), [pe] "+v"(ae), [po] "+v"(ao), [nb] "+s"(nb)
+        :
+        : "v112", "v113", "v114", "v115", "v116", "v117", "v118", "v119", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "scc", "memory");
+    }
+    for (int m = npairs & ~7; m < npairs; m++) {
+        v = __builtin_fmaf(pe[2 * m], pe[2 * m], v);
+        v = __builtin_fmaf(po[2 * m], po[2 * m], v);
+    }
+    return v;
+}
+
 // one wave owns row groups wid, wid + TW, ... (TW = waves in the grid), `per` of
 // them; the chunk stream of consecutive row groups is pipelined without a gap.
 template <int EPI, bool NORM, int MV_U>
@@ -90,15 +174,13 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
         }
     };
 
-    // both register buffers are in flight before the prologue (staging, RMSNorm), and
-    // stay two buffers ahead of the compute afterwards
+    // stage x (and with NORM the RMSNorm weights, into nws behind the staged vector),
+    // four floats per load, several loads in flight per thread; zero past K, so
+    // padding blocks contribute exact zeros.  The vector's first batch is requested
+    // before the weight prefetch so it does not queue behind it; both weight buffers
+    // are then in flight through the prologue and stay two buffers ahead of the
+    // compute afterwards.
     uint4 wA[MV_U], dA[MV_U], wB[MV_U], dB[MV_U];
-    load(wA, dA);
-    load(wB, dB);
-
-    // stage x, four floats per load, several loads in flight per thread (zero past K:
-    // padding blocks then contribute exact zeros); with NORM the RMSNorm weights come
-    // in the same batches, into nws behind the staged vector
     float* nws = xs + 16 * XS;
     const int nk4 = K / 4;
     {
@@ -106,17 +188,21 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
         const float4* x4 = reinterpret_cast<const float4*>(x);
         const float4* w4 = reinterpret_cast<const float4*>(nw);
         constexpr int SU = NORM ? 4 : 8;  // loads per thread per batch (x and w with NORM)
-        for (int base = tid; base < nv4; base += SU * blockDim.x) {
+        for (int b0 = 0; b0 < nv4; b0 += SU * blockDim.x) {
             float4 v[SU], wv[SU];
 #pragma unroll
             for (int u = 0; u < SU; u++) {
-                const int i = base + u * blockDim.x;
+                const int i = b0 + tid + u * blockDim.x;
                 v[u] = (i < nv4 && i < nk4) ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 if (NORM) wv[u] = i < nk4 ? w4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
+            if (b0 == 0) {
+                load(wA, dA);
+                load(wB, dB);
+            }
 #pragma unroll
             for (int u = 0; u < SU; u++) {
-                const int i = base + u * blockDim.x;
+                const int i = b0 + tid + u * blockDim.x;
                 if (i < nv4) {
                     const int k = 4 * i;
                     xs[xs_index(k, XS)] = v[u].x;
@@ -144,11 +230,7 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
                 const float* pe = xs + (lane >> 1) * XS + (lane & 1);
                 const float* po = pe + 8 * XS;
                 const int npairs = n16 >> 5;
-#pragma unroll 8
-                for (int m = 0; m < npairs; m++) {
-                    v = __builtin_fmaf(pe[2 * m], pe[2 * m], v);
-                    v = __builtin_fmaf(po[2 * m], po[2 * m], v);
-                }
+                v = norm_chain(pe, po, npairs, v);
                 if (n16 & 16) {  // an odd number of 16-element groups ends on an even c
                     const float e = pe[2 * npairs];
                     v = __builtin_fmaf(e, e, v);
@@ -185,9 +267,29 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
         __syncthreads();
         const float scale = red[16];
         const bool zero = red[17] != 0.0f;
-        for (int k = tid; k < K; k += blockDim.x) {
-            const int xi = xs_index(k, XS);
-            xs[xi] = zero ? 0.0f : (xs[xi] * scale) * nws[k];
+        // x = (x*scale)*w: a thread's four-element groups, all reads before the writes
+        for (int b0 = 0; b0 < nk4; b0 += 4 * blockDim.x) {
+            float xv[4][4];
+            float4 wv[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int i = b0 + tid + u * blockDim.x;
+                if (i < nk4) {
+                    wv[u] = reinterpret_cast<const float4*>(nws)[i];
+#pragma unroll
+                    for (int c = 0; c < 4; c++) xv[u][c] = xs[xs_index(4 * i + c, XS)];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int i = b0 + tid + u * blockDim.x;
+                if (i < nk4) {
+                    const float w4[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+#pragma unroll
+                    for (int c = 0; c < 4; c++)
+                        xs[xs_index(4 * i + c, XS)] = zero ? 0.0f : (xv[u][c] * scale) * w4[c];
+                }
+            }
         }
         __syncthreads();
     }
@@ -349,8 +451,8 @@ __global__ __launch_bounds__(256) void argmax_finish_kernel(const float* __restr
 static int g_cus = 256;
 
 // launch shape: 4 waves per workgroup, at most 4 workgroups per CU; each wave owns
-// `per` row groups so the prologue (staging x) is paid once per workgroup
-static void mv_shape(const Q8Dev& W, int* grid, int* per) {
+// `per` row groups so the prologue (staging, RMSNorm) is paid once per workgroup
+static void mv_shape(const Q8Dev& W, bool norm, int* grid, int* per) {
     const int nwv = 4;
     const int groups = (W.rows + 3) / 4;
     const int max_waves = 4 * g_cus * nwv;
@@ -358,18 +460,20 @@ static void mv_shape(const Q8Dev& W, int* grid, int* per) {
     *grid = (groups + nwv * *per - 1) / (nwv * *per);
 }
 
+// workgroups of an lm_head launch (one partial maximum each), normalising or not
 int argmax_partials(int rows) {
     Q8Dev w;
     w.rows = rows;
-    int grid, per;
-    mv_shape(w, &grid, &per);
-    return grid;
+    int grid = 0, per = 0, g2 = 0;
+    mv_shape(w, false, &grid, &per);
+    mv_shape(w, true, &g2, &per);
+    return std::max(grid, g2);
 }
 
 template <int EPI, bool NORM>
 static void mv_launch(const Q8Dev& W, const float* x, const float* nw, float* out, const MvArgs& a, hipStream_t st) {
     int grid, per;
-    mv_shape(W, &grid, &per);
+    mv_shape(W, NORM, &grid, &per);
     const size_t lds = ((size_t)16 * (2 * W.nbp + 4) + (NORM ? (size_t)W.cols : 0)) * sizeof(float);
     if (W.U == 4)
         hipLaunchKernelGGL((matvec_q8_kernel<EPI, NORM, 4>), dim3(grid), dim3(256), lds, st, W, x, nw, out, a, per);
