@@ -178,7 +178,7 @@ def main():
     ap.add_argument("--prompt-len", type=int, default=1024)
     ap.add_argument("--max-seq", type=int, default=4096)
     ap.add_argument("--cpu-prompt", type=int, default=8)
-    ap.add_argument("--cpu-tokens", type=int, default=6)
+    ap.add_argument("--cpu-tokens", type=int, default=96)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernel", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
