@@ -2,8 +2,9 @@
 
     python -m jieyu_amd.build        # or: from jieyu_amd.build import build; build()
 
-Sources: csrc/*.hip and csrc/*.cpp through hipcc, csrc/*.c through gcc.  The
-library lands next to this file so it travels with the source tree.
+Sources: csrc/*.hip and csrc/*.cpp through hipcc, csrc/*.c through gcc, and the
+host-only text layer csrc/*.cc through g++.  The library lands next to this
+file so it travels with the source tree.
 """
 import os
 import shutil
@@ -29,6 +30,7 @@ HIP_FLAGS = [
     "-Wno-unused-command-line-argument", "-I", INCLUDE, "-I", CSRC,
 ]
 C_FLAGS = ["-std=c11", "-O2", "-ffp-contract=off", "-fno-fast-math", "-fopenmp", "-fPIC", "-I", INCLUDE]
+CXX_FLAGS = ["-std=c++17", "-O2", "-fPIC", "-fvisibility=hidden", "-Wall", "-I", INCLUDE, "-I", CSRC]
 
 
 def _run(cmd):
@@ -53,6 +55,8 @@ def build(verbose=False):
                     cmd[1:1] = ["-x", "hip"]
             elif s.endswith(".c"):
                 cmd = ["gcc", *C_FLAGS, "-c", path, "-o", obj]
+            elif s.endswith(".cc"):
+                cmd = ["g++", *CXX_FLAGS, "-c", path, "-o", obj]
             else:
                 continue
             if verbose:

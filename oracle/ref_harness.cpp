@@ -16,7 +16,8 @@
 #include <vector>
 
 #include "model_libs/generate.h"   /* generate / forward_cached / transformer_layer and every kernel */
-#include "date_libs/consten_pool.h"
+#include "main.hpp"                 /* the text C ABI (jieyu_load / jieyu_generate ...), pipeline, tokenizer,
+                                       consten_pool */
 
 #include "jieyu_model.h"
 
@@ -199,4 +200,104 @@ JYREF_API int jyref_generate(const jy_model_desc* m, const int* prompt_ids, int 
     } catch (const std::exception&) {
         return -1;
     }
+}
+
+/* ---------------------------------------------------------------- text layer
+ * The reference's tokenizer, JSON lookups, model-directory bind and BPE trainer,
+ * for the text-path checks.  The C ABI itself (jieyu_load, jieyu_generate, ...) is
+ * exported by main.hpp above under its own names. */
+
+JYREF_API void* jyref_tok_load(const char* vocab, const char* merges) {
+    auto* t = new json_libs::Tokenizer();
+    if (!t->load(vocab, merges)) {
+        delete t;
+        return nullptr;
+    }
+    return t;
+}
+
+JYREF_API void jyref_tok_free(void* t) { delete (json_libs::Tokenizer*)t; }
+
+JYREF_API int jyref_tok_info(void* t, int* vocab_size, int* bos, int* eos, int* unk) {
+    auto* k = (json_libs::Tokenizer*)t;
+    *vocab_size = (int)k->vocab_size();
+    *bos = k->bos_id();
+    *eos = k->eos_id();
+    *unk = k->unk_id();
+    return 0;
+}
+
+JYREF_API int jyref_tok_add_special(void* t, const char* piece) {
+    return ((json_libs::Tokenizer*)t)->add_special_token(piece);
+}
+
+JYREF_API int jyref_tok_encode(void* t, const char* text, size_t len, int32_t* ids, int cap) {
+    const std::vector<int32_t> v = ((json_libs::Tokenizer*)t)->encode(std::string(text, len));
+    for (int i = 0; i < (int)v.size() && i < cap; i++) ids[i] = v[(size_t)i];
+    return (int)v.size();
+}
+
+JYREF_API int jyref_tok_decode(void* t, const int32_t* ids, int n, char* out, int cap) {
+    const std::string s = ((json_libs::Tokenizer*)t)->decode(std::vector<int32_t>(ids, ids + n));
+    if (cap > 0) memcpy(out, s.data(), std::min<size_t>(s.size(), (size_t)cap));
+    return (int)s.size();
+}
+
+JYREF_API int jyref_info_int(const char* path, const char* key, int fallback) {
+    return pipeline::read_info_int(path, key, fallback);
+}
+
+JYREF_API int jyref_info_str(const char* path, const char* key, const char* fallback, char* out, int cap) {
+    const std::string v = pipeline::read_info_str(path, key, fallback);
+    if (cap > 0) {
+        const size_t n = std::min<size_t>(v.size(), (size_t)cap - 1);
+        memcpy(out, v.data(), n);
+        out[n] = 0;
+    }
+    return (int)v.size();
+}
+
+/* install_model + bind_model; hp as jytext_model_bind's first nine entries */
+JYREF_API int jyref_model_bind(const char* dir, int max_seq, int* hp, char* err, int cap) {
+    std::string e;
+    bool ok = false;
+    pipeline::ModelRefs r;
+    free_model_map();
+    try {
+        install_model(std::filesystem::path(dir));
+        ok = pipeline::bind_model(r, max_seq, &e);
+    } catch (const std::exception& x) {
+        e = std::string("装载 model.bf 失败: ") + x.what();
+    }
+    if (cap > 0) {
+        const size_t n = std::min<size_t>(e.size(), (size_t)cap - 1);
+        memcpy(err, e.data(), n);
+        err[n] = 0;
+    }
+    if (ok && hp) {
+        const int v[9] = {r.num_layers, r.hidden, r.num_heads, r.num_kv_heads, r.head_dim, r.intermediate,
+                          r.vocab_size, r.add_bos ? 1 : 0, r.qkv_bias ? 1 : 0};
+        memcpy(hp, v, sizeof v);
+    }
+    r.free();
+    free_model_map();
+    return ok ? 0 : -1;
+}
+
+/* BPETrainer (libs/tokenizer_libs/include/trainer.h:63-132, :370-395) */
+JYREF_API int jyref_train_bpe(const char* corpus, int target_vocab, const char* out_dir) {
+    json_libs::BPETrainer t(target_vocab);
+    if (!t.load_corpus(corpus)) return -1;
+    t.train();
+    return t.save(out_dir) ? (int)t.vocab_size() : -1;
+}
+
+/* write_byte_level_vocab (libs/tokenizer_libs/include/byte_vocab.h:15-38) */
+JYREF_API int jyref_write_byte_vocab(const char* vocab, const char* merges) {
+    try {
+        json_libs::write_byte_level_vocab(vocab, merges);
+    } catch (const std::exception&) {
+        return -1;
+    }
+    return 0;
 }

@@ -17,7 +17,7 @@ def declared(header):
     text = open(os.path.join(ROOT, "include", header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     text = re.sub(r"//[^\n]*", "", text)
-    names = re.findall(r"\b((?:jyhip|jysyn)_[a-z0-9_]+)\s*\(", text)
+    names = re.findall(r"\b((?:jyhip|jysyn|jytext|jieyu)_[a-z0-9_]+)\s*\(", text)
     return sorted(set(names))
 
 
@@ -33,7 +33,10 @@ def syms():
     return exported()
 
 
-@pytest.mark.parametrize("header", ["jieyu_amd.h", "jieyu_synth.h"])
+HEADERS = ["jieyu_amd.h", "jieyu_synth.h", "jieyu_api.h", "jieyu_text.h"]
+
+
+@pytest.mark.parametrize("header", HEADERS)
 def test_header_symbols_exported(syms, header):
     names = declared(header)
     assert names, header
@@ -42,11 +45,23 @@ def test_header_symbols_exported(syms, header):
 
 
 def test_no_undeclared_exports(syms):
-    ours = {s for s in syms if s.startswith(("jyhip_", "jysyn_"))}
-    decl = set(declared("jieyu_amd.h")) | set(declared("jieyu_synth.h"))
+    ours = {s for s in syms if s.startswith(("jyhip_", "jysyn_", "jytext_", "jieyu_"))}
+    decl = set().union(*(declared(h) for h in HEADERS))
     assert ours <= decl, f"exported but not declared: {sorted(ours - decl)}"
     # C++ internals stay hidden
-    assert not any(s.startswith("_ZN2jy") for s in syms)
+    assert not any(s.startswith(("_ZN2jy", "_ZN6jytext")) for s in syms)
+
+
+def test_text_abi_matches_reference_header():
+    """the eight entry points of JieyuAI_api.h:47-67, and the public handle layout
+    {char dir[512]; char error[256]; int max_seq} (JieyuAI_api.h:42-46)"""
+    assert declared("jieyu_api.h") == sorted(
+        ["jieyu_load", "jieyu_free", "jieyu_last_error", "jieyu_version", "jieyu_context_length",
+         "jieyu_model_dir", "jieyu_generate", "jieyu_generate_jsonl"])
+    text = open(os.path.join(ROOT, "include", "jieyu_api.h")).read()
+    assert re.search(r"char dir\[JIEYU_PATH_MAX\];\s*/\*[^*]*\*/\s*char error\[JIEYU_ERR_MAX\];"
+                     r"\s*/\*[^*]*\*/\s*int max_seq;", text)
+    assert "#define JIEYU_PATH_MAX 512" in text and "#define JIEYU_ERR_MAX 256" in text
 
 
 def test_library_loads_and_binds():
