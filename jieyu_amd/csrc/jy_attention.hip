@@ -31,6 +31,17 @@ static constexpr int ATT_U = 2;        // key loads per lane in the scores kerne
 
 // ------------------------------------------------------------------ scores
 
+// Sum of each group of LP adjacent lanes (LP a power of two, at most 16) into the
+// group's last lane, by DPP row shifts (exact: integer adds).
+__device__ __forceinline__ int group_sum_last(int d, int LP) {
+    if (LP > 1) d += __builtin_amdgcn_update_dpp(0, d, 0x111, 0xf, 0xf, true);  // row_shr:1
+    if (LP > 2) d += __builtin_amdgcn_update_dpp(0, d, 0x112, 0xf, 0xf, true);  // row_shr:2
+    if (LP > 4) d += __builtin_amdgcn_update_dpp(0, d, 0x114, 0xf, 0xf, true);  // row_shr:4
+    if (LP > 8) d += __builtin_amdgcn_update_dpp(0, d, 0x118, 0xf, 0xf, true);  // row_shr:8
+    return d;
+}
+
+
 __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a, int kc) {
     __shared__ __align__(16) int8_t qv8[ATT_GB][256];
     __shared__ __align__(16) int8_t kloc[256];
@@ -102,8 +113,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a, in
                 float amax = 0.0f;
 #pragma unroll
                 for (int c = 0; c < 4; c++) amax = fmaxf(amax, fabsf(vals[t][c]));
-#pragma unroll
-                for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+                amax = wave_max64(amax);
                 const float inv = quant_inv(amax);
                 int8_t* dst = i < gh ? qv8[i] : (i == gh ? kloc : vloc);
 #pragma unroll
@@ -160,10 +170,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a, in
                 d = __builtin_amdgcn_sdot4(qw[hh].y, k4[u].y, d, false);
                 d = __builtin_amdgcn_sdot4(qw[hh].z, k4[u].z, d, false);
                 d = __builtin_amdgcn_sdot4(qw[hh].w, k4[u].w, d, false);
-                for (int o = 1; o < LP; o <<= 1) d += __shfl_xor(d, o);
-                dot[hh] = d;
+                dot[hh] = group_sum_last(d, LP);
             }
-            if (piece == 0 && j < jend) {
+            if (piece == LP - 1 && j < jend) {
 #pragma unroll
                 for (int hh = 0; hh < ATT_GB; hh++)
                     if (hh < gh) S[(size_t)hh * a.max_keys + j] = (float)dot[hh] * ((ksv[u] * qsc[hh]) * scale);
@@ -194,207 +203,314 @@ __device__ __forceinline__ uint32_t lds_off(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
 }
 
-__device__ __forceinline__ float hx(uint32_t w, int hi) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? (w >> 16) : w));
-}
-
 // The two sequential chains of the reference softmax/PV, one dependent VALU op per
-// step.  Their LDS operands stream through two register sets of 32 steps each: the
-// loads of one set are in flight while the chain runs through the other.  Written
-// as GCN assembly because the compiler turns a C ping-pong of register arrays into
-// one register copy per step; the loops are short, fixed and wait on lgkmcnt only
-// for the set they are about to read (LDS returns in order).  Batches of 64 steps;
-// the tail is C.
+// step, written as GCN assembly: the compiler turns a C ping-pong of register
+// arrays into one register copy per step.  The loops are short and fixed, and wait
+// on lgkmcnt only for the register set they are about to read (LDS returns in
+// order); the tails are C.
 //
-// sum += e[j], j ascending (libs/model_libs/attention/x86/x86_classic.txt:55-58)
-__device__ __forceinline__ float chain_sum(const float* e, int n, float sum) {
+// sum += e[j], j ascending (libs/model_libs/attention/x86/x86_classic.txt:55-58).
+// Lanes 0..15 of the calling wave read 64 consecutive e values with one
+// ds_read_b128 (lane k holds e[4k .. 4k+3]) and lane 0 adds them in order, taking
+// lane k's registers with a DPP row shift: one LDS read per 64 steps.  Two 64-step
+// register sets, one in flight while the other is consumed (the last set may be
+// read past n, inside the caller's LDS allocation, and is then unused).  Lanes
+// 1..15 compute values that are discarded; lane 0 returns the sum.
+__device__ __forceinline__ float chain_sum16(const float* e, int n, float sum) {
     int nb = n >> 6;
     if (nb > 0) {
-        uint32_t pa = lds_off(e);
+        uint32_t pa = lds_off(e) + 16u * (threadIdx.x & 15u);
         asm volatile(
         "s_waitcnt lgkmcnt(0)\n"
         "ds_read_b128 v[100:103], %[pa]\n"
-        "ds_read_b128 v[104:107], %[pa] offset:16\n"
-        "ds_read_b128 v[108:111], %[pa] offset:32\n"
-        "ds_read_b128 v[112:115], %[pa] offset:48\n"
-        "ds_read_b128 v[116:119], %[pa] offset:64\n"
-        "ds_read_b128 v[120:123], %[pa] offset:80\n"
-        "ds_read_b128 v[124:127], %[pa] offset:96\n"
-        "ds_read_b128 v[128:131], %[pa] offset:112\n"
-        "ds_read_b128 v[132:135], %[pa] offset:128\n"
-        "ds_read_b128 v[136:139], %[pa] offset:144\n"
-        "ds_read_b128 v[140:143], %[pa] offset:160\n"
-        "ds_read_b128 v[144:147], %[pa] offset:176\n"
-        "ds_read_b128 v[148:151], %[pa] offset:192\n"
-        "ds_read_b128 v[152:155], %[pa] offset:208\n"
-        "ds_read_b128 v[156:159], %[pa] offset:224\n"
-        "ds_read_b128 v[160:163], %[pa] offset:240\n"
+        "ds_read_b128 v[104:107], %[pa] offset:256\n"
         "s_sub_u32 %[nb], %[nb], 1\n"
-        "L_sum_loop_%=:\n"
+        "L_s16_loop_%=:\n"
         "s_cmp_eq_u32 %[nb], 0\n"
-        "s_cbranch_scc1 L_sum_last_%=\n"
-        "s_waitcnt lgkmcnt(8)\n"
-        "v_add_f32 %[s], %[s], v100\n"
-        "v_add_f32 %[s], %[s], v101\n"
-        "v_add_f32 %[s], %[s], v102\n"
-        "v_add_f32 %[s], %[s], v103\n"
-        "v_add_f32 %[s], %[s], v104\n"
-        "v_add_f32 %[s], %[s], v105\n"
-        "v_add_f32 %[s], %[s], v106\n"
-        "v_add_f32 %[s], %[s], v107\n"
-        "v_add_f32 %[s], %[s], v108\n"
-        "v_add_f32 %[s], %[s], v109\n"
-        "v_add_f32 %[s], %[s], v110\n"
-        "v_add_f32 %[s], %[s], v111\n"
-        "v_add_f32 %[s], %[s], v112\n"
-        "v_add_f32 %[s], %[s], v113\n"
-        "v_add_f32 %[s], %[s], v114\n"
-        "v_add_f32 %[s], %[s], v115\n"
-        "v_add_f32 %[s], %[s], v116\n"
-        "v_add_f32 %[s], %[s], v117\n"
-        "v_add_f32 %[s], %[s], v118\n"
-        "v_add_f32 %[s], %[s], v119\n"
-        "v_add_f32 %[s], %[s], v120\n"
-        "v_add_f32 %[s], %[s], v121\n"
-        "v_add_f32 %[s], %[s], v122\n"
-        "v_add_f32 %[s], %[s], v123\n"
-        "v_add_f32 %[s], %[s], v124\n"
-        "v_add_f32 %[s], %[s], v125\n"
-        "v_add_f32 %[s], %[s], v126\n"
-        "v_add_f32 %[s], %[s], v127\n"
-        "v_add_f32 %[s], %[s], v128\n"
-        "v_add_f32 %[s], %[s], v129\n"
-        "v_add_f32 %[s], %[s], v130\n"
-        "v_add_f32 %[s], %[s], v131\n"
-        "v_add_u32_e32 %[pa], 0x100, %[pa]\n"
+        "s_cbranch_scc1 L_s16_lastA_%=\n"
+        "s_waitcnt lgkmcnt(1)\n"
+        "v_add_f32 %[s], v100, %[s]\n"
+        "v_add_f32 %[s], v101, %[s]\n"
+        "v_add_f32 %[s], v102, %[s]\n"
+        "v_add_f32 %[s], v103, %[s]\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "v_add_u32_e32 %[pa], 0x200, %[pa]\n"
         "ds_read_b128 v[100:103], %[pa]\n"
-        "ds_read_b128 v[104:107], %[pa] offset:16\n"
-        "ds_read_b128 v[108:111], %[pa] offset:32\n"
-        "ds_read_b128 v[112:115], %[pa] offset:48\n"
-        "ds_read_b128 v[116:119], %[pa] offset:64\n"
-        "ds_read_b128 v[120:123], %[pa] offset:80\n"
-        "ds_read_b128 v[124:127], %[pa] offset:96\n"
-        "ds_read_b128 v[128:131], %[pa] offset:112\n"
-        "s_waitcnt lgkmcnt(8)\n"
-        "v_add_f32 %[s], %[s], v132\n"
-        "v_add_f32 %[s], %[s], v133\n"
-        "v_add_f32 %[s], %[s], v134\n"
-        "v_add_f32 %[s], %[s], v135\n"
-        "v_add_f32 %[s], %[s], v136\n"
-        "v_add_f32 %[s], %[s], v137\n"
-        "v_add_f32 %[s], %[s], v138\n"
-        "v_add_f32 %[s], %[s], v139\n"
-        "v_add_f32 %[s], %[s], v140\n"
-        "v_add_f32 %[s], %[s], v141\n"
-        "v_add_f32 %[s], %[s], v142\n"
-        "v_add_f32 %[s], %[s], v143\n"
-        "v_add_f32 %[s], %[s], v144\n"
-        "v_add_f32 %[s], %[s], v145\n"
-        "v_add_f32 %[s], %[s], v146\n"
-        "v_add_f32 %[s], %[s], v147\n"
-        "v_add_f32 %[s], %[s], v148\n"
-        "v_add_f32 %[s], %[s], v149\n"
-        "v_add_f32 %[s], %[s], v150\n"
-        "v_add_f32 %[s], %[s], v151\n"
-        "v_add_f32 %[s], %[s], v152\n"
-        "v_add_f32 %[s], %[s], v153\n"
-        "v_add_f32 %[s], %[s], v154\n"
-        "v_add_f32 %[s], %[s], v155\n"
-        "v_add_f32 %[s], %[s], v156\n"
-        "v_add_f32 %[s], %[s], v157\n"
-        "v_add_f32 %[s], %[s], v158\n"
-        "v_add_f32 %[s], %[s], v159\n"
-        "v_add_f32 %[s], %[s], v160\n"
-        "v_add_f32 %[s], %[s], v161\n"
-        "v_add_f32 %[s], %[s], v162\n"
-        "v_add_f32 %[s], %[s], v163\n"
-        "ds_read_b128 v[132:135], %[pa] offset:128\n"
-        "ds_read_b128 v[136:139], %[pa] offset:144\n"
-        "ds_read_b128 v[140:143], %[pa] offset:160\n"
-        "ds_read_b128 v[144:147], %[pa] offset:176\n"
-        "ds_read_b128 v[148:151], %[pa] offset:192\n"
-        "ds_read_b128 v[152:155], %[pa] offset:208\n"
-        "ds_read_b128 v[156:159], %[pa] offset:224\n"
-        "ds_read_b128 v[160:163], %[pa] offset:240\n"
         "s_sub_u32 %[nb], %[nb], 1\n"
-        "s_branch L_sum_loop_%=\n"
-        "L_sum_last_%=:\n"
-        "s_waitcnt lgkmcnt(8)\n"
-        "v_add_f32 %[s], %[s], v100\n"
-        "v_add_f32 %[s], %[s], v101\n"
-        "v_add_f32 %[s], %[s], v102\n"
-        "v_add_f32 %[s], %[s], v103\n"
-        "v_add_f32 %[s], %[s], v104\n"
-        "v_add_f32 %[s], %[s], v105\n"
-        "v_add_f32 %[s], %[s], v106\n"
-        "v_add_f32 %[s], %[s], v107\n"
-        "v_add_f32 %[s], %[s], v108\n"
-        "v_add_f32 %[s], %[s], v109\n"
-        "v_add_f32 %[s], %[s], v110\n"
-        "v_add_f32 %[s], %[s], v111\n"
-        "v_add_f32 %[s], %[s], v112\n"
-        "v_add_f32 %[s], %[s], v113\n"
-        "v_add_f32 %[s], %[s], v114\n"
-        "v_add_f32 %[s], %[s], v115\n"
-        "v_add_f32 %[s], %[s], v116\n"
-        "v_add_f32 %[s], %[s], v117\n"
-        "v_add_f32 %[s], %[s], v118\n"
-        "v_add_f32 %[s], %[s], v119\n"
-        "v_add_f32 %[s], %[s], v120\n"
-        "v_add_f32 %[s], %[s], v121\n"
-        "v_add_f32 %[s], %[s], v122\n"
-        "v_add_f32 %[s], %[s], v123\n"
-        "v_add_f32 %[s], %[s], v124\n"
-        "v_add_f32 %[s], %[s], v125\n"
-        "v_add_f32 %[s], %[s], v126\n"
-        "v_add_f32 %[s], %[s], v127\n"
-        "v_add_f32 %[s], %[s], v128\n"
-        "v_add_f32 %[s], %[s], v129\n"
-        "v_add_f32 %[s], %[s], v130\n"
-        "v_add_f32 %[s], %[s], v131\n"
+        "s_cmp_eq_u32 %[nb], 0\n"
+        "s_cbranch_scc1 L_s16_lastB_%=\n"
+        "s_waitcnt lgkmcnt(1)\n"
+        "v_add_f32 %[s], v104, %[s]\n"
+        "v_add_f32 %[s], v105, %[s]\n"
+        "v_add_f32 %[s], v106, %[s]\n"
+        "v_add_f32 %[s], v107, %[s]\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "ds_read_b128 v[104:107], %[pa] offset:256\n"
+        "s_sub_u32 %[nb], %[nb], 1\n"
+        "s_branch L_s16_loop_%=\n"
+        "L_s16_lastB_%=:\n"
         "s_waitcnt lgkmcnt(0)\n"
-        "v_add_f32 %[s], %[s], v132\n"
-        "v_add_f32 %[s], %[s], v133\n"
-        "v_add_f32 %[s], %[s], v134\n"
-        "v_add_f32 %[s], %[s], v135\n"
-        "v_add_f32 %[s], %[s], v136\n"
-        "v_add_f32 %[s], %[s], v137\n"
-        "v_add_f32 %[s], %[s], v138\n"
-        "v_add_f32 %[s], %[s], v139\n"
-        "v_add_f32 %[s], %[s], v140\n"
-        "v_add_f32 %[s], %[s], v141\n"
-        "v_add_f32 %[s], %[s], v142\n"
-        "v_add_f32 %[s], %[s], v143\n"
-        "v_add_f32 %[s], %[s], v144\n"
-        "v_add_f32 %[s], %[s], v145\n"
-        "v_add_f32 %[s], %[s], v146\n"
-        "v_add_f32 %[s], %[s], v147\n"
-        "v_add_f32 %[s], %[s], v148\n"
-        "v_add_f32 %[s], %[s], v149\n"
-        "v_add_f32 %[s], %[s], v150\n"
-        "v_add_f32 %[s], %[s], v151\n"
-        "v_add_f32 %[s], %[s], v152\n"
-        "v_add_f32 %[s], %[s], v153\n"
-        "v_add_f32 %[s], %[s], v154\n"
-        "v_add_f32 %[s], %[s], v155\n"
-        "v_add_f32 %[s], %[s], v156\n"
-        "v_add_f32 %[s], %[s], v157\n"
-        "v_add_f32 %[s], %[s], v158\n"
-        "v_add_f32 %[s], %[s], v159\n"
-        "v_add_f32 %[s], %[s], v160\n"
-        "v_add_f32 %[s], %[s], v161\n"
-        "v_add_f32 %[s], %[s], v162\n"
-        "v_add_f32 %[s], %[s], v163\n"
+        "v_add_f32 %[s], v104, %[s]\n"
+        "v_add_f32 %[s], v105, %[s]\n"
+        "v_add_f32 %[s], v106, %[s]\n"
+        "v_add_f32 %[s], v107, %[s]\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v104, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v105, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v106, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v107, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "s_branch L_s16_end_%=\n"
+        "L_s16_lastA_%=:\n"
+        "s_waitcnt lgkmcnt(0)\n"
+        "v_add_f32 %[s], v100, %[s]\n"
+        "v_add_f32 %[s], v101, %[s]\n"
+        "v_add_f32 %[s], v102, %[s]\n"
+        "v_add_f32 %[s], v103, %[s]\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:1 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:2 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:3 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:4 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:5 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:6 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:7 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:8 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:9 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:10 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:11 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:12 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:13 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:14 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v100, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v101, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v102, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "v_add_f32_dpp %[s], v103, %[s] row_shl:15 row_mask:0xf bank_mask:0xf\n"
+        "L_s16_end_%=:\n"
         : [s] "+v"(sum), [pa] "+v"(pa), [nb] "+s"(nb)
         :
-        : "v100", "v101", "v102", "v103", "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111", "v112", "v113", "v114", "v115", "v116", "v117", "v118", "v119", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "v128", "v129", "v130", "v131", "v132", "v133", "v134", "v135", "v136", "v137", "v138", "v139", "v140", "v141", "v142", "v143", "v144", "v145", "v146", "v147", "v148", "v149", "v150", "v151", "v152", "v153", "v154", "v155", "v156", "v157", "v158", "v159", "v160", "v161", "v162", "v163", "scc", "memory");
+        : "v100", "v101", "v102", "v103", "v104", "v105", "v106", "v107", "scc", "memory");
     }
     for (int j = n & ~63; j < n; j++) sum += e[j];
     return sum;
 }
 
 // o = fma(p_j, v_j, o), j ascending; v as fp16 (exact for int8), so each step is one
-// v_fma_mix (libs/model_libs/attention/x86/x86_classic.txt:63-70)
+// v_fma_mix (libs/model_libs/attention/x86/x86_classic.txt:63-70).  Operands stream
+// through two register sets of 32 steps.
 __device__ __forceinline__ float chain_pv(const float* P, const _Float16* vr, float o, int n) {
     int nb = n >> 6;
     if (nb > 0) {
@@ -599,8 +715,7 @@ __device__ __forceinline__ float chain_pv(const float* P, const _Float16* vr, fl
 }
 
 __device__ __forceinline__ float att_block_max(float v, float* red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    v = wave_max64(v);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lane == 0) red[wave] = v;
     __syncthreads();
@@ -619,7 +734,40 @@ __device__ __forceinline__ void att_stage_v(const int8_t* V, int hd, int d0, int
     if (t < 0) return;
     uint32_t* VW = reinterpret_cast<uint32_t*>(VH);
     const int wstr = vstr >> 1, pairs = (cnt + 1) >> 1;
-    if ((ds & 15) == 0 && ds <= 64) {
+    if (ds == 32) {
+        // 32 dims = two 16-byte pieces per key; four key pairs per thread in flight
+        for (int kp0 = t; kp0 < pairs; kp0 += 4 * nthr) {
+            uint4 w[4][4];  // [pair][piece of key a, piece of key b]
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int kp = kp0 + u * nthr, ja = j0 + 2 * kp;
+                const bool ok = kp < pairs, hasb = ok && 2 * kp + 1 < cnt;
+                const int8_t* ra = V + (size_t)ja * hd + d0;
+                w[u][0] = ok ? *reinterpret_cast<const uint4*>(ra) : make_uint4(0, 0, 0, 0);
+                w[u][1] = ok ? *reinterpret_cast<const uint4*>(ra + 16) : make_uint4(0, 0, 0, 0);
+                w[u][2] = hasb ? *reinterpret_cast<const uint4*>(ra + hd) : make_uint4(0, 0, 0, 0);
+                w[u][3] = hasb ? *reinterpret_cast<const uint4*>(ra + hd + 16) : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int kp = kp0 + u * nthr;
+                if (kp < pairs) {
+#pragma unroll
+                    for (int pc = 0; pc < 2; pc++) {
+                        const uint32_t xa[4] = {w[u][pc].x, w[u][pc].y, w[u][pc].z, w[u][pc].w};
+                        const uint32_t xb[4] = {w[u][2 + pc].x, w[u][2 + pc].y, w[u][2 + pc].z, w[u][2 + pc].w};
+#pragma unroll
+                        for (int b = 0; b < 16; b++) {
+                            const _Float16 lo = (_Float16)(int8_t)(xa[b >> 2] >> (8 * (b & 3)));
+                            const _Float16 hi = (_Float16)(int8_t)(xb[b >> 2] >> (8 * (b & 3)));
+                            VW[(size_t)(pc * 16 + b) * wstr + kp] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+                                                                    ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+                        }
+                    }
+                }
+            }
+        }
+    } else if ((ds & 15) == 0 && ds <= 64) {
         const int pieces = ds >> 4;
         for (int kp = t; kp < pairs; kp += nthr) {
             const int ja = j0 + 2 * kp;
@@ -694,25 +842,28 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_softmax_pv_kernel(AttnArgs a
         }
         const float mx = att_block_max(lmax, red);
         for (int j = tid; j < nk; j += blockDim.x) E[j] = expf_libm(E[j] - mx);
-        __syncthreads();
-        // the sum chain on one lane while the other waves stage the first run of V
+        // the V scales of this thread's keys, in flight through the sum chain
+        constexpr int NV = ATT_ECAP / ATT_THREADS;
+        float vsr[NV];
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int j = tid + k * ATT_THREADS;
+            vsr[k] = j < nk ? VS[j] : 0.0f;
+        }
+        lds_barrier();
+        // the sum chain on wave 0 while the other waves stage the first run of V
         const int c0 = min(nk, vcap);
-        if (tid == 0) s_inv = 1.0f / chain_sum(E, nk, 0.0f);
+        if (tid < 16) {
+            const float sum = chain_sum16(E, nk, 0.0f);
+            if (tid == 0) s_inv = 1.0f / sum;
+        }
         if (wave > 0) att_stage_v(V, hd, d0, ds, 0, c0, VH, vstr, 64);
-        __syncthreads();
+        lds_barrier();
         const float inv = s_inv;
-        for (int base = tid; base < nk; base += 8 * blockDim.x) {  // p_j * vs_j
-            float vsv[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int j = base + u * blockDim.x;
-                if (j < nk) vsv[u] = VS[j];
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int j = base + u * blockDim.x;
-                if (j < nk) E[j] = (E[j] * inv) * vsv[u];
-            }
+        for (int k = 0; k < NV; k++) {  // p_j * vs_j
+            const int j = tid + k * ATT_THREADS;
+            if (j < nk) E[j] = (E[j] * inv) * vsr[k];
         }
         __syncthreads();
         for (int cs = 0; cs < nk; cs += vcap) {
@@ -735,7 +886,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_softmax_pv_kernel(AttnArgs a
             const int cnt = min(ATT_ECAP, nk - w0);
             for (int j = tid; j < cnt; j += blockDim.x) E[j] = expf_libm(S[w0 + j] - mx);
             __syncthreads();
-            if (tid == 0) sum = chain_sum(E, cnt, sum);
+            if (tid < 16) sum = chain_sum16(E, cnt, sum);
             __syncthreads();
         }
         if (tid == 0) s_inv = 1.0f / sum;

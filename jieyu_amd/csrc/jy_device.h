@@ -95,4 +95,46 @@ __host__ __device__ __forceinline__ int8_t quant_i8(float v, float inv) {
 __host__ __device__ __forceinline__ float quant_inv(float amax) { return amax > 1e-8f ? 127.0f / amax : 0.0f; }
 __host__ __device__ __forceinline__ float quant_scale(float amax) { return amax > 1e-8f ? amax / 127.0f : 0.0f; }
 
+// Cross-lane moves within rows of 16 lanes by DPP (VALU, no LDS round trip): lane l
+// receives the value of lane
+//   0xB1  quad_perm [1,0,3,2]  l ^ 1
+//   0x4E  quad_perm [2,3,0,1]  l ^ 2
+//   0x120 + n  row_ror:n       (l - n) mod 16 of its row (so row_ror:12 gives l + 4)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+#else
+    return v;  // host pass: never called
+#endif
+}
+
+__device__ __forceinline__ float read_lane(float v, int lane) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+#else
+    return v;  // host pass: never called
+#endif
+}
+
+// Workgroup barrier that orders LDS only: global loads in flight stay in flight
+// (__syncthreads also waits for every outstanding load of the calling wave).
+__device__ __forceinline__ void lds_barrier() {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+#endif
+}
+
+// maximum over the 64 lanes of a wave, in every lane (fmaxf: order-independent for
+// the non-negative / finite values it is used on)
+__device__ __forceinline__ float wave_max64(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x124>(v));
+    v = fmaxf(v, dpp_f<0x128>(v));  // every lane: its row's maximum
+    return fmaxf(fmaxf(read_lane(v, 0), read_lane(v, 16)), fmaxf(read_lane(v, 32), read_lane(v, 48)));
+}
+
 }  // namespace jy

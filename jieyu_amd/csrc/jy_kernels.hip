@@ -78,19 +78,21 @@ void launch_repack_q8(const uint8_t* src, int rows, int cols, const Q8Dev& dst, 
 // ---------------------------------------------------------------- embedding
 
 // embedding rows (libs/model_libs/wmat_kernel.h:18-29)
+// grid (rows, ceil(hidden / 256)): one element per thread, so every element's loads
+// are in flight at once
 __global__ void embed_kernel(Q8Dev W, const float* __restrict__ f32, int hidden, const int* __restrict__ ids,
                              int id0, const int* __restrict__ state, float* __restrict__ X) {
-    const int i = blockIdx.x;
+    const int i = blockIdx.x, c = blockIdx.y * blockDim.x + threadIdx.x;
+    if (c >= hidden) return;
     const int id = state ? ids[state[0] - 1] : ids[id0 + i];
-    float* x = X + (size_t)i * hidden;
-    for (int c = threadIdx.x; c < hidden; c += blockDim.x)
-        x[c] = f32 ? f32[(size_t)id * hidden + c] : q8_elem(W, id, c);
+    X[(size_t)i * hidden + c] = f32 ? f32[(size_t)id * hidden + c] : q8_elem(W, id, c);
 }
 
 void launch_embed(const Q8Dev* q8, const float* f32, int hidden, const int* ids_dev, int id_index0,
                   const int* state, int seq, float* X, hipStream_t st) {
     Q8Dev w = q8 ? *q8 : Q8Dev{};
-    hipLaunchKernelGGL(embed_kernel, dim3(seq), dim3(256), 0, st, w, f32, hidden, ids_dev, id_index0, state, X);
+    hipLaunchKernelGGL(embed_kernel, dim3(seq, (hidden + 255) / 256), dim3(256), 0, st, w, f32, hidden, ids_dev,
+                       id_index0, state, X);
 }
 
 // ---------------------------------------------------------------- RMSNorm
@@ -296,11 +298,7 @@ void launch_silu_mul(const float* g, const float* u, int interleaved, int m, int
 
 // ---------------------------------------------------------------- RoPE + int8 packing
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
+__device__ __forceinline__ float wave_max(float v) { return wave_max64(v); }
 
 // One workgroup per token row.  Rotation of pair m of a head uses the table row of
 // position pos; within every full group of 8 pairs the reference's store order puts

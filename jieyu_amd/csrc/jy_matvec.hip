@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
             }
         }
     }
-    __syncthreads();
+    lds_barrier();  // the weight prefetch stays in flight
     if (NORM) {
         // RMSNorm of the staged vector (libs/model_libs/rmsnorm/x86/x86_classic.txt:2-26):
         // lanes 0..15 of wave 0 run the 16 FMA chains (lane l: elements 16c+l, an 8-wide
@@ -242,10 +242,10 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
             }
             // fold ((v0+v1) -> halves -> two hadds) as butterflies; every add of the tree
             // is commutative, so lane 0 ends with the reference's value bit for bit
-            float t = v + __shfl_xor(v, 8);   // s[i] = v[i] + v[8+i]
-            t = t + __shfl_xor(t, 4);         // q[i] = s[i] + s[4+i]
-            t = t + __shfl_xor(t, 1);         // q0+q1 (lane 0), q2+q3 (lane 2)
-            float ss = t + __shfl_xor(t, 2);  // (q0+q1) + (q2+q3)
+            float t = v + dpp_f<0x128>(v);    // s[i] = v[i] + v[8+i]
+            t = t + dpp_f<0x12C>(t);          // q[i] = s[i] + s[4+i]
+            t = t + dpp_f<0xB1>(t);           // q0+q1 (lane 0), q2+q3 (lane 2)
+            float ss = t + dpp_f<0x4E>(t);    // (q0+q1) + (q2+q3)
             if (lane == 0) {
                 // the scalar tail as GCC builds it: with four or more left, the first four
                 // squares are rounded products added in order, the rest fused
@@ -264,7 +264,7 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
                 red[16] = den <= 0.0f ? 0.0f : 1.0f / sqrtf(den);
             }
         }
-        __syncthreads();
+        lds_barrier();
         const float scale = red[16];
         const bool zero = red[17] != 0.0f;
         // x = (x*scale)*w: a thread's four-element groups, all reads before the writes
@@ -291,7 +291,7 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
                 }
             }
         }
-        __syncthreads();
+        lds_barrier();
     }
 
     const float* xrow = xs + g * XS;
@@ -316,14 +316,16 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
             load(wB, dB);
         }
         // lanes 2g, 2g+1 -> the reference's reduction tree
-        a0 += __shfl_xor(a0, 4);
-        a1 += __shfl_xor(a1, 4);
-        a0 += __shfl_xor(a0, 8);
-        a1 += __shfl_xor(a1, 8);
-        a0 += __shfl_xor(a0, 2);
-        a1 += __shfl_xor(a1, 2);
+        // (row rotations give lane g the lanes g+4 and g+8 of its 16-lane row: the
+        // partners g ^ 4, g ^ 8 of the lanes the tree keeps)
+        a0 += dpp_f<0x12C>(a0);
+        a1 += dpp_f<0x12C>(a1);
+        a0 += dpp_f<0x128>(a0);
+        a1 += dpp_f<0x128>(a1);
+        a0 += dpp_f<0x4E>(a0);
+        a1 += dpp_f<0x4E>(a1);
         const float t = a0 + a1;
-        const float y = t + __shfl_xor(t, 1);
+        const float y = t + dpp_f<0xB1>(t);
         const int row = rg * 4 + r;
         const bool own = active && g == 0 && row < W.rows;
 
