@@ -196,7 +196,7 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
                 v[u] = (i < nv4 && i < nk4) ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 if (NORM) wv[u] = i < nk4 ? w4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
-            if (b0 == 0) {
+            if (!NORM && b0 == 0) {
                 load(wA, dA);
                 load(wB, dB);
             }
@@ -216,6 +216,10 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
     }
     lds_barrier();  // the weight prefetch stays in flight
     if (NORM) {
+        // the weights are first needed after the normalisation: their prefetch starts
+        // once the vector is in, so the vector's loads do not queue behind it
+        load(wA, dA);
+        load(wB, dB);
         // RMSNorm of the staged vector (libs/model_libs/rmsnorm/x86/x86_classic.txt:2-26):
         // lanes 0..15 of wave 0 run the 16 FMA chains (lane l: elements 16c+l, an 8-wide
         // remainder pass feeds lanes 0..7), the fold ((v0+v1) -> halves -> two hadds) is
