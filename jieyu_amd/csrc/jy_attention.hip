@@ -726,14 +726,15 @@ __device__ __forceinline__ float att_block_max(float v, float* red) {
 }
 
 // V[j0 .. j0+cnt)[d0 .. d0+ds) -> VH (fp16, [d][j] with row stride vstr halves), by
-// the threads t0.. of the workgroup; each takes two adjacent keys so its stores are
-// whole 32-bit words (adjacent lanes -> adjacent words)
-__device__ __forceinline__ void att_stage_v(const int8_t* V, int hd, int d0, int ds, int j0, int cnt, _Float16* VH,
-                                            int vstr, int t0) {
+// the threads t0.. of the workgroup, key slots cnt .. cpad-1 (cpad even) written as
+// zeros; each thread takes two adjacent keys so its stores are whole 32-bit words
+// (adjacent lanes -> adjacent words)
+__device__ __forceinline__ void att_stage_v(const int8_t* V, int hd, int d0, int ds, int j0, int cnt, int cpad,
+                                            _Float16* VH, int vstr, int t0) {
     const int nthr = (int)blockDim.x - t0, t = (int)threadIdx.x - t0;
     if (t < 0) return;
     uint32_t* VW = reinterpret_cast<uint32_t*>(VH);
-    const int wstr = vstr >> 1, pairs = (cnt + 1) >> 1;
+    const int wstr = vstr >> 1, pairs = cpad >> 1;
     if (ds == 32) {
         // 32 dims = two 16-byte pieces per key; four key pairs per thread in flight
         for (int kp0 = t; kp0 < pairs; kp0 += 4 * nthr) {
@@ -741,7 +742,7 @@ __device__ __forceinline__ void att_stage_v(const int8_t* V, int hd, int d0, int
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int kp = kp0 + u * nthr, ja = j0 + 2 * kp;
-                const bool ok = kp < pairs, hasb = ok && 2 * kp + 1 < cnt;
+                const bool ok = 2 * kp < cnt, hasb = 2 * kp + 1 < cnt;
                 const int8_t* ra = V + (size_t)ja * hd + d0;
                 w[u][0] = ok ? *reinterpret_cast<const uint4*>(ra) : make_uint4(0, 0, 0, 0);
                 w[u][1] = ok ? *reinterpret_cast<const uint4*>(ra + 16) : make_uint4(0, 0, 0, 0);
@@ -771,12 +772,13 @@ __device__ __forceinline__ void att_stage_v(const int8_t* V, int hd, int d0, int
         const int pieces = ds >> 4;
         for (int kp = t; kp < pairs; kp += nthr) {
             const int ja = j0 + 2 * kp;
-            const bool hasb = 2 * kp + 1 < cnt;
+            const bool hasa = 2 * kp < cnt, hasb = 2 * kp + 1 < cnt;
             uint4 wa[4], wb[4];
 #pragma unroll
             for (int pc = 0; pc < 4; pc++)
                 if (pc < pieces) {
-                    wa[pc] = *reinterpret_cast<const uint4*>(V + (size_t)ja * hd + d0 + pc * 16);
+                    wa[pc] = hasa ? *reinterpret_cast<const uint4*>(V + (size_t)ja * hd + d0 + pc * 16)
+                                  : make_uint4(0, 0, 0, 0);
                     wb[pc] = hasb ? *reinterpret_cast<const uint4*>(V + (size_t)(ja + 1) * hd + d0 + pc * 16)
                                   : make_uint4(0, 0, 0, 0);
                 }
@@ -798,7 +800,8 @@ __device__ __forceinline__ void att_stage_v(const int8_t* V, int hd, int d0, int
         const int words = ds >> 2;
         for (int e = t; e < pairs * words; e += nthr) {
             const int kp = e / words, wd = e - kp * words, ja = j0 + 2 * kp;
-            const uint32_t xa = *reinterpret_cast<const uint32_t*>(V + (size_t)ja * hd + d0 + wd * 4);
+            const uint32_t xa =
+                2 * kp < cnt ? *reinterpret_cast<const uint32_t*>(V + (size_t)ja * hd + d0 + wd * 4) : 0u;
             const uint32_t xb =
                 2 * kp + 1 < cnt ? *reinterpret_cast<const uint32_t*>(V + (size_t)(ja + 1) * hd + d0 + wd * 4) : 0u;
 #pragma unroll
@@ -816,6 +819,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_softmax_pv_kernel(AttnArgs a
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float red[8];
     __shared__ float s_inv;
+    __shared__ uint64_t exp_tab[32];
     float* E = reinterpret_cast<float*>(smem);                                   // [ATT_ECAP]
     _Float16* VH = reinterpret_cast<_Float16*>(smem + ATT_ECAP * sizeof(float));  // [ds][vstr]
 
@@ -831,6 +835,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_softmax_pv_kernel(AttnArgs a
     const float* VS = a.kv.vs + head * a.kv.max_seq;
     const float* S = a.scratch + ((size_t)rr * nh + h) * a.max_keys;
 
+    {
+        constexpr uint64_t tab[32] = JY_EXP2_TABLE;
+        if (tid < 32) exp_tab[tid] = tab[tid];  // published by the barriers of the block max
+    }
     float o = 0.0f;
     if (nk <= ATT_ECAP) {
         // scores -> LDS, max, e_j in place
@@ -841,7 +849,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_softmax_pv_kernel(AttnArgs a
             lmax = fmaxf(lmax, s);
         }
         const float mx = att_block_max(lmax, red);
-        for (int j = tid; j < nk; j += blockDim.x) E[j] = expf_libm(E[j] - mx);
+        // e_j, and exact zeros up to a multiple of 64 keys so the chains need no tail
+        const int nk64 = (nk + 63) & ~63;
+        for (int j = tid; j < nk64; j += blockDim.x) E[j] = j < nk ? expf_tab(E[j] - mx, exp_tab) : 0.0f;
         // the V scales of this thread's keys, in flight through the sum chain
         constexpr int NV = ATT_ECAP / ATT_THREADS;
         float vsr[NV];
@@ -854,10 +864,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_softmax_pv_kernel(AttnArgs a
         // the sum chain on wave 0 while the other waves stage the first run of V
         const int c0 = min(nk, vcap);
         if (tid < 16) {
-            const float sum = chain_sum16(E, nk, 0.0f);
+            const float sum = chain_sum16(E, nk64, 0.0f);  // + 0.0 for the padding: exact
             if (tid == 0) s_inv = 1.0f / sum;
         }
-        if (wave > 0) att_stage_v(V, hd, d0, ds, 0, c0, VH, vstr, 64);
+        if (wave > 0) att_stage_v(V, hd, d0, ds, 0, c0, (c0 + 63) & ~63, VH, vstr, 64);
         lds_barrier();
         const float inv = s_inv;
 #pragma unroll
@@ -866,14 +876,15 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_softmax_pv_kernel(AttnArgs a
             if (j < nk) E[j] = (E[j] * inv) * vsr[k];
         }
         __syncthreads();
+        // the PV chain over whole 64-key blocks: the padding adds fma(0, 0, o) = o
         for (int cs = 0; cs < nk; cs += vcap) {
-            const int cnt = min(vcap, nk - cs);
+            const int cnt = min(vcap, nk - cs), cpad = (cnt + 63) & ~63;
             if (cs > 0) {
                 __syncthreads();
-                att_stage_v(V, hd, d0, ds, cs, cnt, VH, vstr, 0);
+                att_stage_v(V, hd, d0, ds, cs, cnt, cpad, VH, vstr, 0);
                 __syncthreads();
             }
-            if (tid < ds) o = chain_pv(E + cs, VH + (size_t)tid * vstr, o, cnt);
+            if (tid < ds) o = chain_pv(E + cs, VH + (size_t)tid * vstr, o, cpad);
         }
     } else {
         // long contexts: scores stay in the global array; e_j is recomputed from them
@@ -883,21 +894,22 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_softmax_pv_kernel(AttnArgs a
         const float mx = att_block_max(lmax, red);
         float sum = 0.0f;
         for (int w0 = 0; w0 < nk; w0 += ATT_ECAP) {
-            const int cnt = min(ATT_ECAP, nk - w0);
-            for (int j = tid; j < cnt; j += blockDim.x) E[j] = expf_libm(S[w0 + j] - mx);
+            const int cnt = min(ATT_ECAP, nk - w0), cpad = (cnt + 63) & ~63;
+            for (int j = tid; j < cpad; j += blockDim.x) E[j] = j < cnt ? expf_tab(S[w0 + j] - mx, exp_tab) : 0.0f;
             __syncthreads();
-            if (tid < 16) sum = chain_sum16(E, cnt, sum);
+            if (tid < 16) sum = chain_sum16(E, cpad, sum);
             __syncthreads();
         }
         if (tid == 0) s_inv = 1.0f / sum;
         __syncthreads();
         const float inv = s_inv;
         for (int cs = 0; cs < nk; cs += vcap) {
-            const int cnt = min(vcap, nk - cs);
-            for (int j = tid; j < cnt; j += blockDim.x) E[j] = (expf_libm(S[cs + j] - mx) * inv) * VS[cs + j];
-            att_stage_v(V, hd, d0, ds, cs, cnt, VH, vstr, 0);
+            const int cnt = min(vcap, nk - cs), cpad = (cnt + 63) & ~63;
+            for (int j = tid; j < cpad; j += blockDim.x)
+                E[j] = j < cnt ? (expf_tab(S[cs + j] - mx, exp_tab) * inv) * VS[cs + j] : 0.0f;
+            att_stage_v(V, hd, d0, ds, cs, cnt, cpad, VH, vstr, 0);
             __syncthreads();
-            if (tid < ds) o = chain_pv(E, VH + (size_t)tid * vstr, o, cnt);
+            if (tid < ds) o = chain_pv(E, VH + (size_t)tid * vstr, o, cpad);
             __syncthreads();
         }
     }

@@ -22,20 +22,23 @@ __host__ __device__ __forceinline__ float half_to_float(uint16_t h) {
 // optimized-routines (32-entry table, cubic in double), with the contractions
 // GCC forms when that C is built with FMA.  Checked bit-exact against glibc's
 // expf on all 2^32 inputs on the host; the softmax only feeds it x <= 0.
-__host__ __device__ __forceinline__ float expf_libm(float x) {
-    // 2^(i/32) as double bits minus i<<47: the table of the exp2f-family reduction
-    // (exp(x) = 2^(k/32) * 2^(r/32)); entry i is the correctly rounded double of
-    // 2^(i/32) with the exponent contribution of i/32 taken out.
-    static constexpr uint64_t kExp2Tab[32] = {
-        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
-        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
-        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
-        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
-        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
-        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
-        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
-        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
-    };
+// 2^(i/32) as double bits minus i<<47: the table of the exp2f-family reduction
+// (exp(x) = 2^(k/32) * 2^(r/32)); entry i is the correctly rounded double of
+// 2^(i/32) with the exponent contribution of i/32 taken out.
+#define JY_EXP2_TABLE { \
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull, \
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull, \
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull, \
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull, \
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull, \
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull, \
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull, \
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull, \
+}
+
+// expf_libm with the table at `tab` (a kernel that calls it in bulk passes a copy in
+// LDS: the constant-memory table is a global-memory load per call)
+__host__ __device__ __forceinline__ float expf_tab(float x, const uint64_t* tab) {
     const uint32_t ux = __builtin_bit_cast(uint32_t, x);
     const uint32_t abstop = (ux >> 20) & 0x7ffu;
     if (abstop >= 0x42bu) {                      // |x| >= 88 or non-finite
@@ -54,7 +57,7 @@ __host__ __device__ __forceinline__ float expf_libm(float x) {
     const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd -= shift;
     const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    uint64_t t = kExp2Tab[ki & 31u];
+    uint64_t t = tab[ki & 31u];
     t += ki << 47;
     const double s = __builtin_bit_cast(double, t);
     const double z = __builtin_fma(c0, r, c1);
@@ -63,6 +66,11 @@ __host__ __device__ __forceinline__ float expf_libm(float x) {
     y = __builtin_fma(z, r2, y);
     y = y * s;
     return (float)y;
+}
+
+__host__ __device__ __forceinline__ float expf_libm(float x) {
+    static constexpr uint64_t kExp2Tab[32] = JY_EXP2_TABLE;
+    return expf_tab(x, kExp2Tab);
 }
 
 // SiLU of libs/model_libs/silu/x86/x86_classic.txt:2-28 as GCC -O3 builds it with
