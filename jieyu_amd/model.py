@@ -7,7 +7,11 @@ configurations the decode-path measurements use.
 import ctypes as C
 
 JY_F32 = 0
+JY_F16 = 1
 JY_Q8_0 = 3
+JY_Q4_K = 5
+JY_Q5_K = 6
+JY_Q6_K = 7
 
 
 class WMat(C.Structure):

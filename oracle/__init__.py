@@ -40,6 +40,14 @@ def load_oracle():
     lib = bind_synth(C.CDLL(ORACLE_SO))
     _proto(lib, "jyo_f16_to_f32", F, C.c_uint16)
     _proto(lib, "jyo_q8_row_dot", F, P, P, I)
+    _proto(lib, "jyo_q_row_dot", F, P, P, I, I)
+    _proto(lib, "jyo_block_elems", I, I)
+    _proto(lib, "jyo_block_bytes", I, I)
+    _proto(lib, "jyo_dequant_block", None, I, P, P)
+    _proto(lib, "jyo_matmul_q", None, P, P, P, I, I, I, I)
+    _proto(lib, "jyo_matmul_f16", None, I, I, I, P, P, P)
+    _proto(lib, "jyo_matmul_w", None, P, I, I, I, P, P)
+    _proto(lib, "jyo_embed_row", None, P, I, I, P)
     _proto(lib, "jyo_matmul_q8", None, P, P, P, I, I, I)
     _proto(lib, "jyo_matmul_f32", None, I, I, I, P, P, P)
     _proto(lib, "jyo_rmsnorm", None, P, P, P, I, F)
@@ -68,6 +76,8 @@ def load_ref():
     _proto(lib, "jyref_version", C.c_char_p)
     _proto(lib, "jyref_matmul_q8", None, P, P, P, I, I, I)
     _proto(lib, "jyref_matmul_f32", None, I, I, I, P, P, P)
+    _proto(lib, "jyref_matmul_w", None, P, I, I, I, P, P)
+    _proto(lib, "jyref_wmat_row", None, P, I, I, P)
     _proto(lib, "jyref_rmsnorm", None, P, P, P, I, F)
     _proto(lib, "jyref_rope_table", None, I, I, F, P, P)
     _proto(lib, "jyref_rope", None, P, I, I, I, I, P, P)

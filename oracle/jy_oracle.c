@@ -39,20 +39,102 @@ float jyo_f16_to_f32(uint16_t h) {
 
 static inline float blk_scale(const uint8_t* b) { return jyo_f16_to_f32((uint16_t)(b[0] | (b[1] << 8))); }
 
-/* libs/matmul_libs/matmul_q.h:111-132: four 8-wide FMA accumulators = 32 virtual
- * lanes, lane L takes element 32b+L of every block b in order; the block is
- * dequantized exactly (int8 * fp16 fits in 19 bits, matmul_q.h:101-105). */
-float jyo_q8_row_dot(const float* x, const uint8_t* row, int k) {
-    float a[32];
-    for (int L = 0; L < 32; L++) a[L] = 0.0f;
-    const int nb = k / 32;
-    for (int b = 0; b < nb; b++) {
-        const uint8_t* blk = row + (size_t)b * 34;
-        const float d = blk_scale(blk);
-        for (int L = 0; L < 32; L++) {
-            const float w = (float)(int8_t)blk[2 + L] * d;
-            a[L] = fmaf(x[32 * b + L], w, a[L]);
+/* libs/matmul_libs/matmul_q.h:22-33 (get_scale_min_k4): the 6-bit scale and min of
+ * sub-block j of a Q4_K / Q5_K super-block */
+static void scale_min_k4(int j, const uint8_t* q, int* sc, int* mn) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *mn = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        *mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+int jyo_block_elems(int type) { return type == JY_Q8_0 ? 32 : 256; }
+
+int jyo_block_bytes(int type) {
+    switch (type) {
+        case JY_Q8_0: return 34;
+        case JY_Q4_K: return 144;
+        case JY_Q5_K: return 176;
+        case JY_Q6_K: return 210;
+        default: return 0;
+    }
+}
+
+/* dequant_block (libs/matmul_libs/matmul_q.h:47-100; Q4_K through
+ * libs/file_libs/q4/q4.h:8-35, whose AVX2+FMA form q4_fma.txt computes
+ * fma(q, d*sc, -(dmin*m))).  Every product here is exact in float: d*sc and
+ * dmin*m are an fp16 times a 6-bit integer (<= 17 significant bits), d1*q adds
+ * 4-5 bits, and Q6_K's (d*sc)*q is 11 + 8 + 6 bits.  So the fused and unfused
+ * forms GCC might emit agree: Q4_K / Q5_K values are the one rounding of
+ * d1*q - n1, Q6_K values are exact. */
+void jyo_dequant_block(int type, const uint8_t* b, float* dst) {
+    switch (type) {
+        case JY_Q8_0: {
+            const float d = blk_scale(b);
+            for (int l = 0; l < 32; l++) dst[l] = (float)(int8_t)b[2 + l] * d;
+            return;
         }
+        case JY_Q4_K:
+        case JY_Q5_K: {
+            const float d = blk_scale(b), dmin = blk_scale(b + 2);
+            const uint8_t* sc = b + 4;
+            const uint8_t* qh = b + 16; /* Q5_K only */
+            const uint8_t* qs = type == JY_Q4_K ? b + 16 : b + 48;
+            for (int g = 0; g < 4; g++) {
+                for (int half = 0; half < 2; half++) {
+                    const int j = 2 * g + half;
+                    int s, m;
+                    scale_min_k4(j, sc, &s, &m);
+                    const float d1 = d * (float)s, n1 = dmin * (float)m;
+                    for (int l = 0; l < 32; l++) {
+                        int q = half ? (qs[32 * g + l] >> 4) : (qs[32 * g + l] & 0xF);
+                        if (type == JY_Q5_K && (qh[l] >> j) & 1) q += 16;
+                        dst[64 * g + 32 * half + l] = fmaf((float)q, d1, -n1);
+                    }
+                }
+            }
+            return;
+        }
+        case JY_Q6_K: {
+            const uint8_t* ql = b;
+            const uint8_t* qh = b + 128;
+            const int8_t* sc = (const int8_t*)(b + 192);
+            const float d = blk_scale(b + 208);
+            for (int nn = 0; nn < 2; nn++) {
+                for (int l = 0; l < 32; l++) {
+                    const int is = l / 16;
+                    const int q1 = ((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                    const int q2 = ((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                    const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                    const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                    dst[128 * nn + l] = (d * (float)sc[is]) * (float)q1;
+                    dst[128 * nn + l + 32] = (d * (float)sc[is + 2]) * (float)q2;
+                    dst[128 * nn + l + 64] = (d * (float)sc[is + 4]) * (float)q3;
+                    dst[128 * nn + l + 96] = (d * (float)sc[is + 6]) * (float)q4;
+                }
+                ql += 64;
+                qh += 32;
+                sc += 8;
+            }
+            return;
+        }
+        default: return;
+    }
+}
+
+/* libs/matmul_libs/matmul_q.h:111-132: four 8-wide FMA accumulators = 32 virtual
+ * lanes, lane L takes element 32c+L of every 32-element step c in order, each
+ * block dequantized first (dequant_block above). */
+float jyo_q_row_dot(const float* x, const uint8_t* row, int type, int k) {
+    float a[32], blk[256];
+    for (int L = 0; L < 32; L++) a[L] = 0.0f;
+    const int be = jyo_block_elems(type), bb = jyo_block_bytes(type), nb = k / be;
+    for (int b = 0; b < nb; b++) {
+        jyo_dequant_block(type, row + (size_t)b * bb, blk);
+        for (int l = 0; l < be; l++) a[l & 31] = fmaf(x[(size_t)b * be + l], blk[l], a[l & 31]);
     }
     /* matmul_q.h:127-131: (s0+s1)+(s2+s3), then 128-bit halves, then two hadds */
     float s[8], r[4];
@@ -61,12 +143,14 @@ float jyo_q8_row_dot(const float* x, const uint8_t* row, int k) {
     return (r[0] + r[1]) + (r[2] + r[3]);
 }
 
-void jyo_matmul_q8(const float* a, const uint8_t* w, float* c, int m, int n, int k) {
-    const int nb = k / 32;
-    const size_t rbytes = (size_t)nb * 34;
+float jyo_q8_row_dot(const float* x, const uint8_t* row, int k) { return jyo_q_row_dot(x, row, JY_Q8_0, k); }
+
+void jyo_matmul_q(const float* a, const uint8_t* w, float* c, int m, int n, int k, int type) {
+    const int be = jyo_block_elems(type), bb = jyo_block_bytes(type), nb = k / be;
+    const size_t rbytes = (size_t)nb * bb;
     if (m == 1) { /* matmul_q.h:139-143 (AVX2+FMA host) */
 #pragma omp parallel for schedule(static)
-        for (int j = 0; j < n; j++) c[j] = jyo_q8_row_dot(a, w + (size_t)j * rbytes, k);
+        for (int j = 0; j < n; j++) c[j] = jyo_q_row_dot(a, w + (size_t)j * rbytes, type, k);
         return;
     }
     /* matmul_q.h:145-161: sequential k, product and sum rounded separately (no FMA:
@@ -74,15 +158,16 @@ void jyo_matmul_q8(const float* a, const uint8_t* w, float* c, int m, int n, int
 #pragma omp parallel
     {
         float* acc = (float*)malloc(sizeof(float) * (size_t)m);
+        float blk[256];
 #pragma omp for schedule(static)
         for (int j = 0; j < n; j++) {
             const uint8_t* row = w + (size_t)j * rbytes;
             for (int i = 0; i < m; i++) acc[i] = 0.0f;
             for (int b = 0; b < nb; b++) {
-                const float d = blk_scale(row + (size_t)b * 34);
-                for (int l = 0; l < 32; l++) {
-                    const float bv = (float)(int8_t)row[(size_t)b * 34 + 2 + l] * d;
-                    const size_t off = (size_t)b * 32 + (size_t)l;
+                jyo_dequant_block(type, row + (size_t)b * bb, blk);
+                for (int l = 0; l < be; l++) {
+                    const float bv = blk[l];
+                    const size_t off = (size_t)b * be + (size_t)l;
                     for (int i = 0; i < m; i++) {
                         const float p = a[(size_t)i * k + off] * bv;
                         acc[i] = acc[i] + p;
@@ -93,6 +178,10 @@ void jyo_matmul_q8(const float* a, const uint8_t* w, float* c, int m, int n, int
         }
         free(acc);
     }
+}
+
+void jyo_matmul_q8(const float* a, const uint8_t* w, float* c, int m, int n, int k) {
+    jyo_matmul_q(a, w, c, m, n, k, JY_Q8_0);
 }
 
 /* libs/matmul_libs/matmul.h:7-8 + x86/x86_classic.txt:2-16: C = 0, then for p in
@@ -112,23 +201,45 @@ void jyo_matmul_f32(int m, int n, int k, const float* A, const float* B, float* 
     }
 }
 
-void jyo_matmul_w(const jy_wmat* w, int m, int n, int k, const float* A, float* C) {
-    if (w->type == JY_Q8_0)
-        jyo_matmul_q8(A, (const uint8_t*)w->data, C, m, n, k);
-    else
-        jyo_matmul_f32(m, n, k, A, (const float*)w->data, C);
+/* libs/model_libs/wmat_kernel.h:12-15 + libs/matmul_libs/matmul_f16.h:19-41: C = 0
+ * (memset), then for p in order C[i][j] = fma(A[i][p], (float)B[p][j], C[i][j]);
+ * half -> float is exact and the n%8 tail is the same expression contracted by
+ * GCC (the function is compiled with fma). */
+void jyo_matmul_f16(int m, int n, int k, const float* A, const uint16_t* B, float* C) {
+    memset(C, 0, sizeof(float) * (size_t)m * (size_t)n);
+#pragma omp parallel for schedule(static) if (m >= 4)
+    for (int i = 0; i < m; i++) {
+        float* crow = C + (size_t)i * n;
+        const float* arow = A + (size_t)i * k;
+        for (int p = 0; p < k; p++) {
+            const float av = arow[p];
+            const uint16_t* brow = B + (size_t)p * n;
+            for (int j = 0; j < n; j++) crow[j] = fmaf(av, jyo_f16_to_f32(brow[j]), crow[j]);
+        }
+    }
 }
 
+void jyo_matmul_w(const jy_wmat* w, int m, int n, int k, const float* A, float* C) {
+    if (w->type == JY_F32)
+        jyo_matmul_f32(m, n, k, A, (const float*)w->data, C);
+    else if (w->type == JY_F16)
+        jyo_matmul_f16(m, n, k, A, (const uint16_t*)w->data, C);
+    else
+        jyo_matmul_q(A, (const uint8_t*)w->data, C, m, n, k, w->type);
+}
+
+/* wmat_row (libs/model_libs/wmat_kernel.h:18-29): f32 copy, f16 converted, or the
+ * row's blocks dequantized */
 void jyo_embed_row(const jy_wmat* w, int id, int width, float* dst) {
-    if (w->type == JY_Q8_0) { /* wmat_kernel.h:24-28 */
-        const int nb = width / 32;
-        const uint8_t* row = (const uint8_t*)w->data + (size_t)id * nb * 34;
-        for (int b = 0; b < nb; b++) {
-            const float d = blk_scale(row + (size_t)b * 34);
-            for (int l = 0; l < 32; l++) dst[b * 32 + l] = (float)(int8_t)row[(size_t)b * 34 + 2 + l] * d;
-        }
-    } else {
+    if (w->type == JY_F32) {
         memcpy(dst, (const float*)w->data + (size_t)id * width, sizeof(float) * (size_t)width);
+    } else if (w->type == JY_F16) {
+        const uint16_t* row = (const uint16_t*)w->data + (size_t)id * width;
+        for (int i = 0; i < width; i++) dst[i] = jyo_f16_to_f32(row[i]);
+    } else {
+        const int be = jyo_block_elems(w->type), bb = jyo_block_bytes(w->type), nb = width / be;
+        const uint8_t* row = (const uint8_t*)w->data + (size_t)id * nb * bb;
+        for (int b = 0; b < nb; b++) jyo_dequant_block(w->type, row + (size_t)b * bb, dst + (size_t)b * be);
     }
 }
 

@@ -28,12 +28,21 @@ extern "C" {
 
 float jyo_f16_to_f32(uint16_t h);
 
+/* block geometry of a quantized type (libs/matmul_libs/matmul_q.h:35-45) */
+int jyo_block_elems(int type);
+int jyo_block_bytes(int type);
+/* dequant_block: Q8_0 / Q4_K / Q5_K / Q6_K (libs/matmul_libs/matmul_q.h:47-100) */
+void jyo_dequant_block(int type, const uint8_t* block, float* dst);
 /* decode row dot, 32 virtual FMA lanes (libs/matmul_libs/matmul_q.h:111-132) */
+float jyo_q_row_dot(const float* x, const uint8_t* row, int type, int k);
 float jyo_q8_row_dot(const float* x, const uint8_t* row, int k);
-/* qmat::matmul_q for Q8_0 (libs/matmul_libs/matmul_q.h:134-162) */
+/* qmat::matmul_q (libs/matmul_libs/matmul_q.h:134-162) */
+void jyo_matmul_q(const float* a, const uint8_t* w, float* c, int m, int n, int k, int type);
 void jyo_matmul_q8(const float* a, const uint8_t* w, float* c, int m, int n, int k);
 /* matmul f32, B = [k][n] (libs/matmul_libs/matmul.h:7-76, x86/x86_classic.txt:1-16) */
 void jyo_matmul_f32(int m, int n, int k, const float* A, const float* B, float* C);
+/* matmul f16, B = [k][n] halves (libs/matmul_libs/matmul_f16.h:19-41) */
+void jyo_matmul_f16(int m, int n, int k, const float* A, const uint16_t* B, float* C);
 /* matmul_w dispatch (libs/model_libs/wmat_kernel.h:9-16) */
 void jyo_matmul_w(const jy_wmat* w, int m, int n, int k, const float* A, float* C);
 /* wmat_row (libs/model_libs/wmat_kernel.h:18-29) */

@@ -27,8 +27,14 @@ namespace {
 
 WMat to_wmat(const jy_wmat& w) {
     if (w.data == nullptr) return WMat();
-    if (w.type == JY_Q8_0) return WMat(w.data, (uint8_t)qmat::Q8_0);
-    return WMat((const float*)w.data);
+    switch (w.type) {
+        case JY_Q8_0: return WMat(w.data, (uint8_t)qmat::Q8_0);
+        case JY_Q4_K: return WMat(w.data, (uint8_t)qmat::Q4K);
+        case JY_Q5_K: return WMat(w.data, (uint8_t)qmat::Q5K);
+        case JY_Q6_K: return WMat(w.data, (uint8_t)qmat::Q6K);
+        case JY_F16: return WMat((const uint16_t*)w.data);
+        default: return WMat((const float*)w.data);
+    }
 }
 
 std::vector<LayerWeights> to_layers(const jy_model_desc* m) {
@@ -65,6 +71,16 @@ JYREF_API const char* jyref_version(void) { return consten_pool.version.charv.c_
 
 JYREF_API void jyref_matmul_q8(const float* a, const void* w, float* c, int m, int n, int k) {
     qmat::matmul_q(a, w, c, m, n, k, qmat::Q8_0);
+}
+
+/* matmul_w (libs/model_libs/wmat_kernel.h:9-16) for any weight type, and wmat_row
+ * (:18-29), the embedding gather */
+JYREF_API void jyref_matmul_w(const jy_wmat* w, int m, int n, int k, const float* A, float* C) {
+    matmul_w(to_wmat(*w), m, n, k, A, C);
+}
+
+JYREF_API void jyref_wmat_row(const jy_wmat* w, int id, int width, float* dst) {
+    wmat_row(to_wmat(*w), (size_t)id, width, dst);
 }
 
 JYREF_API void jyref_matmul_f32(int m, int n, int k, const float* A, const float* B, float* C) {
