@@ -117,6 +117,20 @@ JYHIP_API int jyhip_q8_matvec(jyhip_q8mat* m, const float* x, float* y);
  * (RMSNorm prologue over x, SwiGLU epilogue over interleaved row pairs). */
 JYHIP_API int jyhip_q8_matvec_time(jyhip_q8mat* m, const float* x, int variant, int iters, double* avg_us);
 
+/* One weight matrix of any bound type in HBM: matmul_w (libs/model_libs/wmat_kernel.h:9-16)
+ * with B = w, n output rows, k inputs (f32 / f16 [k][n]; Q8_0 / k-quants [n][k/block]).
+ * jyhip_wmat_matmul computes C[m][n] = A[m][k] x B from host buffers in the
+ * reference's order for w's type: m == 1 the decode kernel (dot_row_avx2 for
+ * quantized rows, matmul_q.h:111-143), m > 1 the prompt GEMM (:145-161; dense
+ * [k][n]: the fma chain of matmul.h / matmul_f16.h).  `copies` device copies let
+ * jyhip_wmat_time rotate through more bytes than the last-level cache: it times
+ * `iters` decode launches with HIP events on the launch stream (mean us). */
+typedef struct jyhip_wmat jyhip_wmat;
+JYHIP_API jyhip_wmat* jyhip_wmat_upload(const jy_wmat* w, int n, int k, int copies);
+JYHIP_API void jyhip_wmat_free(jyhip_wmat* w);
+JYHIP_API int jyhip_wmat_matmul(jyhip_wmat* w, int m, const float* A, float* C);
+JYHIP_API int jyhip_wmat_time(jyhip_wmat* w, const float* x, int iters, double* avg_us);
+
 #ifdef __cplusplus
 }
 #endif

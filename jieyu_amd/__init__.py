@@ -9,8 +9,8 @@ import os
 
 import numpy as np
 
-from .model import (CONFIGS, JY_F32, JY_Q8_0, LayerWeights, ModelDesc, Synth, SynthConfig,
-                    bind_synth, synth_config)
+from .model import (CONFIGS, JY_F16, JY_F32, JY_Q4_K, JY_Q5_K, JY_Q6_K, JY_Q8_0, LayerWeights, ModelDesc, Synth,
+                    SynthConfig, WMat, bind_synth, synth_config)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libjieyu_amd.so")
@@ -75,6 +75,10 @@ def lib():
     _proto(L, "jyhip_q8_free", None, P)
     _proto(L, "jyhip_q8_matvec", I, P, P, P)
     _proto(L, "jyhip_q8_matvec_time", I, P, P, I, I, C.POINTER(C.c_double))
+    _proto(L, "jyhip_wmat_upload", P, C.POINTER(WMat), I, I, I)
+    _proto(L, "jyhip_wmat_free", None, P)
+    _proto(L, "jyhip_wmat_matmul", I, P, I, P, P)
+    _proto(L, "jyhip_wmat_time", I, P, P, I, C.POINTER(C.c_double))
     _lib = L
     return L
 
@@ -296,5 +300,45 @@ class Q8Matrix:
             pass
 
 
-__all__ = ["lib", "last_error", "device_count", "GpuModel", "KVCache", "Q8Matrix", "Stats", "JyError",
-           "ModelDesc", "LayerWeights", "SynthConfig", "Synth", "synth_config", "CONFIGS", "JY_F32", "JY_Q8_0"]
+class WeightMatrix:
+    """One weight matrix of any bound type in HBM (matmul_w's B operand): n outputs,
+    k inputs; `data` in the type's host layout (f32 / f16 [k][n], quantized
+    [n][k/block] blocks)."""
+
+    def __init__(self, data, wtype, n, k, copies=1):
+        self._lib = lib()
+        self.n, self.k, self.wtype = n, k, wtype
+        self._data = np.ascontiguousarray(data)
+        w = WMat(_ptr(self._data), wtype)
+        self.h = self._lib.jyhip_wmat_upload(C.byref(w), n, k, copies)
+        if not self.h:
+            raise JyError(last_error())
+
+    def matmul(self, A):
+        """C[m][n] for A[m][k] (m == 1: the decode kernel, m > 1: the prompt GEMM)"""
+        A = np.ascontiguousarray(A, np.float32).reshape(-1, self.k)
+        out = np.zeros((A.shape[0], self.n), np.float32)
+        _check(self._lib.jyhip_wmat_matmul(self.h, A.shape[0], _ptr(A), _ptr(out)))
+        return out
+
+    def time(self, x, iters):
+        x = np.ascontiguousarray(x, np.float32)
+        us = C.c_double()
+        _check(self._lib.jyhip_wmat_time(self.h, _ptr(x), iters, C.byref(us)))
+        return us.value
+
+    def close(self):
+        if self.h:
+            self._lib.jyhip_wmat_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+__all__ = ["lib", "last_error", "device_count", "GpuModel", "KVCache", "Q8Matrix", "WeightMatrix", "Stats", "JyError",
+           "ModelDesc", "LayerWeights", "SynthConfig", "Synth", "synth_config", "CONFIGS", "JY_F32", "JY_F16",
+           "JY_Q8_0", "JY_Q4_K", "JY_Q5_K", "JY_Q6_K"]

@@ -109,18 +109,9 @@ bool load_dir(Loaded& m, const std::string& dir, int max_seq, std::string& err) 
     m.vocab = md.desc.vocab_size;
     m.max_seq = md.max_seq;
 
-    // the device runs f32 and q8_0 weights
+    // every weight type the bind produces (f32, f16, q8_0, q4_K, q5_K, q6_K) runs on
+    // the device; the upload reports shapes it cannot run
     const jy_model_desc& d = md.desc;
-    auto supported = [](const jy_wmat& w) { return w.type == JY_F32 || w.type == JY_Q8_0; };
-    bool ok = supported(d.embed) && supported(d.lm_head);
-    for (int l = 0; ok && l < d.num_layers; l++)
-        for (const jy_wmat* w : {&d.layers[l].Wq, &d.layers[l].Wk, &d.layers[l].Wv, &d.layers[l].Wo,
-                                 &d.layers[l].W1, &d.layers[l].W2, &d.layers[l].W3})
-            ok = ok && supported(*w);
-    if (!ok) {
-        err = "model.bf: the device path runs f32 and q8_0 weights; this model has f16 or k-quant tensors";
-        return false;
-    }
     m.dev = jyhip_model_upload(&d, m.max_seq);
     if (!m.dev) {
         err = std::string("device upload failed: ") + jyhip_last_error();

@@ -956,6 +956,7 @@ void launch_attention(const AttnArgs& a, hipStream_t st) {
 }
 
 hipError_t matvec_init();
+hipError_t quant_init();
 
 hipError_t kernels_init() {
     int dev = 0, mx = 0;
@@ -965,6 +966,8 @@ hipError_t kernels_init() {
     g_att_lds_max = mx;
     e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_softmax_pv_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, mx - 2048);
+    if (e != hipSuccess) return e;
+    e = quant_init();
     if (e != hipSuccess) return e;
     return matvec_init();
 }

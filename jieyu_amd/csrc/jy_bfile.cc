@@ -166,9 +166,8 @@ const float* ModelDir::f32(const std::string& name) const {
     return e && e->dtype == BF_F32 ? static_cast<const float*>(data(e)) : nullptr;
 }
 
-// a 2-D weight as the forward pass sees it (load_weights.h:26-35): f32 and q8_0
-// carry their jy type; f16 and the k-quants bind (so shape checks and error
-// texts match the reference) with type -1-dtype, which the device upload rejects
+// a 2-D weight as the forward pass sees it (load_weights.h:26-35): f32, f16,
+// q8_0 and the k-quants, each with its jy type
 bool ModelDir::wmat(const std::string& name, jy_wmat& out) const {
     out = jy_wmat{nullptr, JY_F32};
     const BfEntry* e = find(name);
@@ -176,7 +175,10 @@ bool ModelDir::wmat(const std::string& name, jy_wmat& out) const {
     switch (e->dtype) {
         case BF_F32: out = jy_wmat{data(e), JY_F32}; return true;
         case BF_Q8_0: out = jy_wmat{data(e), JY_Q8_0}; return true;
-        case BF_F16: case BF_Q4K: case BF_Q5K: case BF_Q6K: out = jy_wmat{data(e), -1 - (int)e->dtype}; return true;
+        case BF_F16: out = jy_wmat{data(e), JY_F16}; return true;
+        case BF_Q4K: out = jy_wmat{data(e), JY_Q4_K}; return true;
+        case BF_Q5K: out = jy_wmat{data(e), JY_Q5_K}; return true;
+        case BF_Q6K: out = jy_wmat{data(e), JY_Q6_K}; return true;
         default: return false;  // bf16 / i8 / i32 are not weight types
     }
 }

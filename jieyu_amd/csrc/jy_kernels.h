@@ -23,6 +23,38 @@ struct Q8Dev {
     int U = 0;     // decode matvec register-buffer depth (chunks per buffer, two buffers)
 };
 
+// A Q4_K / Q5_K / Q6_K matrix of rows x cols (cols a multiple of 256), repacked so
+// that one 256-weight super-block of four rows is read by one wave, thread
+// t = ri*16 + g (row ri of the group, lane pair g) owning weights 32c + 2g and
+// 32c + 2g + 1 of the eight 32-weight steps c, as in the Q8_0 layout.  Chunk
+// = (row group, super-block), chunk index (R >> 2) * nsb + sb:
+//   nib : 512 B per chunk, 8 B per thread: nibble i = 2c + t is the low 4 bits
+//         of weight 32c + 2g + t
+//   hi  : Q5_K 2 B per thread (bit i = the fifth bit), Q6_K 4 B per thread
+//         (bits 2i, 2i+1 = the top two bits); absent for Q4_K
+//   hdr : 16 B per row: Q4_K / Q5_K the block's d, dmin and 12 scale bytes,
+//         Q6_K the 16 int8 scales
+//   d6  : Q6_K: the fp16 d of each row (4 per chunk)
+// Bytes per 256 weights stay 144 / 176 / 210; only the order changes.
+struct KQDev {
+    int type = 0;  // JY_Q4_K | JY_Q5_K | JY_Q6_K
+    int rows = 0, cols = 0, nsb = 0, groups = 0;
+    uint8_t* nib = nullptr;
+    uint8_t* hi = nullptr;
+    uint8_t* hdr = nullptr;
+    uint16_t* d6 = nullptr;
+};
+
+// One weight matrix of any bound type (jieyu's WMat, libs/date_libs/wmat.h:32-44):
+// JY_F32 / JY_F16 [in][out] dense, JY_Q8_0 in the Q8 layout, k-quants in KQDev.
+struct DevW {
+    int type = 0;
+    int in = 0, out = 0;
+    const void* dense = nullptr;
+    Q8Dev q8;
+    KQDev kq;
+};
+
 struct KVDev {
     int8_t* k = nullptr;
     int8_t* v = nullptr;
@@ -79,6 +111,9 @@ size_t matvec_lds_limit();
 // f32 [K][N] matvec, fma chain over k; EPI_SWIGLU takes B2 as the up matrix.
 void launch_matvec_f32(const float* B, const float* B2, int K, int N, const float* x, float* out,
                        const float* aux, Epi epi, hipStream_t st);
+// f16 [K][N] matvec (halves converted exactly), fma chain over k
+void launch_matvec_f16(const uint16_t* B, int K, int N, const float* x, float* out, const float* aux, Epi epi,
+                       hipStream_t st);
 // prefill GEMMs, C[m][N] (+ epilogue: EPI_STORE / EPI_BIAS / EPI_RESID)
 void launch_gemm_q8(const Q8Dev& W, int m, const float* A, float* C, const float* aux, Epi epi, hipStream_t st);
 void launch_gemm_f32(const float* B, int K, int N, int m, const float* A, float* C, const float* aux, Epi epi,
@@ -124,5 +159,24 @@ void launch_kv_export(int8_t* k_ref, float* ks_ref, int8_t* v_ref, float* vs_ref
 
 // argmax partials workspace for an EPI_ARGMAX matvec of `rows` rows
 int argmax_partials(int rows);
+
+// ---- weights of any type (jy_quant.hip)
+KQDev kq_shape(int type, int rows, int cols);
+size_t kq_bytes(const KQDev& w, int part);  // part 0 nib, 1 hi, 2 hdr, 3 d6
+// src: GGML blocks [rows][cols/256] (device copy) -> dst
+void launch_repack_kq(const uint8_t* src, const KQDev& dst, hipStream_t st);
+// y = W x for one token, in the reference's order for W's type (32-lane dot for
+// quantized rows, fma chain over k for dense [in][out]); EPI_STORE / EPI_BIAS /
+// EPI_RESID
+void launch_mv(const DevW& W, const float* x, float* out, Epi epi, const float* aux, hipStream_t st);
+// C[i][j] (row stride ldc) for m > 1 rows: the generic quantized path (product and
+// sum rounded apart, k ascending) or the dense fma chain
+void launch_gemm(const DevW& W, int m, const float* A, float* C, int ldc, const float* aux, Epi epi,
+                 hipStream_t st);
+// embedding rows of any type (wmat_row, libs/model_libs/wmat_kernel.h:18-29)
+void launch_embed_w(const DevW& E, int hidden, const int* ids_dev, int id_index0, const int* state, int seq,
+                    float* X, hipStream_t st);
+size_t mv_kq_lds_bytes(int cols);
+hipError_t quant_init();
 
 }  // namespace jy

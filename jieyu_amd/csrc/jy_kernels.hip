@@ -77,22 +77,43 @@ void launch_repack_q8(const uint8_t* src, int rows, int cols, const Q8Dev& dst, 
 
 // ---------------------------------------------------------------- embedding
 
-// embedding rows (libs/model_libs/wmat_kernel.h:18-29)
-// grid (rows, ceil(hidden / 256)): one element per thread, so every element's loads
-// are in flight at once
-__global__ void embed_kernel(Q8Dev W, const float* __restrict__ f32, int hidden, const int* __restrict__ ids,
-                             int id0, const int* __restrict__ state, float* __restrict__ X) {
+// embedding rows (libs/model_libs/wmat_kernel.h:18-29): f32 copied, f16 converted,
+// quantized rows dequantized (exact for Q8_0 and Q6_K, the one rounding of
+// dequant_block for Q4_K / Q5_K).  grid (rows, ceil(hidden / 256)): one element per
+// thread, so every element's loads are in flight at once
+__global__ void embed_kernel(DevW E, int hidden, const int* __restrict__ ids, int id0, const int* __restrict__ state,
+                             float* __restrict__ X) {
     const int i = blockIdx.x, c = blockIdx.y * blockDim.x + threadIdx.x;
     if (c >= hidden) return;
     const int id = state ? ids[state[0] - 1] : ids[id0 + i];
-    X[(size_t)i * hidden + c] = f32 ? f32[(size_t)id * hidden + c] : q8_elem(W, id, c);
+    const size_t e = (size_t)id * hidden + c;
+    float v;
+    switch (E.type) {
+        case JY_F32: v = static_cast<const float*>(E.dense)[e]; break;
+        case JY_F16: v = half_to_float(static_cast<const uint16_t*>(E.dense)[e]); break;
+        case JY_Q8_0: v = q8_elem(E.q8, id, c); break;
+        default: v = kq_elem(E.kq, id, c); break;
+    }
+    X[(size_t)i * hidden + c] = v;
+}
+
+void launch_embed_w(const DevW& E, int hidden, const int* ids_dev, int id_index0, const int* state, int seq,
+                    float* X, hipStream_t st) {
+    hipLaunchKernelGGL(embed_kernel, dim3(seq, (hidden + 255) / 256), dim3(256), 0, st, E, hidden, ids_dev,
+                       id_index0, state, X);
 }
 
 void launch_embed(const Q8Dev* q8, const float* f32, int hidden, const int* ids_dev, int id_index0,
                   const int* state, int seq, float* X, hipStream_t st) {
-    Q8Dev w = q8 ? *q8 : Q8Dev{};
-    hipLaunchKernelGGL(embed_kernel, dim3(seq, (hidden + 255) / 256), dim3(256), 0, st, w, f32, hidden, ids_dev,
-                       id_index0, state, X);
+    DevW e;
+    if (q8) {
+        e.type = JY_Q8_0;
+        e.q8 = *q8;
+    } else {
+        e.type = JY_F32;
+        e.dense = f32;
+    }
+    launch_embed_w(e, hidden, ids_dev, id_index0, state, seq, X, st);
 }
 
 // ---------------------------------------------------------------- RMSNorm
@@ -112,20 +133,25 @@ void launch_rmsnorm(const float* X, float* Y, const float* w, int n, int rows, h
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), (size_t)n * sizeof(float), st, X, Y, w, n);
 }
 
-// ---------------------------------------------------------------- f32 matvec (decode, [K][N] weights)
+// ---------------------------------------------------------------- dense matvec (decode, [K][N] weights)
 
-template <int EPI>
-__global__ __launch_bounds__(256) void matvec_f32_kernel(const float* __restrict__ B, const float* __restrict__ B2,
-                                                         int K, int N, const float* __restrict__ x,
-                                                         float* __restrict__ out, const float* __restrict__ aux) {
+// f32 or f16 weights (an f16 weight converts to float exactly): per output an fma
+// chain over k from 0 (libs/matmul_libs/x86/x86_classic.txt:2-16, matmul_f16.h:19-41)
+__device__ __forceinline__ float dense_w(const float* B, size_t i) { return B[i]; }
+__device__ __forceinline__ float dense_w(const uint16_t* B, size_t i) { return half_to_float(B[i]); }
+
+template <typename T, int EPI>
+__global__ __launch_bounds__(256) void matvec_dense_kernel(const T* __restrict__ B, const T* __restrict__ B2, int K,
+                                                           int N, const float* __restrict__ x,
+                                                           float* __restrict__ out, const float* __restrict__ aux) {
     const int j = blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= N) return;
     float acc = 0.0f, acc2 = 0.0f;
 #pragma unroll 8
     for (int p = 0; p < K; p++) {
         const float xv = x[p];
-        acc = __builtin_fmaf(xv, B[(size_t)p * N + j], acc);
-        if (EPI == EPI_SWIGLU) acc2 = __builtin_fmaf(xv, B2[(size_t)p * N + j], acc2);
+        acc = __builtin_fmaf(xv, dense_w(B, (size_t)p * N + j), acc);
+        if (EPI == EPI_SWIGLU) acc2 = __builtin_fmaf(xv, dense_w(B2, (size_t)p * N + j), acc2);
     }
     if (EPI == EPI_STORE) out[j] = acc;
     if (EPI == EPI_BIAS) out[j] = acc + aux[j];
@@ -133,51 +159,74 @@ __global__ __launch_bounds__(256) void matvec_f32_kernel(const float* __restrict
     if (EPI == EPI_SWIGLU) out[j] = silu_ref(acc) * acc2;
 }
 
-void launch_matvec_f32(const float* B, const float* B2, int K, int N, const float* x, float* out, const float* aux,
-                       Epi epi, hipStream_t st) {
+template <typename T>
+static void matvec_dense(const T* B, const T* B2, int K, int N, const float* x, float* out, const float* aux, Epi epi,
+                         hipStream_t st) {
     const dim3 grid((unsigned)((N + 255) / 256)), block(256);
     switch (epi) {
     case EPI_STORE:
-        hipLaunchKernelGGL(matvec_f32_kernel<EPI_STORE>, grid, block, 0, st, B, B2, K, N, x, out, aux);
+        hipLaunchKernelGGL((matvec_dense_kernel<T, EPI_STORE>), grid, block, 0, st, B, B2, K, N, x, out, aux);
         break;
     case EPI_BIAS:
-        hipLaunchKernelGGL(matvec_f32_kernel<EPI_BIAS>, grid, block, 0, st, B, B2, K, N, x, out, aux);
+        hipLaunchKernelGGL((matvec_dense_kernel<T, EPI_BIAS>), grid, block, 0, st, B, B2, K, N, x, out, aux);
         break;
     case EPI_RESID:
-        hipLaunchKernelGGL(matvec_f32_kernel<EPI_RESID>, grid, block, 0, st, B, B2, K, N, x, out, aux);
+        hipLaunchKernelGGL((matvec_dense_kernel<T, EPI_RESID>), grid, block, 0, st, B, B2, K, N, x, out, aux);
         break;
     case EPI_SWIGLU:
-        hipLaunchKernelGGL(matvec_f32_kernel<EPI_SWIGLU>, grid, block, 0, st, B, B2, K, N, x, out, aux);
+        hipLaunchKernelGGL((matvec_dense_kernel<T, EPI_SWIGLU>), grid, block, 0, st, B, B2, K, N, x, out, aux);
         break;
+    default: break;
     }
+}
+
+void launch_matvec_f32(const float* B, const float* B2, int K, int N, const float* x, float* out, const float* aux,
+                       Epi epi, hipStream_t st) {
+    matvec_dense<float>(B, B2, K, N, x, out, aux, epi, st);
+}
+
+void launch_matvec_f16(const uint16_t* B, int K, int N, const float* x, float* out, const float* aux, Epi epi,
+                       hipStream_t st) {
+    matvec_dense<uint16_t>(B, nullptr, K, N, x, out, aux, epi, st);
 }
 
 // ---------------------------------------------------------------- prefill GEMMs (m > 1)
 
 // 64 tokens x 64 output rows per workgroup, 4x4 outputs per thread, k in order.
-// Q8: acc = acc + x*w, rounded separately (the generic path of matmul_q).
-template <int EPI>
-__global__ __launch_bounds__(256) void gemm_q8_kernel(Q8Dev W, int m, const float* __restrict__ A,
-                                                      float* __restrict__ Cm, const float* __restrict__ aux) {
+// Quantized weights: acc = acc + x*w, rounded separately (the generic path of
+// matmul_q, libs/matmul_libs/matmul_q.h:145-161); the weight accessor dequantizes
+// exactly as dequant_block does.
+struct Q8Acc {
+    Q8Dev W;
+    __device__ float operator()(int R, int k) const { return q8_elem(W, R, k); }
+};
+struct KQAcc {
+    KQDev W;
+    __device__ float operator()(int R, int k) const { return kq_elem(W, R, k); }
+};
+
+template <class Acc, int EPI>
+__global__ __launch_bounds__(256) void gemm_quant_kernel(Acc W, int K, int N, int m, const float* __restrict__ A,
+                                                         float* __restrict__ Cm, int ldc,
+                                                         const float* __restrict__ aux) {
     __shared__ float xs[32][68];
     __shared__ float ws[32][68];
     const int t = threadIdx.x, ti = t & 15, tj = t >> 4;
     const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-    const int K = W.cols, N = W.rows;
     float acc[4][4];
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
         for (int b = 0; b < 4; b++) acc[a][b] = 0.0f;
     const int lt = t >> 2, lc = (t & 3) * 8;  // loader: token/row lt, k offset lc
-    for (int blk = 0; blk < W.nb; blk++) {
+    for (int k0 = 0; k0 < K; k0 += 32) {
         {
             const int tok = m0 + lt;
 #pragma unroll
-            for (int c = 0; c < 8; c++) xs[lc + c][lt] = tok < m ? A[(size_t)tok * K + blk * 32 + lc + c] : 0.0f;
+            for (int c = 0; c < 8; c++) xs[lc + c][lt] = tok < m ? A[(size_t)tok * K + k0 + lc + c] : 0.0f;
             const int R = n0 + lt;
 #pragma unroll
-            for (int c = 0; c < 8; c++) ws[lc + c][lt] = R < N ? q8_elem(W, R, blk * 32 + lc + c) : 0.0f;
+            for (int c = 0; c < 8; c++) ws[lc + c][lt] = R < N ? W(R, k0 + lc + c) : 0.0f;
         }
         __syncthreads();
 #pragma unroll 4
@@ -200,7 +249,7 @@ __global__ __launch_bounds__(256) void gemm_q8_kernel(Q8Dev W, int m, const floa
         for (int b = 0; b < 4; b++) {
             const int j = n0 + tj * 4 + b;
             if (j >= N) continue;
-            float* c = Cm + (size_t)i * N + j;
+            float* c = Cm + (size_t)i * ldc + j;
             if (EPI == EPI_STORE) *c = acc[a][b];
             if (EPI == EPI_BIAS) *c = acc[a][b] + aux[j];
             if (EPI == EPI_RESID) *c = *c + acc[a][b];
@@ -208,11 +257,11 @@ __global__ __launch_bounds__(256) void gemm_q8_kernel(Q8Dev W, int m, const floa
     }
 }
 
-// f32 [K][N]: C = fma(A[i][p], B[p][j], C) in order of p.
-template <int EPI>
-__global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ B, int K, int N, int m,
-                                                       const float* __restrict__ A, float* __restrict__ Cm,
-                                                       const float* __restrict__ aux) {
+// dense [K][N] (f32, or f16 converted exactly): C = fma(A[i][p], B[p][j], C) in order of p.
+template <typename T, int EPI>
+__global__ __launch_bounds__(256) void gemm_dense_kernel(const T* __restrict__ B, int K, int N, int m,
+                                                         const float* __restrict__ A, float* __restrict__ Cm, int ldc,
+                                                         const float* __restrict__ aux) {
     __shared__ float xs[32][68];
     __shared__ float ws[32][68];
     const int t = threadIdx.x, ti = t & 15, tj = t >> 4;
@@ -235,7 +284,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
         for (int c = 0; c < 8; c++) {
             const int e = t * 8 + c, kk = e >> 6, col = e & 63;
             const int k = k0 + kk, j = n0 + col;
-            ws[kk][col] = (k < K && j < N) ? B[(size_t)k * N + j] : 0.0f;
+            ws[kk][col] = (k < K && j < N) ? dense_w(B, (size_t)k * N + j) : 0.0f;
         }
         __syncthreads();
         const int kmax = K - k0 < 32 ? K - k0 : 32;
@@ -258,7 +307,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
         for (int b = 0; b < 4; b++) {
             const int j = n0 + tj * 4 + b;
             if (j >= N) continue;
-            float* c = Cm + (size_t)i * N + j;
+            float* c = Cm + (size_t)i * ldc + j;
             if (EPI == EPI_STORE) *c = acc[a][b];
             if (EPI == EPI_BIAS) *c = acc[a][b] + aux[j];
             if (EPI == EPI_RESID) *c = *c + acc[a][b];
@@ -266,19 +315,47 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
     }
 }
 
+template <class Acc>
+static void gemm_quant(const Acc& W, int K, int N, int m, const float* A, float* C, int ldc, const float* aux,
+                       Epi epi, hipStream_t st) {
+    const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((m + 63) / 64)), block(256);
+    if (epi == EPI_STORE)
+        hipLaunchKernelGGL((gemm_quant_kernel<Acc, EPI_STORE>), grid, block, 0, st, W, K, N, m, A, C, ldc, aux);
+    if (epi == EPI_BIAS)
+        hipLaunchKernelGGL((gemm_quant_kernel<Acc, EPI_BIAS>), grid, block, 0, st, W, K, N, m, A, C, ldc, aux);
+    if (epi == EPI_RESID)
+        hipLaunchKernelGGL((gemm_quant_kernel<Acc, EPI_RESID>), grid, block, 0, st, W, K, N, m, A, C, ldc, aux);
+}
+
+template <typename T>
+static void gemm_dense(const T* B, int K, int N, int m, const float* A, float* C, int ldc, const float* aux, Epi epi,
+                       hipStream_t st) {
+    const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((m + 63) / 64)), block(256);
+    if (epi == EPI_STORE)
+        hipLaunchKernelGGL((gemm_dense_kernel<T, EPI_STORE>), grid, block, 0, st, B, K, N, m, A, C, ldc, aux);
+    if (epi == EPI_BIAS)
+        hipLaunchKernelGGL((gemm_dense_kernel<T, EPI_BIAS>), grid, block, 0, st, B, K, N, m, A, C, ldc, aux);
+    if (epi == EPI_RESID)
+        hipLaunchKernelGGL((gemm_dense_kernel<T, EPI_RESID>), grid, block, 0, st, B, K, N, m, A, C, ldc, aux);
+}
+
 void launch_gemm_q8(const Q8Dev& W, int m, const float* A, float* C, const float* aux, Epi epi, hipStream_t st) {
-    const dim3 grid((unsigned)((W.rows + 63) / 64), (unsigned)((m + 63) / 64)), block(256);
-    if (epi == EPI_STORE) hipLaunchKernelGGL(gemm_q8_kernel<EPI_STORE>, grid, block, 0, st, W, m, A, C, aux);
-    if (epi == EPI_BIAS) hipLaunchKernelGGL(gemm_q8_kernel<EPI_BIAS>, grid, block, 0, st, W, m, A, C, aux);
-    if (epi == EPI_RESID) hipLaunchKernelGGL(gemm_q8_kernel<EPI_RESID>, grid, block, 0, st, W, m, A, C, aux);
+    gemm_quant(Q8Acc{W}, W.cols, W.rows, m, A, C, W.rows, aux, epi, st);
 }
 
 void launch_gemm_f32(const float* B, int K, int N, int m, const float* A, float* C, const float* aux, Epi epi,
                      hipStream_t st) {
-    const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((m + 63) / 64)), block(256);
-    if (epi == EPI_STORE) hipLaunchKernelGGL(gemm_f32_kernel<EPI_STORE>, grid, block, 0, st, B, K, N, m, A, C, aux);
-    if (epi == EPI_BIAS) hipLaunchKernelGGL(gemm_f32_kernel<EPI_BIAS>, grid, block, 0, st, B, K, N, m, A, C, aux);
-    if (epi == EPI_RESID) hipLaunchKernelGGL(gemm_f32_kernel<EPI_RESID>, grid, block, 0, st, B, K, N, m, A, C, aux);
+    gemm_dense<float>(B, K, N, m, A, C, N, aux, epi, st);
+}
+
+void launch_gemm(const DevW& W, int m, const float* A, float* C, int ldc, const float* aux, Epi epi,
+                 hipStream_t st) {
+    switch (W.type) {
+        case JY_F32: gemm_dense(static_cast<const float*>(W.dense), W.in, W.out, m, A, C, ldc, aux, epi, st); break;
+        case JY_F16: gemm_dense(static_cast<const uint16_t*>(W.dense), W.in, W.out, m, A, C, ldc, aux, epi, st); break;
+        case JY_Q8_0: gemm_quant(Q8Acc{W.q8}, W.in, W.out, m, A, C, ldc, aux, epi, st); break;
+        default: gemm_quant(KQAcc{W.kq}, W.in, W.out, m, A, C, ldc, aux, epi, st); break;
+    }
 }
 
 __global__ void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u, int interleaved, int m,

@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "jieyu_model.h"
 #include "jy_device.h"
 #include "jy_kernels.h"
 
@@ -33,6 +34,50 @@ __device__ __forceinline__ float q8_elem(const Q8Dev& W, int R, int k) {
     const size_t chunk = q8_chunk(W, R, ch);
     const int8_t q = (int8_t)W.qs[chunk * 1024 + (size_t)(ri * 16 + g) * 16 + j * 2 + c];
     return (float)q * half_to_float(W.d[chunk * 32 + ri * 8 + j]);
+}
+
+// ---- k-quants (KQDev in jy_kernels.h)
+//
+// Weight values (libs/matmul_libs/matmul_q.h:47-100, libs/file_libs/q4/q4.h:8-35):
+//   Q4_K / Q5_K: fma(q, d*sc, -(dmin*m)) with the 6-bit (sc, m) of 32-weight step c
+//                (get_scale_min_k4, matmul_q.h:22-33) and q the nibble (+16 * the
+//                fifth bit for Q5_K).  d*sc, dmin*m and q*(d*sc) are exact in float
+//                (<= 22 significant bits), so this is the reference's one rounding of
+//                d1*q - n1 whether or not it is fused.
+//   Q6_K:        (d * sc) * (q - 32) with the int8 scale of each 16 weights: exact.
+
+__device__ __forceinline__ void kq_scale_min(int j, const uint8_t* q, int& sc, int& mn) {
+    if (j < 4) {
+        sc = q[j] & 63;
+        mn = q[j + 4] & 63;
+    } else {
+        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+// weight (row R, column k) of a repacked k-quant matrix
+__device__ __forceinline__ float kq_elem(const KQDev& W, int R, int k) {
+    const int sb = k >> 8, e = k & 255, c = e >> 5, L = e & 31, g = L >> 1, i = 2 * c + (L & 1), ri = R & 3;
+    const size_t chunk = (size_t)(R >> 2) * W.nsb + sb;
+    const int t = ri * 16 + g;
+    const uint8_t nb = W.nib[(chunk * 64 + t) * 8 + (i >> 1)];
+    int q = (i & 1) ? (nb >> 4) : (nb & 15);
+    const uint8_t* h = W.hdr + chunk * 64 + ri * 16;
+    if (W.type == JY_Q6_K) {
+        const uint32_t hb = *reinterpret_cast<const uint32_t*>(W.hi + (chunk * 64 + t) * 4);
+        q = (q | (int)(((hb >> (2 * i)) & 3u) << 4)) - 32;
+        const int8_t sc = (int8_t)h[(c >> 2) * 8 + (g >> 3) + 2 * (c & 3)];
+        return (half_to_float(W.d6[chunk * 4 + ri]) * (float)sc) * (float)q;
+    }
+    if (W.type == JY_Q5_K) {
+        const uint16_t hb = *reinterpret_cast<const uint16_t*>(W.hi + (chunk * 64 + t) * 2);
+        q += ((hb >> i) & 1) << 4;
+    }
+    int sc, mn;
+    kq_scale_min(c, h + 4, sc, mn);
+    const float d = half_to_float((uint16_t)(h[0] | (h[1] << 8))), dmin = half_to_float((uint16_t)(h[2] | (h[3] << 8)));
+    return __builtin_fmaf((float)q, d * (float)sc, -(dmin * (float)mn));
 }
 
 // RMSNorm of one row already staged in LDS, by the whole workgroup, written to y

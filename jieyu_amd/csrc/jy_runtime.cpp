@@ -76,6 +76,10 @@ void init_device_kernels(int device) {
 
 }  // namespace
 
+// Models whose 2-D weights are not all Q8_0 or all f32 (f16, k-quants, or a mix,
+// one type per matrix as jieyu's WMat allows) run each matrix on its own kernel.
+constexpr int WT_MIXED = -1;
+
 struct DevLayer {
     float* rms1 = nullptr;
     float* rms2 = nullptr;
@@ -83,6 +87,7 @@ struct DevLayer {
     Q8Dev qkv, o, gu, down;                        // JY_Q8_0
     float *f_qkv = nullptr, *f_o = nullptr;        // JY_F32 [K][N]
     float *f_w1 = nullptr, *f_w3 = nullptr, *f_w2 = nullptr;
+    DevW w[7];                                     // WT_MIXED: Wq Wk Wv Wo W1 W2 W3
 };
 
 struct Workspace {
@@ -106,6 +111,7 @@ struct jyhip_model {
     Q8Dev embed_q8, lm_q8;
     bool lm_shares_embed = false;
     float *embed_f32 = nullptr, *lm_f32 = nullptr;
+    DevW embed_w, lm_w;  // WT_MIXED
     float* final_rms = nullptr;
     std::vector<DevLayer> layers;
     size_t weight_bytes = 0;
@@ -126,6 +132,13 @@ struct jyhip_kv {
     KVDev dev;
     int current_len = 0;
     int device = 0;
+};
+
+struct jyhip_wmat {
+    std::vector<DevW> copies;
+    std::vector<void*> owned;
+    int n = 0, k = 0;
+    hipStream_t stream = nullptr;
 };
 
 struct jyhip_q8mat {
@@ -196,7 +209,14 @@ void ensure_scores(jyhip_model* m, size_t n) {
     w.scores_n = n;
 }
 
-void check_desc(const jy_model_desc* d) {
+bool known_type(int t) {
+    return t == JY_F32 || t == JY_F16 || t == JY_Q8_0 || t == JY_Q4_K || t == JY_Q5_K || t == JY_Q6_K;
+}
+
+int block_of(int t) { return t == JY_Q8_0 ? 32 : (t == JY_Q4_K || t == JY_Q5_K || t == JY_Q6_K) ? 256 : 1; }
+
+// the path a model runs: JY_Q8_0 (every matrix Q8_0), JY_F32 (every matrix f32), else WT_MIXED
+int check_desc(const jy_model_desc* d) {
     if (!d) fail("model description is NULL");
     if (d->num_layers <= 0 || d->hidden <= 0 || d->num_heads <= 0 || d->num_kv_heads <= 0 || d->head_dim <= 0 ||
         d->intermediate <= 0 || d->vocab_size <= 0)
@@ -204,24 +224,126 @@ void check_desc(const jy_model_desc* d) {
     if (d->num_heads % d->num_kv_heads) fail("num_heads must be a multiple of num_kv_heads");
     if (d->head_dim % 4 || d->head_dim > 256) fail("head_dim must be a multiple of 4 and at most 256");
     if (!d->layers || !d->final_rms_weight) fail("layers / final norm missing");
-    const int t = d->layers[0].Wq.type;
-    if (t != JY_F32 && t != JY_Q8_0) fail("unsupported weight type");
+    const int H = d->hidden, qd = d->num_heads * d->head_dim, F = d->intermediate;
+    int first = d->layers[0].Wq.type;
+    bool same = true;
+    auto check = [&](const jy_wmat& x, int in, const char* what) {
+        if (!x.data) fail(std::string(what) + " missing");
+        if (!known_type(x.type)) fail(std::string("unsupported weight type for ") + what);
+        if (in % block_of(x.type))
+            fail(std::string(what) + ": input width " + std::to_string(in) + " is not a multiple of its block size");
+        same = same && x.type == first;
+    };
     for (int l = 0; l < d->num_layers; l++) {
         const jy_layer_weights& w = d->layers[l];
-        for (const jy_wmat* x : {&w.Wq, &w.Wk, &w.Wv, &w.Wo, &w.W1, &w.W2, &w.W3})
-            if (!x->data || x->type != t) fail("2-D weights must all be present and of one type");
+        check(w.Wq, H, "Wq");
+        check(w.Wk, H, "Wk");
+        check(w.Wv, H, "Wv");
+        check(w.Wo, qd, "Wo");
+        check(w.W1, H, "W1");
+        check(w.W2, F, "W2");
+        check(w.W3, H, "W3");
         if (!w.rms1_weight || !w.rms2_weight) fail("norm weights missing");
         if ((w.bq != nullptr) != (d->layers[0].bq != nullptr)) fail("q/k/v biases must be on every layer or none");
         if ((w.bq == nullptr) != (w.bk == nullptr) || (w.bq == nullptr) != (w.bv == nullptr))
             fail("q/k/v biases must come together");
     }
-    if (!d->embed.data || !d->lm_head.data) fail("embedding / lm_head missing");
-    if (d->embed.type != t || d->lm_head.type != t) fail("embedding / lm_head type differs from the layers");
-    if (t == JY_Q8_0 && (d->hidden % 32 || d->intermediate % 32 || (d->num_heads * d->head_dim) % 32))
-        fail("Q8_0 needs hidden, intermediate and q_dim divisible by 32");
+    check(d->embed, H, "embedding");
+    // a quantized lm_head is [vocab][hidden] (input width hidden); f32 / f16 is [hidden][vocab]
+    check(d->lm_head, H, "lm_head");
+    if (same && (first == JY_Q8_0 || first == JY_F32)) {
+        if (first == JY_Q8_0 && (H % 32 || F % 32 || qd % 32))
+            fail("Q8_0 needs hidden, intermediate and q_dim divisible by 32");
+        return first;
+    }
+    return WT_MIXED;
 }
 
-void upload(jyhip_model* m, const jy_model_desc* d, int max_seq) {
+size_t wbytes(int type, size_t out, size_t in) {
+    switch (type) {
+        case JY_F32: return out * in * 4;
+        case JY_F16: return out * in * 2;
+        case JY_Q8_0: return out * (in / 32) * 34;
+        case JY_Q4_K: return out * (in / 256) * 144;
+        case JY_Q5_K: return out * (in / 256) * 176;
+        default: return out * (in / 256) * 210;
+    }
+}
+
+// one matrix of out x in weights (quantized [out][in]; f32 / f16 [in][out]) into HBM
+DevW put_w(jyhip_model* m, uint8_t* staging, const jy_wmat& src, int out, int in) {
+    DevW w;
+    w.type = src.type;
+    w.in = in;
+    w.out = out;
+    const size_t nb = wbytes(src.type, out, in);
+    if (src.type == JY_F32 || src.type == JY_F16) {
+        void* p = own(m, dalloc<uint8_t>(nb, false));
+        CK(hipMemcpy(p, src.data, nb, hipMemcpyHostToDevice));
+        w.dense = p;
+    } else if (src.type == JY_Q8_0) {
+        w.q8 = q8_alloc(m, out, in);
+        q8_put(m, staging, src.data, out, in, w.q8, 0, 1);
+    } else {
+        w.kq = kq_shape(src.type, out, in);
+        w.kq.nib = (uint8_t*)own(m, dalloc<uint8_t>(kq_bytes(w.kq, 0)));
+        if (kq_bytes(w.kq, 1)) w.kq.hi = (uint8_t*)own(m, dalloc<uint8_t>(kq_bytes(w.kq, 1)));
+        w.kq.hdr = (uint8_t*)own(m, dalloc<uint8_t>(kq_bytes(w.kq, 2)));
+        if (kq_bytes(w.kq, 3)) w.kq.d6 = (uint16_t*)own(m, dalloc<uint8_t>(kq_bytes(w.kq, 3)));
+        CK(hipMemcpy(staging, src.data, nb, hipMemcpyHostToDevice));
+        launch_repack_kq(staging, w.kq, m->stream);
+        CK(hipGetLastError());
+        CK(hipStreamSynchronize(m->stream));
+    }
+    return w;
+}
+
+void upload_mixed(jyhip_model* m, const jy_model_desc* d) {
+    const int H = m->H, qd = m->qd, kvd = m->kvd, F = m->F, V = m->V;
+    // the x vector of a k-quant decode matvec is staged in LDS
+    for (int in : {H, qd, F})
+        if (mv_kq_lds_bytes(in) > matvec_lds_limit() || matvec_lds_bytes(in, false) > matvec_lds_limit())
+            fail("hidden / q_dim / intermediate too large for the decode matvec's LDS staging");
+    size_t stage = std::max(wbytes(d->embed.type, V, H), wbytes(d->lm_head.type, V, H));
+    for (int l = 0; l < m->L; l++) {
+        const jy_layer_weights& w = d->layers[l];
+        stage = std::max({stage, wbytes(w.Wq.type, qd, H), wbytes(w.Wk.type, kvd, H), wbytes(w.Wv.type, kvd, H),
+                          wbytes(w.Wo.type, H, qd), wbytes(w.W1.type, F, H), wbytes(w.W2.type, H, F),
+                          wbytes(w.W3.type, F, H)});
+    }
+    uint8_t* staging = dalloc<uint8_t>(stage, false);
+    size_t total = 0;
+    try {
+        m->embed_w = put_w(m, staging, d->embed, V, H);
+        total += wbytes(d->embed.type, V, H);
+        const bool dense_lm = d->lm_head.type == JY_F32 || d->lm_head.type == JY_F16;
+        if (d->lm_head.data == d->embed.data && d->lm_head.type == d->embed.type && !dense_lm) {
+            m->lm_w = m->embed_w;  // tied (load_weights.h:143-144)
+        } else {
+            m->lm_w = put_w(m, staging, d->lm_head, V, H);
+            total += wbytes(d->lm_head.type, V, H);
+        }
+        for (int l = 0; l < m->L; l++) {
+            const jy_layer_weights& w = d->layers[l];
+            DevLayer& D = m->layers[l];
+            D.rms1 = f32_put(m, w.rms1_weight, H);
+            D.rms2 = f32_put(m, w.rms2_weight, H);
+            const jy_wmat* src[7] = {&w.Wq, &w.Wk, &w.Wv, &w.Wo, &w.W1, &w.W2, &w.W3};
+            const int outs[7] = {qd, kvd, kvd, H, F, H, F}, ins[7] = {H, H, H, qd, H, F, H};
+            for (int i = 0; i < 7; i++) {
+                D.w[i] = put_w(m, staging, *src[i], outs[i], ins[i]);
+                total += wbytes(src[i]->type, outs[i], ins[i]);
+            }
+        }
+    } catch (...) {
+        dfree(staging);
+        throw;
+    }
+    dfree(staging);
+    m->weight_bytes = total;
+}
+
+void upload(jyhip_model* m, const jy_model_desc* d, int max_seq, int wtype) {
     m->L = d->num_layers;
     m->H = d->hidden;
     m->nh = d->num_heads;
@@ -231,7 +353,7 @@ void upload(jyhip_model* m, const jy_model_desc* d, int max_seq) {
     m->V = d->vocab_size;
     m->qd = m->nh * m->hd;
     m->kvd = m->nkv * m->hd;
-    m->wtype = d->layers[0].Wq.type;
+    m->wtype = wtype;
     m->bias = d->layers[0].bq != nullptr;
     m->max_seq = max_seq;
     m->theta = d->rope_theta;
@@ -245,7 +367,9 @@ void upload(jyhip_model* m, const jy_model_desc* d, int max_seq) {
 
     const int H = m->H, qd = m->qd, kvd = m->kvd, F = m->F, V = m->V;
     m->layers.resize(m->L);
-    if (m->wtype == JY_Q8_0) {
+    if (m->wtype == WT_MIXED) {
+        upload_mixed(m, d);
+    } else if (m->wtype == JY_Q8_0) {
         // the decode matvec stages its whole input vector in LDS (with the norm weights
         // where it normalises): hidden for QKV / gate-up / lm_head, q_dim for O, F for down
         if (matvec_lds_bytes(H, true) > matvec_lds_limit() || matvec_lds_bytes(qd, false) > matvec_lds_limit() ||
@@ -388,6 +512,26 @@ void run_decode_layers(jyhip_model* m, const KVDev& kv, const int* state, int po
             launch_matvec_q8(D.o, w.att, nullptr, w.X, EPI_RESID, none, st);
             launch_matvec_q8(D.gu, w.X, D.rms2, w.h, EPI_SWIGLU, none, st);
             launch_matvec_q8(D.down, w.h, nullptr, w.X, EPI_RESID, none, st);
+        } else if (m->wtype == WT_MIXED) {
+            // one kernel per matrix, each in its own type's order
+            const int qd = m->qd, kvd = m->kvd;
+            const Epi qe = D.bqkv ? EPI_BIAS : EPI_STORE;
+            launch_rmsnorm(w.X, w.xn, D.rms1, H, 1, st);
+            launch_mv(D.w[0], w.xn, w.qkv, qe, D.bqkv, st);
+            launch_mv(D.w[1], w.xn, w.qkv + qd, qe, D.bqkv ? D.bqkv + qd : nullptr, st);
+            launch_mv(D.w[2], w.xn, w.qkv + qd + kvd, qe, D.bqkv ? D.bqkv + qd + kvd : nullptr, st);
+            launch_rope_pack(w.qkv, 1, pos0, state, m->nh, m->nkv, m->hd, m->cos_t, m->sin_t, kv, l, w.q8, w.qsc, st);
+            at.fused = false;
+            at.q8 = w.q8;
+            at.qsc = w.qsc;
+            at.row0 = 0;
+            launch_attention(at, st);
+            launch_mv(D.w[3], w.att, w.X, EPI_RESID, nullptr, st);
+            launch_rmsnorm(w.X, w.xn, D.rms2, H, 1, st);
+            launch_mv(D.w[4], w.xn, w.g, EPI_STORE, nullptr, st);
+            launch_mv(D.w[6], w.xn, w.u, EPI_STORE, nullptr, st);
+            launch_silu_mul(w.g, w.u, 0, 1, F, w.h, st);
+            launch_mv(D.w[5], w.h, w.X, EPI_RESID, nullptr, st);
         } else {
             launch_rmsnorm(w.X, w.xn, D.rms1, H, 1, st);
             launch_matvec_f32(D.f_qkv, nullptr, H, NQ, w.xn, w.qkv, D.bqkv, D.bqkv ? EPI_BIAS : EPI_STORE, st);
@@ -416,7 +560,7 @@ void run_prefill_layers(jyhip_model* m, const KVDev& kv, int seq, int start_pos,
                         int max_keys) {
     Workspace& w = m->ws;
     hipStream_t st = m->stream;
-    const bool q8 = m->wtype == JY_Q8_0;
+    const bool q8 = m->wtype == JY_Q8_0, mixed = m->wtype == WT_MIXED;
     const int H = m->H, NQ = m->qd + 2 * m->kvd, F = m->F;
     // attention rows per launch keep the HBM score scratch within its allocation
     const size_t per_row = (size_t)m->nh * max_keys;
@@ -437,10 +581,16 @@ void run_prefill_layers(jyhip_model* m, const KVDev& kv, int seq, int start_pos,
         const DevLayer& D = m->layers[l];
         launch_rmsnorm(w.X, w.xn, D.rms1, H, seq, st);
         const Epi qkv_epi = D.bqkv ? EPI_BIAS : EPI_STORE;
-        if (q8)
+        if (mixed) {
+            const int qd = m->qd, kvd = m->kvd;
+            launch_gemm(D.w[0], seq, w.xn, w.qkv, NQ, D.bqkv, qkv_epi, st);
+            launch_gemm(D.w[1], seq, w.xn, w.qkv + qd, NQ, D.bqkv ? D.bqkv + qd : nullptr, qkv_epi, st);
+            launch_gemm(D.w[2], seq, w.xn, w.qkv + qd + kvd, NQ, D.bqkv ? D.bqkv + qd + kvd : nullptr, qkv_epi, st);
+        } else if (q8) {
             launch_gemm_q8(D.qkv, seq, w.xn, w.qkv, D.bqkv, qkv_epi, st);
-        else
+        } else {
             launch_gemm_f32(D.f_qkv, H, NQ, seq, w.xn, w.qkv, D.bqkv, qkv_epi, st);
+        }
         launch_rope_pack(w.qkv, seq, start_pos, nullptr, m->nh, m->nkv, m->hd, m->cos_t, m->sin_t, kv, l, w.q8,
                          w.qsc, st);
         at.layer = l;
@@ -449,12 +599,19 @@ void run_prefill_layers(jyhip_model* m, const KVDev& kv, int seq, int start_pos,
             at.nrows = std::min(chunk, seq - r0);
             launch_attention(at, st);
         }
-        if (q8)
+        if (mixed)
+            launch_gemm(D.w[3], seq, w.att, w.X, H, nullptr, EPI_RESID, st);
+        else if (q8)
             launch_gemm_q8(D.o, seq, w.att, w.X, nullptr, EPI_RESID, st);
         else
             launch_gemm_f32(D.f_o, m->qd, H, seq, w.att, w.X, nullptr, EPI_RESID, st);
         launch_rmsnorm(w.X, w.xn, D.rms2, H, seq, st);
-        if (q8) {
+        if (mixed) {
+            launch_gemm(D.w[4], seq, w.xn, w.g, F, nullptr, EPI_STORE, st);
+            launch_gemm(D.w[6], seq, w.xn, w.u, F, nullptr, EPI_STORE, st);
+            launch_silu_mul(w.g, w.u, 0, seq, F, w.h, st);
+            launch_gemm(D.w[5], seq, w.h, w.X, H, nullptr, EPI_RESID, st);
+        } else if (q8) {
             launch_gemm_q8(D.gu, seq, w.xn, w.g, nullptr, EPI_STORE, st);
             launch_silu_mul(w.g, nullptr, 1, seq, F, w.h, st);
             launch_gemm_q8(D.down, seq, w.h, w.X, nullptr, EPI_RESID, st);
@@ -496,6 +653,9 @@ void final_and_head(jyhip_model* m, const float* xlast, bool argmax, int neos) {
             a.part_idx = m->part_idx;
         }
         launch_matvec_q8(m->lm_q8, xlast, m->final_rms, m->logits, argmax ? EPI_ARGMAX : EPI_STORE, a, m->stream);
+    } else if (m->wtype == WT_MIXED) {
+        launch_rmsnorm(xlast, m->ws.xn, m->final_rms, m->H, 1, m->stream);
+        launch_mv(m->lm_w, m->ws.xn, m->logits, EPI_STORE, nullptr, m->stream);
     } else {
         launch_rmsnorm(xlast, m->ws.xn, m->final_rms, m->H, 1, m->stream);
         launch_matvec_f32(m->lm_f32, nullptr, m->H, m->V, m->ws.xn, m->logits, nullptr, EPI_STORE, m->stream);
@@ -510,11 +670,19 @@ void head_and_pick(jyhip_model* m, const float* xlast, bool greedy, float rp, in
     if (greedy && !fused) launch_argmax(m->logits, m->V, m->ids, m->state, m->eos, neos, rp, prompt_len, m->stream);
 }
 
+// embedding rows of ids[id0 + i] (or ids[state[0]-1]) into X
+void embed_rows(jyhip_model* m, int id0, const int* state, int seq, float* X) {
+    if (m->wtype == WT_MIXED)
+        launch_embed_w(m->embed_w, m->H, m->ids, id0, state, seq, X, m->stream);
+    else
+        launch_embed(m->wtype == JY_Q8_0 ? &m->embed_q8 : nullptr, m->embed_f32, m->H, m->ids, id0, state, seq, X,
+                     m->stream);
+}
+
 // one decode step: embed ids[len-1], layers, final norm, lm_head, greedy pick
 void decode_step(jyhip_model* m, const KVDev& kv, int max_keys, bool greedy, float rp, int prompt_len, int neos) {
     Workspace& w = m->ws;
-    launch_embed(m->wtype == JY_Q8_0 ? &m->embed_q8 : nullptr, m->embed_f32, m->H, m->ids, 0, m->state, 1, w.X,
-                 m->stream);
+    embed_rows(m, 0, m->state, 1, w.X);
     run_decode_layers(m, kv, m->state, 0, nullptr, max_keys);
     head_and_pick(m, w.X, greedy, rp, prompt_len, neos);
 }
@@ -671,8 +839,7 @@ struct Session {
         // step 0: the prompt (generate.h:43-49 with seq = prompt_len)
         CK(hipEventRecord(ev[0], st));
         Workspace& w = m->ws;
-        launch_embed(m->wtype == JY_Q8_0 ? &m->embed_q8 : nullptr, m->embed_f32, m->H, m->ids, 0, nullptr, plen, w.X,
-                     st);
+        embed_rows(m, 0, nullptr, plen, w.X);
         run_layers(m, kv->dev, plen, 0, nullptr, nullptr, max_keys);
         head_and_pick(m, w.X + (size_t)(plen - 1) * m->H, greedy, rp, plen, neos);
         CK(hipEventRecord(ev[1], st));
@@ -820,14 +987,14 @@ JYHIP_API int jyhip_set_device(int device) {
 
 JYHIP_API jyhip_model* jyhip_model_upload(const jy_model_desc* d, int max_seq) {
     return guarded([&]() -> jyhip_model* {
-        check_desc(d);
+        const int wtype = check_desc(d);
         if (max_seq <= 0) fail("max_seq must be positive");
         jyhip_model* m = new jyhip_model();
         try {
             CK(hipGetDevice(&m->device));
             init_device_kernels(m->device);
             const auto t0 = std::chrono::steady_clock::now();
-            upload(m, d, max_seq);
+            upload(m, d, max_seq, wtype);
             CK(hipDeviceSynchronize());
             m->upload_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         } catch (...) {
@@ -1126,6 +1293,116 @@ JYHIP_API int jyhip_q8_matvec_time(jyhip_q8mat* q, const float* x, int variant, 
         (void)hipEventDestroy(b);
         CK(hipGetLastError());
         *avg_us = 1000.0 * ms / iters;
+        return 0;
+    }, -1);
+}
+
+JYHIP_API jyhip_wmat* jyhip_wmat_upload(const jy_wmat* w, int n, int k, int copies) {
+    return guarded([&]() -> jyhip_wmat* {
+        if (!w || !w->data || n <= 0 || k <= 0) fail("bad weight matrix");
+        if (!known_type(w->type)) fail("unsupported weight type");
+        if (k % block_of(w->type)) fail("k is not a multiple of the type's block size");
+        if ((w->type == JY_Q8_0 && matvec_lds_bytes(k, false) > matvec_lds_limit()) ||
+            (block_of(w->type) == 256 && mv_kq_lds_bytes(k) > matvec_lds_limit()))
+            fail("k too large for the decode matvec's LDS staging");
+        if (copies <= 0) copies = 1;
+        jyhip_wmat* h = new jyhip_wmat();
+        h->n = n;
+        h->k = k;
+        jyhip_model holder;  // borrows put_w's bookkeeping
+        try {
+            int dev = 0;
+            CK(hipGetDevice(&dev));
+            init_device_kernels(dev);
+            CK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
+            holder.stream = h->stream;
+            uint8_t* staging = dalloc<uint8_t>(wbytes(w->type, n, k), false);
+            try {
+                for (int c = 0; c < copies; c++) h->copies.push_back(put_w(&holder, staging, *w, n, k));
+            } catch (...) {
+                dfree(staging);
+                throw;
+            }
+            dfree(staging);
+        } catch (...) {
+            for (void* p : holder.owned) dfree(p);
+            if (h->stream) (void)hipStreamDestroy(h->stream);
+            delete h;
+            throw;
+        }
+        h->owned.swap(holder.owned);
+        holder.stream = nullptr;
+        return h;
+    }, nullptr);
+}
+
+JYHIP_API void jyhip_wmat_free(jyhip_wmat* h) {
+    if (!h) return;
+    (void)hipStreamSynchronize(h->stream);
+    for (void* p : h->owned) dfree(p);
+    (void)hipStreamDestroy(h->stream);
+    delete h;
+}
+
+JYHIP_API int jyhip_wmat_matmul(jyhip_wmat* h, int m, const float* A, float* Cout) {
+    return guarded([&]() {
+        if (!h || !A || !Cout || m <= 0) fail("bad argument");
+        const DevW& w = h->copies[0];
+        float* a = dalloc<float>((size_t)m * h->k, false);
+        float* c = dalloc<float>((size_t)m * h->n);
+        try {
+            CK(hipMemcpyAsync(a, A, sizeof(float) * (size_t)m * h->k, hipMemcpyHostToDevice, h->stream));
+            if (m == 1)
+                launch_mv(w, a, c, EPI_STORE, nullptr, h->stream);
+            else
+                launch_gemm(w, m, a, c, h->n, nullptr, EPI_STORE, h->stream);
+            CK(hipGetLastError());
+            CK(hipMemcpyAsync(Cout, c, sizeof(float) * (size_t)m * h->n, hipMemcpyDeviceToHost, h->stream));
+            CK(hipStreamSynchronize(h->stream));
+        } catch (...) {
+            (void)hipStreamSynchronize(h->stream);
+            dfree(a);
+            dfree(c);
+            throw;
+        }
+        dfree(a);
+        dfree(c);
+        return 0;
+    }, -1);
+}
+
+JYHIP_API int jyhip_wmat_time(jyhip_wmat* h, const float* x, int iters, double* avg_us) {
+    return guarded([&]() {
+        if (!h || !x || !avg_us || iters <= 0) fail("bad argument");
+        float* xd = dalloc<float>(h->k, false);
+        float* yd = dalloc<float>(h->n);
+        hipEvent_t a = nullptr, b = nullptr;
+        try {
+            CK(hipMemcpyAsync(xd, x, sizeof(float) * h->k, hipMemcpyHostToDevice, h->stream));
+            for (const DevW& w : h->copies) launch_mv(w, xd, yd, EPI_STORE, nullptr, h->stream);  // warm
+            CK(hipEventCreate(&a));
+            CK(hipEventCreate(&b));
+            CK(hipEventRecord(a, h->stream));
+            for (int i = 0; i < iters; i++)
+                launch_mv(h->copies[(size_t)i % h->copies.size()], xd, yd, EPI_STORE, nullptr, h->stream);
+            CK(hipEventRecord(b, h->stream));
+            CK(hipEventSynchronize(b));
+            float ms = 0.0f;
+            CK(hipEventElapsedTime(&ms, a, b));
+            CK(hipGetLastError());
+            *avg_us = 1000.0 * ms / iters;
+        } catch (...) {
+            (void)hipStreamSynchronize(h->stream);
+            if (a) (void)hipEventDestroy(a);
+            if (b) (void)hipEventDestroy(b);
+            dfree(xd);
+            dfree(yd);
+            throw;
+        }
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        dfree(xd);
+        dfree(yd);
         return 0;
     }, -1);
 }
