@@ -46,10 +46,21 @@ JYTEXT_API int jytext_info_str(const char* path, const char* key, const char* fa
 
 /* install_model + bind_model of a model directory, host only.  hp receives
  * {layers, hidden, heads, kv_heads, head_dim, intermediate, vocab, add_bos,
- *  qkv_bias, embed_type, lm_head_type, layer_type} (types: 0 f32, 3 q8_0,
- * -1-dtype for bfile types the device does not run).  -1 and the reference's
- * error text on failure. */
+ *  qkv_bias, embed_type, lm_head_type, layer_type} (jieyu_model.h types: 0 f32,
+ * 1 f16, 3 q8_0, 5 q4_K, 6 q5_K, 7 q6_K).  -1 and the reference's error text on
+ * failure. */
 JYTEXT_API int jytext_model_bind(const char* dir, int max_seq, int* hp);
+
+/* GGUF (v2 / v3) file -> model directory: model.bf, model_info.json, vocab.json,
+ * merges.txt, as ggufc::convert writes them (libs/gguf_libs/gguf_convert.h:260-421).
+ * out_dtype: model.bf dtype of the non-quantized 2-D weights (0 f32, 1 f16, 2 bf16);
+ * quant != 0 keeps Q4_K / Q5_K / Q6_K / Q8_0 blocks (q / k rows permuted), else
+ * every tensor is dequantized.  info (optional, 16 values) receives {hidden, layers,
+ * heads, kv_heads, head_dim, intermediate, vocab, rope_theta, max_position,
+ * tensor_count, transposed, permuted, quant, tied_lm_head, eos_id, file_size}.
+ * 0, or -1 and the reference's error text. */
+JYTEXT_API int jytext_gguf_convert(const char* src, const char* out_dir, int out_dtype, int quant, int verbose,
+                                   long long* info);
 
 #ifdef __cplusplus
 }

@@ -30,7 +30,8 @@ def abi():
               ("jytext_tokenizer_add_special", I, [P, S]),
               ("jytext_tokenizer_encode", I, [P, S, C.c_size_t, P, I]),
               ("jytext_tokenizer_decode", I, [P, P, I, P, I]), ("jytext_info_int", I, [S, S, I]),
-              ("jytext_info_str", I, [S, S, S, P, I]), ("jytext_model_bind", I, [S, I, P]))
+              ("jytext_info_str", I, [S, S, S, P, I]), ("jytext_model_bind", I, [S, I, P]),
+              ("jytext_gguf_convert", I, [S, S, I, I, I, P]))
     for name, res, args in protos:
         fn = getattr(L, name)
         fn.restype, fn.argtypes = res, args
@@ -183,3 +184,22 @@ def model_bind(dir, max_seq=16):
     keys = ("layers", "hidden", "heads", "kv_heads", "head_dim", "intermediate", "vocab", "add_bos", "qkv_bias",
             "embed_type", "lm_head_type", "layer_type")
     return dict(zip(keys, list(hp)))
+
+
+GGUF_INFO = ("hidden", "layers", "heads", "kv_heads", "head_dim", "intermediate", "vocab", "rope_theta",
+             "max_position", "tensor_count", "transposed", "permuted", "quant", "tied_lm_head", "eos_id", "file_size")
+
+
+def gguf_convert(src, out_dir, out_dtype="f32", quant=True, verbose=False):
+    """GGUF file -> model directory (ggufc::convert, libs/gguf_libs/gguf_convert.h:260-421):
+    model.bf, model_info.json, vocab.json, merges.txt.  out_dtype ("f32", "f16", "bf16"
+    or the model.bf dtype code) applies to the non-quantized 2-D weights; quant keeps
+    Q4_K / Q5_K / Q6_K / Q8_0 blocks.  Returns the converter's report, or raises with
+    jieyu's error text."""
+    L = abi()
+    code = {"f32": 0, "f16": 1, "bf16": 2}.get(out_dtype, out_dtype)
+    info = (C.c_longlong * 16)()
+    if L.jytext_gguf_convert(_b(src), _b(out_dir), int(code), 1 if quant else 0, 1 if verbose else 0, info) != 0:
+        raise JieyuError(L.jytext_last_error().decode("utf-8", "replace"))
+    return dict(zip(GGUF_INFO, list(info)))
+

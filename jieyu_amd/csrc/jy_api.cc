@@ -460,6 +460,29 @@ JYTEXT_API int jytext_info_str(const char* path, const char* key, const char* fa
     return copy_out(v, out, cap);
 }
 
+JYTEXT_API int jytext_gguf_convert(const char* src, const char* out_dir, int out_dtype, int quant, int verbose,
+                                   long long* info) {
+    g_text_error.clear();
+    if (!src || !out_dir) {
+        g_text_error = "src / out_dir is NULL";
+        return -1;
+    }
+    try {
+        const jytext::GgufResult r = jytext::gguf_convert(src, out_dir, (uint8_t)out_dtype, quant != 0, verbose != 0);
+        if (info) {
+            const long long v[16] = {(long long)r.hidden, (long long)r.layers, r.num_heads, r.num_kv_heads, r.head_dim,
+                                     (long long)r.intermediate, (long long)r.vocab, r.rope_theta, r.max_position,
+                                     (long long)r.tensor_count, r.transposed, r.permuted, r.quant,
+                                     r.tied_lm_head ? 1 : 0, r.eos_id, (long long)r.file_size};
+            memcpy(info, v, sizeof v);
+        }
+    } catch (const std::exception& e) {
+        g_text_error = e.what();
+        return -1;
+    }
+    return 0;
+}
+
 JYTEXT_API int jytext_model_bind(const char* dir, int max_seq, int* hp) {
     g_text_error.clear();
     if (!dir) {

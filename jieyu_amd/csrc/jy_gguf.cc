@@ -1,0 +1,1027 @@
+// jy_gguf.cc — GGUF (v2 / v3) reader and the GGUF -> model-directory converter
+// (libs/gguf_libs/gguf.h, libs/gguf_libs/gguf_convert.h): the other on-disk format
+// jieyu's decode path is fed from.  Host C++17, no device code.
+//
+// The converter writes what jieyu's does, byte for byte:
+//   model.bf          bfile v2 (libs/model_libs/bfile.h:276-341): every GGUF tensor
+//                     with a Hugging Face name; Q4_K / Q5_K / Q6_K / Q8_0 2-D blocks
+//                     copied row by row (quant = true), everything else dequantized
+//                     and written as out_dtype, 2-D weights transposed to [in][out]
+//                     (the embedding stays [vocab][hidden]); q / k rows permuted from
+//                     GGUF's interleaved RoPE halves back to adjacent pairs (perm_row)
+//   model_info.json   the header's hyper-parameters and tokenizer markers, merged into
+//                     an existing file the way json_file::WriteJsonKey does
+//   vocab.json, merges.txt  from tokenizer.ggml.tokens / .merges
+// Errors are std::runtime_error with the reference's texts.
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <filesystem>
+#include <fstream>
+#include <stdexcept>
+
+#include "jy_text.h"
+
+namespace jytext {
+
+namespace {
+
+namespace fs = std::filesystem;
+using std::runtime_error;
+using std::string;
+using std::vector;
+
+// ---------------------------------------------------------------- GGUF types (GGML's codes)
+
+enum : uint32_t {
+    G_F32 = 0, G_F16 = 1, G_Q4_0 = 2, G_Q4_1 = 3, G_Q5_0 = 6, G_Q5_1 = 7, G_Q8_0 = 8, G_Q8_1 = 9, G_Q2_K = 10,
+    G_Q3_K = 11, G_Q4_K = 12, G_Q5_K = 13, G_Q6_K = 14, G_Q8_K = 15, G_IQ4_NL = 20, G_IQ4_XS = 23, G_I8 = 24,
+    G_I16 = 25, G_I32 = 26, G_I64 = 27, G_F64 = 28, G_BF16 = 30
+};
+enum : uint32_t { M_U8 = 0, M_I8, M_U16, M_I16, M_U32, M_I32, M_F32, M_BOOL, M_STR, M_ARR, M_U64, M_I64, M_F64 };
+
+const char* gtype_name(uint32_t t) {
+    switch (t) {
+        case G_F32: return "f32";
+        case G_F16: return "f16";
+        case G_BF16: return "bf16";
+        case G_Q4_0: return "q4_0";
+        case G_Q4_1: return "q4_1";
+        case G_Q5_0: return "q5_0";
+        case G_Q5_1: return "q5_1";
+        case G_Q8_0: return "q8_0";
+        case G_Q8_1: return "q8_1";
+        case G_Q2_K: return "q2_K";
+        case G_Q3_K: return "q3_K";
+        case G_Q4_K: return "q4_K";
+        case G_Q5_K: return "q5_K";
+        case G_Q6_K: return "q6_K";
+        case G_IQ4_NL: return "iq4_nl";
+        case G_IQ4_XS: return "iq4_xs";
+        case G_I8: return "i8";
+        case G_I16: return "i16";
+        case G_I32: return "i32";
+        case G_I64: return "i64";
+        case G_F64: return "f64";
+        default: return "?";
+    }
+}
+
+// (elements, bytes) per block; (0, 0) for a type GGUF files may name but jieyu does not know
+std::pair<size_t, size_t> gblock(uint32_t t) {
+    switch (t) {
+        case G_F32: case G_I32: return {1, 4};
+        case G_F16: case G_BF16: case G_I16: return {1, 2};
+        case G_F64: case G_I64: return {1, 8};
+        case G_I8: return {1, 1};
+        case G_Q4_0: case G_IQ4_NL: return {32, 18};
+        case G_Q4_1: return {32, 20};
+        case G_Q5_0: return {32, 22};
+        case G_Q5_1: return {32, 24};
+        case G_Q8_0: return {32, 34};
+        case G_Q8_1: return {32, 36};
+        case G_Q2_K: return {256, 84};
+        case G_Q3_K: return {256, 110};
+        case G_Q4_K: return {256, 144};
+        case G_Q5_K: return {256, 176};
+        case G_Q6_K: return {256, 210};
+        case G_Q8_K: return {256, 292};
+        case G_IQ4_XS: return {256, 136};
+        default: return {0, 0};
+    }
+}
+
+uint64_t gtype_bytes(uint32_t t, uint64_t n) {
+    const auto [be, bb] = gblock(t);
+    if (!be) throw runtime_error(string("gguf: 不认识的量化类型 ") + gtype_name(t));
+    if (n % be) throw runtime_error("gguf: 元素个数不是块的整数倍");
+    return n / be * bb;
+}
+
+float h2f(const unsigned char* p) {
+    const uint16_t h = (uint16_t)(p[0] | (p[1] << 8));
+    const uint32_t s = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 31u;
+    uint32_t m = h & 0x3FFu, bits;
+    if (e == 0 && m == 0) {
+        bits = s;
+    } else if (e == 0) {  // subnormal: normalise
+        int k = 0;
+        while (!(m & 0x400u)) {
+            m <<= 1;
+            k++;
+        }
+        bits = s | ((uint32_t)(113 - k) << 23) | ((m & 0x3FFu) << 13);
+    } else if (e == 31) {
+        bits = s | 0x7F800000u | (m << 13);
+    } else {
+        bits = s | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+float bf2f(const unsigned char* p) {
+    const uint32_t bits = (uint32_t)(p[0] | (p[1] << 8)) << 16;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+void scale_min_k4(int j, const unsigned char* q, int& sc, int& mn) {
+    if (j < 4) {
+        sc = q[j] & 63;
+        mn = q[j + 4] & 63;
+    } else {
+        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+// gguf::dequant (libs/gguf_libs/gguf.h:145-315): n elements of type t to float.  Every
+// product below is exact in float, so the one rounding of each sum is the reference's.
+void dequant(uint32_t t, const unsigned char* src, float* dst, uint64_t n) {
+    switch (t) {
+        case G_F32: memcpy(dst, src, (size_t)n * 4); return;
+        case G_F16:
+            for (uint64_t i = 0; i < n; i++) dst[i] = h2f(src + 2 * i);
+            return;
+        case G_BF16:
+            for (uint64_t i = 0; i < n; i++) dst[i] = bf2f(src + 2 * i);
+            return;
+        case G_Q8_0:
+            for (uint64_t b = 0; b < n / 32; b++) {
+                const unsigned char* p = src + b * 34;
+                const float d = h2f(p);
+                for (int j = 0; j < 32; j++) dst[b * 32 + j] = (float)(int8_t)p[2 + j] * d;
+            }
+            return;
+        case G_Q4_0: case G_Q4_1: case G_Q5_0: case G_Q5_1: {
+            const bool min = t == G_Q4_1 || t == G_Q5_1, five = t == G_Q5_0 || t == G_Q5_1;
+            const size_t bb = gblock(t).second;
+            for (uint64_t b = 0; b < n / 32; b++) {
+                const unsigned char* p = src + b * bb;
+                const float d = h2f(p), m = min ? h2f(p + 2) : 0.0f;
+                uint32_t qh = 0;
+                if (five) memcpy(&qh, p + (min ? 4 : 2), 4);
+                const unsigned char* q = p + (min ? 4 : 2) + (five ? 4 : 0);
+                for (int j = 0; j < 16; j++) {
+                    int x0 = q[j] & 0xF, x1 = q[j] >> 4;
+                    if (five) {
+                        x0 |= (int)(((qh >> j) & 1u) << 4);
+                        x1 |= (int)(((qh >> (j + 16)) & 1u) << 4);
+                    }
+                    if (min) {
+                        dst[b * 32 + j] = (float)x0 * d + m;
+                        dst[b * 32 + j + 16] = (float)x1 * d + m;
+                    } else {
+                        const int off = five ? 16 : 8;
+                        dst[b * 32 + j] = (float)(x0 - off) * d;
+                        dst[b * 32 + j + 16] = (float)(x1 - off) * d;
+                    }
+                }
+            }
+            return;
+        }
+        case G_Q4_K: case G_Q5_K:
+            for (uint64_t b = 0; b < n / 256; b++) {
+                const unsigned char* p = src + b * (t == G_Q4_K ? 144 : 176);
+                const float d = h2f(p), dmin = h2f(p + 2);
+                const unsigned char* qh = p + 16;
+                const unsigned char* qs = p + (t == G_Q4_K ? 16 : 48);
+                float* y = dst + b * 256;
+                for (int j = 0; j < 8; j++) {  // 32-weight steps; even j low nibbles, odd j high
+                    int sc, mn;
+                    scale_min_k4(j, p + 4, sc, mn);
+                    const float d1 = d * (float)sc, n1 = dmin * (float)mn;
+                    for (int l = 0; l < 32; l++) {
+                        const unsigned char qb = qs[(j >> 1) * 32 + l];
+                        int q = (j & 1) ? (qb >> 4) : (qb & 0xF);
+                        if (t == G_Q5_K && ((qh[l] >> j) & 1)) q += 16;
+                        y[32 * j + l] = d1 * (float)q - n1;
+                    }
+                }
+            }
+            return;
+        case G_Q6_K:
+            for (uint64_t b = 0; b < n / 256; b++) {
+                const unsigned char* p = src + b * 210;
+                const float d = h2f(p + 208);
+                float* y = dst + b * 256;
+                for (int e = 0; e < 256; e++) {
+                    const int half = e >> 7, quarter = (e >> 5) & 3, l = e & 31;
+                    const unsigned char qb = p[half * 64 + l + 32 * (quarter & 1)];
+                    const int lo = quarter < 2 ? (qb & 0xF) : (qb >> 4);
+                    const int hi = (p[128 + half * 32 + l] >> (2 * quarter)) & 3;
+                    const int8_t sc = (int8_t)p[192 + half * 8 + l / 16 + 2 * quarter];
+                    y[e] = d * (float)sc * (float)((lo | (hi << 4)) - 32);
+                }
+            }
+            return;
+        default: throw runtime_error(string("gguf: 还没写这种量化的反量化 ") + gtype_name(t));
+    }
+}
+
+// ---------------------------------------------------------------- file
+
+struct Meta {
+    uint32_t type = 0, elem_type = 0;
+    uint64_t n = 0;
+    long long i = 0;
+    double f = 0.0;
+    string s;
+    vector<long long> ints;
+    vector<double> floats;
+    vector<string> strs;
+    // as_int / as_float (gguf.h:329-336): the scalar's own field, or an array's first element
+    long long as_int(long long d) const { return type != M_ARR ? i : (ints.empty() ? d : ints[0]); }
+    double as_float(double d) const { return type != M_ARR ? f : (floats.empty() ? d : floats[0]); }
+};
+
+struct GTensor {
+    string name;
+    uint32_t type = 0;
+    vector<uint64_t> shape;
+    uint64_t offset = 0, n_elem = 0, nbytes = 0;
+};
+
+class Reader {
+public:
+    Reader(std::istream& in, uint64_t size) : in_(in), size_(size) {}
+    void bytes(void* p, size_t n) {
+        if (!n) return;
+        in_.read(static_cast<char*>(p), (std::streamsize)n);
+        if (!in_) throw runtime_error("gguf: 文件被截断");
+    }
+    uint64_t u(int n) {
+        unsigned char b[8];
+        bytes(b, (size_t)n);
+        uint64_t v = 0;
+        for (int k = 0; k < n; k++) v |= (uint64_t)b[k] << (8 * k);
+        return v;
+    }
+    string str(bool v3) {
+        const uint64_t n = v3 ? u(8) : u(4);
+        // a length past the end of the file is a truncated file (checked before allocating)
+        if (n > size_) throw runtime_error("gguf: 文件被截断");
+        string s((size_t)n, '\0');
+        bytes(&s[0], (size_t)n);
+        return s;
+    }
+    void scalar(uint32_t t, Meta& m) {
+        switch (t) {
+            case M_U8: m.i = (long long)u(1); break;
+            case M_I8: m.i = (long long)(int8_t)u(1); break;
+            case M_U16: m.i = (long long)u(2); break;
+            case M_I16: m.i = (long long)(int16_t)u(2); break;
+            case M_U32: m.i = (long long)u(4); break;
+            case M_I32: m.i = (long long)(int32_t)u(4); break;
+            case M_F32: {
+                const uint32_t v = (uint32_t)u(4);
+                float x;
+                memcpy(&x, &v, 4);
+                m.f = (double)x;
+                break;
+            }
+            case M_BOOL: m.i = u(1) != 0 ? 1 : 0; break;
+            case M_U64: case M_I64: m.i = (long long)u(8); break;
+            case M_F64: {
+                const uint64_t v = u(8);
+                memcpy(&m.f, &v, 8);
+                break;
+            }
+            default: throw runtime_error("gguf: 不认识的元数据类型 " + std::to_string(t));
+        }
+    }
+    // meta_value (gguf.h:423-458)
+    void value(bool v3, Meta& m) {
+        m.type = (uint32_t)u(4);
+        if (m.type == M_STR) {
+            m.s = str(v3);
+            return;
+        }
+        if (m.type != M_ARR) {
+            scalar(m.type, m);
+            return;
+        }
+        m.elem_type = (uint32_t)u(4);
+        m.n = v3 ? u(8) : u(4);
+        if (m.elem_type == M_ARR) throw runtime_error("gguf: 不支持嵌套数组");
+        for (uint64_t k = 0; k < m.n; k++) {
+            if (m.elem_type == M_STR) {
+                m.strs.push_back(str(v3));
+                continue;
+            }
+            Meta e;
+            scalar(m.elem_type, e);
+            if (m.elem_type == M_F32 || m.elem_type == M_F64)
+                m.floats.push_back(e.f);
+            else
+                m.ints.push_back(e.i);
+        }
+    }
+
+private:
+    std::istream& in_;
+    uint64_t size_;
+};
+
+struct GFile {
+    string path;
+    uint32_t version = 0;
+    uint64_t align = 32, data_off = 0, file_size = 0;
+    vector<std::pair<string, Meta>> kvs;
+    vector<GTensor> tensors;
+
+    const Meta* meta(const string& k) const {
+        for (const auto& kv : kvs)
+            if (kv.first == k) return &kv.second;
+        return nullptr;
+    }
+    const GTensor* find(const string& n) const {
+        for (const GTensor& t : tensors)
+            if (t.name == n) return &t;
+        return nullptr;
+    }
+};
+
+// gguf::open (gguf.h:495-541)
+GFile gguf_open(const string& path) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) throw runtime_error("gguf: 打不开 " + path);
+    f.seekg(0, std::ios::end);
+    const uint64_t size = (uint64_t)f.tellg();
+    f.seekg(0);
+    Reader r(f, size);
+    GFile g;
+    g.path = path;
+    g.file_size = size;
+    char magic[4];
+    r.bytes(magic, 4);
+    if (memcmp(magic, "GGUF", 4) != 0) throw runtime_error("gguf: magic 不是 GGUF");
+    g.version = (uint32_t)r.u(4);
+    if (g.version < 2 || g.version > 3) throw runtime_error("gguf: 只支持 v2/v3，遇到 v" + std::to_string(g.version));
+    const bool v3 = g.version == 3;
+    const uint64_t nt = v3 ? r.u(8) : r.u(4), nk = v3 ? r.u(8) : r.u(4);
+    for (uint64_t k = 0; k < nk; k++) {
+        string key = r.str(v3);
+        Meta m;
+        r.value(v3, m);
+        g.kvs.emplace_back(std::move(key), std::move(m));
+    }
+    for (uint64_t k = 0; k < nt; k++) {
+        GTensor t;
+        t.name = r.str(v3);
+        const uint32_t nd = (uint32_t)r.u(4);
+        if (nd == 0 || nd > 4) throw runtime_error("gguf: 维度数不对 " + t.name);
+        t.n_elem = 1;
+        for (uint32_t d = 0; d < nd; d++) {
+            t.shape.push_back(r.u(8));
+            t.n_elem *= t.shape.back();
+        }
+        t.type = (uint32_t)r.u(4);
+        t.offset = r.u(8);
+        t.nbytes = gtype_bytes(t.type, t.n_elem);
+        g.tensors.push_back(std::move(t));
+    }
+    if (const Meta* al = g.meta("general.alignment")) {
+        const long long a = al->as_int(32);
+        if (a > 0) g.align = (uint64_t)a;
+    }
+    const uint64_t here = (uint64_t)f.tellg();
+    g.data_off = (here + g.align - 1) / g.align * g.align;
+    return g;
+}
+
+// ---------------------------------------------------------------- output formats
+
+uint16_t f2h(float v) {  // converter.h:55-79: truncating exponent logic, mantissa rounded half up
+    uint32_t b;
+    memcpy(&b, &v, 4);
+    const uint32_t sign = (b >> 31) << 15, exp = (b >> 23) & 0xFFu;
+    uint32_t man = b & 0x7FFFFFu;
+    if (exp == 0xFFu) return (uint16_t)(sign | 0x7C00u | (man ? 0x200u : 0u));
+    int e = (int)exp - 127 + 15;
+    if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        man = (man | 0x800000u) >> (unsigned)(1 - e);
+        return (uint16_t)(sign | ((man + 0x1000u) >> 13));
+    }
+    uint32_t hm = (man + 0x1000u) >> 13;
+    if (hm == 0x400u) {
+        hm = 0;
+        if (++e >= 31) return (uint16_t)(sign | 0x7C00u);
+    }
+    return (uint16_t)(sign | ((uint32_t)e << 10) | hm);
+}
+
+uint16_t f2bf(float v) {  // converter.h:81-86: + 0x8000 unless inf / nan
+    uint32_t b;
+    memcpy(&b, &v, 4);
+    if ((b & 0x7F800000u) != 0x7F800000u) b += 0x8000u;
+    return (uint16_t)(b >> 16);
+}
+
+// write_as (converter.h:88-100)
+void write_as(std::ostream& f, const float* v, uint64_t n, uint8_t dtype) {
+    if (dtype == BF_F32) {
+        f.write(reinterpret_cast<const char*>(v), (std::streamsize)(n * 4));
+        return;
+    }
+    vector<unsigned char> out((size_t)n * 2);
+    for (uint64_t i = 0; i < n; i++) {
+        const uint16_t h = dtype == BF_F16 ? f2h(v[i]) : f2bf(v[i]);
+        out[2 * i] = (unsigned char)(h & 0xFF);
+        out[2 * i + 1] = (unsigned char)(h >> 8);
+    }
+    f.write(reinterpret_cast<const char*>(out.data()), (std::streamsize)out.size());
+}
+
+size_t bf_elem_bytes(uint8_t d) { return d == BF_F32 || d == BF_I32 ? 4 : (d == BF_F16 || d == BF_BF16) ? 2 : d == BF_I8 ? 1 : 0; }
+
+// One model.bf tensor written from the GGUF file (bfile::StreamTensor)
+struct Sink {
+    string name;
+    uint8_t dtype = BF_F32;
+    vector<uint32_t> shape;
+    uint64_t nbytes = 0;
+    const GTensor* src = nullptr;
+    bool raw = false, transpose = false, permute = false;
+};
+
+// GGUF stores q / k rows with each head's RoPE pairs split into halves; jieyu's
+// rope_at takes adjacent pairs, so output row r of a head reads source row
+// perm_row(r) (gguf_convert.h:67-70)
+uint64_t perm_row(uint64_t r, int hd) {
+    const uint64_t h = r / hd, k = r % hd;
+    return h * hd + ((k & 1) ? hd / 2 + k / 2 : k / 2);
+}
+
+bool read_at(std::ifstream& in, uint64_t off, unsigned char* p, uint64_t n) {
+    in.seekg((std::streamoff)off);
+    in.read(reinterpret_cast<char*>(p), (std::streamsize)n);
+    return (uint64_t)in.gcount() == n;
+}
+
+// the tensor's bytes in model.bf order (make_sink / make_raw_sink, gguf_convert.h:115-229)
+bool emit(const GFile& g, const Sink& s, int hd, std::ostream& f) {
+    std::ifstream in(g.path, std::ios::binary);
+    if (!in) return false;
+    const GTensor& t = *s.src;
+    const uint64_t base = g.data_off + t.offset;
+    const auto [be, bb] = gblock(t.type);
+    {
+        if (s.raw) {  // quantized rows copied, q / k rows permuted
+            const uint64_t k = t.shape[0], n = t.shape[1], rb = k / be * bb;
+            vector<unsigned char> row((size_t)rb);
+            for (uint64_t j = 0; j < n; j++) {
+                if (!read_at(in, base + (s.permute ? perm_row(j, hd) : j) * rb, row.data(), rb)) return false;
+                f.write(reinterpret_cast<const char*>(row.data()), (std::streamsize)rb);
+            }
+            return (bool)f;
+        }
+        const uint64_t total = t.n_elem, in_dim = t.shape[0], out_dim = t.shape.size() > 1 ? t.shape[1] : 0;
+        vector<unsigned char> raw;
+        vector<float> tmp;
+        if (s.permute && !s.transpose) {  // a q / k bias (1-D)
+            raw.resize((size_t)t.nbytes);
+            if (!read_at(in, base, raw.data(), raw.size())) return false;
+            tmp.resize((size_t)total);
+            dequant(t.type, raw.data(), tmp.data(), total);
+            vector<float> o((size_t)total);
+            for (uint64_t i = 0; i < total; i++) o[i] = tmp[perm_row(i, hd)];
+            write_as(f, o.data(), total, s.dtype);
+            return (bool)f;
+        }
+        if (!s.transpose) {  // in order, ~4 MiB of source at a time
+            const uint64_t chunk = ((4u << 20) / bb) * be;
+            for (uint64_t done = 0; done < total;) {
+                const uint64_t n = std::min(chunk, total - done), bytes = n / be * bb;
+                raw.resize((size_t)bytes);
+                if (!read_at(in, base + done / be * bb, raw.data(), bytes)) return false;
+                tmp.resize((size_t)n);
+                dequant(t.type, raw.data(), tmp.data(), n);
+                write_as(f, tmp.data(), n, s.dtype);
+                done += n;
+            }
+            return (bool)f;
+        }
+        // [out][in] -> [in][out]: output tiles of `tile` input columns (<= 128 MiB of
+        // floats), each filled from whole-head runs of source rows (~8 MiB)
+        uint64_t tile = std::max<uint64_t>(1, (128u << 20) / (4 * out_dim));
+        tile = std::min(tile, in_dim);
+        uint64_t rb = (8u << 20) / (4 * in_dim) / (uint64_t)hd * (uint64_t)hd;
+        rb = std::min(std::max(rb, (uint64_t)hd), out_dim);
+        vector<float> dst;
+        for (uint64_t t0 = 0; t0 < in_dim; t0 += tile) {
+            const uint64_t t1 = std::min(in_dim, t0 + tile);
+            dst.assign((size_t)((t1 - t0) * out_dim), 0.0f);
+            for (uint64_t j0 = 0; j0 < out_dim; j0 += rb) {
+                const uint64_t j1 = std::min(out_dim, j0 + rb), n = (j1 - j0) * in_dim, bytes = n / be * bb;
+                raw.resize((size_t)bytes);
+                if (!read_at(in, base + (j0 * in_dim) / be * bb, raw.data(), bytes)) return false;
+                tmp.resize((size_t)n);
+                dequant(t.type, raw.data(), tmp.data(), n);
+                for (uint64_t j = j0; j < j1; j++) {
+                    const uint64_t r2 = s.permute ? perm_row(j, hd) : j;
+                    const float* srow = tmp.data() + (r2 - j0) * in_dim;
+                    for (uint64_t c = t0; c < t1; c++) dst[(size_t)((c - t0) * out_dim + j)] = srow[c];
+                }
+            }
+            write_as(f, dst.data(), dst.size(), s.dtype);
+        }
+        return (bool)f;
+    }
+}
+
+void put32(unsigned char* p, uint32_t v) {
+    for (int k = 0; k < 4; k++) p[k] = (unsigned char)(v >> (8 * k));
+}
+void put64(unsigned char* p, uint64_t v) {
+    for (int k = 0; k < 8; k++) p[k] = (unsigned char)(v >> (8 * k));
+}
+uint64_t up64(uint64_t v) { return (v + 63) / 64 * 64; }
+
+uint64_t bf_tensor_bytes(uint8_t d, uint64_t elems) {
+    if (d == BF_Q4K || d == BF_Q5K || d == BF_Q6K)
+        return elems % 256 ? ~0ull : elems / 256 * (d == BF_Q4K ? 144 : d == BF_Q5K ? 176 : 210);
+    if (d == BF_Q8_0) return elems % 32 ? ~0ull : elems / 32 * 34;
+    const size_t eb = bf_elem_bytes(d);
+    return eb ? elems * eb : ~0ull;
+}
+
+// write_bfile_stream (bfile.h:276-341): 64-byte header, 104-byte entries, data at
+// 64-byte aligned offsets after the table
+void write_bfile(const string& path, const GgufResult& r, const GFile& g, const vector<Sink>& ts) {
+    const uint64_t dir_bytes = ts.size() * 104, header = up64(64 + dir_bytes);
+    if (header > 0xFFFFFFFFull) throw runtime_error("bfile: 张量太多");
+    vector<uint64_t> offs(ts.size());
+    uint64_t cur = 0;
+    for (size_t i = 0; i < ts.size(); i++) {  // check_tensor_meta (bfile.h:258-273)
+        const Sink& s = ts[i];
+        if (s.name.empty() || s.name.size() > 63) throw runtime_error("bfile: 张量名长度必须 1..63: " + s.name);
+        if (s.shape.size() > 4) throw runtime_error("bfile: 维度超过 4: " + s.name);
+        if (s.dtype > BF_Q8_0) throw runtime_error("bfile: 不认识的 dtype: " + s.name);
+        uint64_t elems = 1;
+        for (uint32_t d : s.shape) elems *= d;
+        if (bf_tensor_bytes(s.dtype, elems) != s.nbytes) throw runtime_error("bfile: shape 与数据长度不符: " + s.name);
+        offs[i] = cur;
+        cur = up64(cur + s.nbytes);
+    }
+    std::ofstream f(path, std::ios::binary | std::ios::trunc);
+    if (!f) throw runtime_error("bfile: 无法写入 " + path);
+    unsigned char head[64] = {};
+    memcpy(head, "JYAIBF", 6);
+    put64(head + 6, r.hidden);
+    put64(head + 14, r.layers);
+    head[22] = 1;  // mode
+    head[23] = (unsigned char)r.num_heads;
+    head[24] = (unsigned char)r.num_kv_heads;
+    head[25] = (unsigned char)r.head_dim;
+    put32(head + 26, r.intermediate);
+    put64(head + 30, r.vocab);
+    put32(head + 38, 2);
+    put32(head + 42, (uint32_t)ts.size());
+    put32(head + 46, (uint32_t)header);
+    put32(head + 50, 104);
+    f.write(reinterpret_cast<const char*>(head), 64);
+    for (size_t i = 0; i < ts.size(); i++) {
+        unsigned char e[104] = {};
+        memcpy(e, ts[i].name.data(), ts[i].name.size());
+        e[64] = ts[i].dtype;
+        e[65] = (unsigned char)ts[i].shape.size();
+        for (size_t d = 0; d < ts[i].shape.size(); d++) put32(e + 68 + 4 * d, ts[i].shape[d]);
+        put64(e + 88, offs[i]);
+        put64(e + 96, ts[i].nbytes);
+        f.write(reinterpret_cast<const char*>(e), 104);
+    }
+    const vector<char> pad((size_t)(header - 64 - dir_bytes), 0);
+    f.write(pad.data(), (std::streamsize)pad.size());
+    uint64_t written = 0;
+    for (size_t i = 0; i < ts.size(); i++) {
+        if (offs[i] > written) {
+            const vector<char> z((size_t)(offs[i] - written), 0);
+            f.write(z.data(), (std::streamsize)z.size());
+            written = offs[i];
+        }
+        if (!emit(g, ts[i], r.head_dim, f)) throw runtime_error("bfile: 写张量失败: " + ts[i].name);
+        written += ts[i].nbytes;
+    }
+    f.flush();
+    if (!f) throw runtime_error("bfile: 写入失败 " + path);
+}
+
+// ---------------------------------------------------------------- model_info.json
+
+// is_json_number (libs/json_libs/json_value.h:107-150)
+bool json_number(const string& t) {
+    size_t i = 0;
+    const size_t n = t.size();
+    if (i < n && t[i] == '-') i++;
+    if (i >= n) return false;
+    if (t[i] == '0') {
+        if (++i < n && t[i] >= '0' && t[i] <= '9') return false;
+    } else if (t[i] >= '1' && t[i] <= '9') {
+        while (i < n && t[i] >= '0' && t[i] <= '9') i++;
+    } else {
+        return false;
+    }
+    if (i < n && t[i] == '.') {
+        const size_t d = ++i;
+        while (i < n && t[i] >= '0' && t[i] <= '9') i++;
+        if (i == d) return false;
+    }
+    if (i < n && (t[i] == 'e' || t[i] == 'E')) {
+        if (++i < n && (t[i] == '+' || t[i] == '-')) i++;
+        const size_t d = i;
+        while (i < n && t[i] >= '0' && t[i] <= '9') i++;
+        if (i == d) return false;
+    }
+    return i == n;
+}
+
+void json_escape(string& out, const string& s) {
+    out.push_back('"');
+    for (const unsigned char c : s) {
+        switch (c) {
+            case '"': out += "\\\""; break;
+            case '\\': out += "\\\\"; break;
+            case '\b': out += "\\b"; break;
+            case '\f': out += "\\f"; break;
+            case '\n': out += "\\n"; break;
+            case '\r': out += "\\r"; break;
+            case '\t': out += "\\t"; break;
+            default:
+                if (c < 0x20u) {
+                    char b[8];
+                    snprintf(b, sizeof b, "\\u%04x", (unsigned)c);
+                    out += b;
+                } else {
+                    out.push_back((char)c);
+                }
+        }
+    }
+    out.push_back('"');
+}
+
+// write_value (libs/json_libs/json_value.h:54-105): two-space indentation, "key": value
+void json_write(string& out, const JValue& v, int level) {
+    switch (v.kind) {
+        case JValue::Null: out += "null"; return;
+        case JValue::Bool: case JValue::Number: out += v.raw.empty() ? string("null") : v.raw; return;
+        case JValue::String: json_escape(out, v.text); return;
+        case JValue::Array:
+            if (v.items.empty()) {
+                out += "[]";
+                return;
+            }
+            out += "[\n";
+            for (size_t i = 0; i < v.items.size(); i++) {
+                out.append((size_t)(level + 1) * 2, ' ');
+                json_write(out, v.items[i], level + 1);
+                out += i + 1 < v.items.size() ? ",\n" : "\n";
+            }
+            out.append((size_t)level * 2, ' ');
+            out += "]";
+            return;
+        case JValue::Object:
+            if (v.members.empty()) {
+                out += "{}";
+                return;
+            }
+            out += "{\n";
+            for (size_t i = 0; i < v.members.size(); i++) {
+                out.append((size_t)(level + 1) * 2, ' ');
+                json_escape(out, v.members[i].first);
+                out += ": ";
+                json_write(out, v.members[i].second, level + 1);
+                out += i + 1 < v.members.size() ? ",\n" : "\n";
+            }
+            out.append((size_t)level * 2, ' ');
+            out += "}";
+            return;
+    }
+}
+
+// json_file::SetJsonWay + WriteJsonKey (libs/json_libs/json.h:20-47, :146-176, :240-313)
+// for the flat keys the converter writes: an existing file is loaded and updated,
+// a missing or blank one starts empty, an unreadable one is left alone (every
+// write is refused); the whole document is rewritten after each key.
+class InfoFile {
+public:
+    explicit InfoFile(const string& path) : path_(path) {
+        string text;
+        JValue v;
+        if (read_file(resolve_path(path_), text) && json_parse(text, v)) {
+            root_ = std::move(v);  // kept as parsed, whatever its kind
+            ok_ = true;
+        } else if (text.find_first_not_of(" \t\r\n") == string::npos) {
+            root_.kind = JValue::Object;  // missing or blank: a new object
+            ok_ = true;
+        }
+    }
+    void set(const string& key, const string& value) {
+        if (!ok_) return;
+        JValue v;  // make_value (json_parser.h:291-320)
+        if (json_number(value)) {
+            v.kind = JValue::Number;
+            v.raw = value;
+        } else if (value == "true" || value == "false") {
+            v.kind = JValue::Bool;
+            v.raw = value;
+        } else if (value == "null") {
+            v.kind = JValue::Null;
+        } else if (!value.empty() && (value[0] == '{' || value[0] == '[') && json_parse(value, v)) {
+        } else {
+            v = JValue();
+            v.kind = JValue::String;
+            v.text = value;
+        }
+        bool found = false;
+        for (auto& m : root_.members)
+            if (m.first == key) {
+                m.second = v;
+                found = true;
+                break;
+            }
+        if (!found) root_.members.emplace_back(key, v);
+        string out;
+        json_write(out, root_, 0);
+        out.push_back('\n');
+        std::ofstream f(resolve_path(path_), std::ios::binary);
+        f.write(out.data(), (std::streamsize)out.size());
+    }
+
+private:
+    string path_;
+    JValue root_;
+    bool ok_ = false;
+};
+
+// ---------------------------------------------------------------- names
+
+const char* suffix_map(const string& s) {
+    static const std::pair<const char*, const char*> m[] = {
+        {"attn_norm.weight", "input_layernorm.weight"},   {"attn_q.weight", "self_attn.q_proj.weight"},
+        {"attn_q.bias", "self_attn.q_proj.bias"},         {"attn_k.weight", "self_attn.k_proj.weight"},
+        {"attn_k.bias", "self_attn.k_proj.bias"},         {"attn_v.weight", "self_attn.v_proj.weight"},
+        {"attn_v.bias", "self_attn.v_proj.bias"},         {"attn_output.weight", "self_attn.o_proj.weight"},
+        {"ffn_norm.weight", "post_attention_layernorm.weight"}, {"ffn_gate.weight", "mlp.gate_proj.weight"},
+        {"ffn_down.weight", "mlp.down_proj.weight"},      {"ffn_up.weight", "mlp.up_proj.weight"},
+    };
+    for (const auto& p : m)
+        if (s == p.first) return p.second;
+    return nullptr;
+}
+
+// GGUF tensor name -> the Hugging Face name model.bf uses (gguf_convert.h:88-103); "" = skipped
+string hf_name(const string& n) {
+    if (n == "token_embd.weight") return "model.embed_tokens.weight";
+    if (n == "output_norm.weight") return "model.norm.weight";
+    if (n == "output.weight") return "lm_head.weight";
+    if (n.size() > 4 && n.compare(0, 4, "blk.") == 0) {
+        const size_t b = n.find('.', 4);
+        if (b == string::npos) return "";
+        const string idx = n.substr(4, b - 4);
+        if (idx.empty() || idx.find_first_not_of("0123456789") != string::npos) return "";
+        const char* sfx = suffix_map(n.substr(b + 1));
+        return sfx ? "model.layers." + idx + "." + sfx : "";
+    }
+    return "";
+}
+
+int quant_code(uint32_t t) {
+    switch (t) {
+        case G_Q4_K: return BF_Q4K;
+        case G_Q5_K: return BF_Q5K;
+        case G_Q6_K: return BF_Q6K;
+        case G_Q8_0: return BF_Q8_0;
+        default: return -1;
+    }
+}
+
+const char* dtype_name(uint8_t d) {
+    switch (d) {
+        case BF_F32: return "f32";
+        case BF_F16: return "f16";
+        case BF_BF16: return "bf16";
+        case BF_I8: return "i8";
+        case BF_I32: return "i32";
+        case BF_Q4K: return "q4_K";
+        case BF_Q5K: return "q5_K";
+        case BF_Q6K: return "q6_K";
+        case BF_Q8_0: return "q8_0";
+        default: return "?";
+    }
+}
+
+string jesc(const string& s) {  // vocab.json keys: only '"' and '\\' escaped (gguf_convert.h:56-65)
+    string o;
+    for (const char c : s) {
+        if (c == '"')
+            o += "\\\"";
+        else if (c == '\\')
+            o += "\\\\";
+        else
+            o += c;
+    }
+    return o;
+}
+
+long long meta_int(const GFile& g, const string& k, long long d) {
+    const Meta* m = g.meta(k);
+    return m ? m->as_int(d) : d;
+}
+
+double meta_float(const GFile& g, const string& k, double d) {
+    const Meta* m = g.meta(k);
+    return m ? m->as_float(d) : d;
+}
+
+}  // namespace
+
+// ggufc::convert (libs/gguf_libs/gguf_convert.h:260-421)
+GgufResult gguf_convert(const std::string& src, const std::string& out_dir, uint8_t out_dtype, bool quant,
+                        bool verbose) {
+    const GFile g = gguf_open(src);
+    GgufResult r;
+    const Meta* am = g.meta("general.architecture");
+    r.arch = am && !am->s.empty() ? am->s : string("llama");
+    const string pre = r.arch + ".";
+    if (verbose) printf("GGUF v%u  %s  tensors %zu\n", g.version, r.arch.c_str(), g.tensors.size());
+
+    long long hidden = meta_int(g, pre + "embedding_length", 0), nl = meta_int(g, pre + "block_count", 0);
+    const long long inter = meta_int(g, pre + "feed_forward_length", 0), nh = meta_int(g, pre + "attention.head_count", 0);
+    const long long nkv = meta_int(g, pre + "attention.head_count_kv", nh);
+    long long hd = meta_int(g, pre + "attention.key_length", 0);
+    const double rope = meta_float(g, pre + "rope.freq_base", 10000.0);
+    const long long ctx = meta_int(g, pre + "context_length", 1024);
+
+    const GTensor* emb = g.find("token_embd.weight");
+    long long vocab = 0;
+    if (emb && emb->shape.size() >= 2) {
+        if (hidden <= 0) hidden = (long long)emb->shape[0];
+        vocab = (long long)emb->shape[1];
+    }
+    if (vocab <= 0)
+        if (const Meta* tk = g.meta("tokenizer.ggml.tokens")) vocab = (long long)tk->n;
+    if (nl <= 0)
+        for (const GTensor& t : g.tensors)
+            if (t.name.size() > 4 && t.name.compare(0, 4, "blk.") == 0) nl = std::max(nl, atoll(t.name.c_str() + 4) + 1);
+    if (hidden <= 0 || vocab <= 0 || nl <= 0 || inter <= 0)
+        throw runtime_error("gguf: 超参不全（hidden / layers / intermediate / vocab）");
+    if (nh <= 0) throw runtime_error("gguf: 没有 attention.head_count");
+    if (hd <= 0) hd = hidden / nh;
+    if (nh > 255 || nkv > 255 || hd > 255) throw runtime_error("gguf: num_heads / num_kv_heads / head_dim 必须落在 1..255");
+    if (nkv <= 0 || nh % nkv != 0) throw runtime_error("gguf: num_heads 必须能被 num_kv_heads 整除");
+    if (hidden != nh * hd) printf("[警告] hidden(%lld) != num_heads*head_dim(%lld)\n", hidden, nh * hd);
+    for (const GTensor& t : g.tensors)
+        if (t.shape.size() == 2 && t.shape[0] % gblock(t.type).first != 0)
+            throw runtime_error("gguf: " + t.name + " 的行长不是量化块的整数倍");
+
+    // the sinks, in GGUF tensor order
+    auto dense = [&](const GTensor& t, const string& name, bool tr, bool pm, uint8_t dt) {
+        Sink s;
+        s.name = name;
+        s.dtype = dt;
+        s.src = &t;
+        s.transpose = tr;
+        s.permute = pm;
+        if (t.shape.size() == 1)
+            s.shape = {(uint32_t)t.shape[0]};
+        else if (tr)
+            s.shape = {(uint32_t)t.shape[0], (uint32_t)t.shape[1]};
+        else
+            s.shape = {(uint32_t)(t.shape.size() > 1 ? t.shape[1] : 0), (uint32_t)t.shape[0]};
+        uint64_t e = 1;
+        for (uint32_t d : s.shape) e *= d;
+        s.nbytes = e * bf_elem_bytes(dt);
+        return s;
+    };
+    vector<Sink> sinks;
+    vector<string> skipped;
+    for (const GTensor& t : g.tensors) {
+        const string hf = hf_name(t.name);
+        if (hf.empty()) {
+            skipped.push_back(t.name);
+            continue;
+        }
+        const bool is_emb = t.name == "token_embd.weight", tr = t.shape.size() == 2 && !is_emb;
+        const bool pm = t.name.find(".attn_q.") != string::npos || t.name.find(".attn_k.") != string::npos;
+        const int qc = t.shape.size() == 2 ? quant_code(t.type) : -1;
+        if (quant && qc >= 0) {  // make_raw_sink (gguf_convert.h:201-229)
+            Sink s;
+            s.name = hf;
+            s.dtype = (uint8_t)qc;
+            s.src = &t;
+            s.raw = true;
+            s.permute = pm;
+            s.shape = {(uint32_t)t.shape[1], (uint32_t)t.shape[0]};
+            s.nbytes = t.shape[1] * (t.shape[0] / gblock(t.type).first) * gblock(t.type).second;
+            sinks.push_back(s);
+            r.quant++;
+        } else {
+            sinks.push_back(dense(t, hf, tr, pm, t.shape.size() == 2 ? out_dtype : (uint8_t)BF_F32));
+            if (tr) r.transposed++;
+        }
+        if (pm) r.permuted++;
+    }
+    if (!g.find("output.weight")) {
+        if (!emb) throw runtime_error("gguf: 既没有 output.weight 也没有 token_embd.weight");
+        r.tied_lm_head = true;
+        if (!(quant && quant_code(emb->type) >= 0)) {
+            sinks.push_back(dense(*emb, "lm_head.weight", true, false, out_dtype));
+            r.transposed++;
+        }
+    }
+    if (verbose && !skipped.empty()) {
+        printf("  skipped %zu unknown tensors:", skipped.size());
+        for (size_t i = 0; i < skipped.size() && i < 6; i++) printf(" %s", skipped[i].c_str());
+        printf(skipped.size() > 6 ? " ...\n" : "\n");
+    }
+
+    r.hidden = (uint64_t)hidden;
+    r.layers = (uint64_t)nl;
+    r.num_heads = (int)(uint8_t)nh;
+    r.num_kv_heads = (int)(uint8_t)nkv;
+    r.head_dim = (int)(uint8_t)hd;
+    r.intermediate = (uint32_t)inter;
+    r.vocab = (uint64_t)vocab;
+    r.rope_theta = (long long)(rope < 0 ? -rope : rope);
+    r.max_position = ctx;
+
+    fs::create_directories(out_dir);
+    const string bf = (fs::path(out_dir) / "model.bf").string();
+    write_bfile(bf, r, g, sinks);
+    r.tensor_count = sinks.size();
+    r.file_size = fs::file_size(bf);
+
+    {
+        InfoFile info((fs::path(out_dir) / "model_info.json").string());
+        info.set("hidden_size", std::to_string(r.hidden));
+        info.set("layer_count", std::to_string(r.layers));
+        info.set("mode", "1");
+        info.set("num_heads", std::to_string(r.num_heads));
+        info.set("num_kv_heads", std::to_string(r.num_kv_heads));
+        info.set("head_dim", std::to_string(r.head_dim));
+        info.set("intermediate_size", std::to_string(r.intermediate));
+        info.set("vocab_size", std::to_string(r.vocab));
+        info.set("rope_theta", std::to_string(r.rope_theta));
+        info.set("max_position_embeddings", std::to_string(r.max_position));
+        info.set("dtype", quant ? string("quant") : string(dtype_name(out_dtype)));
+        info.set("add_bos_token", "0");
+        info.set("rope_style", "adjacent_after_permute");
+        info.set("source_arch", r.arch);
+        info.set("source_file", fs::path(src).filename().string());
+        if (const Meta* nm = g.meta("general.name"))
+            if (!nm->s.empty()) info.set("source_name", nm->s);
+        if (const Meta* tk = g.meta("tokenizer.ggml.tokens")) {
+            auto has = [&](const string& s) { return std::find(tk->strs.begin(), tk->strs.end(), s) != tk->strs.end(); };
+            auto pick = [&](const char* key, std::initializer_list<const char*> cands) {
+                for (const char* c : cands)
+                    if (has(c)) {
+                        info.set(key, c);
+                        return;
+                    }
+            };
+            pick("message_start", {"<|im_start|>", "<|start_header_id|>"});
+            pick("message_end", {"<|im_end|>", "<|eot_id|>", "<|end_of_turn|>"});
+            pick("text_end", {"<|endoftext|>", "<|end_of_text|>", "</s>"});
+            // DeepSeek's markers use U+FF5C (fullwidth vertical line) and U+2581 (lower one eighth block)
+            const string bar = "\xEF\xBD\x9C", sp = "\xE2\x96\x81";
+            const string user = "<" + bar + "User" + bar + ">", asst = "<" + bar + "Assistant" + bar + ">";
+            if (has(user) && has(asst)) {
+                info.set("template", "deepseek");
+                info.set("bos_text", "<" + bar + "begin" + sp + "of" + sp + "sentence" + bar + ">");
+                info.set("user_start", user);
+                info.set("assistant_start", asst);
+                info.set("turn_end", "<" + bar + "end" + sp + "of" + sp + "sentence" + bar + ">");
+            }
+        }
+    }
+
+    // write_tokenizer (gguf_convert.h:231-258)
+    const Meta* tk = g.meta("tokenizer.ggml.tokens");
+    if (!tk || tk->strs.empty()) throw runtime_error("gguf: 没有 tokenizer.ggml.tokens，抽不出词表");
+    r.eos_id = (int)meta_int(g, "tokenizer.ggml.eos_token_id", -1);
+    if (r.eos_id < 0) r.eos_id = (int)meta_int(g, "tokenizer.ggml.bos_token_id", -1);
+    {
+        std::ofstream v((fs::path(out_dir) / "vocab.json").string(), std::ios::binary | std::ios::trunc);
+        if (!v) throw runtime_error("gguf: 写不了 vocab.json");
+        v << "{\n";
+        for (size_t i = 0; i < tk->strs.size(); i++) v << (i ? ",\n" : "") << "  \"" << jesc(tk->strs[i]) << "\": " << i;
+        v << "\n}\n";
+    }
+    {
+        std::ofstream m((fs::path(out_dir) / "merges.txt").string(), std::ios::binary | std::ios::trunc);
+        if (!m) throw runtime_error("gguf: 写不了 merges.txt");
+        m << "#version: 0.2\n";
+        if (const Meta* mg = g.meta("tokenizer.ggml.merges"))
+            for (const string& s : mg->strs) m << s << "\n";
+    }
+    if (verbose) printf("  vocab %zu tokens, eos=%d\n", tk->strs.size(), r.eos_id);
+    return r;
+}
+
+}  // namespace jytext

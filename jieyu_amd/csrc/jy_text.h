@@ -156,4 +156,27 @@ private:
     std::vector<BfEntry> entries_;
 };
 
+// ---------------------------------------------------------------- GGUF
+
+// what ggufc::convert reports (libs/gguf_libs/gguf_convert.h:25-34)
+struct GgufResult {
+    uint64_t hidden = 0, layers = 0, vocab = 0;
+    int num_heads = 0, num_kv_heads = 0, head_dim = 0;
+    uint32_t intermediate = 0;
+    long long rope_theta = 10000, max_position = 32768;
+    size_t tensor_count = 0;
+    uint64_t file_size = 0;
+    int transposed = 0, permuted = 0, quant = 0;
+    bool tied_lm_head = false;
+    int eos_id = -1;
+    std::string arch;
+};
+
+// GGUF file -> model directory (ggufc::convert, libs/gguf_libs/gguf_convert.h:260-421);
+// out_dtype is the model.bf dtype of the non-quantized 2-D weights (BF_F32 / BF_F16 /
+// BF_BF16), quant keeps Q4_K / Q5_K / Q6_K / Q8_0 blocks as they are.  Throws
+// std::runtime_error with the reference's texts.
+GgufResult gguf_convert(const std::string& src, const std::string& out_dir, uint8_t out_dtype, bool quant,
+                        bool verbose);
+
 }  // namespace jytext

@@ -18,6 +18,7 @@
 #include "model_libs/generate.h"   /* generate / forward_cached / transformer_layer and every kernel */
 #include "main.hpp"                 /* the text C ABI (jieyu_load / jieyu_generate ...), pipeline, tokenizer,
                                        consten_pool */
+#include "gguf_libs/gguf_convert.h" /* GGUF -> model directory */
 
 #include "jieyu_model.h"
 
@@ -316,4 +317,33 @@ JYREF_API int jyref_write_byte_vocab(const char* vocab, const char* merges) {
         return -1;
     }
     return 0;
+}
+
+/* ggufc::convert (libs/gguf_libs/gguf_convert.h:260-421): 0, or -1 with the error text */
+JYREF_API int jyref_gguf_convert(const char* src, const char* out_dir, int out_dtype, int quant, long long* info,
+                                 char* err, int cap) {
+    try {
+        ggufc::Options o;
+        o.src = src;
+        o.out_dir = out_dir;
+        o.out_dtype = (uint8_t)out_dtype;
+        o.quant = quant != 0;
+        o.verbose = false;
+        const ggufc::Result r = ggufc::convert(o);
+        if (info) {
+            const long long v[16] = {(long long)r.head.hidden, (long long)r.head.layers, r.head.num_heads,
+                                     r.head.num_kv_heads, r.head.head_dim, (long long)r.head.intermediate,
+                                     (long long)r.head.vocab_size, r.rope_theta, r.max_position,
+                                     (long long)r.tensor_count, r.transposed, r.permuted, r.quant,
+                                     r.tied_lm_head ? 1 : 0, r.eos_id, (long long)r.file_size};
+            std::memcpy(info, v, sizeof v);
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        if (err && cap > 0) {
+            std::strncpy(err, e.what(), (size_t)cap - 1);
+            err[cap - 1] = 0;
+        }
+        return -1;
+    }
 }

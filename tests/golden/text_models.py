@@ -205,6 +205,23 @@ SCRIPTS = [
         ("gen", b"the theory of the thing", 40, 0.7, 1.1, 4096),
         ("jsonl", "chat.jsonl", None, None, 24, 0.0, 1.0, 4096),
     ]),
+    # GGUF files converted to model directories (jytext_gguf_convert, quant = true):
+    # Q4_K / Q5_K / Q6_K matrices with the Q6_K embedding as the tied head ...
+    ("gguf_q4km", 64, [
+        ("gen", b"hello world", 16, 0.0, 1.0, 4096),
+        ("gen", b"<|im_start|>user\nhi<|im_end|>\n<|im_start|>assistant\n", 24, 0.0, 1.0, 4096),
+        ("gen", b"abc", 20, 0.8, 1.1, 4096),
+        ("gen", b"abc", 20, 0.0, 1.3, 4096),
+        ("info",),
+    ]),
+    # ... and Q8_0 matrices beside f32 ones dequantized from Q4_0 / Q4_1 / Q5_0 / Q5_1 /
+    # f16 / bf16, q/k/v biases, untied Q8_0 head
+    ("gguf_qwen", 64, [
+        ("gen", b"abcd abc", 16, 0.0, 1.0, 4096),
+        ("gen", b"Hello, qwen!", 20, 0.7, 1.1, 4096),
+        ("gen", b"<|im_start|>user\ncd ab<|im_end|>\n", 16, 0.0, 1.2, 4096),
+        ("jsonl", "chat.jsonl", None, None, 16, 0.0, 1.0, 4096),
+    ]),
 ]
 
 LOAD_ERRORS = ["bind:wrong_shape", "bind:missing", "nodir", "noinfo", "novocab", "badmagic"]
@@ -225,6 +242,12 @@ def build_dir(kind, root, lib=None):
         bpe_f32_dir(path)
     elif kind == "bpe_q8":
         bpe_q8_dir(path, lib)
+    elif kind in ("gguf_q4km", "gguf_qwen"):
+        import gguf_models
+        from jieyu_amd import api
+        model = {"gguf_q4km": gguf_models.llama_q4km, "gguf_qwen": gguf_models.qwen_mixed}[kind]()
+        src = model.write(path + ".gguf")
+        api.gguf_convert(src, path, "f32", True)
     elif kind == "nodir":
         return path  # never created
     elif kind == "noinfo":

@@ -1,0 +1,135 @@
+"""GGUF -> model directory (jytext_gguf_convert) against jieyu's own converter
+(ggufc::convert, libs/gguf_libs/gguf_convert.h:260-421).
+
+The GGUF inputs are rebuilt from tests/golden/gguf_models.py; tests/golden/gguf.json
+holds, per case, what the reference converter wrote (sha256 and size of model.bf,
+model_info.json, vocab.json, merges.txt), its report, or its error text
+(make_gguf_golden.py).  Where oracle/_ref is built the reference also runs on the
+same files here and the outputs are compared byte for byte.  CPU only: the
+converter is host code.
+"""
+import ctypes as C
+import hashlib
+import json
+import os
+import sys
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLD = os.path.join(HERE, "golden")
+sys.path.insert(0, GOLD)
+
+import gguf_models as GM  # noqa: E402
+from jieyu_amd import api  # noqa: E402
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with open(os.path.join(GOLD, "gguf.json"), encoding="utf-8") as f:
+        return json.load(f)
+
+
+def digest(out):
+    res = {}
+    for f in GM.OUT_FILES:
+        p = os.path.join(out, f)
+        if os.path.exists(p):
+            data = open(p, "rb").read()
+            res[f] = [hashlib.sha256(data).hexdigest(), len(data)]
+    return res
+
+
+def convert(src, out, dtype, quant):
+    try:
+        info = api.gguf_convert(src, out, dtype, bool(quant))
+        return 0, [info[k] for k in api.GGUF_INFO], ""
+    except api.JieyuError as e:
+        return -1, None, str(e)
+
+
+@pytest.mark.parametrize("case", [c[0] for c in GM.CONVERT_CASES])
+def test_convert_matches_reference(tmp_path, gold, case):
+    _, model, dtype, quant, pre = next(c for c in GM.CONVERT_CASES if c[0] == case)
+    src = GM.MODELS[model]().write(str(tmp_path / (model + ".gguf")))
+    out = str(tmp_path / "out")
+    if pre is not None:  # an existing model_info.json is updated, its other keys kept
+        os.makedirs(out)
+        open(os.path.join(out, "model_info.json"), "w").write(pre)
+    rc, info, err = convert(src, out, dtype, quant)
+    assert rc == 0, err
+    want = gold["convert"][case]
+    assert info == want["info"]
+    got = digest(out)
+    for f in GM.OUT_FILES:
+        assert got.get(f) == want["files"].get(f), f"{case}: {f} differs (size {got.get(f, [0, 0])[1]} vs " \
+                                                    f"{want['files'].get(f, [0, 0])[1]})"
+
+
+@pytest.mark.parametrize("name", [b[0] for b in GM.bad_files()])
+def test_errors_match_reference(tmp_path, gold, name):
+    data = dict(GM.bad_files())[name]
+    src = str(tmp_path / (name + ".gguf"))
+    open(src, "wb").write(data)
+    out = str(tmp_path / "out")
+    rc, _, err = convert(src, out, 0, 1)
+    want = gold["errors"][name]
+    assert rc == want["rc"]
+    assert err == want["error"]
+    assert digest(out) == want["files"]  # what was written before the failure, byte for byte
+
+
+def test_converted_model_binds(tmp_path):
+    """the quantized conversion binds with jieyu's checks: k-quant matrices, Q6_K
+    embedding as the tied head"""
+    src = GM.llama_q4km().write(str(tmp_path / "m.gguf"))
+    out = str(tmp_path / "m")
+    api.gguf_convert(src, out, "f32", True)
+    hp = api.model_bind(out, 64)
+    assert hp["hidden"] == 256 and hp["vocab"] == 259 and hp["layers"] == 2
+    assert hp["embed_type"] == 7 and hp["lm_head_type"] == 7 and hp["layer_type"] == 5  # q6_K, q6_K, q4_K
+
+
+def test_perm_row_restores_adjacent_pairs(tmp_path):
+    """q rows come back in jieyu's adjacent-pair order: f32 output row j of a head is
+    GGUF row perm_row(j) = (j odd ? hd/2 + j/2 : j/2) of that head"""
+    import numpy as np
+    import gguf_writer as G
+    hidden, hd = 64, 16
+    g = GM.deepseek_f32()
+    q = np.arange(hidden * hidden, dtype=np.float32).reshape(hidden, hidden)  # GGUF rows (out) x in
+    g.tensors = [(n, s, t, q.tobytes() if n == "blk.0.attn_q.weight" else d) for (n, s, t, d) in g.tensors]
+    g.kv.append(("llama.attention.key_length", G.U32, hd, None))
+    src = g.write(str(tmp_path / "p.gguf"))
+    out = str(tmp_path / "p")
+    api.gguf_convert(src, out, "f32", True)
+    raw = open(os.path.join(out, "model.bf"), "rb").read()
+    n = int.from_bytes(raw[42:46], "little")
+    data_off = int.from_bytes(raw[46:50], "little")
+    for i in range(n):
+        e = raw[64 + 104 * i: 64 + 104 * (i + 1)]
+        if e[:64].split(b"\0")[0] == b"model.layers.0.self_attn.q_proj.weight":
+            off, nb = int.from_bytes(e[88:96], "little"), int.from_bytes(e[96:104], "little")
+            w = np.frombuffer(raw[data_off + off: data_off + off + nb], np.float32).reshape(hidden, hidden)  # [in][out]
+            perm = [(j // hd) * hd + ((j % hd) // 2 + (hd // 2 if j % 2 else 0)) for j in range(hidden)]
+            assert np.array_equal(w.T, q[perm])
+            return
+    pytest.fail("q_proj not found")
+
+
+def test_reference_live(tmp_path):
+    """the reference converter on the same GGUF bytes, compared file by file"""
+    import oracle
+    if not oracle.ref_available():
+        pytest.skip("oracle/_ref/libjyref.so not built")
+    ref = oracle.load_ref()
+    ref.jyref_gguf_convert.restype = C.c_int
+    ref.jyref_gguf_convert.argtypes = [C.c_char_p, C.c_char_p, C.c_int, C.c_int, C.c_void_p, C.c_char_p, C.c_int]
+    for case, model, dtype, quant, pre in GM.CONVERT_CASES[:5]:
+        src = GM.MODELS[model]().write(str(tmp_path / (model + ".gguf")))
+        a, b = str(tmp_path / (case + "-ref")), str(tmp_path / (case + "-ours"))
+        err = C.create_string_buffer(256)
+        assert ref.jyref_gguf_convert(src.encode(), a.encode(), dtype, quant, None, err, 256) == 0, err.value
+        convert(src, b, dtype, quant)
+        for f in GM.OUT_FILES:
+            assert open(os.path.join(a, f), "rb").read() == open(os.path.join(b, f), "rb").read(), (case, f)
