@@ -5,9 +5,9 @@ merges.txt -- what ``jieyu_load`` (include/jieyu_api.h) reads.  The writer lays
 model.bf out the way jieyu's own writer does (libs/model_libs/bfile.h:17-22,
 :124-135, :237-307): a 64-byte header, a 104-byte table entry per tensor, the
 data area starting at the 64-aligned end of the table, every tensor at a
-64-aligned offset.  2-D f32 weights are stored [in][out], Q8_0 weights
-[out][in/32] x 34 bytes, as jieyu's bind_model expects
-(libs/model_libs/pipeline.h:103-117).
+64-aligned offset.  2-D f32 / f16 weights are stored [in][out], block-quantized
+ones (Q8_0, Q4_K, Q5_K, Q6_K) [out][in/block] x block bytes, as jieyu's
+bind_model expects (libs/model_libs/pipeline.h:103-117).
 """
 import json
 import os
@@ -57,9 +57,19 @@ class Tensor:
         return Tensor(name, F32, a.shape, a.tobytes())
 
     @staticmethod
+    def f16(name, arr):
+        a = np.ascontiguousarray(arr, dtype="<f2")
+        return Tensor(name, F16, a.shape, a.tobytes())
+
+    @staticmethod
     def q8_0(name, rows, cols, blob):
         """blob: [rows][cols/32] x 34 bytes (fp16 scale + 32 int8), as jieyu stores it"""
         return Tensor(name, Q8_0, (rows, cols), np.asarray(blob, np.uint8).tobytes())
+
+    @staticmethod
+    def quant(name, dtype, rows, cols, blob):
+        """a block-quantized matrix (Q8_0 / Q4K / Q5K / Q6K): [rows][cols/block] blocks"""
+        return Tensor(name, dtype, (rows, cols), np.asarray(blob, np.uint8).tobytes())
 
 
 def write_bfile(path, tensors, hidden, layers, num_heads, num_kv_heads, head_dim, intermediate, vocab, mode=1):
@@ -132,20 +142,26 @@ def layer_name(l, suffix):
     return f"model.layers.{l}.{suffix}"
 
 
-def decoder_tensors(embed, lm_head, final_norm, layers, q8=None):
+def decoder_tensors(embed, lm_head, final_norm, layers, q8=None, quant=None):
     """Tensor list of a decoder in jieyu's names.
 
     layers: dicts with rms1, rms2 (float [hidden]) and Wq, Wk, Wv, Wo, W1, W2, W3.
-    f32 weights are [in][out] arrays; with q8 given (dict name -> (rows, cols,
-    blob)), the named weights are Q8_0 instead.  embed: [vocab][hidden] f32 or
-    Q8_0; lm_head: f32 [hidden][vocab], Q8_0 [vocab][hidden], or None (tied to the
-    embedding, which must then be Q8_0)."""
-    q8 = q8 or {}
+    Dense weights are [in][out] arrays, written f16 when the array is float16 and
+    f32 otherwise; with q8 (dict name -> (rows, cols, blob)) or quant (dict name ->
+    (dtype, rows, cols, blob)) given, the named weights are block-quantized instead.
+    embed: [vocab][hidden] dense or quantized; lm_head: dense [hidden][vocab],
+    quantized [vocab][hidden], or None (tied to the embedding, which must then be
+    quantized)."""
+    quant = dict(quant or {})
+    for name, (r, c, blob) in (q8 or {}).items():
+        quant[name] = (Q8_0, r, c, blob)
 
     def w(name, arr):
-        if name in q8:
-            r, c, blob = q8[name]
-            return Tensor.q8_0(name, r, c, blob)
+        if name in quant:
+            dt, r, c, blob = quant[name]
+            return Tensor.quant(name, dt, r, c, blob)
+        if arr is not None and np.asarray(arr).dtype == np.float16:
+            return Tensor.f16(name, arr)
         return Tensor.f32(name, arr)
 
     ts = [w("model.embed_tokens.weight", embed)]
@@ -163,7 +179,7 @@ def decoder_tensors(embed, lm_head, final_norm, layers, q8=None):
             if L.get(b) is not None:
                 ts.append(Tensor.f32(layer_name(l, f"self_attn.{b[1]}_proj.bias"), L[b]))
     ts.append(Tensor.f32("model.norm.weight", final_norm))
-    if lm_head is not None or "lm_head.weight" in q8:
+    if lm_head is not None or "lm_head.weight" in quant:
         ts.append(w("lm_head.weight", lm_head))
     return ts
 

@@ -133,3 +133,35 @@ def test_reference_live(tmp_path):
         convert(src, b, dtype, quant)
         for f in GM.OUT_FILES:
             assert open(os.path.join(a, f), "rb").read() == open(os.path.join(b, f), "rb").read(), (case, f)
+
+
+def test_bfile_writer_kquant_directory_binds(tmp_path):
+    """jieyu_amd.bfile writes k-quant, Q8_0 and f16 tensors that bind with jieyu's
+    checks, each slot keeping its own type"""
+    import numpy as np
+    import quant_models as QM
+    import jieyu_amd.bfile as B
+    m = QM.build_model("kq-mixed")
+    code = {QM.JY_Q8_0: B.Q8_0, QM.JY_Q4_K: B.Q4K, QM.JY_Q5_K: B.Q5K, QM.JY_Q6_K: B.Q6K}
+    names = dict(Wq="self_attn.q_proj.weight", Wk="self_attn.k_proj.weight", Wv="self_attn.v_proj.weight",
+                 Wo="self_attn.o_proj.weight", W1="mlp.gate_proj.weight", W2="mlp.down_proj.weight",
+                 W3="mlp.up_proj.weight")
+    H, F, qd, kvd, V = m["hidden"], m["inter"], m["heads"] * m["hd"], m["kv"] * m["hd"], m["vocab"]
+    dims = dict(Wq=(qd, H), Wk=(kvd, H), Wv=(kvd, H), Wo=(H, qd), W1=(F, H), W2=(H, F), W3=(F, H))
+    quant, layers = {}, []
+    for l, L in enumerate(m["layers"]):
+        layers.append(dict(rms1=L["rms1"], rms2=L["rms2"]))
+        for slot, nm in names.items():
+            t, blob = L[slot]
+            quant[B.layer_name(l, nm)] = (code[t], *dims[slot], blob)
+    quant["model.embed_tokens.weight"] = (code[m["embed"][0]], V, H, m["embed"][1])
+    quant["lm_head.weight"] = (code[m["lm"][0]], V, H, m["lm"][1])
+    ts = B.decoder_tensors(None, None, m["final"], layers, quant=quant)
+    hp = dict(hidden=H, layers=len(layers), num_heads=m["heads"], num_kv_heads=m["kv"], head_dim=m["hd"],
+              intermediate=F, vocab=V)
+    d = B.write_model_dir(str(tmp_path / "kq"), ts, hp)
+    got = api.model_bind(d, 32)
+    assert (got["embed_type"], got["lm_head_type"], got["layer_type"]) == (QM.JY_Q6_K, QM.JY_Q4_K, QM.JY_Q4_K)
+    # an f16 tensor round-trips as dtype F16
+    t = B.Tensor.f16("x", np.ones((2, 3), np.float16))
+    assert t.dtype == B.F16 and len(t.data) == 12
