@@ -115,6 +115,33 @@ def isolated_matvecs(jy, olib, iters=64):
     return res
 
 
+def isolated_other_types(jy, iters=64):
+    """The decode matvec of the other weight types jieyu binds (f16, Q4_K, Q5_K, Q6_K) at
+    Llama-3-8B's FFN shape 14336 x 4096 (random blocks, x ~ N(0,1)), rotating >1 GB of
+    copies; GB/s counts the weight bytes plus x and y."""
+    from jieyu_amd.model import JY_F16, JY_Q4_K, JY_Q5_K, JY_Q6_K
+    rng = np.random.default_rng(5)
+    res = {}
+    n, k = 14336, 4096
+    x = rng.standard_normal(k).astype(np.float32)
+    for name, t, (be, bb) in (("q4_K", JY_Q4_K, (256, 144)), ("q5_K", JY_Q5_K, (256, 176)),
+                              ("q6_K", JY_Q6_K, (256, 210)), ("f16", JY_F16, (1, 2))):
+        nbytes = n * (k // be) * bb
+        if t == JY_F16:
+            w = (0.02 * rng.standard_normal((k, n))).astype(np.float16).view(np.uint16)
+        else:
+            w = rng.integers(0, 256, (n * (k // be), bb), dtype=np.uint8)
+            dcol = 208 if t == JY_Q6_K else 0  # small fp16 scales keep the sums finite
+            w[:, dcol:dcol + 2] = rng.uniform(1e-5, 4e-5, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        copies = max(2, int(np.ceil(1.2e9 / nbytes)))
+        m = jy.WeightMatrix(w, t, n, k, copies=copies)
+        us = m.time(x, iters)
+        m.close()
+        algo = nbytes + k * 4 + n * 4
+        res[f"{name}_{n}x{k}"] = {"us": round(us, 3), "GB/s": round(algo / (us * 1e-6) / 1e9, 1)}
+    return res
+
+
 def copy_calibration(mb):
     """A plain device copy of known size for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE."""
     import torch
@@ -238,13 +265,15 @@ def main():
     log(f"  {K} steps: {wall_ms:.1f} ms wall ({dev_ms:.1f} ms device) -> {tok_s:.1f} tok/s, "
         f"{hbm_gbs:.0f} GB/s = {100 * hbm_gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s")
 
-    roof = iso = None
+    roof = iso = other = None
     if not args.no_kernel:
         log("dominant kernel in isolation ...")
         roof = dominant_kernel_roofline(jy, olib, d)
         log(f"  {roof['kernel']}: {roof['avg_launch_us']} us -> {roof['achieved']} GB/s")
         iso = isolated_matvecs(jy, olib)
         log(f"  isolated matvec shapes: {iso}")
+        other = isolated_other_types(jy)
+        log(f"  other weight types: {other}")
 
     cpu = None
     if not args.no_cpu:
@@ -271,7 +300,7 @@ def main():
         "prefill_ms": round(st.prefill_ms, 2), "prefill_tokens_s": round(args.prompt_len / (st.prefill_ms / 1e3), 1),
         "upload_s": round(st.upload_ms / 1e3, 2),
         "last_ids": ids[-8:].tolist(),
-        "roofline": roof, "cpu_baseline": cpu, "isolated_q8_matvec": iso,
+        "roofline": roof, "cpu_baseline": cpu, "isolated_q8_matvec": iso, "isolated_other_matvec": other,
     }
     print(json.dumps(out), flush=True)
 
