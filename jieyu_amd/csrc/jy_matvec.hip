@@ -177,9 +177,10 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
     // stage x (and with NORM the RMSNorm weights, into nws behind the staged vector),
     // four floats per load, several loads in flight per thread; zero past K, so
     // padding blocks contribute exact zeros.  The vector's first batch is requested
-    // before the weight prefetch so it does not queue behind it; both weight buffers
-    // are then in flight through the prologue and stay two buffers ahead of the
-    // compute afterwards.
+    // before the weight prefetch so it does not queue behind it.  Without NORM both
+    // weight buffers follow it at once; with NORM only the first does, and the second
+    // once the vector is in (a full prefetch ahead of the vector's later loads delays
+    // them).  The buffers then stay two ahead of the compute.
     uint4 wA[MV_U], dA[MV_U], wB[MV_U], dB[MV_U];
     float* nws = xs + 16 * XS;
     const int nk4 = K / 4;
@@ -196,9 +197,9 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
                 v[u] = (i < nv4 && i < nk4) ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 if (NORM) wv[u] = i < nk4 ? w4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
-            if (!NORM && b0 == 0) {
+            if (b0 == 0) {
                 load(wA, dA);
-                load(wB, dB);
+                if (!NORM) load(wB, dB);
             }
 #pragma unroll
             for (int u = 0; u < SU; u++) {
@@ -216,9 +217,8 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
     }
     lds_barrier();  // the weight prefetch stays in flight
     if (NORM) {
-        // the weights are first needed after the normalisation: their prefetch starts
-        // once the vector is in, so the vector's loads do not queue behind it
-        load(wA, dA);
+        // the second weight buffer, now that the vector is in: the weights are first
+        // needed after the normalisation
         load(wB, dB);
         // RMSNorm of the staged vector (libs/model_libs/rmsnorm/x86/x86_classic.txt:2-26):
         // lanes 0..15 of wave 0 run the 16 FMA chains (lane l: elements 16c+l, an 8-wide
