@@ -25,24 +25,28 @@ struct Q8Dev {
 
 // A Q4_K / Q5_K / Q6_K matrix of rows x cols (cols a multiple of 256), repacked so
 // that one 256-weight super-block of four rows is read by one wave, thread
-// t = ri*16 + g (row ri of the group, lane pair g) owning weights 32c + 2g and
-// 32c + 2g + 1 of the eight 32-weight steps c, as in the Q8_0 layout.  Chunk
-// = (row group, super-block), chunk index (R >> 2) * nsb + sb:
-//   nib : 512 B per chunk, 8 B per thread: nibble i = 2c + t is the low 4 bits
-//         of weight 32c + 2g + t
-//   hi  : Q5_K 2 B per thread (bit i = the fifth bit), Q6_K 4 B per thread
-//         (bits 2i, 2i+1 = the top two bits); absent for Q4_K
-//   hdr : 16 B per row: Q4_K / Q5_K the block's d, dmin and 12 scale bytes,
-//         Q6_K the 16 int8 scales
-//   d6  : Q6_K: the fp16 d of each row (4 per chunk)
-// Bytes per 256 weights stay 144 / 176 / 210; only the order changes.
+// t = ri*16 + g (row ri of the group, lane pair g) owning weights 32c + 2g + u
+// (u = 0, 1) of the eight 32-weight steps c, as in the Q8_0 layout.  Chunk =
+// (row group, super-block), chunk index (R >> 2) * nsb + sb.  A thread's 16 weights
+// are addressed as (target T, byte k): T = 2*(c >> 2) + u, k = c & 3, so that each
+// of its four 32-bit nibble words (T) holds one weight per byte after a mask.
+//   nib : 512 B per chunk, 8 B per thread: nibble 2c + u (c = 0..7) is the low 4
+//         bits of weight (c, u), so word 0 holds c = 0..3 and word 1 c = 4..7
+//   hi  : Q5_K 2 B per thread, bit 4T + k = the fifth bit of weight (T, k);
+//         Q6_K 4 B per thread, bits 8k + 2T, 8k + 2T + 1 = the top two bits
+//   hdr : 16 B per row: Q4_K / Q5_K the eight 6-bit scales then the eight 6-bit
+//         mins, one per byte; Q6_K the int8 scale of each step c for the row's
+//         first 16 weights (bytes 0..7) and last 16 (bytes 8..15)
+//   dm  : 4 B per row: fp16 d (and Q4_K / Q5_K dmin in the high half)
+// Bytes per 256 weights: 148 / 180 / 212 (GGML's 144 / 176 / 210 with the scales
+// unpacked).
 struct KQDev {
     int type = 0;  // JY_Q4_K | JY_Q5_K | JY_Q6_K
     int rows = 0, cols = 0, nsb = 0, groups = 0;
     uint8_t* nib = nullptr;
     uint8_t* hi = nullptr;
     uint8_t* hdr = nullptr;
-    uint16_t* d6 = nullptr;
+    uint32_t* dm = nullptr;
 };
 
 // One weight matrix of any bound type (jieyu's WMat, libs/date_libs/wmat.h:32-44):
@@ -162,7 +166,7 @@ int argmax_partials(int rows);
 
 // ---- weights of any type (jy_quant.hip)
 KQDev kq_shape(int type, int rows, int cols);
-size_t kq_bytes(const KQDev& w, int part);  // part 0 nib, 1 hi, 2 hdr, 3 d6
+size_t kq_bytes(const KQDev& w, int part);  // part 0 nib, 1 hi, 2 hdr, 3 dm
 // src: GGML blocks [rows][cols/256] (device copy) -> dst
 void launch_repack_kq(const uint8_t* src, const KQDev& dst, hipStream_t st);
 // y = W x for one token, in the reference's order for W's type (32-lane dot for

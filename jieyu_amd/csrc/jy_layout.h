@@ -46,38 +46,29 @@ __device__ __forceinline__ float q8_elem(const Q8Dev& W, int R, int k) {
 //                d1*q - n1 whether or not it is fused.
 //   Q6_K:        (d * sc) * (q - 32) with the int8 scale of each 16 weights: exact.
 
-__device__ __forceinline__ void kq_scale_min(int j, const uint8_t* q, int& sc, int& mn) {
-    if (j < 4) {
-        sc = q[j] & 63;
-        mn = q[j + 4] & 63;
-    } else {
-        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
-        mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
-    }
-}
-
 // weight (row R, column k) of a repacked k-quant matrix
 __device__ __forceinline__ float kq_elem(const KQDev& W, int R, int k) {
-    const int sb = k >> 8, e = k & 255, c = e >> 5, L = e & 31, g = L >> 1, i = 2 * c + (L & 1), ri = R & 3;
+    const int sb = k >> 8, e = k & 255, c = e >> 5, L = e & 31, g = L >> 1, u = L & 1, ri = R & 3;
+    const int T = 2 * (c >> 2) + u, kb = c & 3;
     const size_t chunk = (size_t)(R >> 2) * W.nsb + sb;
     const int t = ri * 16 + g;
-    const uint8_t nb = W.nib[(chunk * 64 + t) * 8 + (i >> 1)];
-    int q = (i & 1) ? (nb >> 4) : (nb & 15);
+    const uint8_t nb = W.nib[(chunk * 64 + t) * 8 + c];
+    int q = u ? (nb >> 4) : (nb & 15);
     const uint8_t* h = W.hdr + chunk * 64 + ri * 16;
+    const uint32_t dm = W.dm[chunk * 4 + ri];
+    const float d = half_to_float((uint16_t)(dm & 0xffffu));
     if (W.type == JY_Q6_K) {
         const uint32_t hb = *reinterpret_cast<const uint32_t*>(W.hi + (chunk * 64 + t) * 4);
-        q = (q | (int)(((hb >> (2 * i)) & 3u) << 4)) - 32;
-        const int8_t sc = (int8_t)h[(c >> 2) * 8 + (g >> 3) + 2 * (c & 3)];
-        return (half_to_float(W.d6[chunk * 4 + ri]) * (float)sc) * (float)q;
+        q = (q | (int)(((hb >> (8 * kb + 2 * T)) & 3u) << 4)) - 32;
+        const int8_t sc = (int8_t)h[(g >> 3) * 8 + c];
+        return (d * (float)sc) * (float)q;
     }
     if (W.type == JY_Q5_K) {
         const uint16_t hb = *reinterpret_cast<const uint16_t*>(W.hi + (chunk * 64 + t) * 2);
-        q += ((hb >> i) & 1) << 4;
+        q += ((hb >> (4 * T + kb)) & 1) << 4;
     }
-    int sc, mn;
-    kq_scale_min(c, h + 4, sc, mn);
-    const float d = half_to_float((uint16_t)(h[0] | (h[1] << 8))), dmin = half_to_float((uint16_t)(h[2] | (h[3] << 8)));
-    return __builtin_fmaf((float)q, d * (float)sc, -(dmin * (float)mn));
+    const float dmin = half_to_float((uint16_t)(dm >> 16));
+    return __builtin_fmaf((float)q, d * (float)h[c], -(dmin * (float)h[8 + c]));
 }
 
 // RMSNorm of one row already staged in LDS, by the whole workgroup, written to y

@@ -32,15 +32,26 @@ size_t kq_bytes(const KQDev& w, int part) {
         case 0: return chunks * 512;
         case 1: return w.type == JY_Q5_K ? chunks * 128 : w.type == JY_Q6_K ? chunks * 256 : 0;
         case 2: return chunks * 64;
-        default: return w.type == JY_Q6_K ? chunks * 8 : 0;
+        default: return chunks * 16;
     }
 }
 
 __host__ __device__ static inline int kq_block_bytes(int type) { return type == JY_Q4_K ? 144 : type == JY_Q5_K ? 176 : 210; }
 
-// one thread per (row, super-block): GGML block -> the thread-major pieces.
-// Weight 32c + L (L = 2g + t) of the block becomes nibble / high bits i = 2c + t of
-// thread (row & 3) * 16 + g.
+// get_scale_min_k4 (libs/matmul_libs/matmul_q.h:22-33): the 6-bit scale and min of
+// 32-weight step j of a Q4_K / Q5_K super-block
+__device__ __forceinline__ void kq_scale_min(int j, const uint8_t* q, int& sc, int& mn) {
+    if (j < 4) {
+        sc = q[j] & 63;
+        mn = q[j + 4] & 63;
+    } else {
+        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+// one thread per (row, super-block): GGML block -> the thread-major pieces.  Weight
+// 32c + L (L = 2g + u) of the block goes to thread (row & 3) * 16 + g as weight (c, u).
 __global__ void repack_kq_kernel(const uint8_t* __restrict__ src, KQDev W) {
     const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (id >= (size_t)W.rows * W.nsb) return;
@@ -50,34 +61,44 @@ __global__ void repack_kq_kernel(const uint8_t* __restrict__ src, KQDev W) {
     for (int g = 0; g < 16; g++) {
         uint64_t nib = 0;
         uint32_t hb = 0;
-        for (int i = 0; i < 16; i++) {
-            const int c = i >> 1, L = 2 * g + (i & 1);
-            uint32_t lo, hi;
-            if (W.type == JY_Q6_K) {  // matmul_q.h:78-96
-                const int nn = c >> 2, tq = c & 3;
-                const uint8_t qb = b[nn * 64 + L + 32 * (tq & 1)];
-                lo = tq < 2 ? (qb & 15u) : (qb >> 4);
-                hi = (b[128 + nn * 32 + L] >> (2 * tq)) & 3u;
-                hb |= hi << (2 * i);
-            } else {  // q4.h:23-33, matmul_q.h:52-76
-                const uint8_t* qs = b + (W.type == JY_Q4_K ? 16 : 48);
-                const uint8_t qb = qs[(c >> 1) * 32 + L];
-                lo = (c & 1) ? (qb >> 4) : (qb & 15u);
-                if (W.type == JY_Q5_K) {
-                    hi = (b[16 + L] >> c) & 1u;
-                    hb |= hi << i;
+        for (int c = 0; c < 8; c++)
+            for (int u = 0; u < 2; u++) {
+                const int L = 2 * g + u, T = 2 * (c >> 2) + u, kb = c & 3;
+                uint32_t lo;
+                if (W.type == JY_Q6_K) {  // matmul_q.h:78-96
+                    const int nn = c >> 2, tq = c & 3;
+                    const uint8_t qb = b[nn * 64 + L + 32 * (tq & 1)];
+                    lo = tq < 2 ? (qb & 15u) : (qb >> 4);
+                    hb |= ((b[128 + nn * 32 + L] >> (2 * tq)) & 3u) << (8 * kb + 2 * T);
+                } else {  // q4.h:23-33, matmul_q.h:52-76
+                    const uint8_t* qs = b + (W.type == JY_Q4_K ? 16 : 48);
+                    const uint8_t qb = qs[(c >> 1) * 32 + L];
+                    lo = (c & 1) ? (qb >> 4) : (qb & 15u);
+                    if (W.type == JY_Q5_K) hb |= ((b[16 + L] >> c) & 1u) << (4 * T + kb);
                 }
+                nib |= (uint64_t)lo << (4 * (2 * c + u));
             }
-            nib |= (uint64_t)lo << (4 * i);
-        }
         const size_t t = chunk * 64 + ri * 16 + g;
         *reinterpret_cast<uint64_t*>(W.nib + t * 8) = nib;
         if (W.type == JY_Q5_K) *reinterpret_cast<uint16_t*>(W.hi + t * 2) = (uint16_t)hb;
         if (W.type == JY_Q6_K) *reinterpret_cast<uint32_t*>(W.hi + t * 4) = hb;
     }
     uint8_t* h = W.hdr + chunk * 64 + ri * 16;
-    for (int j = 0; j < 16; j++) h[j] = W.type == JY_Q6_K ? b[192 + j] : b[j];
-    if (W.type == JY_Q6_K) W.d6[chunk * 4 + ri] = (uint16_t)(b[208] | (b[209] << 8));
+    if (W.type == JY_Q6_K) {
+        // scale of step c for weights L < 16 (bytes 0..7) and L >= 16 (bytes 8..15):
+        // sc[(c >> 2) * 8 + L / 16 + 2 * (c & 3)] of the block (matmul_q.h:83-90)
+        for (int half = 0; half < 2; half++)
+            for (int c = 0; c < 8; c++) h[half * 8 + c] = b[192 + (c >> 2) * 8 + half + 2 * (c & 3)];
+        W.dm[chunk * 4 + ri] = (uint32_t)(b[208] | (b[209] << 8));
+    } else {
+        for (int c = 0; c < 8; c++) {
+            int sc, mn;
+            kq_scale_min(c, b + 4, sc, mn);
+            h[c] = (uint8_t)sc;
+            h[8 + c] = (uint8_t)mn;
+        }
+        W.dm[chunk * 4 + ri] = (uint32_t)(b[0] | (b[1] << 8) | (b[2] << 16) | ((uint32_t)b[3] << 24));
+    }
 }
 
 void launch_repack_kq(const uint8_t* src, const KQDev& dst, hipStream_t st) {
@@ -87,67 +108,59 @@ void launch_repack_kq(const uint8_t* src, const KQDev& dst, hipStream_t st) {
 
 // ---------------------------------------------------------------- decode matvec
 
-// byte j (compile-time after unrolling) of the 12 scale bytes in words y, z, w
-__device__ __forceinline__ uint32_t sbyte(const uint4& h, int j) {
-    const uint32_t w = j < 4 ? h.y : (j < 8 ? h.z : h.w);
-    return (w >> (8 * (j & 3))) & 255u;
-}
+// byte j (a compile-time constant after unrolling) of a word, as a float: v_cvt_f32_ubyte
+__device__ __forceinline__ float ubyte_f(uint32_t w, int j) { return (float)((w >> (8 * j)) & 255u); }
 
-// the 16 weights of this thread in one chunk, fed to its two FMA lanes in order
+// the 16 weights of this thread in one chunk, fed to its two FMA lanes in order.
+// Target word T (= 2*(c >> 2) + u) holds weight (c, u) in byte c & 3 after the mask,
+// with the Q5_K / Q6_K high bits merged in above the nibble.
 template <int TYPE>
-__device__ __forceinline__ void kq_chunk(const uint2& nb, uint32_t hb, const uint4& h, uint16_t d6, int g,
+__device__ __forceinline__ void kq_chunk(const uint2& nb, uint32_t hb, const uint4& h, uint32_t dmw, int g,
                                          const float* xv, float& a0, float& a1) {
+    uint32_t wt[4] = {nb.x & 0x0F0F0F0Fu, (nb.x >> 4) & 0x0F0F0F0Fu, nb.y & 0x0F0F0F0Fu, (nb.y >> 4) & 0x0F0F0F0Fu};
+    const float d = half_to_float((uint16_t)(dmw & 0xffffu));
     if (TYPE == JY_Q6_K) {
-        const float d = half_to_float(d6);
-        const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
-        const int gb = g >> 3;  // weights 2g, 2g+1 take the scale of their 16-weight half
+        // bits 8k + 2T of hb -> bits 4, 5 of byte k of word T
+#pragma unroll
+        for (int T = 0; T < 4; T++) wt[T] |= (T < 2 ? hb << (4 - 2 * T) : hb >> (2 * T - 4)) & 0x30303030u;
+        const uint32_t s0 = g < 8 ? h.x : h.z, s1 = g < 8 ? h.y : h.w;  // the scales of this lane's half
 #pragma unroll
         for (int c = 0; c < 8; c++) {
-            const int base = (c >> 2) * 8 + 2 * (c & 3);
-            const int8_t sc = (int8_t)(hw[base >> 2] >> (8 * ((base & 3) + gb)));
+            const int8_t sc = (int8_t)((c < 4 ? s0 : s1) >> (8 * (c & 3)));
             const float ds = d * (float)sc;
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const int i = 2 * c + t;
-                const uint32_t word = i < 8 ? nb.x : nb.y;
-                const int q = (int)(((word >> (4 * (i & 7))) & 15u) | (((hb >> (2 * i)) & 3u) << 4)) - 32;
-                const float w = ds * (float)q;
-                if (t == 0)
-                    a0 = __builtin_fmaf(xv[i], w, a0);
+            for (int u = 0; u < 2; u++) {
+                // (d*sc) * (q - 32), the reference's expression; q - 32 is exact
+                const float w = ds * (ubyte_f(wt[2 * (c >> 2) + u], c & 3) - 32.0f);
+                if (u == 0)
+                    a0 = __builtin_fmaf(xv[2 * c], w, a0);
                 else
-                    a1 = __builtin_fmaf(xv[i], w, a1);
+                    a1 = __builtin_fmaf(xv[2 * c + 1], w, a1);
             }
         }
     } else {
-        const float d = half_to_float((uint16_t)(h.x & 0xffffu)), dmin = half_to_float((uint16_t)(h.x >> 16));
+        if (TYPE == JY_Q5_K) {
+            // bit 4T + k of hb -> bit 4 of byte k of word T: spread the nibble by a multiply
+#pragma unroll
+            for (int T = 0; T < 4; T++) wt[T] |= ((((hb >> (4 * T)) & 15u) * 0x00204081u) << 4) & 0x10101010u;
+        }
+        const float dmin = half_to_float((uint16_t)(dmw >> 16));
 #pragma unroll
         for (int c = 0; c < 8; c++) {
-            uint32_t sc, mn;  // get_scale_min_k4 (matmul_q.h:22-33)
-            if (c < 4) {
-                sc = sbyte(h, c) & 63u;
-                mn = sbyte(h, c + 4) & 63u;
-            } else {
-                sc = (sbyte(h, c + 4) & 15u) | ((sbyte(h, c - 4) >> 6) << 4);
-                mn = (sbyte(h, c + 4) >> 4) | ((sbyte(h, c) >> 6) << 4);
-            }
-            const float d1 = d * (float)sc, n1 = dmin * (float)mn;
+            const float d1 = d * ubyte_f(c < 4 ? h.x : h.y, c & 3), n1 = dmin * ubyte_f(c < 4 ? h.z : h.w, c & 3);
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const int i = 2 * c + t;
-                const uint32_t word = i < 8 ? nb.x : nb.y;
-                uint32_t q = (word >> (4 * (i & 7))) & 15u;
-                if (TYPE == JY_Q5_K) q |= ((hb >> i) & 1u) << 4;
-                const float w = __builtin_fmaf((float)q, d1, -n1);
-                if (t == 0)
-                    a0 = __builtin_fmaf(xv[i], w, a0);
+            for (int u = 0; u < 2; u++) {
+                const float w = __builtin_fmaf(ubyte_f(wt[2 * (c >> 2) + u], c & 3), d1, -n1);
+                if (u == 0)
+                    a0 = __builtin_fmaf(xv[2 * c], w, a0);
                 else
-                    a1 = __builtin_fmaf(xv[i], w, a1);
+                    a1 = __builtin_fmaf(xv[2 * c + 1], w, a1);
             }
         }
     }
 }
 
-static constexpr int KQ_U = 4;  // chunks whose loads are issued together
+static constexpr int KQ_U = 4;  // chunks per register buffer (two buffers)
 
 // one row group per wave, 4 waves per workgroup
 template <int TYPE, int EPI>
@@ -164,21 +177,27 @@ __global__ __launch_bounds__(256) void matvec_kq_kernel(KQDev W, const float* __
     const float* xrow = xs + g * XS;
     float a0 = 0.0f, a1 = 0.0f;
     const size_t c0 = (size_t)rg * nsb;
-    for (int s0 = 0; s0 < nsb; s0 += KQ_U) {
+    // two buffers of KQ_U chunks: the next buffer's loads are in flight while the
+    // current one is computed (chunk indices past the row clamp to its last chunk)
+    struct Buf {
         uint2 nb[KQ_U];
         uint32_t hb[KQ_U];
         uint4 h[KQ_U];
-        uint16_t d6[KQ_U];
+        uint32_t dm[KQ_U];
+    };
+    auto load = [&](Buf& b, int s0) {
 #pragma unroll
         for (int u = 0; u < KQ_U; u++) {
             const size_t c = c0 + min(s0 + u, nsb - 1);
-            nb[u] = *reinterpret_cast<const uint2*>(W.nib + (c * 64 + lane) * 8);
-            hb[u] = TYPE == JY_Q5_K   ? *reinterpret_cast<const uint16_t*>(W.hi + (c * 64 + lane) * 2)
-                    : TYPE == JY_Q6_K ? *reinterpret_cast<const uint32_t*>(W.hi + (c * 64 + lane) * 4)
-                                      : 0u;
-            h[u] = *reinterpret_cast<const uint4*>(W.hdr + c * 64 + r * 16);
-            d6[u] = TYPE == JY_Q6_K ? W.d6[c * 4 + r] : (uint16_t)0;
+            b.nb[u] = *reinterpret_cast<const uint2*>(W.nib + (c * 64 + lane) * 8);
+            b.hb[u] = TYPE == JY_Q5_K   ? *reinterpret_cast<const uint16_t*>(W.hi + (c * 64 + lane) * 2)
+                      : TYPE == JY_Q6_K ? *reinterpret_cast<const uint32_t*>(W.hi + (c * 64 + lane) * 4)
+                                        : 0u;
+            b.h[u] = *reinterpret_cast<const uint4*>(W.hdr + c * 64 + r * 16);
+            b.dm[u] = W.dm[c * 4 + r];
         }
+    };
+    auto compute = [&](const Buf& b, int s0) {
 #pragma unroll
         for (int u = 0; u < KQ_U; u++) {
             if (s0 + u < nsb) {
@@ -192,9 +211,17 @@ __global__ __launch_bounds__(256) void matvec_kq_kernel(KQDev W, const float* __
                     xv[4 * q + 2] = v.z;
                     xv[4 * q + 3] = v.w;
                 }
-                kq_chunk<TYPE>(nb[u], hb[u], h[u], d6[u], g, xv, a0, a1);
+                kq_chunk<TYPE>(b.nb[u], b.hb[u], b.h[u], b.dm[u], g, xv, a0, a1);
             }
         }
+    };
+    Buf A, B;
+    load(A, 0);
+    for (int s0 = 0; s0 < nsb; s0 += 2 * KQ_U) {
+        load(B, s0 + KQ_U);
+        compute(A, s0);
+        if (s0 + 2 * KQ_U < nsb) load(A, s0 + 2 * KQ_U);
+        compute(B, s0 + KQ_U);
     }
     // lanes 2g, 2g+1 -> the reference's reduction tree (as in the Q8_0 matvec)
     a0 += dpp_f<0x12C>(a0);

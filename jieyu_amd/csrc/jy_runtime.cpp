@@ -289,7 +289,7 @@ DevW put_w(jyhip_model* m, uint8_t* staging, const jy_wmat& src, int out, int in
         w.kq.nib = (uint8_t*)own(m, dalloc<uint8_t>(kq_bytes(w.kq, 0)));
         if (kq_bytes(w.kq, 1)) w.kq.hi = (uint8_t*)own(m, dalloc<uint8_t>(kq_bytes(w.kq, 1)));
         w.kq.hdr = (uint8_t*)own(m, dalloc<uint8_t>(kq_bytes(w.kq, 2)));
-        if (kq_bytes(w.kq, 3)) w.kq.d6 = (uint16_t*)own(m, dalloc<uint8_t>(kq_bytes(w.kq, 3)));
+        w.kq.dm = (uint32_t*)own(m, dalloc<uint8_t>(kq_bytes(w.kq, 3)));
         CK(hipMemcpy(staging, src.data, nb, hipMemcpyHostToDevice));
         launch_repack_kq(staging, w.kq, m->stream);
         CK(hipGetLastError());
