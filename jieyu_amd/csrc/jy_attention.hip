@@ -971,6 +971,7 @@ void launch_attention(const AttnArgs& a, hipStream_t st) {
 
 hipError_t matvec_init();
 hipError_t quant_init();
+hipError_t dense_init();
 
 hipError_t kernels_init() {
     int dev = 0, mx = 0;
@@ -982,6 +983,7 @@ hipError_t kernels_init() {
                             hipFuncAttributeMaxDynamicSharedMemorySize, mx - 2048);
     if (e != hipSuccess) return e;
     e = quant_init();
+    if (e == hipSuccess) e = dense_init();
     if (e != hipSuccess) return e;
     return matvec_init();
 }

@@ -112,10 +112,10 @@ void launch_matvec_q8(const Q8Dev& W, const float* x, const float* norm_w, float
 // NORM), and what one workgroup may take (valid after kernels_init)
 size_t matvec_lds_bytes(int cols, bool norm);
 size_t matvec_lds_limit();
-// f32 [K][N] matvec, fma chain over k; EPI_SWIGLU takes B2 as the up matrix.
-void launch_matvec_f32(const float* B, const float* B2, int K, int N, const float* x, float* out,
-                       const float* aux, Epi epi, hipStream_t st);
-// f16 [K][N] matvec (halves converted exactly), fma chain over k
+// dense [K][N] matvec (f32, or f16 converted exactly), fma chain over k per output
+// column: EPI_STORE / EPI_BIAS / EPI_RESID
+void launch_matvec_f32(const float* B, int K, int N, const float* x, float* out, const float* aux, Epi epi,
+                       hipStream_t st);
 void launch_matvec_f16(const uint16_t* B, int K, int N, const float* x, float* out, const float* aux, Epi epi,
                        hipStream_t st);
 // prefill GEMMs, C[m][N] (+ epilogue: EPI_STORE / EPI_BIAS / EPI_RESID)

@@ -136,58 +136,174 @@ void launch_rmsnorm(const float* X, float* Y, const float* w, int n, int rows, h
 // ---------------------------------------------------------------- dense matvec (decode, [K][N] weights)
 
 // f32 or f16 weights (an f16 weight converts to float exactly): per output an fma
-// chain over k from 0 (libs/matmul_libs/x86/x86_classic.txt:2-16, matmul_f16.h:19-41)
+// chain over k from 0 (libs/matmul_libs/x86/x86_classic.txt:2-16, matmul_f16.h:19-41).
+// The chains are sequential in k, so the parallelism is one chain per output
+// column.  One workgroup owns 64 columns: all 256 threads stream blocks of RB rows
+// of the tile (16-byte row pieces, plus the block's slice of x) into a
+// double-buffered, column-transposed LDS tile while wave 0 runs the 64 chains over
+// the previous block, one 16-byte LDS read per PER steps.  Rows past K and columns
+// past N read as zeros; a zero product leaves a chain unchanged (it starts at +0
+// and never becomes -0).
 __device__ __forceinline__ float dense_w(const float* B, size_t i) { return B[i]; }
 __device__ __forceinline__ float dense_w(const uint16_t* B, size_t i) { return half_to_float(B[i]); }
 
-template <typename T, int EPI>
-__global__ __launch_bounds__(256) void matvec_dense_kernel(const T* __restrict__ B, const T* __restrict__ B2, int K,
-                                                           int N, const float* __restrict__ x,
-                                                           float* __restrict__ out, const float* __restrict__ aux) {
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= N) return;
-    float acc = 0.0f, acc2 = 0.0f;
-#pragma unroll 8
-    for (int p = 0; p < K; p++) {
-        const float xv = x[p];
-        acc = __builtin_fmaf(xv, dense_w(B, (size_t)p * N + j), acc);
-        if (EPI == EPI_SWIGLU) acc2 = __builtin_fmaf(xv, dense_w(B2, (size_t)p * N + j), acc2);
+static constexpr int DN_COLS = 64;
+template <typename T> struct DnShape {
+    static constexpr int RB = sizeof(T) == 2 ? 512 : 256;  // rows per block (64 KiB of tile; a multiple of 8*PER)
+    static constexpr int PER = 16 / (int)sizeof(T);         // elements per 16-byte piece
+    static constexpr int LPR = DN_COLS / PER;               // pieces per tile row
+    static constexpr int LOADS = RB * LPR / 256;            // pieces per thread per block
+    static constexpr int CS = RB + 8;                       // LDS column stride (elements)
+    static constexpr size_t lds() { return (size_t)2 * DN_COLS * CS * sizeof(T) + (size_t)2 * RB * sizeof(float); }
+};
+
+template <typename T>
+__device__ __forceinline__ void dn_unpack(const uint4& v, T* e);
+template <> __device__ __forceinline__ void dn_unpack<float>(const uint4& v, float* e) {
+    e[0] = __builtin_bit_cast(float, v.x);
+    e[1] = __builtin_bit_cast(float, v.y);
+    e[2] = __builtin_bit_cast(float, v.z);
+    e[3] = __builtin_bit_cast(float, v.w);
+}
+template <> __device__ __forceinline__ void dn_unpack<uint16_t>(const uint4& v, uint16_t* e) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        e[2 * i] = (uint16_t)(w[i] & 0xffffu);
+        e[2 * i + 1] = (uint16_t)(w[i] >> 16);
     }
-    if (EPI == EPI_STORE) out[j] = acc;
-    if (EPI == EPI_BIAS) out[j] = acc + aux[j];
-    if (EPI == EPI_RESID) out[j] = out[j] + acc;
-    if (EPI == EPI_SWIGLU) out[j] = silu_ref(acc) * acc2;
+}
+
+template <typename T, int EPI>
+__global__ __launch_bounds__(256) void matvec_dense_kernel(const T* __restrict__ B, int K, int N,
+                                                           const float* __restrict__ x, float* __restrict__ out,
+                                                           const float* __restrict__ aux) {
+    using S = DnShape<T>;
+    constexpr int RB = S::RB, PER = S::PER, LPR = S::LPR, LOADS = S::LOADS, CS = S::CS;
+    extern __shared__ __align__(16) unsigned char dsm[];
+    T* tile = reinterpret_cast<T*>(dsm);                                          // [2][64][CS]
+    float* xb = reinterpret_cast<float*>(dsm + (size_t)2 * DN_COLS * CS * sizeof(T));  // [2][RB]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j0 = blockIdx.x * DN_COLS;
+    const bool vec = ((size_t)N * sizeof(T)) % 16 == 0;
+    const int nblk = (K + RB - 1) / RB;
+    constexpr int XL = (RB + 255) / 256;  // x values per thread per block
+    uint4 v[LOADS];
+    float xv[XL];
+    // block b's pieces into registers: piece e = tid + 256u is row e / LPR, columns
+    // (e % LPR) * PER .. + PER - 1; rows tid, tid + 256, ... of the block's x too
+    auto gload = [&](int b) {
+#pragma unroll
+        for (int u = 0; u < LOADS; u++) {
+            const int e = tid + 256 * u, row = b * RB + e / LPR, col = j0 + (e % LPR) * PER;
+            if (row < K && vec && col + PER <= N) {
+                v[u] = *reinterpret_cast<const uint4*>(B + (size_t)row * N + col);
+            } else {
+                T el[PER];
+#pragma unroll
+                for (int k = 0; k < PER; k++) el[k] = (row < K && col + k < N) ? B[(size_t)row * N + col + k] : (T)0;
+                __builtin_memcpy(&v[u], el, 16);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < XL; i++) {
+            const int rr = tid + 256 * i;
+            if (rr < RB) xv[i] = b * RB + rr < K ? x[b * RB + rr] : 0.0f;
+        }
+    };
+    auto lstore = [&](int buf) {
+        T* tb = tile + (size_t)buf * DN_COLS * CS;
+#pragma unroll
+        for (int u = 0; u < LOADS; u++) {
+            const int e = tid + 256 * u, r = e / LPR, c0 = (e % LPR) * PER;
+            T el[PER];
+            dn_unpack<T>(v[u], el);
+            // row r of column c sits at r ^ (PER * (piece & 7)): the pieces of one store
+            // instruction then fall in different LDS banks, and a column's rows stay
+            // in aligned runs of PER for the 16-byte reads
+            const int rs = r ^ (PER * ((e % LPR) & 7));
+#pragma unroll
+            for (int k = 0; k < PER; k++) tb[(size_t)(c0 + k) * CS + rs] = el[k];
+        }
+#pragma unroll
+        for (int i = 0; i < XL; i++) {
+            const int rr = tid + 256 * i;
+            if (rr < RB) xb[buf * RB + rr] = xv[i];
+        }
+    };
+    float acc = 0.0f;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int b = 0; b < nblk; b++) {
+        const int buf = b & 1;
+        if (b + 1 < nblk) gload(b + 1);
+        if (wave == 0) {
+            const T* col = tile + (size_t)buf * DN_COLS * CS + (size_t)lane * CS;
+            const float* xr = xb + buf * RB;
+            const int swz = PER * ((lane / PER) & 7);
+#pragma unroll 4
+            for (int p = 0; p < RB; p += PER) {
+                T el[PER];
+                dn_unpack<T>(*reinterpret_cast<const uint4*>(col + (p ^ swz)), el);
+#pragma unroll
+                for (int k = 0; k < PER; k++) acc = __builtin_fmaf(xr[p + k], dense_w(el, k), acc);
+            }
+        }
+        if (b + 1 < nblk) lstore(buf ^ 1);
+        __syncthreads();
+    }
+    const int j = j0 + lane;
+    if (wave == 0 && j < N) {
+        if (EPI == EPI_STORE) out[j] = acc;
+        if (EPI == EPI_BIAS) out[j] = acc + aux[j];
+        if (EPI == EPI_RESID) out[j] = out[j] + acc;
+    }
 }
 
 template <typename T>
-static void matvec_dense(const T* B, const T* B2, int K, int N, const float* x, float* out, const float* aux, Epi epi,
+static void matvec_dense(const T* B, int K, int N, const float* x, float* out, const float* aux, Epi epi,
                          hipStream_t st) {
-    const dim3 grid((unsigned)((N + 255) / 256)), block(256);
+    const dim3 grid((unsigned)((N + DN_COLS - 1) / DN_COLS)), block(256);
+    const size_t lds = DnShape<T>::lds();
     switch (epi) {
     case EPI_STORE:
-        hipLaunchKernelGGL((matvec_dense_kernel<T, EPI_STORE>), grid, block, 0, st, B, B2, K, N, x, out, aux);
+        hipLaunchKernelGGL((matvec_dense_kernel<T, EPI_STORE>), grid, block, lds, st, B, K, N, x, out, aux);
         break;
     case EPI_BIAS:
-        hipLaunchKernelGGL((matvec_dense_kernel<T, EPI_BIAS>), grid, block, 0, st, B, B2, K, N, x, out, aux);
+        hipLaunchKernelGGL((matvec_dense_kernel<T, EPI_BIAS>), grid, block, lds, st, B, K, N, x, out, aux);
         break;
     case EPI_RESID:
-        hipLaunchKernelGGL((matvec_dense_kernel<T, EPI_RESID>), grid, block, 0, st, B, B2, K, N, x, out, aux);
-        break;
-    case EPI_SWIGLU:
-        hipLaunchKernelGGL((matvec_dense_kernel<T, EPI_SWIGLU>), grid, block, 0, st, B, B2, K, N, x, out, aux);
+        hipLaunchKernelGGL((matvec_dense_kernel<T, EPI_RESID>), grid, block, lds, st, B, K, N, x, out, aux);
         break;
     default: break;
     }
 }
 
-void launch_matvec_f32(const float* B, const float* B2, int K, int N, const float* x, float* out, const float* aux,
-                       Epi epi, hipStream_t st) {
-    matvec_dense<float>(B, B2, K, N, x, out, aux, epi, st);
+void launch_matvec_f32(const float* B, int K, int N, const float* x, float* out, const float* aux, Epi epi,
+                       hipStream_t st) {
+    matvec_dense<float>(B, K, N, x, out, aux, epi, st);
 }
 
 void launch_matvec_f16(const uint16_t* B, int K, int N, const float* x, float* out, const float* aux, Epi epi,
                        hipStream_t st) {
-    matvec_dense<uint16_t>(B, nullptr, K, N, x, out, aux, epi, st);
+    matvec_dense<uint16_t>(B, K, N, x, out, aux, epi, st);
+}
+
+template <typename T>
+static hipError_t dense_attr() {
+    hipError_t e = hipSuccess;
+    for (const void* f : {reinterpret_cast<const void*>(&matvec_dense_kernel<T, EPI_STORE>),
+                          reinterpret_cast<const void*>(&matvec_dense_kernel<T, EPI_BIAS>),
+                          reinterpret_cast<const void*>(&matvec_dense_kernel<T, EPI_RESID>)})
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)DnShape<T>::lds());
+    return e;
+}
+
+hipError_t dense_init() {
+    const hipError_t a = dense_attr<float>(), b = dense_attr<uint16_t>();
+    return a != hipSuccess ? a : b;
 }
 
 // ---------------------------------------------------------------- prefill GEMMs (m > 1)

@@ -254,7 +254,7 @@ static void mv_kq(const KQDev& W, const float* x, float* out, Epi epi, const flo
 void launch_mv(const DevW& W, const float* x, float* out, Epi epi, const float* aux, hipStream_t st) {
     switch (W.type) {
         case JY_F32:
-            launch_matvec_f32(static_cast<const float*>(W.dense), nullptr, W.in, W.out, x, out, aux, epi, st);
+            launch_matvec_f32(static_cast<const float*>(W.dense), W.in, W.out, x, out, aux, epi, st);
             break;
         case JY_F16: launch_matvec_f16(static_cast<const uint16_t*>(W.dense), W.in, W.out, x, out, aux, epi, st); break;
         case JY_Q8_0: {

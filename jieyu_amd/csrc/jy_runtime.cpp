@@ -534,17 +534,19 @@ void run_decode_layers(jyhip_model* m, const KVDev& kv, const int* state, int po
             launch_mv(D.w[5], w.h, w.X, EPI_RESID, nullptr, st);
         } else {
             launch_rmsnorm(w.X, w.xn, D.rms1, H, 1, st);
-            launch_matvec_f32(D.f_qkv, nullptr, H, NQ, w.xn, w.qkv, D.bqkv, D.bqkv ? EPI_BIAS : EPI_STORE, st);
+            launch_matvec_f32(D.f_qkv, H, NQ, w.xn, w.qkv, D.bqkv, D.bqkv ? EPI_BIAS : EPI_STORE, st);
             launch_rope_pack(w.qkv, 1, pos0, state, m->nh, m->nkv, m->hd, m->cos_t, m->sin_t, kv, l, w.q8, w.qsc, st);
             at.fused = false;
             at.q8 = w.q8;
             at.qsc = w.qsc;
             at.row0 = 0;
             launch_attention(at, st);
-            launch_matvec_f32(D.f_o, nullptr, m->qd, H, w.att, w.X, nullptr, EPI_RESID, st);
+            launch_matvec_f32(D.f_o, m->qd, H, w.att, w.X, nullptr, EPI_RESID, st);
             launch_rmsnorm(w.X, w.xn, D.rms2, H, 1, st);
-            launch_matvec_f32(D.f_w1, D.f_w3, H, F, w.xn, w.h, nullptr, EPI_SWIGLU, st);
-            launch_matvec_f32(D.f_w2, nullptr, F, H, w.h, w.X, nullptr, EPI_RESID, st);
+            launch_matvec_f32(D.f_w1, H, F, w.xn, w.g, nullptr, EPI_STORE, st);
+            launch_matvec_f32(D.f_w3, H, F, w.xn, w.u, nullptr, EPI_STORE, st);
+            launch_silu_mul(w.g, w.u, 0, 1, F, w.h, st);  // silu(gate) * up, as the fused form computed it
+            launch_matvec_f32(D.f_w2, F, H, w.h, w.X, nullptr, EPI_RESID, st);
         }
         if (layer_out_host) {
             CK(hipMemcpyAsync(layer_out_host + (size_t)l * H, w.X, sizeof(float) * H, hipMemcpyDeviceToHost, st));
@@ -658,7 +660,7 @@ void final_and_head(jyhip_model* m, const float* xlast, bool argmax, int neos) {
         launch_mv(m->lm_w, m->ws.xn, m->logits, EPI_STORE, nullptr, m->stream);
     } else {
         launch_rmsnorm(xlast, m->ws.xn, m->final_rms, m->H, 1, m->stream);
-        launch_matvec_f32(m->lm_f32, nullptr, m->H, m->V, m->ws.xn, m->logits, nullptr, EPI_STORE, m->stream);
+        launch_matvec_f32(m->lm_f32, m->H, m->V, m->ws.xn, m->logits, nullptr, EPI_STORE, m->stream);
     }
 }
 
