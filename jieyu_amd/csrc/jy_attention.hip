@@ -66,12 +66,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a, in
     const int8_t* K = a.kv.k + head * a.kv.max_seq * hd;
     const float* KS = a.kv.ks + head * a.kv.max_seq;
 
-    // ---- the keys: their loads depend only on the position, so they are in flight
-    // while the token's vectors are quantised (issued after the token's own loads,
-    // which are on the critical path and would otherwise queue behind them).  One
-    // key's 16-byte pieces sit on LP adjacent lanes (the pieces of hd rounded up to a
-    // power of two); a wave covers KW = 64/LP keys per load and each lane ATT_U loads
-    // (kc = 4*KW*ATT_U).
+    // ---- the keys first: their loads depend only on the position, so they are in
+    // flight while the token's vectors are quantised.  One key's 16-byte pieces sit
+    // on LP adjacent lanes (the pieces of hd rounded up to a power of two); a wave
+    // covers KW = 64/LP keys per load and each lane ATT_U loads (kc = 4*KW*ATT_U).
     const bool vec = (hd & 15) == 0;
     const int P = hd >> 4;
     int LP = 1;
@@ -80,15 +78,13 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a, in
     const bool live = vec && piece < P;
     int4 k4[ATT_U];
     float ksv[ATT_U];
-    auto load_keys = [&]() {
 #pragma unroll
-        for (int u = 0; u < ATT_U; u++) {
-            const int j = j0 + (u * (ATT_THREADS / 64) + wave) * KW + kl;
-            const int jc = min(j, jend - 1);
-            k4[u] = live ? *reinterpret_cast<const int4*>(K + (size_t)jc * hd + piece * 16) : make_int4(0, 0, 0, 0);
-            ksv[u] = vec ? KS[jc] : 0.0f;
-        }
-    };
+    for (int u = 0; u < ATT_U; u++) {
+        const int j = j0 + (u * (ATT_THREADS / 64) + wave) * KW + kl;
+        const int jc = min(j, jend - 1);
+        k4[u] = live ? *reinterpret_cast<const int4*>(K + (size_t)jc * hd + piece * 16) : make_int4(0, 0, 0, 0);
+        ksv[u] = vec ? KS[jc] : 0.0f;
+    }
 
     // ---- this token's q (and, fused, k and v) as int8: absmax, lrintf (kv_pack_q8,
     // attention_q8.h:29-35); wave w takes items w, w+4, w+8 with all their loads
@@ -110,7 +106,6 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a, in
                 }
             }
         }
-        load_keys();
 #pragma unroll
         for (int t = 0; t < 3; t++) {
             const int i = wave + 4 * t;
@@ -135,7 +130,6 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a, in
             }
         }
     } else {
-        load_keys();
         for (int i = tid; i < gh * hd; i += blockDim.x) {
             const int hh = i / hd, d = i - hh * hd;
             qv8[hh][d] = a.q8[((size_t)r * nh + h0 + hh) * hd + d];
@@ -847,27 +841,19 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_softmax_pv_kernel(AttnArgs a
     }
     float o = 0.0f;
     if (nk <= ATT_ECAP) {
-        // scores -> LDS, max, e_j in place; every load is issued before the first is
-        // used (a loop would wait for each in turn)
-        constexpr int NV = ATT_ECAP / ATT_THREADS;
-        float sv[NV];
-#pragma unroll
-        for (int k = 0; k < NV; k++) {
-            const int j = tid + k * ATT_THREADS;
-            sv[k] = j < nk ? S[j] : -1e30f;
-        }
+        // scores -> LDS, max, e_j in place
         float lmax = -1e30f;
-#pragma unroll
-        for (int k = 0; k < NV; k++) {
-            const int j = tid + k * ATT_THREADS;
-            if (j < nk) E[j] = sv[k];
-            lmax = fmaxf(lmax, sv[k]);
+        for (int j = tid; j < nk; j += blockDim.x) {
+            const float s = S[j];
+            E[j] = s;
+            lmax = fmaxf(lmax, s);
         }
         const float mx = att_block_max(lmax, red);
         // e_j, and exact zeros up to a multiple of 64 keys so the chains need no tail
         const int nk64 = (nk + 63) & ~63;
         for (int j = tid; j < nk64; j += blockDim.x) E[j] = j < nk ? expf_tab(E[j] - mx, exp_tab) : 0.0f;
         // the V scales of this thread's keys, in flight through the sum chain
+        constexpr int NV = ATT_ECAP / ATT_THREADS;
         float vsr[NV];
 #pragma unroll
         for (int k = 0; k < NV; k++) {
