@@ -67,17 +67,18 @@ def pmc_traffic(path=PMC_SUMMARY):
     return None
 
 
-def dominant_kernel_roofline(jy, olib, d, iters=64):
+def dominant_kernel_roofline(jy, d, iters=64):
     """The decode step's gate/up launch (2F x hidden interleaved rows, RMSNorm prologue,
     SwiGLU epilogue), timed in isolation with HIP events on its stream over enough
     copies to defeat the 256 MiB infinity cache."""
     rows, cols = 2 * d.intermediate, d.hidden
     nbytes = q8b(rows, cols)
     copies = max(2, int(np.ceil(1.2e9 / nbytes)))
+    syn = jy.lib()
     x = np.zeros(rows * cols, np.float32)
-    olib.jysyn_normal_fill(11, 5, 0.02, ptr(x), x.size)
+    syn.jysyn_normal_fill(11, 5, 0.02, ptr(x), x.size)
     w = np.zeros(nbytes, np.uint8)
-    olib.jysyn_quantize_q8_0(ptr(x), ptr(w), x.size)
+    syn.jysyn_quantize_q8_0(ptr(x), ptr(w), x.size)
     del x
     xin = np.random.default_rng(0).standard_normal(cols).astype(np.float32)
     m = jy.Q8Matrix(w, rows, cols, copies=copies)
@@ -91,21 +92,22 @@ def dominant_kernel_roofline(jy, olib, d, iters=64):
             "bytes_per_launch": algo, "avg_launch_us": round(us, 3), "launches": iters, "copies": copies}
 
 
-def isolated_matvecs(jy, olib, iters=64):
+def isolated_matvecs(jy, iters=64):
     """The plain Q8 matvec at the isolated-kernel shapes (int8 ~ U[-127,127], scales
     U(0.001,0.01), x ~ N(0,1), seed 1), rotating >1 GB of copies."""
+    syn = jy.lib()
     res = {}
     for rows, cols in ((4096, 4096), (14336, 4096), (4096, 14336)):
         nb = rows * (cols // 32)
         q = np.zeros(nb * 32, np.int32)
-        olib.jysyn_uniform_int_fill(1, 11, -127, 127, ptr(q), q.size)
+        syn.jysyn_uniform_int_fill(1, 11, -127, 127, ptr(q), q.size)
         dsc = np.zeros(nb, np.float32)
-        olib.jysyn_uniform_fill(1, 12, 0.001, 0.01, ptr(dsc), dsc.size)
+        syn.jysyn_uniform_fill(1, 12, 0.001, 0.01, ptr(dsc), dsc.size)
         blk = np.zeros((nb, 34), np.uint8)
         blk[:, 0:2] = dsc.astype(np.float16).view(np.uint8).reshape(nb, 2)
         blk[:, 2:] = q.astype(np.int8).view(np.uint8).reshape(nb, 32)
         x = np.zeros(cols, np.float32)
-        olib.jysyn_normal_fill(1, 13, 1.0, ptr(x), cols)
+        syn.jysyn_normal_fill(1, 13, 1.0, ptr(x), cols)
         copies = max(2, int(np.ceil(1.2e9 / blk.size)))
         m = jy.Q8Matrix(blk.reshape(-1), rows, cols, copies=copies)
         us = m.time(x, iters)
@@ -139,6 +141,77 @@ def isolated_other_types(jy, iters=64):
         m.close()
         algo = nbytes + k * 4 + n * 4
         res[f"{name}_{n}x{k}"] = {"us": round(us, 3), "GB/s": round(algo / (us * 1e-6) / 1e9, 1)}
+    return res
+
+
+def pack_kv_rows(x):
+    """float32 [npos][nkv][hd] -> int8 rows and one fp32 scale per (position, head), the
+    cache's own format (libs/model_libs/attention/attention_q8.h:20-37: absmax / 127 scale, round to
+    nearest even, clamp to +-127)."""
+    amax = np.abs(x).max(axis=-1)
+    ok = amax > 1e-8
+    inv = np.where(ok, np.float32(127.0) / np.where(ok, amax, 1), 0).astype(np.float32)
+    sc = np.where(ok, amax / np.float32(127.0), 0).astype(np.float32)
+    q = np.rint(np.clip(x * inv[..., None], -127, 127)).astype(np.int8)
+    return q, sc
+
+
+# (name, prompt tokens, new tokens, positions pre-filled in the cache before the prompt)
+OTHER_CONFIGS = (("tiny-f32", 16, 128, 0), ("qwen2.5-0.5b", 512, 256, 0), ("qwen2.5-7b", 1, 128, 32768))
+
+
+def other_config(jy, name, prompt_len, n_new, prefilled):
+    """Decode rate of one more model workload through the same session path.  With
+    `prefilled` > 0 the cache first holds that many positions of N(0,1) K/V (one draw,
+    packed like the cache's own rows, written to every layer), and the session resumes
+    over it: the prompt's last token runs at position `prefilled`, then n_new - 1 graph
+    steps are timed."""
+    from jieyu_amd.model import Synth, synth_config
+    cfg = synth_config(name)
+    t = time.time()
+    syn = Synth(jy.lib(), cfg)
+    d = syn.desc
+    max_seq = (prefilled + prompt_len + n_new + 7) // 8 * 8
+    g = jy.GpuModel(d, max_seq)
+    gen_s = time.time() - t
+    prompt = np.zeros(prefilled + prompt_len, np.int32)
+    jy.lib().jysyn_uniform_int_fill(cfg.seed, 99, 0, d.vocab_size - 1, ptr(prompt), len(prompt))
+    kv = None
+    if prefilled:
+        kv = g.kv(max_seq)
+        nkv, hd = d.num_kv_heads, d.head_dim
+        kf = np.zeros(prefilled * nkv * hd, np.float32)
+        jy.lib().jysyn_normal_fill(9, 1000, 1.0, ptr(kf), kf.size)
+        k8, ks = pack_kv_rows(kf.reshape(prefilled, nkv, hd))
+        jy.lib().jysyn_normal_fill(9, 1001, 1.0, ptr(kf), kf.size)
+        v8, vs = pack_kv_rows(kf.reshape(prefilled, nkv, hd))
+        del kf
+        for layer in range(d.num_layers):
+            kv.write(layer, 0, k8, ks, v8, vs)
+        kv.set_len(prefilled)
+    sess = g.session(prompt, n_new, max_seq=max_seq, kv=kv, resume=bool(prefilled))
+    pre_ms = sess.stats().prefill_ms
+    steps = n_new - 1
+    t0 = time.perf_counter()
+    made = sess.step(steps)
+    wall = time.perf_counter() - t0
+    sess.close()
+    assert made == steps, f"{name}: produced {made} of {steps} steps"
+    p0 = prefilled + prompt_len
+    nbytes = sum(token_bytes(d, g.weight_bytes, p) for p in range(p0, p0 + steps))
+    res = {"decode_tokens_s": round(steps / wall, 2), "ms_per_step": round(wall * 1e3 / steps, 4),
+           "hbm_frac": round(nbytes / wall / 1e9 / HBM_PEAK_GBS, 4),
+           "prompt_tokens": prompt_len, "prefill_ms": round(pre_ms, 2), "timed_steps": steps,
+           "positions": [p0, p0 + steps - 1], "weights": "f32" if d.embed.type == 0 else "Q8_0"}
+    if prefilled:
+        res["prefilled_kv_positions"] = prefilled
+    else:
+        res["prefill_tokens_s"] = round(prompt_len / (pre_ms / 1e3), 1)
+    if kv is not None:
+        kv.close()
+    g.close()
+    syn.close()
+    log(f"  {name}: {res} (model built in {gen_s:.1f} s)")
     return res
 
 
@@ -208,6 +281,7 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=96)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernel", action="store_true")
+    ap.add_argument("--no-other", action="store_true", help="skip the other model workloads")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB MiB (rocprofv3 counter scaling) and exit")
     args = ap.parse_args()
@@ -221,13 +295,11 @@ def main():
         return
 
     import jieyu_amd as jy
-    import oracle
     from jieyu_amd.model import Synth, synth_config
 
     if jy.device_count() < 1:
         log("no HIP device visible")
         sys.exit(1)
-    olib = oracle.load_oracle()
     cfg = synth_config(args.config)
     t = time.time()
     log(f"generating the {args.config} model on the host (seed {cfg.seed}) ...")
@@ -238,7 +310,7 @@ def main():
     log(f"  uploaded + repacked in {g.upload_ms / 1e3:.1f} s")
 
     prompt = np.zeros(args.prompt_len, np.int32)
-    olib.jysyn_uniform_int_fill(cfg.seed, 99, 0, d.vocab_size - 1, ptr(prompt), len(prompt))
+    jy.lib().jysyn_uniform_int_fill(cfg.seed, 99, 0, d.vocab_size - 1, ptr(prompt), len(prompt))
     K, W = args.steps, args.warmup
     total_new = 1 + W + K
     assert args.prompt_len + total_new <= args.max_seq
@@ -268,9 +340,9 @@ def main():
     roof = iso = other = None
     if not args.no_kernel:
         log("dominant kernel in isolation ...")
-        roof = dominant_kernel_roofline(jy, olib, d)
+        roof = dominant_kernel_roofline(jy, d)
         log(f"  {roof['kernel']}: {roof['avg_launch_us']} us -> {roof['achieved']} GB/s")
-        iso = isolated_matvecs(jy, olib)
+        iso = isolated_matvecs(jy)
         log(f"  isolated matvec shapes: {iso}")
         other = isolated_other_types(jy)
         log(f"  other weight types: {other}")
@@ -285,6 +357,11 @@ def main():
              "head_dim": d.head_dim, "ffn": d.intermediate, "vocab": d.vocab_size, "rope_theta": d.rope_theta}
     g.close()
     syn.close()
+
+    others = None
+    if not args.no_other:
+        log("other model workloads ...")
+        others = {name: other_config(jy, name, *rest) for name, *rest in OTHER_CONFIGS}
 
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -301,6 +378,7 @@ def main():
         "upload_s": round(st.upload_ms / 1e3, 2),
         "last_ids": ids[-8:].tolist(),
         "roofline": roof, "cpu_baseline": cpu, "isolated_q8_matvec": iso, "isolated_other_matvec": other,
+        "other_configs": others,
     }
     print(json.dumps(out), flush=True)
 

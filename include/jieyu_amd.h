@@ -97,6 +97,16 @@ typedef struct jyhip_session jyhip_session;
 JYHIP_API jyhip_session* jyhip_session_begin(jyhip_model* model, jyhip_kv* kv, const int* prompt_ids,
                                              int prompt_len, const int* eos_ids, int num_eos, int max_seq,
                                              int max_new, float temperature, float repetition_penalty);
+/* A generation over a cache that already holds kv's current length (c) positions of
+ * ids[0 .. n_ids): ids[c .. n_ids) run as one chunk at start_pos c, as forward_cached
+ * does (libs/model_libs/forward.h:95), then decoding continues as in begin; the
+ * repetition penalty covers only the tokens generated here.  Needs 0 <= c < n_ids.
+ * The reference has no such entry (generate_cached, generate.h:31, always starts the
+ * cache at 0); it serves decoding after a cache filled by other means (long-context
+ * measurement, a conversation's earlier turns). */
+JYHIP_API jyhip_session* jyhip_session_resume(jyhip_model* model, jyhip_kv* kv, const int* ids, int n_ids,
+                                              const int* eos_ids, int num_eos, int max_seq, int max_new,
+                                              float temperature, float repetition_penalty);
 JYHIP_API int jyhip_session_step(jyhip_session* s, int n);
 JYHIP_API int jyhip_session_remaining(const jyhip_session* s);
 JYHIP_API int jyhip_session_len(const jyhip_session* s);

@@ -65,6 +65,7 @@ def lib():
     _proto(L, "jyhip_forward_cached", I, P, P, P, I, I, P)
     _proto(L, "jyhip_generate", I, P, P, P, I, P, I, I, I, F, F, P, TOKEN_CB, P, P, C.POINTER(Stats))
     _proto(L, "jyhip_session_begin", P, P, P, P, I, P, I, I, I, F, F)
+    _proto(L, "jyhip_session_resume", P, P, P, P, I, P, I, I, I, F, F)
     _proto(L, "jyhip_session_step", I, P, I)
     _proto(L, "jyhip_session_remaining", I, P)
     _proto(L, "jyhip_session_len", I, P)
@@ -201,8 +202,12 @@ class GpuModel:
             return out[:n].copy(), st, logits
         return out[:n].copy(), st
 
-    def session(self, prompt, max_new, max_seq=None, temperature=0.0, repetition_penalty=1.0, eos=None, kv=None):
-        return Session(self, prompt, max_new, max_seq or self.max_seq, temperature, repetition_penalty, eos, kv)
+    def session(self, prompt, max_new, max_seq=None, temperature=0.0, repetition_penalty=1.0, eos=None, kv=None,
+                resume=False):
+        """resume=True: kv already holds the first kv.len positions of `prompt`; only the
+        rest runs before decoding (jyhip_session_resume)."""
+        return Session(self, prompt, max_new, max_seq or self.max_seq, temperature, repetition_penalty, eos, kv,
+                       resume)
 
     def close(self):
         if self.h:
@@ -219,13 +224,14 @@ class GpuModel:
 class Session:
     """A generation driven step by step (jyhip_session_*): the prompt runs on creation."""
 
-    def __init__(self, model, prompt, max_new, max_seq, temperature, repetition_penalty, eos, kv):
+    def __init__(self, model, prompt, max_new, max_seq, temperature, repetition_penalty, eos, kv, resume=False):
         self._lib = lib()
         self.model = model
         self.max_seq = max_seq
         prompt = np.ascontiguousarray(prompt, np.int32)
         eos_a = None if eos is None else np.ascontiguousarray(eos, np.int32)
-        self.h = self._lib.jyhip_session_begin(model.h, kv.h if kv is not None else None, _ptr(prompt), len(prompt),
+        opener = self._lib.jyhip_session_resume if resume else self._lib.jyhip_session_begin
+        self.h = opener(model.h, kv.h if kv is not None else None, _ptr(prompt), len(prompt),
                                                _ptr(eos_a), 0 if eos_a is None else len(eos_a), max_seq, max_new,
                                                temperature, repetition_penalty)
         if not self.h:

@@ -25,7 +25,11 @@
 namespace jy {
 
 static constexpr int ATT_THREADS = 256;
+static constexpr int SPV_THREADS = 512;  // softmax/PV: wave 0 runs a chain, waves 1..7 feed it
 static constexpr int ATT_ECAP = 4096;  // scores kept in LDS up to this many keys
+static constexpr int ATT_LW = 1536;    // sum-chain window past that
+static constexpr int ATT_LC = 1024;    // largest PV chunk past that
+constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 static constexpr int ATT_GB = 8;       // query heads per scores workgroup
 static constexpr int ATT_U = 2;        // key loads per lane in the scores kernel
 
@@ -725,6 +729,18 @@ __device__ __forceinline__ float att_block_max(float v, float* red) {
     return r;
 }
 
+// byte k of a and byte k of b (int8) -> one word of two fp16, a's in the low half.
+// Exact: v_perm places each byte under a 0x64 high byte, the XOR turns x into x + 128,
+// so each half reads as the fp16 1024 + (x + 128), and one packed fp16 subtract of
+// 1152 leaves x (integers to 2048 are exact in fp16; 0 comes out as +0).
+__device__ __forceinline__ uint32_t i8x2_to_f16x2(uint32_t a, uint32_t b, int k) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const uint32_t sel = (uint32_t)k | (0x0cu << 8) | ((uint32_t)(k + 4) << 16) | (0x0cu << 24);
+    const uint32_t w = __builtin_amdgcn_perm(b, a, sel) ^ 0x64806480u;  // bytes 0..3 from a, 4..7 from b
+    const h2 r = __builtin_bit_cast(h2, w) - (h2){(_Float16)1152.0f, (_Float16)1152.0f};
+    return __builtin_bit_cast(uint32_t, r);
+}
+
 // V[j0 .. j0+cnt)[d0 .. d0+ds) -> VH (fp16, [d][j] with row stride vstr halves), by
 // the threads t0.. of the workgroup, key slots cnt .. cpad-1 (cpad even) written as
 // zeros; each thread takes two adjacent keys so its stores are whole 32-bit words
@@ -758,12 +774,8 @@ __device__ __forceinline__ void att_stage_v(const int8_t* V, int hd, int d0, int
                         const uint32_t xa[4] = {w[u][pc].x, w[u][pc].y, w[u][pc].z, w[u][pc].w};
                         const uint32_t xb[4] = {w[u][2 + pc].x, w[u][2 + pc].y, w[u][2 + pc].z, w[u][2 + pc].w};
 #pragma unroll
-                        for (int b = 0; b < 16; b++) {
-                            const _Float16 lo = (_Float16)(int8_t)(xa[b >> 2] >> (8 * (b & 3)));
-                            const _Float16 hi = (_Float16)(int8_t)(xb[b >> 2] >> (8 * (b & 3)));
-                            VW[(size_t)(pc * 16 + b) * wstr + kp] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
-                                                                    ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-                        }
+                        for (int b = 0; b < 16; b++)
+                            VW[(size_t)(pc * 16 + b) * wstr + kp] = i8x2_to_f16x2(xa[b >> 2], xb[b >> 2], b & 3);
                     }
                 }
             }
@@ -788,12 +800,8 @@ __device__ __forceinline__ void att_stage_v(const int8_t* V, int hd, int d0, int
                     const uint32_t xa[4] = {wa[pc].x, wa[pc].y, wa[pc].z, wa[pc].w};
                     const uint32_t xb[4] = {wb[pc].x, wb[pc].y, wb[pc].z, wb[pc].w};
 #pragma unroll
-                    for (int b = 0; b < 16; b++) {
-                        const _Float16 lo = (_Float16)(int8_t)(xa[b >> 2] >> (8 * (b & 3)));
-                        const _Float16 hi = (_Float16)(int8_t)(xb[b >> 2] >> (8 * (b & 3)));
-                        VW[(size_t)(pc * 16 + b) * wstr + kp] =
-                            (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-                    }
+                    for (int b = 0; b < 16; b++)
+                        VW[(size_t)(pc * 16 + b) * wstr + kp] = i8x2_to_f16x2(xa[b >> 2], xb[b >> 2], b & 3);
                 }
         }
     } else {  // any ds that is a multiple of 4: 4-byte words
@@ -805,17 +813,90 @@ __device__ __forceinline__ void att_stage_v(const int8_t* V, int hd, int d0, int
             const uint32_t xb =
                 2 * kp + 1 < cnt ? *reinterpret_cast<const uint32_t*>(V + (size_t)(ja + 1) * hd + d0 + wd * 4) : 0u;
 #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const _Float16 lo = (_Float16)(int8_t)(xa >> (8 * b));
-                const _Float16 hi = (_Float16)(int8_t)(xb >> (8 * b));
-                VW[(size_t)(wd * 4 + b) * wstr + kp] =
-                    (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-            }
+            for (int b = 0; b < 4; b++) VW[(size_t)(wd * 4 + b) * wstr + kp] = i8x2_to_f16x2(xa, xb, b);
         }
     }
 }
 
-__global__ __launch_bounds__(ATT_THREADS) void attn_softmax_pv_kernel(AttnArgs a, int ds, int vcap, int vstr) {
+// e_j = expf(s_j - max) for keys n0 .. n0+cnt of a long context into dst, and exact
+// zeros up to the next multiple of 64, by nthr threads (t = 0 .. nthr-1), each taking
+// PER keys whose scores it loads in one batch
+template <int PER>
+__device__ __forceinline__ void att_fill_e(float* dst, const float* S, int n0, int cnt, float mx,
+                                           const uint64_t* tab, int t, int nthr) {
+    const int cpad = (cnt + 63) & ~63;
+    float sv[PER];
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int j = t + u * nthr;
+        sv[u] = j < cnt ? S[n0 + j] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int j = t + u * nthr;
+        if (j < cpad) dst[j] = j < cnt ? expf_tab(sv[u] - mx, tab) : 0.0f;
+    }
+}
+
+// p_j * vs_j = (e_j * (1/sum)) * vs_j for keys n0 .. n0+cnt: the loads, then (after the
+// caller has issued its own) the values, zero-padded to a multiple of 64
+template <int PER>
+__device__ __forceinline__ void att_load_p(float* sv, float* vv, const float* S, const float* VS, int n0, int cnt,
+                                           int t, int nthr) {
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int j = t + u * nthr;
+        sv[u] = j < cnt ? S[n0 + j] : 0.0f;
+        vv[u] = j < cnt ? VS[n0 + j] : 0.0f;
+    }
+}
+
+template <int PER>
+__device__ __forceinline__ void att_store_p(float* dst, const float* sv, const float* vv, int cnt, float mx,
+                                            float inv, const uint64_t* tab, int t, int nthr) {
+    const int cpad = (cnt + 63) & ~63;
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int j = t + u * nthr;
+        if (j < cpad) dst[j] = j < cnt ? (expf_tab(sv[u] - mx, tab) * inv) * vv[u] : 0.0f;
+    }
+}
+
+// One long-context V chunk of a 32-dim slice: keys n0 .. n0+cnt (32 bytes of each key
+// row) -> fp16 [32][ATT_LC + 8], four keys per thread (t < ATT_LC / 4), zeros to the
+// next multiple of 64.  The loads go out first (att_load_v32) so the caller can issue
+// its own beside them; the stores use fixed row offsets.
+__device__ __forceinline__ void att_load_v32(uint4 (&w)[4][2], const int8_t* V, int hd, int d0, int n0, int cnt,
+                                             int t) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int j = 4 * t + k;
+        const int8_t* row = V + (size_t)(n0 + j) * hd + d0;
+        w[k][0] = j < cnt ? *reinterpret_cast<const uint4*>(row) : make_uint4(0, 0, 0, 0);
+        w[k][1] = j < cnt ? *reinterpret_cast<const uint4*>(row + 16) : make_uint4(0, 0, 0, 0);
+    }
+}
+
+__device__ __forceinline__ void att_store_v32(const uint4 (&w)[4][2], _Float16* VH, int cnt, int t) {
+    constexpr int WSTR = (ATT_LC + 8) / 2;  // words per dim row
+    if (4 * t >= ((cnt + 63) & ~63)) return;
+    uint32_t* base = reinterpret_cast<uint32_t*>(VH) + 2 * t;
+#pragma unroll
+    for (int pc = 0; pc < 2; pc++) {
+        const uint32_t x[4][4] = {{w[0][pc].x, w[0][pc].y, w[0][pc].z, w[0][pc].w},
+                                  {w[1][pc].x, w[1][pc].y, w[1][pc].z, w[1][pc].w},
+                                  {w[2][pc].x, w[2][pc].y, w[2][pc].z, w[2][pc].w},
+                                  {w[3][pc].x, w[3][pc].y, w[3][pc].z, w[3][pc].w}};
+#pragma unroll
+        for (int b = 0; b < 16; b++) {
+            const uint32_t lo = i8x2_to_f16x2(x[0][b >> 2], x[1][b >> 2], b & 3);  // keys 4t, 4t+1
+            const uint32_t hi = i8x2_to_f16x2(x[2][b >> 2], x[3][b >> 2], b & 3);  // keys 4t+2, 4t+3
+            *reinterpret_cast<uint2*>(base + (pc * 16 + b) * WSTR) = make_uint2(lo, hi);
+        }
+    }
+}
+
+__global__ __launch_bounds__(SPV_THREADS) void attn_softmax_pv_kernel(AttnArgs a, int ds, int vcap, int vstr, int lc) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float red[8];
     __shared__ float s_inv;
@@ -841,24 +922,29 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_softmax_pv_kernel(AttnArgs a
     }
     float o = 0.0f;
     if (nk <= ATT_ECAP) {
-        // scores -> LDS, max, e_j in place
-        float lmax = -1e30f;
-        for (int j = tid; j < nk; j += blockDim.x) {
-            const float s = S[j];
-            E[j] = s;
-            lmax = fmaxf(lmax, s);
-        }
-        const float mx = att_block_max(lmax, red);
-        // e_j, and exact zeros up to a multiple of 64 keys so the chains need no tail
-        const int nk64 = (nk + 63) & ~63;
-        for (int j = tid; j < nk64; j += blockDim.x) E[j] = j < nk ? expf_tab(E[j] - mx, exp_tab) : 0.0f;
-        // the V scales of this thread's keys, in flight through the sum chain
-        constexpr int NV = ATT_ECAP / ATT_THREADS;
-        float vsr[NV];
+        // the scores and V scales of this thread's keys in one batch of loads, the max,
+        // then e_j in registers and in LDS, with exact zeros up to a multiple of 64 keys
+        // so the chains need no tail
+        constexpr int NV = ATT_ECAP / SPV_THREADS;
+        float ev[NV], vsr[NV];
 #pragma unroll
         for (int k = 0; k < NV; k++) {
-            const int j = tid + k * ATT_THREADS;
+            const int j = tid + k * SPV_THREADS;
+            ev[k] = j < nk ? S[j] : -1e30f;
             vsr[k] = j < nk ? VS[j] : 0.0f;
+        }
+        float lmax = -1e30f;
+#pragma unroll
+        for (int k = 0; k < NV; k++) lmax = fmaxf(lmax, ev[k]);
+        const float mx = att_block_max(lmax, red);
+        const int nk64 = (nk + 63) & ~63;
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int j = tid + k * SPV_THREADS;
+            if (j < nk64) {
+                ev[k] = j < nk ? expf_tab(ev[k] - mx, exp_tab) : 0.0f;
+                E[j] = ev[k];
+            }
         }
         lds_barrier();
         // the sum chain on wave 0 while the other waves stage the first run of V
@@ -872,8 +958,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_softmax_pv_kernel(AttnArgs a
         const float inv = s_inv;
 #pragma unroll
         for (int k = 0; k < NV; k++) {  // p_j * vs_j
-            const int j = tid + k * ATT_THREADS;
-            if (j < nk) E[j] = (E[j] * inv) * vsr[k];
+            const int j = tid + k * SPV_THREADS;
+            if (j < nk) E[j] = (ev[k] * inv) * vsr[k];
         }
         __syncthreads();
         // the PV chain over whole 64-key blocks: the padding adds fma(0, 0, o) = o
@@ -887,29 +973,96 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_softmax_pv_kernel(AttnArgs a
             if (tid < ds) o = chain_pv(E + cs, VH + (size_t)tid * vstr, o, cpad);
         }
     } else {
-        // long contexts: scores stay in the global array; e_j is recomputed from them
-        // (expf is deterministic) window by window instead of being written back
+        // Long contexts.  e_j is recomputed from the scores (expf is deterministic)
+        // instead of being written back: in windows of ATT_LW keys for the sum chain, and
+        // again as p_j * vs_j in chunks of lc keys for the PV chain.  Each is double-
+        // buffered: wave 0 runs the chain over one buffer (ds <= 64 lanes) while waves
+        // 1..7 fill the other, and every hand-over is one workgroup barrier, so the
+        // chains run back to back.
+        float* EW = reinterpret_cast<float*>(smem);                 // [2][ATT_LW]
+        float* PB = EW + 2 * ATT_LW;                                  // [2][lc], lc <= ATT_LC
+        _Float16* VB = reinterpret_cast<_Float16*>(PB + 2 * lc);      // [2][ds][lc + 8]
+        const int lvstr = lc + 8;
+        const size_t vbuf = (size_t)ds * lvstr;
+        const int pt = tid - 64;  // producer index on waves 1..7
+        const bool v32 = ds == 32 && lc == ATT_LC;  // the fixed-stride V producer applies
         float lmax = -1e30f;
-        for (int j = tid; j < nk; j += blockDim.x) lmax = fmaxf(lmax, S[j]);
+        {
+            float lm[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) lm[u] = -1e30f;
+            for (int j0 = tid; j0 < nk; j0 += 8 * SPV_THREADS) {
+                float sv[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) sv[u] = j0 + u * SPV_THREADS < nk ? S[j0 + u * SPV_THREADS] : -1e30f;
+#pragma unroll
+                for (int u = 0; u < 8; u++) lm[u] = fmaxf(lm[u], sv[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) lmax = fmaxf(lmax, lm[u]);
+        }
         const float mx = att_block_max(lmax, red);
+        const int nw = (nk + ATT_LW - 1) / ATT_LW;
+        att_fill_e<cdiv(ATT_LW, SPV_THREADS)>(EW, S, 0, min(ATT_LW, nk), mx, exp_tab, tid, SPV_THREADS);
+        __syncthreads();
         float sum = 0.0f;
-        for (int w0 = 0; w0 < nk; w0 += ATT_ECAP) {
-            const int cnt = min(ATT_ECAP, nk - w0), cpad = (cnt + 63) & ~63;
-            for (int j = tid; j < cpad; j += blockDim.x) E[j] = j < cnt ? expf_tab(S[w0 + j] - mx, exp_tab) : 0.0f;
-            __syncthreads();
-            if (tid < 16) sum = chain_sum16(E, cpad, sum);
+        for (int w = 0; w < nw; w++) {
+            const int cnt = min(ATT_LW, nk - w * ATT_LW), cpad = (cnt + 63) & ~63;
+            if (wave == 0) {
+                if (tid < 16) sum = chain_sum16(EW + (w & 1) * ATT_LW, cpad, sum);  // + 0.0 padding: exact
+            } else {
+                if (w + 1 < nw) {
+                    const int n0 = (w + 1) * ATT_LW;
+                    att_fill_e<cdiv(ATT_LW, SPV_THREADS - 64)>(EW + ((w + 1) & 1) * ATT_LW, S, n0, min(ATT_LW, nk - n0),
+                                                            mx, exp_tab, pt, SPV_THREADS - 64);
+                }
+                if (w == 0) {  // the first V chunk, while the sum chain runs
+                    const int vcnt = min(lc, nk);
+                    if (v32) {
+                        if (pt < ATT_LC / 4) {
+                            uint4 vw[4][2];
+                            att_load_v32(vw, V, hd, d0, 0, vcnt, pt);
+                            att_store_v32(vw, VB, vcnt, pt);
+                        }
+                    } else {
+                        att_stage_v(V, hd, d0, ds, 0, vcnt, (vcnt + 63) & ~63, VB, lvstr, 64);
+                    }
+                }
+            }
             __syncthreads();
         }
         if (tid == 0) s_inv = 1.0f / sum;
         __syncthreads();
         const float inv = s_inv;
-        for (int cs = 0; cs < nk; cs += vcap) {
-            const int cnt = min(vcap, nk - cs), cpad = (cnt + 63) & ~63;
-            for (int j = tid; j < cpad; j += blockDim.x)
-                E[j] = j < cnt ? (expf_tab(S[cs + j] - mx, exp_tab) * inv) * VS[cs + j] : 0.0f;
-            att_stage_v(V, hd, d0, ds, cs, cnt, cpad, VH, vstr, 0);
-            __syncthreads();
-            if (tid < ds) o = chain_pv(E, VH + (size_t)tid * vstr, o, cpad);
+        const int nc = (nk + lc - 1) / lc;
+        {
+            constexpr int PER = cdiv(ATT_LC, SPV_THREADS);
+            float sv[PER], vv[PER];
+            att_load_p<PER>(sv, vv, S, VS, 0, min(lc, nk), tid, SPV_THREADS);
+            att_store_p<PER>(PB, sv, vv, min(lc, nk), mx, inv, exp_tab, tid, SPV_THREADS);
+        }
+        __syncthreads();
+        for (int c = 0; c < nc; c++) {
+            const int cnt = min(lc, nk - c * lc), cpad = (cnt + 63) & ~63;
+            if (wave == 0) {
+                if (tid < ds) o = chain_pv(PB + (c & 1) * lc, VB + (c & 1) * vbuf + (size_t)tid * lvstr, o, cpad);
+            } else if (c + 1 < nc) {
+                // the next chunk's scores, V scales and V rows in one round of loads
+                const int n0 = (c + 1) * lc, ncnt = min(lc, nk - n0), npad = (ncnt + 63) & ~63;
+                constexpr int PER = cdiv(ATT_LC, SPV_THREADS - 64);
+                float sv[PER], vv[PER];
+                att_load_p<PER>(sv, vv, S, VS, n0, ncnt, pt, SPV_THREADS - 64);
+                _Float16* vh = VB + ((c + 1) & 1) * vbuf;
+                if (v32) {
+                    uint4 vw[4][2];
+                    if (pt < ATT_LC / 4) att_load_v32(vw, V, hd, d0, n0, ncnt, pt);
+                    att_store_p<PER>(PB + ((c + 1) & 1) * lc, sv, vv, ncnt, mx, inv, exp_tab, pt, SPV_THREADS - 64);
+                    if (pt < ATT_LC / 4) att_store_v32(vw, vh, ncnt, pt);
+                } else {
+                    att_stage_v(V, hd, d0, ds, n0, ncnt, npad, vh, lvstr, 64);
+                    att_store_p<PER>(PB + ((c + 1) & 1) * lc, sv, vv, ncnt, mx, inv, exp_tab, pt, SPV_THREADS - 64);
+                }
+            }
             __syncthreads();
         }
     }
@@ -921,15 +1074,31 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_softmax_pv_kernel(AttnArgs a
 static int g_att_lds_max = 0;
 
 // output dims per softmax/PV workgroup and the V run it stages (fp16 rows of
-// vstr = vcap + 8 halves: 16 bytes of padding per row)
-static void att_shape(int hd, int* ds, int* vcap, int* vstr) {
-    *ds = (hd % 32 == 0) ? 32 : hd;
-    const int budget = (g_att_lds_max > 0 ? g_att_lds_max : 65536) - ATT_ECAP * 4 - 2048;
+// vstr = vcap + 8 halves: 16 bytes of padding per row); lc: the chunk of the long-
+// context form (two P chunks and two V chunks after the two e windows); lds: the
+// dynamic LDS that covers both forms
+static void att_shape(int hd, int* ds, int* vcap, int* vstr, int* lc, size_t* lds) {
+    // 32 dims, else the largest multiple of 4 up to 64 that divides hd (hd % 4 == 0 is
+    // checked at upload): the PV chain then fits in wave 0
+    int d = 32;
+    if (hd % 32) {
+        d = 4;
+        for (int c = 8; c <= 64 && c <= hd; c += 4)
+            if (hd % c == 0) d = c;
+    }
+    *ds = d;
+    const int avail = (g_att_lds_max > 0 ? g_att_lds_max : 65536) - 2048;
+    const int budget = avail - ATT_ECAP * 4;
     int v = ATT_ECAP;
     while (v > 64 && (size_t)(*ds) * (v + 8) * 2 > (size_t)budget) v >>= 1;
     if (v > ATT_ECAP) v = ATT_ECAP;
     *vcap = v;
     *vstr = v + 8;
+    auto long_bytes = [&](int c) { return (size_t)2 * ATT_LW * 4 + (size_t)2 * c * 4 + (size_t)2 * (*ds) * (c + 8) * 2; };
+    int c = ATT_LC;  // the producers' per-thread key counts are sized for ATT_LC
+    while (c > 64 && long_bytes(c) > (size_t)avail) c -= 64;
+    *lc = c;
+    *lds = std::max((size_t)ATT_ECAP * 4 + (size_t)(*ds) * (*vstr) * 2, long_bytes(c));
 }
 
 static int att_keys_per_wg(int hd) {
@@ -948,11 +1117,11 @@ void launch_attention(const AttnArgs& a, hipStream_t st) {
     const int nb = (group + ATT_GB - 1) / ATT_GB;
     hipLaunchKernelGGL(attn_scores_kernel, dim3(a.nkv * nb, (keys + kc - 1) / kc, a.nrows), dim3(ATT_THREADS), 0, st,
                        a, kc);
-    int ds, vcap, vstr;
-    att_shape(a.hd, &ds, &vcap, &vstr);
-    const size_t lds = (size_t)ATT_ECAP * 4 + (size_t)ds * vstr * 2;
-    hipLaunchKernelGGL(attn_softmax_pv_kernel, dim3(a.nh, a.nrows, a.hd / ds), dim3(ATT_THREADS), lds, st, a, ds,
-                       vcap, vstr);
+    int ds, vcap, vstr, lc;
+    size_t lds;
+    att_shape(a.hd, &ds, &vcap, &vstr, &lc, &lds);
+    hipLaunchKernelGGL(attn_softmax_pv_kernel, dim3(a.nh, a.nrows, a.hd / ds), dim3(SPV_THREADS), lds, st, a, ds,
+                       vcap, vstr, lc);
 }
 
 hipError_t matvec_init();

@@ -793,7 +793,7 @@ struct Session {
     // returns false when generate() would return before the loop (generate.h:25-32)
     bool begin(jyhip_model* model, jyhip_kv* kv_in, const int* prompt, int plen_, const int* eos_ids, int neos_,
                int max_seq_, int max_new, float temperature_, float rp_, jyhip_token_cb cb_, void* ud_,
-               int* prompt_out) {
+               int* prompt_out, bool resume = false) {
         m = model;
         plen = plen_;
         max_seq = max_seq_;
@@ -808,6 +808,7 @@ struct Session {
         if (neos_ > m->eos_cap) fail("too many eos ids");
         for (int i = 0; i < plen; i++)
             if (prompt[i] < 0 || prompt[i] >= m->V) fail("prompt id out of vocabulary");
+        if (resume && !kv_in) fail("resume: no KV cache given");
         if (kv_in) {
             kv = kv_in;
             if (kv->dev.num_layers < m->L || kv->dev.max_seq < max_seq || kv->dev.nkv != m->nkv || kv->dev.hd != m->hd)
@@ -824,7 +825,11 @@ struct Session {
         if (prompt_out)
             for (int i = 0; i < plen; i++) prompt_out[i] = prompt[i];
         len = plen;
-        kv->current_len = 0;
+        // positions [0, keep) of the prompt are already in the cache (resume); the rest run
+        // as one chunk at start_pos = keep, as forward_cached does (forward.h:95)
+        const int keep = resume ? kv->current_len : 0;
+        if (keep < 0 || keep >= plen) fail("resume: the cache must hold fewer positions than the prompt");
+        kv->current_len = keep;
         if (max_new <= 0) return false;                  // generate.h:32
         total = std::min(max_new, max_seq - plen);        // tokens this generation may produce
         if (total <= 0) return false;                     // generate.h:39: len < max_seq fails at once
@@ -833,7 +838,8 @@ struct Session {
         for (hipEvent_t& e : ev) CK(hipEventCreate(&e));
 
         hipStream_t st = m->stream;
-        ensure_ws(m, plen);
+        const int seq = plen - keep;
+        ensure_ws(m, seq);
         CK(hipMemcpyAsync(m->ids, prompt, sizeof(int) * plen, hipMemcpyHostToDevice, st));
         const int st0[4] = {plen, 0, 0, 0};
         CK(hipMemcpyAsync(m->state, st0, sizeof(st0), hipMemcpyHostToDevice, st));
@@ -841,9 +847,9 @@ struct Session {
         // step 0: the prompt (generate.h:43-49 with seq = prompt_len)
         CK(hipEventRecord(ev[0], st));
         Workspace& w = m->ws;
-        embed_rows(m, 0, nullptr, plen, w.X);
-        run_layers(m, kv->dev, plen, 0, nullptr, nullptr, max_keys);
-        head_and_pick(m, w.X + (size_t)(plen - 1) * m->H, greedy, rp, plen, neos);
+        embed_rows(m, keep, nullptr, seq, w.X);
+        run_layers(m, kv->dev, seq, keep, nullptr, nullptr, max_keys);
+        head_and_pick(m, w.X + (size_t)(seq - 1) * m->H, greedy, rp, plen, neos);
         CK(hipEventRecord(ev[1], st));
         CK(hipGetLastError());
         accept(greedy ? fetch_last() : pick_host());
@@ -1144,15 +1150,15 @@ struct jyhip_session {
     int result = 0;       // what generate() returns in that case
 };
 
-JYHIP_API jyhip_session* jyhip_session_begin(jyhip_model* m, jyhip_kv* kv, const int* prompt_ids, int prompt_len,
-                                             const int* eos_ids, int num_eos, int max_seq, int max_new,
-                                             float temperature, float repetition_penalty) {
+static jyhip_session* session_open(jyhip_model* m, jyhip_kv* kv, const int* prompt_ids, int prompt_len,
+                                   const int* eos_ids, int num_eos, int max_seq, int max_new, float temperature,
+                                   float repetition_penalty, bool resume) {
     return guarded([&]() -> jyhip_session* {
         if (!m) fail("model is NULL");
         jyhip_session* h = new jyhip_session();
         try {
             h->active = h->s.begin(m, kv, prompt_ids, prompt_len, eos_ids, num_eos, max_seq, max_new, temperature,
-                                   repetition_penalty, nullptr, nullptr, nullptr);
+                                   repetition_penalty, nullptr, nullptr, nullptr, resume);
             h->result = h->active ? h->s.len : ((prompt_len <= 0 || prompt_len > max_seq) ? 0 : prompt_len);
         } catch (...) {
             delete h;
@@ -1160,6 +1166,20 @@ JYHIP_API jyhip_session* jyhip_session_begin(jyhip_model* m, jyhip_kv* kv, const
         }
         return h;
     }, nullptr);
+}
+
+JYHIP_API jyhip_session* jyhip_session_begin(jyhip_model* m, jyhip_kv* kv, const int* prompt_ids, int prompt_len,
+                                             const int* eos_ids, int num_eos, int max_seq, int max_new,
+                                             float temperature, float repetition_penalty) {
+    return session_open(m, kv, prompt_ids, prompt_len, eos_ids, num_eos, max_seq, max_new, temperature,
+                        repetition_penalty, false);
+}
+
+JYHIP_API jyhip_session* jyhip_session_resume(jyhip_model* m, jyhip_kv* kv, const int* ids, int n_ids,
+                                              const int* eos_ids, int num_eos, int max_seq, int max_new,
+                                              float temperature, float repetition_penalty) {
+    return session_open(m, kv, ids, n_ids, eos_ids, num_eos, max_seq, max_new, temperature, repetition_penalty,
+                        true);
 }
 
 JYHIP_API int jyhip_session_step(jyhip_session* h, int n) {

@@ -86,3 +86,24 @@ def test_bench_refuses_several_gpus():
                        text=True, timeout=300)
     assert r.returncode != 0
     assert "one GPU" in r.stderr or "--gpus 1" in r.stderr
+
+
+def test_bench_kv_packing_matches_oracle(oracle_lib):
+    """bench.py fills the long-context cache with rows packed like the cache's own: the
+    oracle's packing of attention_q8.h:20-37 (absmax int8 per position and head)."""
+    import importlib.util
+    import ctypes as C
+    import numpy as np
+    from conftest import ptr
+    spec = importlib.util.spec_from_file_location("bench_mod", os.path.join(ROOT, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    x = np.random.default_rng(7).standard_normal((50, 4, 128)).astype(np.float32)
+    x[3, 1] = 0.0          # an all-zero row: scale 0, codes 0
+    x[4, 2, 5] = 1e30      # one huge value
+    q, sc = bench.pack_kv_rows(x)
+    q8 = np.zeros(x.size, np.int8)
+    s8 = np.zeros(50 * 4, np.float32)
+    oracle_lib.jyo_kv_pack(ptr(x), ptr(q8), ptr(s8), 4, 128, 50)
+    assert np.array_equal(q.reshape(-1), q8)
+    assert np.array_equal(sc.reshape(-1).view(np.uint32), s8.view(np.uint32))

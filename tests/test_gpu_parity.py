@@ -174,19 +174,16 @@ def test_forward_cached_layers_and_kv(jy, oracle_lib):
     s.close()
 
 
-def test_prefilled_cache_long_context(jy, oracle_lib):
-    """Decode at start_pos 3000 over a cache pre-filled with packed N(0,1) K/V (the long-context
-    workload's setup, at a reduced model size)."""
-    say("pre-filled cache decode at 3000")
-    s = make_synth(oracle_lib, "hd128-q8")
-    d = s.desc
-    L, H, nkv, hd = d.num_layers, d.hidden, d.num_kv_heads, d.head_dim
-    pre, max_seq = 3000, 3008
-    cos, sin = rope_tables(oracle_lib, max_seq, hd, d.rope_theta)
+def prefill_cache(oracle_lib, d, pre, max_seq, kv):
+    """Pack N(0,1) K/V for positions [0, pre) of every layer into the GPU cache `kv` and
+    into a new oracle cache (returned), as the long-context workload sets up its cache."""
+    L, nkv, hd = d.num_layers, d.num_kv_heads, d.head_dim
     okv = oracle.JyoKV()
     assert oracle_lib.jyo_kv_init(C.byref(okv), L, max_seq, nkv, hd) == 0
-    g = jy.GpuModel(d, max_seq)
-    kv = g.kv(max_seq)
+    ok8 = np.ctypeslib.as_array(C.cast(okv.k, C.POINTER(C.c_int8)), (L * max_seq * nkv * hd,))
+    ov8 = np.ctypeslib.as_array(C.cast(okv.v, C.POINTER(C.c_int8)), (L * max_seq * nkv * hd,))
+    oks = np.ctypeslib.as_array(C.cast(okv.ks, C.POINTER(C.c_float)), (L * max_seq * nkv,))
+    ovs = np.ctypeslib.as_array(C.cast(okv.vs, C.POINTER(C.c_float)), (L * max_seq * nkv,))
     for l in range(L):
         kf = np.zeros(pre * nkv * hd, np.float32)
         vf = np.zeros_like(kf)
@@ -199,10 +196,6 @@ def test_prefilled_cache_long_context(jy, oracle_lib):
         oracle_lib.jyo_kv_pack(ptr(kf), ptr(k8), ptr(ks), nkv, hd, pre)
         oracle_lib.jyo_kv_pack(ptr(vf), ptr(v8), ptr(vs), nkv, hd, pre)
         base = l * max_seq
-        ok8 = np.ctypeslib.as_array(C.cast(okv.k, C.POINTER(C.c_int8)), (L * max_seq * nkv * hd,))
-        ov8 = np.ctypeslib.as_array(C.cast(okv.v, C.POINTER(C.c_int8)), (L * max_seq * nkv * hd,))
-        oks = np.ctypeslib.as_array(C.cast(okv.ks, C.POINTER(C.c_float)), (L * max_seq * nkv,))
-        ovs = np.ctypeslib.as_array(C.cast(okv.vs, C.POINTER(C.c_float)), (L * max_seq * nkv,))
         ok8[base * nkv * hd:(base + pre) * nkv * hd] = k8
         ov8[base * nkv * hd:(base + pre) * nkv * hd] = v8
         oks[base * nkv:(base + pre) * nkv] = ks
@@ -210,6 +203,24 @@ def test_prefilled_cache_long_context(jy, oracle_lib):
         kv.write(l, 0, k8.reshape(pre, nkv, hd), ks.reshape(pre, nkv), v8.reshape(pre, nkv, hd),
                  vs.reshape(pre, nkv))
     kv.set_len(pre)
+    return okv
+
+
+# 3000: every score in LDS; 4094 / 4095: the last positions of that form (4095 / 4096
+# keys) and the first of the windowed form; 9000: windows and chunks with ragged ends
+@pytest.mark.parametrize("pre", [3000, 4094, 9000])
+def test_prefilled_cache_long_context(jy, oracle_lib, pre):
+    """Decode steps at start_pos pre.. over a cache pre-filled with packed N(0,1) K/V (the
+    long-context workload's setup, at a reduced model size)."""
+    say(f"pre-filled cache decode at {pre}")
+    s = make_synth(oracle_lib, "hd128-q8")
+    d = s.desc
+    H, hd = d.hidden, d.head_dim
+    max_seq = pre + 8
+    cos, sin = rope_tables(oracle_lib, max_seq, hd, d.rope_theta)
+    g = jy.GpuModel(d, max_seq)
+    kv = g.kv(max_seq)
+    okv = prefill_cache(oracle_lib, d, pre, max_seq, kv)
     rng = np.random.default_rng(4)
     for i in range(3):
         X = rng.standard_normal((1, H)).astype(np.float32)
@@ -219,6 +230,77 @@ def test_prefilled_cache_long_context(jy, oracle_lib):
         Xg = g.forward_cached(kv, X, pre + i)
         assert bits_equal(Xg, Xo), f"step {i}: max abs diff {np.abs(Xg - Xo).max()}"
     oracle_lib.jyo_kv_free(C.byref(okv))
+    kv.close()
+    g.close()
+    s.close()
+
+
+def test_resume_over_long_prefilled_cache(jy, oracle_lib):
+    """The decode graph (positions read on the device) over a 6000-position pre-filled
+    cache: jyhip_session_resume's greedy tokens against the oracle driven token by token
+    (embedding row, forward_cached at the next position, lm_head, first maximum)."""
+    say("session resume over a 6000-position cache")
+    s = make_synth(oracle_lib, "hd128-q8")
+    d = s.desc
+    H, V, hd = d.hidden, d.vocab_size, d.head_dim
+    pre, n_new = 6000, 8
+    max_seq = pre + 16
+    cos, sin = rope_tables(oracle_lib, max_seq, hd, d.rope_theta)
+    g = jy.GpuModel(d, max_seq)
+    kv = g.kv(max_seq)
+    okv = prefill_cache(oracle_lib, d, pre, max_seq, kv)
+    ids = np.zeros(pre + 1, np.int32)
+    oracle_lib.jysyn_uniform_int_fill(8, 99, 0, V - 1, ptr(ids), len(ids))
+    want = []
+    tok = int(ids[-1])
+    for i in range(n_new):
+        X = np.zeros((1, H), np.float32)
+        oracle_lib.jyo_embed_row(C.byref(d.embed), tok, H, ptr(X))
+        assert oracle_lib.jyo_forward_cached(C.byref(d), ptr(X), ptr(cos), ptr(sin), 1, pre + i, C.byref(okv),
+                                             None) == 0
+        logits = np.zeros(V, np.float32)
+        oracle_lib.jyo_matmul_w(C.byref(d.lm_head), 1, V, H, ptr(X), ptr(logits))
+        tok = int(np.argmax(logits))
+        want.append(tok)
+    ss = g.session(ids, n_new, max_seq=max_seq, kv=kv, resume=True)
+    ss.step(n_new)
+    got = ss.ids()[pre + 1:]
+    ss.close()
+    assert list(got) == want
+    oracle_lib.jyo_kv_free(C.byref(okv))
+    kv.close()
+    g.close()
+    s.close()
+
+
+@pytest.mark.parametrize("key", ["hd128-q8", "tiny-f32"])
+def test_session_resume_matches_oracle(jy, oracle_lib, key):
+    """jyhip_session_resume over a cache holding the prompt's first c positions (written by
+    an earlier session) gives the oracle's tokens for the whole prompt: c = 0, a chunk
+    run at start_pos c (the prefill path), and c = n - 1 (the single-row decode path)."""
+    say(f"session resume {key}")
+    s = make_synth(oracle_lib, key)
+    d = s.desc
+    prompt = np.zeros(19, np.int32)
+    oracle_lib.jysyn_uniform_int_fill(6, 99, 0, d.vocab_size - 1, ptr(prompt), len(prompt))
+    max_seq, max_new = 64, 16
+    ref_ids, _ = oracle_generate(oracle_lib, d, prompt, max_seq, max_new)
+    g = jy.GpuModel(d, max_seq)
+    kv = g.kv(max_seq)
+    for c in (0, 7, len(prompt) - 1):
+        if c:
+            g.session(prompt[:c], 1, kv=kv).close()
+        kv.set_len(c)
+        ss = g.session(prompt, max_new, kv=kv, resume=True)
+        ss.step(max_new)
+        ids = ss.ids()
+        ss.close()
+        assert np.array_equal(ids, ref_ids), f"c={c}: gpu {ids[len(prompt):]} vs oracle {ref_ids[len(prompt):]}"
+    kv.set_len(len(prompt))
+    with pytest.raises(jy.JyError):
+        g.session(prompt, 4, kv=kv, resume=True)  # the cache already holds the whole prompt
+    with pytest.raises(jy.JyError):
+        g.session(prompt, 4, resume=True)  # nothing to resume from
     kv.close()
     g.close()
     s.close()
