@@ -15,10 +15,12 @@
 //     form it also quantises the token's q, k and v, and one workgroup per kv head
 //     appends k/v to the cache (kv_pack_q8 of the new position).
 //  2. attn_softmax_pv_kernel: one workgroup per (query head, token row, slice of
-//     output dims) runs the reference's two ascending chains: the softmax sum on
-//     one lane while the other waves stage this slice of V in LDS (fp16, exact for
-//     int8, rows padded so the chain's 16-byte reads do not collide in a bank),
-//     then one lane per output dim.
+//     output dims) runs the reference's two ascending chains on wave 0: the softmax
+//     sum on one lane, then one lane per output dim, while waves 1..7 stage this
+//     slice of V in LDS (fp16, exact for int8, rows padded so the chain's 16-byte
+//     reads do not collide in a bank).  Up to ATT_ECAP keys every e_j stays in LDS;
+//     past it e_j, p_j * vs_j and V move through double-buffered windows, so the
+//     chains run back to back while the other waves fill the next buffer.
 // Scores travel between the two through a per-row [nh][max_keys] float array.
 #include "jy_layout.h"
 
@@ -26,7 +28,7 @@ namespace jy {
 
 static constexpr int ATT_THREADS = 256;
 static constexpr int SPV_THREADS = 512;  // softmax/PV: wave 0 runs a chain, waves 1..7 feed it
-static constexpr int ATT_ECAP = 4096;  // scores kept in LDS up to this many keys
+static constexpr int ATT_ECAP = 1536;  // keys kept in LDS whole; past this the windowed form (faster there)
 static constexpr int ATT_LW = 1536;    // sum-chain window past that
 static constexpr int ATT_LC = 1024;    // largest PV chunk past that
 constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
@@ -973,7 +975,7 @@ __global__ __launch_bounds__(SPV_THREADS) void attn_softmax_pv_kernel(AttnArgs a
             if (tid < ds) o = chain_pv(E + cs, VH + (size_t)tid * vstr, o, cpad);
         }
     } else {
-        // Long contexts.  e_j is recomputed from the scores (expf is deterministic)
+        // Longer contexts.  e_j is recomputed from the scores (expf is deterministic)
         // instead of being written back: in windows of ATT_LW keys for the sum chain, and
         // again as p_j * vs_j in chunks of lc keys for the PV chain.  Each is double-
         // buffered: wave 0 runs the chain over one buffer (ds <= 64 lanes) while waves

@@ -206,9 +206,9 @@ def prefill_cache(oracle_lib, d, pre, max_seq, kv):
     return okv
 
 
-# 3000: every score in LDS; 4094 / 4095: the last positions of that form (4095 / 4096
-# keys) and the first of the windowed form; 9000: windows and chunks with ragged ends
-@pytest.mark.parametrize("pre", [3000, 4094, 9000])
+# 1534: 1535 / 1536 keys (every score in LDS) then 1537 (the first of the windowed
+# form); 3000: two windows and three chunks; 9000: windows and chunks with ragged ends
+@pytest.mark.parametrize("pre", [1534, 3000, 9000])
 def test_prefilled_cache_long_context(jy, oracle_lib, pre):
     """Decode steps at start_pos pre.. over a cache pre-filled with packed N(0,1) K/V (the
     long-context workload's setup, at a reduced model size)."""
