@@ -12,9 +12,12 @@ synchronised on both sides of the timed region.  Prints one JSON line.
 Extra fields: the achieved HBM rate of the whole step (algorithmic bytes per
 token / time), the dominant kernel's roofline (the fused gate/up matvec shape,
 timed with HIP events on its stream over copies that exceed the last-level
-cache), and a CPU baseline: jieyu's own decode path compiled from the reference
+cache), a CPU baseline (jieyu's own decode path compiled from the reference
 sources (oracle/_ref) on this host, over a bounded sample of the same model,
-whose tokens are also compared with the GPU's.
+whose tokens are also compared with the GPU's), and `other_configs`: the decode
+rate of the other model workloads through the same session path (a tiny f32
+model, the Qwen2.5-0.5B shape after a 512-token prompt, and the Qwen2.5-7B shape
+after a cache pre-filled to 32768 positions).
 """
 import argparse
 import ctypes as C
