@@ -29,6 +29,11 @@ namespace jy {
 static constexpr int ATT_THREADS = 256;
 static constexpr int SPV_THREADS = 512;  // softmax/PV: wave 0 runs a chain, waves 1..7 feed it
 static constexpr int ATT_ECAP = 1536;  // keys kept in LDS whole; past this the windowed form (faster there)
+// decode steps up to this many keys compute the scores inside the softmax/PV workgroups
+// (one kernel); past it every workgroup re-reading its kv head's whole key run costs
+// more than the second launch (measured: one kernel 12.4 vs 14.8 us at 512 keys, 18.4
+// vs 18.0 at 1024)
+static constexpr int ATT_ONE = 768;
 static constexpr int ATT_LW = 1536;    // sum-chain window past that
 static constexpr int ATT_LC = 1024;    // largest PV chunk past that
 constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
@@ -898,11 +903,109 @@ __device__ __forceinline__ void att_store_v32(const uint4 (&w)[4][2], _Float16* 
     }
 }
 
+// One token's scores against every key j <= pos of its kv head, computed inside the
+// softmax/PV workgroup (short contexts: one kernel for the whole attention).  Arithmetic
+// as attn_scores_kernel: the token's q (and, fused, k and v) quantised by waves 0..2,
+// exact int32 dots, score = (float)dot * ((ks_j * qsc) * (1/sqrt(hd))).  The key rows
+// are spread over LP adjacent lanes (16 bytes each) and RB rounds of them are loaded
+// in one batch.  Fused, the first workgroup of each kv head writes the new K/V slot,
+// and every workgroup takes the new key from its own copy (tok8[1], toksc[1]) since
+// the slot is written in this launch.  Scores go to E[0 .. pos]; ends with a barrier.
+__device__ __forceinline__ void att_scores_local(const AttnArgs& a, int h, int kvh, int pos, float* E,
+                                                 int8_t (&tok8)[3][256], float* toksc) {
+    constexpr int RB = 12;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int hd = a.hd, nh = a.nh, nkv = a.nkv, group = nh / nkv, nk = pos + 1;
+    const size_t head = (size_t)a.layer * nkv + kvh;
+    const int8_t* K = a.kv.k + head * a.kv.max_seq * hd;
+    const float* KS = a.kv.ks + head * a.kv.max_seq;
+    const int P = hd >> 4;
+    int LP = 1;
+    while (LP < P) LP <<= 1;
+    const int KW = 64 / LP, piece = lane & (LP - 1), kl = lane / LP;
+    const bool live = piece < P;
+    const int KPR = (SPV_THREADS / 64) * KW;  // keys per round
+    const int R = (nk + KPR - 1) / KPR;
+    const bool fused = a.fused;
+    int4 kb[RB];
+    float ksb[RB];
+    auto issue = [&](int r0) {
+#pragma unroll
+        for (int u = 0; u < RB; u++) {
+            const int j = (r0 + u) * KPR + wave * KW + kl;
+            const bool ok = r0 + u < R && j < nk && !(fused && j == pos);
+            kb[u] = ok && live ? *reinterpret_cast<const int4*>(K + (size_t)j * hd + piece * 16) : make_int4(0, 0, 0, 0);
+            ksb[u] = ok ? KS[j] : 0.0f;
+        }
+    };
+    issue(0);  // the first keys are in flight while the token's vectors are quantised
+    if (fused) {
+        if (wave < 3) {  // q of this head, then k, then v (kv_pack_q8, attention_q8.h:29-35)
+            const float* src = wave == 0 ? a.qkv + (size_t)h * hd : a.qkv + (size_t)((wave == 1 ? nh : nh + nkv) + kvh) * hd;
+            float vals[4];
+            float amax = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int d = lane + 64 * c;
+                vals[c] = d < hd ? src[d] : 0.0f;
+                amax = fmaxf(amax, fabsf(vals[c]));
+            }
+            amax = wave_max64(amax);
+            const float inv = quant_inv(amax);
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int d = lane + 64 * c;
+                if (d < hd) tok8[wave][d] = quant_i8(vals[c], inv);
+            }
+            if (lane == 0) toksc[wave] = quant_scale(amax);
+        }
+    } else {
+        for (int d = tid; d < hd; d += blockDim.x) tok8[0][d] = a.q8[(size_t)h * hd + d];
+        if (tid == 0) toksc[0] = a.qsc[h];
+    }
+    __syncthreads();
+    if (fused && h % group == 0 && blockIdx.z == 0) {  // kv_pack_q8 of the new position, once per kv head
+        const size_t slot = head * a.kv.max_seq + pos;
+        for (int d = tid; d < hd; d += blockDim.x) {
+            a.kv.k[slot * hd + d] = tok8[1][d];
+            a.kv.v[slot * hd + d] = tok8[2][d];
+        }
+        if (tid == 0) {
+            a.kv.ks[slot] = toksc[1];
+            a.kv.vs[slot] = toksc[2];
+        }
+    }
+    const float qsc = toksc[0], scale = 1.0f / sqrtf((float)hd);
+    const int4 qw = live ? *reinterpret_cast<const int4*>(&tok8[0][piece * 16]) : make_int4(0, 0, 0, 0);
+    const int4 knew = fused && live ? *reinterpret_cast<const int4*>(&tok8[1][piece * 16]) : make_int4(0, 0, 0, 0);
+    const float ksnew = fused ? toksc[1] : 0.0f;
+    for (int r0 = 0; r0 < R; r0 += RB) {
+        if (r0 > 0) issue(r0);
+#pragma unroll
+        for (int u = 0; u < RB; u++) {
+            const int j = (r0 + u) * KPR + wave * KW + kl;
+            const bool here = fused && j == pos;
+            const int4 k4 = here ? knew : kb[u];
+            int d = __builtin_amdgcn_sdot4(qw.x, k4.x, 0, false);
+            d = __builtin_amdgcn_sdot4(qw.y, k4.y, d, false);
+            d = __builtin_amdgcn_sdot4(qw.z, k4.z, d, false);
+            d = __builtin_amdgcn_sdot4(qw.w, k4.w, d, false);
+            d = group_sum_last(d, LP);
+            if (piece == LP - 1 && r0 + u < R && j < nk && j < ATT_ECAP)  // ATT_ONE <= ATT_ECAP
+                E[j] = (float)d * (((here ? ksnew : ksb[u]) * qsc) * scale);
+        }
+    }
+    __syncthreads();
+}
+
+template <bool ONE>
 __global__ __launch_bounds__(SPV_THREADS) void attn_softmax_pv_kernel(AttnArgs a, int ds, int vcap, int vstr, int lc) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float red[8];
     __shared__ float s_inv;
     __shared__ uint64_t exp_tab[32];
+    __shared__ __align__(16) int8_t tok8[ONE ? 3 : 1][256];  // ONE: this token's q, k, v as int8
+    __shared__ float toksc[3];
     float* E = reinterpret_cast<float*>(smem);                                   // [ATT_ECAP]
     _Float16* VH = reinterpret_cast<_Float16*>(smem + ATT_ECAP * sizeof(float));  // [ds][vstr]
 
@@ -922,8 +1025,11 @@ __global__ __launch_bounds__(SPV_THREADS) void attn_softmax_pv_kernel(AttnArgs a
         constexpr uint64_t tab[32] = JY_EXP2_TABLE;
         if (tid < 32) exp_tab[tid] = tab[tid];  // published by the barriers of the block max
     }
+    if constexpr (ONE) att_scores_local(a, h, kvh, pos, E, tok8, toksc);
+    // the new position's V row: from this workgroup's own copy when the kernel wrote it
+    const bool vnew = ONE && a.fused;
     float o = 0.0f;
-    if (nk <= ATT_ECAP) {
+    if (ONE || nk <= ATT_ECAP) {
         // the scores and V scales of this thread's keys in one batch of loads, the max,
         // then e_j in registers and in LDS, with exact zeros up to a multiple of 64 keys
         // so the chains need no tail
@@ -932,8 +1038,8 @@ __global__ __launch_bounds__(SPV_THREADS) void attn_softmax_pv_kernel(AttnArgs a
 #pragma unroll
         for (int k = 0; k < NV; k++) {
             const int j = tid + k * SPV_THREADS;
-            ev[k] = j < nk ? S[j] : -1e30f;
-            vsr[k] = j < nk ? VS[j] : 0.0f;
+            ev[k] = j < nk ? (ONE ? E[j] : S[j]) : -1e30f;
+            vsr[k] = j < nk ? (vnew && j == pos ? toksc[2] : VS[j]) : 0.0f;
         }
         float lmax = -1e30f;
 #pragma unroll
@@ -955,7 +1061,7 @@ __global__ __launch_bounds__(SPV_THREADS) void attn_softmax_pv_kernel(AttnArgs a
             const float sum = chain_sum16(E, nk64, 0.0f);  // + 0.0 for the padding: exact
             if (tid == 0) s_inv = 1.0f / sum;
         }
-        if (wave > 0) att_stage_v(V, hd, d0, ds, 0, c0, (c0 + 63) & ~63, VH, vstr, 64);
+        if (wave > 0) att_stage_v(V, hd, d0, ds, 0, vnew ? c0 - 1 : c0, (c0 + 63) & ~63, VH, vstr, 64);
         lds_barrier();
         const float inv = s_inv;
 #pragma unroll
@@ -963,6 +1069,7 @@ __global__ __launch_bounds__(SPV_THREADS) void attn_softmax_pv_kernel(AttnArgs a
             const int j = tid + k * SPV_THREADS;
             if (j < nk) E[j] = (ev[k] * inv) * vsr[k];
         }
+        if (vnew && tid < ds) VH[(size_t)tid * vstr + pos] = (_Float16)(int)tok8[2][d0 + tid];  // exact
         __syncthreads();
         // the PV chain over whole 64-key blocks: the padding adds fma(0, 0, o) = o
         for (int cs = 0; cs < nk; cs += vcap) {
@@ -974,7 +1081,7 @@ __global__ __launch_bounds__(SPV_THREADS) void attn_softmax_pv_kernel(AttnArgs a
             }
             if (tid < ds) o = chain_pv(E + cs, VH + (size_t)tid * vstr, o, cpad);
         }
-    } else {
+    } else if constexpr (!ONE) {
         // Longer contexts.  e_j is recomputed from the scores (expf is deterministic)
         // instead of being written back: in windows of ATT_LW keys for the sum chain, and
         // again as p_j * vs_j in chunks of lc keys for the PV chain.  Each is double-
@@ -1110,7 +1217,23 @@ static int att_keys_per_wg(int hd) {
     return (ATT_THREADS / 64) * (64 / lp) * ATT_U;
 }
 
+int att_short_keys() { return ATT_ONE; }
+
 void launch_attention(const AttnArgs& a, hipStream_t st) {
+    {
+        // one token whose every replayed position attends at most ATT_ONE keys: scores,
+        // softmax and PV in one kernel
+        int ds, vcap, vstr, lc;
+        size_t lds;
+        att_shape(a.hd, &ds, &vcap, &vstr, &lc, &lds);
+        const bool shortk = a.state ? a.short_ctx : a.start_pos + a.row0 + 1 <= ATT_ONE;
+        if (a.nrows == 1 && (a.hd & 15) == 0 && vcap >= ATT_ECAP && shortk) {
+            const size_t lds1 = (size_t)ATT_ECAP * 4 + (size_t)ds * vstr * 2;
+            hipLaunchKernelGGL(attn_softmax_pv_kernel<true>, dim3(a.nh, 1, a.hd / ds), dim3(SPV_THREADS), lds1, st, a,
+                               ds, vcap, vstr, lc);
+            return;
+        }
+    }
     const int kc = att_keys_per_wg(a.hd);
     // with the position on the device (graph replays) every run up to max_keys is launched
     // and the runs past the current length return at once
@@ -1122,8 +1245,8 @@ void launch_attention(const AttnArgs& a, hipStream_t st) {
     int ds, vcap, vstr, lc;
     size_t lds;
     att_shape(a.hd, &ds, &vcap, &vstr, &lc, &lds);
-    hipLaunchKernelGGL(attn_softmax_pv_kernel, dim3(a.nh, a.nrows, a.hd / ds), dim3(SPV_THREADS), lds, st, a, ds,
-                       vcap, vstr, lc);
+    hipLaunchKernelGGL(attn_softmax_pv_kernel<false>, dim3(a.nh, a.nrows, a.hd / ds), dim3(SPV_THREADS), lds, st, a,
+                       ds, vcap, vstr, lc);
 }
 
 hipError_t matvec_init();
@@ -1136,8 +1259,11 @@ hipError_t kernels_init() {
     if (e == hipSuccess) e = hipDeviceGetAttribute(&mx, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
     if (e != hipSuccess) return e;
     g_att_lds_max = mx;
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_softmax_pv_kernel),
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_softmax_pv_kernel<false>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, mx - 2048);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_softmax_pv_kernel<true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, mx - 2048);
     if (e != hipSuccess) return e;
     e = quant_init();
     if (e == hipSuccess) e = dense_init();

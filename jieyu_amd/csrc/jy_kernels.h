@@ -148,8 +148,12 @@ struct AttnArgs {
     float* scratch = nullptr;        // scores between the two attention kernels: nrows*nh*max_keys floats
     int max_keys = 0;
     float* out = nullptr;            // [rows][nh*hd]
+    // with state: every position the launch will be replayed at attends at most
+    // att_short_keys() keys (then one kernel computes the scores too)
+    bool short_ctx = false;
 };
 void launch_attention(const AttnArgs& a, hipStream_t st);
+int att_short_keys();
 
 // greedy next token (with repetition penalty): ids[state[0]] = argmax; state[0]++
 void launch_argmax(const float* logits, int V, int* ids, int* state, const int* eos, int neos, float rep_penalty,

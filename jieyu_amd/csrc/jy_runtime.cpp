@@ -476,7 +476,7 @@ void release(jyhip_model* m) {
 // the two attention kernels with K/V packing, O + residual, RMSNorm + gate/up +
 // SwiGLU, down + residual).
 void run_decode_layers(jyhip_model* m, const KVDev& kv, const int* state, int pos0, float* layer_out_host,
-                       int max_keys) {
+                       int max_keys, bool short_ctx = false) {
     Workspace& w = m->ws;
     hipStream_t st = m->stream;
     const int H = m->H, NQ = m->qd + 2 * m->kvd, F = m->F;
@@ -484,6 +484,7 @@ void run_decode_layers(jyhip_model* m, const KVDev& kv, const int* state, int po
     at.nrows = 1;
     at.start_pos = pos0;
     at.state = state;
+    at.short_ctx = short_ctx;
     at.nh = m->nh;
     at.nkv = m->nkv;
     at.hd = m->hd;
@@ -682,10 +683,12 @@ void embed_rows(jyhip_model* m, int id0, const int* state, int seq, float* X) {
 }
 
 // one decode step: embed ids[len-1], layers, final norm, lm_head, greedy pick
-void decode_step(jyhip_model* m, const KVDev& kv, int max_keys, bool greedy, float rp, int prompt_len, int neos) {
+// short_ctx: the step will only be replayed at sequence lengths up to att_short_keys()
+void decode_step(jyhip_model* m, const KVDev& kv, int max_keys, bool greedy, float rp, int prompt_len, int neos,
+                 bool short_ctx) {
     Workspace& w = m->ws;
     embed_rows(m, 0, m->state, 1, w.X);
-    run_decode_layers(m, kv, m->state, 0, nullptr, max_keys);
+    run_decode_layers(m, kv, m->state, 0, nullptr, max_keys, short_ctx);
     head_and_pick(m, w.X, greedy, rp, prompt_len, neos);
 }
 
@@ -740,7 +743,9 @@ struct Session {
     unsigned rng = 12345u;
     jyhip_token_cb cb = nullptr;
     void* ud = nullptr;
-    hipGraphExec_t exec = nullptr;
+    // the decode step as a graph: [1] for sequence lengths up to att_short_keys() (one
+    // attention kernel), [0] past it; each captured the first time a step call needs it
+    hipGraphExec_t exec[2] = {nullptr, nullptr};
     hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
     double decode_ms = 0.0;
     int decoded = 0;
@@ -748,7 +753,8 @@ struct Session {
     float* logits_out = nullptr;
 
     ~Session() {
-        if (exec) (void)hipGraphExecDestroy(exec);
+        for (hipGraphExec_t e : exec)
+            if (e) (void)hipGraphExecDestroy(e);
         for (hipEvent_t e : ev)
             if (e) (void)hipEventDestroy(e);
         if (kv_owned && kv) jyhip_kv_free(kv);
@@ -858,38 +864,43 @@ struct Session {
 
     int remaining() const { return stopped ? 0 : plen + total - len; }
 
-    void capture() {
+    void capture(int which) {
         hipStream_t st = m->stream;
         hipGraph_t graph = nullptr;
         CK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
         try {
-            decode_step(m, kv->dev, max_keys, greedy, rp, plen, neos);
+            decode_step(m, kv->dev, max_keys, greedy, rp, plen, neos, which == 1);
         } catch (...) {
             (void)hipStreamEndCapture(st, &graph);
             if (graph) (void)hipGraphDestroy(graph);
             throw;
         }
         CK(hipStreamEndCapture(st, &graph));
-        const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        const hipError_t ie = hipGraphInstantiate(&exec[which], graph, nullptr, nullptr, 0);
         (void)hipGraphDestroy(graph);
         ck(ie, "hipGraphInstantiate");
     }
+
+    // the graph for a step over a sequence of `length` tokens (it attends `length` keys)
+    hipGraphExec_t graph_for(int length) const { return exec[length <= att_short_keys() ? 1 : 0]; }
 
     // up to n more tokens; returns how many were produced
     int step(int n) {
         n = std::min(n, remaining());
         if (n <= 0) return 0;
-        if (!exec) capture();
+        // the steps run at lengths len .. len+n-1: capture what they need up front
+        if (len <= att_short_keys() && !exec[1]) capture(1);
+        if (len + n - 1 > att_short_keys() && !exec[0]) capture(0);
         hipStream_t st = m->stream;
         CK(hipEventRecord(ev[2], st));
         int made = 0;
         if (!greedy || cb || neos > 0) {
             for (; made < n && !stopped; made++) {
-                CK(hipGraphLaunch(exec, st));
+                CK(hipGraphLaunch(graph_for(len), st));
                 accept(greedy ? fetch_last() : pick_host());
             }
         } else {
-            for (int s = 0; s < n; s++) CK(hipGraphLaunch(exec, st));
+            for (int s = 0; s < n; s++) CK(hipGraphLaunch(graph_for(len + s), st));
             CK(hipMemcpyAsync(ids.data() + len, m->ids + len, sizeof(int) * n, hipMemcpyDeviceToHost, st));
             made = n;
             len += n;

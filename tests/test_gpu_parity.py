@@ -206,9 +206,10 @@ def prefill_cache(oracle_lib, d, pre, max_seq, kv):
     return okv
 
 
+# 766: 767 / 768 keys (scores inside the softmax/PV kernel) then 769 (two kernels);
 # 1534: 1535 / 1536 keys (every score in LDS) then 1537 (the first of the windowed
 # form); 3000: two windows and three chunks; 9000: windows and chunks with ragged ends
-@pytest.mark.parametrize("pre", [1534, 3000, 9000])
+@pytest.mark.parametrize("pre", [766, 1534, 3000, 9000])
 def test_prefilled_cache_long_context(jy, oracle_lib, pre):
     """Decode steps at start_pos pre.. over a cache pre-filled with packed N(0,1) K/V (the
     long-context workload's setup, at a reduced model size)."""
@@ -235,16 +236,18 @@ def test_prefilled_cache_long_context(jy, oracle_lib, pre):
     s.close()
 
 
-def test_resume_over_long_prefilled_cache(jy, oracle_lib):
-    """The decode graph (positions read on the device) over a 6000-position pre-filled
-    cache: jyhip_session_resume's greedy tokens against the oracle driven token by token
+# 760: the session's steps cross from the one-kernel graph (up to 768 keys) to the
+# two-kernel one; 6000: the windowed form throughout
+@pytest.mark.parametrize("pre,n_new", [(760, 16), (6000, 8)])
+def test_resume_over_long_prefilled_cache(jy, oracle_lib, pre, n_new):
+    """The decode graphs (positions read on the device) over a pre-filled cache:
+    jyhip_session_resume's greedy tokens against the oracle driven token by token
     (embedding row, forward_cached at the next position, lm_head, first maximum)."""
-    say("session resume over a 6000-position cache")
+    say(f"session resume over a {pre}-position cache")
     s = make_synth(oracle_lib, "hd128-q8")
     d = s.desc
     H, V, hd = d.hidden, d.vocab_size, d.head_dim
-    pre, n_new = 6000, 8
-    max_seq = pre + 16
+    max_seq = pre + n_new + 8
     cos, sin = rope_tables(oracle_lib, max_seq, hd, d.rope_theta)
     g = jy.GpuModel(d, max_seq)
     kv = g.kv(max_seq)
