@@ -26,10 +26,18 @@ Q8Dev q8_shape(int rows, int cols) {
     q.nch = (q.nb + 7) / 8;
     q.nbp = q.nch * 8;
     q.rows_pad = (rows + 3) / 4 * 4;
+    // The register buffer depth (chunks per buffer, two buffers), which also sets the
+    // zero padding of each row group to a multiple of 2U chunks.  With at least 4096
+    // row groups (a full grid of waves, 16 per CU) the waves hide latency themselves:
+    // the deepest buffer that needs no padding.  With fewer, each wave needs more
+    // chunks in flight: four per buffer for up to 1/6 extra reads, two for up to 1/16
+    // (measured at Qwen2.5-7B shapes: 3584-wide O 6.9 us at U = 4 vs 9.0 at U = 1,
+    // the 37888-row gate/up 31.5 us at U = 1 vs 35.2 at U = 4).
+    const bool many = q.rows_pad / 4 >= 4096;
     q.U = 1;
     for (int u : {4, 2}) {
-        const int padded = (q.nch + 2 * u - 1) / (2 * u) * (2 * u);
-        if ((padded - q.nch) * 16 <= q.nch) {
+        const int waste = (q.nch + 2 * u - 1) / (2 * u) * (2 * u) - q.nch;
+        if (many ? waste == 0 : waste * (u == 4 ? 6 : 16) <= q.nch) {
             q.U = u;
             break;
         }

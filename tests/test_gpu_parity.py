@@ -39,7 +39,8 @@ def bits_equal(a, b):
 # ---------------------------------------------------------------- Q8 matvec
 
 
-@pytest.mark.parametrize("rows,cols", [(8, 32), (13, 96), (100, 896), (1000, 4864), (517, 1408), (64, 14336)])
+@pytest.mark.parametrize("rows,cols", [(8, 32), (13, 96), (100, 896), (1000, 4864), (517, 1408), (64, 14336),
+                                       (300, 3584), (40, 18944)])
 def test_q8_matvec_bitexact(jy, oracle_lib, rows, cols):
     say(f"q8 matvec {rows}x{cols}")
     w = q8_random_normal(oracle_lib, rows, cols, seed=rows * 7 + cols)
