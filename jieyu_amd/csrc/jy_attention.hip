@@ -22,6 +22,9 @@
 //     past it e_j, p_j * vs_j and V move through double-buffered windows, so the
 //     chains run back to back while the other waves fill the next buffer.
 // Scores travel between the two through a per-row [nh][max_keys] float array.
+// A decode token attending at most ATT_ONE keys takes one kernel instead:
+// attn_softmax_pv_kernel<true> computes its head's scores itself (att_scores_local),
+// with the first workgroup of each kv head appending the new K/V slot.
 #include "jy_layout.h"
 
 namespace jy {
