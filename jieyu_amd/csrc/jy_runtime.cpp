@@ -97,6 +97,7 @@ struct Workspace {
     float* qsc = nullptr;
     float* scores = nullptr;
     size_t scores_n = 0;
+    unsigned gen = 0;  // bumped whenever a buffer above is replaced: graphs captured before are stale
 };
 
 struct jyhip_model {
@@ -118,6 +119,9 @@ struct jyhip_model {
     double upload_ms = 0.0;
     hipStream_t stream = nullptr;
     Workspace ws;
+    // the generation whose token ids and length the device buffers (ids, state) hold:
+    // a session can step only while it is the latest one begun on its model
+    const void* owner = nullptr;
     float* logits = nullptr;
     int* ids = nullptr;      // [max_seq + 1]
     int* state = nullptr;    // [0] = sequence length, [1] = stop flag
@@ -184,10 +188,15 @@ float* f32_put(jyhip_model* m, const void* src, size_t n) {
 void ensure_ws(jyhip_model* m, int rows) {
     Workspace& w = m->ws;
     if (w.rows >= rows) return;
+    const unsigned gen = w.gen;
     for (void* p : {(void*)w.X, (void*)w.xn, (void*)w.qkv, (void*)w.att, (void*)w.g, (void*)w.u, (void*)w.h,
                     (void*)w.q8, (void*)w.qsc})
         dfree(p);
+    float* const scores = w.scores;  // kept: sized by ensure_scores
+    const size_t scores_n = w.scores_n;
     w = Workspace{};
+    w.scores = scores;
+    w.scores_n = scores_n;
     const size_t r = (size_t)rows;
     w.X = dalloc<float>(r * m->H);
     w.xn = dalloc<float>(r * m->H);
@@ -199,6 +208,7 @@ void ensure_ws(jyhip_model* m, int rows) {
     w.q8 = dalloc<int8_t>(r * m->qd);
     w.qsc = dalloc<float>(r * m->nh);
     w.rows = rows;
+    w.gen = gen + 1;
 }
 
 void ensure_scores(jyhip_model* m, size_t n) {
@@ -207,6 +217,7 @@ void ensure_scores(jyhip_model* m, size_t n) {
     dfree(w.scores);
     w.scores = dalloc<float>(n, false);
     w.scores_n = n;
+    w.gen++;
 }
 
 bool known_type(int t) {
@@ -746,6 +757,7 @@ struct Session {
     // the decode step as a graph: [1] for sequence lengths up to att_short_keys() (one
     // attention kernel), [0] past it; each captured the first time a step call needs it
     hipGraphExec_t exec[2] = {nullptr, nullptr};
+    unsigned exec_gen[2] = {0, 0};  // the workspace generation each graph was captured on
     hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
     double decode_ms = 0.0;
     int decoded = 0;
@@ -755,6 +767,7 @@ struct Session {
     ~Session() {
         for (hipGraphExec_t e : exec)
             if (e) (void)hipGraphExecDestroy(e);
+        if (m && m->owner == this) m->owner = nullptr;
         for (hipEvent_t e : ev)
             if (e) (void)hipEventDestroy(e);
         if (kv_owned && kv) jyhip_kv_free(kv);
@@ -846,6 +859,7 @@ struct Session {
         hipStream_t st = m->stream;
         const int seq = plen - keep;
         ensure_ws(m, seq);
+        m->owner = this;
         CK(hipMemcpyAsync(m->ids, prompt, sizeof(int) * plen, hipMemcpyHostToDevice, st));
         const int st0[4] = {plen, 0, 0, 0};
         CK(hipMemcpyAsync(m->state, st0, sizeof(st0), hipMemcpyHostToDevice, st));
@@ -879,6 +893,7 @@ struct Session {
         const hipError_t ie = hipGraphInstantiate(&exec[which], graph, nullptr, nullptr, 0);
         (void)hipGraphDestroy(graph);
         ck(ie, "hipGraphInstantiate");
+        exec_gen[which] = m->ws.gen;
     }
 
     // the graph for a step over a sequence of `length` tokens (it attends `length` keys)
@@ -888,6 +903,15 @@ struct Session {
     int step(int n) {
         n = std::min(n, remaining());
         if (n <= 0) return 0;
+        if (m->owner != this)
+            fail("session: a later generation has started on this model; this one can no longer step");
+        // a graph captured before the workspace was replaced (a longer prompt or chunk
+        // since) would address freed buffers: capture it again
+        for (int i = 0; i < 2; i++)
+            if (exec[i] && exec_gen[i] != m->ws.gen) {
+                (void)hipGraphExecDestroy(exec[i]);
+                exec[i] = nullptr;
+            }
         // the steps run at lengths len .. len+n-1: capture what they need up front
         if (len <= att_short_keys() && !exec[1]) capture(1);
         if (len + n - 1 > att_short_keys() && !exec[0]) capture(0);

@@ -310,6 +310,53 @@ def test_session_resume_matches_oracle(jy, oracle_lib, key):
     s.close()
 
 
+def test_session_survives_workspace_growth(jy, oracle_lib):
+    """A forward_cached chunk longer than the session's prompt replaces the shared
+    workspace between two steps; the session captures its decode graphs again and
+    still gives the oracle's tokens."""
+    say("session across a workspace reallocation")
+    s = make_synth(oracle_lib, "llama-like-q8")
+    d = s.desc
+    prompt = np.arange(30, 35, dtype=np.int32)
+    ref_ids, _ = oracle_generate(oracle_lib, d, prompt, 64, 20)
+    g = jy.GpuModel(d, 64)
+    ss = g.session(prompt, 20)
+    ss.step(4)
+    kv2 = g.kv(64)
+    g.forward_cached(kv2, np.random.default_rng(1).standard_normal((48, d.hidden)).astype(np.float32), 0)
+    ss.step(20)
+    ids = ss.ids()
+    ss.close()
+    kv2.close()
+    g.close()
+    s.close()
+    assert np.array_equal(ids, ref_ids)
+
+
+def test_superseded_session_refuses_to_step(jy, oracle_lib):
+    """The device holds one generation's ids and length per model: once a second session
+    begins, the first one's step is an error, and the second runs as if alone."""
+    say("superseded session")
+    s = make_synth(oracle_lib, "llama-like-q8")
+    d = s.desc
+    p1 = np.arange(40, 47, dtype=np.int32)
+    p2 = np.arange(3, 12, dtype=np.int32)
+    ref2, _ = oracle_generate(oracle_lib, d, p2, 64, 12)
+    g = jy.GpuModel(d, 64)
+    s1 = g.session(p1, 12)
+    s1.step(3)
+    s2 = g.session(p2, 12)
+    with pytest.raises(jy.JyError):
+        s1.step(1)
+    s2.step(12)
+    ids2 = s2.ids()
+    s1.close()
+    s2.close()
+    g.close()
+    s.close()
+    assert np.array_equal(ids2, ref2)
+
+
 def test_sampling_and_penalty(jy, oracle_lib):
     """Temperature sampling (LCG, seed 12345) and the per-occurrence repetition penalty."""
     say("sampling + repetition penalty")
