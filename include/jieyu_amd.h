@@ -92,7 +92,10 @@ JYHIP_API int jyhip_generate(jyhip_model* model, jyhip_kv* kv, const int* prompt
  * or interleave steps).  begin runs the prompt and picks the first token;
  * step produces up to n more (returns how many, 0 when finished); ids copies the
  * sequence so far.  begin returns a finished session (len = what generate()
- * would return) when the prompt is empty/too long or max_new <= 0. */
+ * would return) when the prompt is empty/too long or max_new <= 0.  A model holds
+ * one generation's token ids and length on the device: once another session (or
+ * jyhip_generate) begins on the same model, step on the earlier session returns -1
+ * with an error.  forward_cached calls between steps are allowed. */
 typedef struct jyhip_session jyhip_session;
 JYHIP_API jyhip_session* jyhip_session_begin(jyhip_model* model, jyhip_kv* kv, const int* prompt_ids,
                                              int prompt_len, const int* eos_ids, int num_eos, int max_seq,
