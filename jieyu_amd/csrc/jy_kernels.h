@@ -113,7 +113,7 @@ void launch_matvec_q8(const Q8Dev& W, const float* x, const float* norm_w, float
 size_t matvec_lds_bytes(int cols, bool norm);
 size_t matvec_lds_limit();
 // dense [K][N] matvec (f32, or f16 converted exactly), fma chain over k per output
-// column: EPI_STORE / EPI_BIAS / EPI_RESID
+// column: EPI_STORE / EPI_BIAS / EPI_RESID, or EPI_SWIGLU: out = silu(aux) * (W x)
 void launch_matvec_f32(const float* B, int K, int N, const float* x, float* out, const float* aux, Epi epi,
                        hipStream_t st);
 void launch_matvec_f16(const uint16_t* B, int K, int N, const float* x, float* out, const float* aux, Epi epi,

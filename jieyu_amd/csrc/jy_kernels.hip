@@ -266,6 +266,7 @@ __global__ __launch_bounds__(256) void matvec_dense_kernel(const T* __restrict__
         if (EPI == EPI_STORE) out[j] = acc;
         if (EPI == EPI_BIAS) out[j] = acc + aux[j];
         if (EPI == EPI_RESID) out[j] = out[j] + acc;
+        if (EPI == EPI_SWIGLU) out[j] = silu_ref(aux[j]) * acc;  // aux: the gate row; acc: up
     }
 }
 
@@ -283,6 +284,9 @@ static void matvec_dense(const T* B, int K, int N, const float* x, float* out, c
         break;
     case EPI_RESID:
         hipLaunchKernelGGL((matvec_dense_kernel<T, EPI_RESID>), grid, block, lds, st, B, K, N, x, out, aux);
+        break;
+    case EPI_SWIGLU:
+        hipLaunchKernelGGL((matvec_dense_kernel<T, EPI_SWIGLU>), grid, block, lds, st, B, K, N, x, out, aux);
         break;
     default: break;
     }
@@ -303,7 +307,8 @@ static hipError_t dense_attr() {
     hipError_t e = hipSuccess;
     for (const void* f : {reinterpret_cast<const void*>(&matvec_dense_kernel<T, EPI_STORE>),
                           reinterpret_cast<const void*>(&matvec_dense_kernel<T, EPI_BIAS>),
-                          reinterpret_cast<const void*>(&matvec_dense_kernel<T, EPI_RESID>)})
+                          reinterpret_cast<const void*>(&matvec_dense_kernel<T, EPI_RESID>),
+                          reinterpret_cast<const void*>(&matvec_dense_kernel<T, EPI_SWIGLU>)})
         if (e == hipSuccess)
             e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)DnShape<T>::lds());
     return e;

@@ -556,8 +556,7 @@ void run_decode_layers(jyhip_model* m, const KVDev& kv, const int* state, int po
             launch_matvec_f32(D.f_o, m->qd, H, w.att, w.X, nullptr, EPI_RESID, st);
             launch_rmsnorm(w.X, w.xn, D.rms2, H, 1, st);
             launch_matvec_f32(D.f_w1, H, F, w.xn, w.g, nullptr, EPI_STORE, st);
-            launch_matvec_f32(D.f_w3, H, F, w.xn, w.u, nullptr, EPI_STORE, st);
-            launch_silu_mul(w.g, w.u, 0, 1, F, w.h, st);  // silu(gate) * up, as the fused form computed it
+            launch_matvec_f32(D.f_w3, H, F, w.xn, w.h, w.g, EPI_SWIGLU, st);  // h = silu(gate) * up
             launch_matvec_f32(D.f_w2, F, H, w.h, w.X, nullptr, EPI_RESID, st);
         }
         if (layer_out_host) {
