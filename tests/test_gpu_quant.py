@@ -88,6 +88,23 @@ def test_wmat_matmul_matches_oracle(jy, oracle_lib, t, n, k):
     W.close()
 
 
+# prompts of 128 rows or more take the 128 x 128 tile of the prompt GEMM: ragged m and n
+@pytest.mark.parametrize("t,m,n,k", [(QM.JY_Q8_0, 160, 1031, 1024), (QM.JY_Q8_0, 256, 384, 4096),
+                                     (QM.JY_Q4_K, 130, 300, 768), (QM.JY_Q6_K, 129, 257, 512)])
+def test_prompt_gemm_big_tile_matches_oracle(jy, oracle_lib, t, m, n, k):
+    say(f"prompt gemm {QM.NAMES[t]} m={m} n={n} k={k}")
+    rng = np.random.default_rng(m + n + k + t)
+    w = QM.rand_matrix(rng, t, n, k)
+    W = jy.WeightMatrix(w, t, n, k)
+    wm = QM.WMat(w.ctypes.data_as(C.c_void_p), t)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    want = np.zeros((m, n), np.float32)
+    oracle_lib.jyo_matmul_w(C.byref(wm), m, n, k, ptr(a), ptr(want))
+    got = W.matmul(a)
+    W.close()
+    assert bits_equal(got, want), f"first diffs {first_diff(got, want)}"
+
+
 def test_wmat_rejects_bad_shapes(jy):
     rng = np.random.default_rng(0)
     w = QM.rand_blocks(rng, QM.JY_Q4_K, 4, 256)
