@@ -2,7 +2,8 @@
 //
 // Device data layouts (resident in HBM for the life of a model):
 //  Q8_0 weight matrices: row groups of 4 x chunks of 8 blocks (jy_layout.h).
-//  f32 weight matrices: [K][N] row-major (jieyu's [in][out], libs/matmul_libs/matmul.h:7).
+//  f32 / f16 weight matrices: jieyu's [in][out] (libs/matmul_libs/matmul.h:7) as
+//    ceil(N/64) panels of [K][64] row-major, columns past N zero.
 //  KV cache: K and V int8 [L][nkv][max_seq][hd], scales fp32 [L][nkv][max_seq]
 //    (head-major, so one head's keys are contiguous; jieyu keeps [L][pos][nkv][hd],
 //    libs/date_libs/date.h:89-147 — jyhip_kv_read/_write convert).
@@ -50,7 +51,8 @@ struct KQDev {
 };
 
 // One weight matrix of any bound type (jieyu's WMat, libs/date_libs/wmat.h:32-44):
-// JY_F32 / JY_F16 [in][out] dense, JY_Q8_0 in the Q8 layout, k-quants in KQDev.
+// JY_F32 / JY_F16 [in][out] dense in 64-column panels (the embedding table excepted:
+// [vocab][hidden] rows), JY_Q8_0 in the Q8 layout, k-quants in KQDev.
 struct DevW {
     int type = 0;
     int in = 0, out = 0;
@@ -112,8 +114,9 @@ void launch_matvec_q8(const Q8Dev& W, const float* x, const float* norm_w, float
 // NORM), and what one workgroup may take (valid after kernels_init)
 size_t matvec_lds_bytes(int cols, bool norm);
 size_t matvec_lds_limit();
-// dense [K][N] matvec (f32, or f16 converted exactly), fma chain over k per output
-// column: EPI_STORE / EPI_BIAS / EPI_RESID, or EPI_SWIGLU: out = silu(aux) * (W x)
+// dense [K][N] matvec over the 64-column panel layout (f32, or f16 converted exactly),
+// fma chain over k per output column: EPI_STORE / EPI_BIAS / EPI_RESID, or
+// EPI_SWIGLU: out = silu(aux) * (W x)
 void launch_matvec_f32(const float* B, int K, int N, const float* x, float* out, const float* aux, Epi epi,
                        hipStream_t st);
 void launch_matvec_f16(const uint16_t* B, int K, int N, const float* x, float* out, const float* aux, Epi epi,

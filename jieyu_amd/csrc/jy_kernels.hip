@@ -146,23 +146,24 @@ void launch_rmsnorm(const float* X, float* Y, const float* w, int n, int rows, h
 // f32 or f16 weights (an f16 weight converts to float exactly): per output an fma
 // chain over k from 0 (libs/matmul_libs/x86/x86_classic.txt:2-16, matmul_f16.h:19-41).
 // The chains are sequential in k, so the parallelism is one chain per output
-// column.  One workgroup owns 64 columns: all 256 threads stream blocks of RB rows
-// of the tile (16-byte row pieces, plus the block's slice of x) into a
-// double-buffered, column-transposed LDS tile while wave 0 runs the 64 chains over
-// the previous block, one 16-byte LDS read per PER steps.  Rows past K and columns
-// past N read as zeros; a zero product leaves a chain unchanged (it starts at +0
-// and never becomes -0).
+// column.  The matrix sits in HBM as 64-column panels of 16-byte pieces
+// [ceil(K/PER)][64][PER] (piece (kb, c) holds column c's rows kb*PER .. + PER - 1,
+// zero past K and N), and one workgroup owns one panel: all 256 threads stream
+// blocks of RB rows of it (a contiguous run of pieces, plus the block's slice of x)
+// into a double-buffered LDS copy of the same order while wave 0 runs the 64
+// chains over the previous block, lane c reading column c's pieces (16 bytes per
+// PER steps, consecutive lanes on consecutive pieces).  A zero product leaves a
+// chain unchanged (it starts at +0 and never becomes -0).
 __device__ __forceinline__ float dense_w(const float* B, size_t i) { return B[i]; }
 __device__ __forceinline__ float dense_w(const uint16_t* B, size_t i) { return half_to_float(B[i]); }
 
 static constexpr int DN_COLS = 64;
 template <typename T> struct DnShape {
-    static constexpr int RB = sizeof(T) == 2 ? 512 : 256;  // rows per block (64 KiB of tile; a multiple of 8*PER)
-    static constexpr int PER = 16 / (int)sizeof(T);         // elements per 16-byte piece
-    static constexpr int LPR = DN_COLS / PER;               // pieces per tile row
-    static constexpr int LOADS = RB * LPR / 256;            // pieces per thread per block
-    static constexpr int CS = RB + 8;                       // LDS column stride (elements)
-    static constexpr size_t lds() { return (size_t)2 * DN_COLS * CS * sizeof(T) + (size_t)2 * RB * sizeof(float); }
+    static constexpr int RB = sizeof(T) == 2 ? 512 : 256;  // rows per block (64 KiB of panel)
+    static constexpr int PER = 16 / (int)sizeof(T);         // rows per 16-byte piece
+    static constexpr int PIECES = RB / PER * DN_COLS;      // pieces per block
+    static constexpr int LOADS = PIECES / 256;              // pieces per thread per block
+    static constexpr size_t lds() { return (size_t)2 * PIECES * 16 + (size_t)2 * RB * sizeof(float); }
 };
 
 template <typename T>
@@ -182,84 +183,123 @@ template <> __device__ __forceinline__ void dn_unpack<uint16_t>(const uint4& v, 
     }
 }
 
+// element (k, j) of a dense matrix in the panel layout with K rows
+template <typename T>
+__device__ __forceinline__ size_t dense_index(int K, int k, int j) {
+    constexpr int PER = 16 / (int)sizeof(T);
+    const int nkb = (K + PER - 1) / PER;
+    return (((size_t)(j / DN_COLS) * nkb + k / PER) * DN_COLS + j % DN_COLS) * PER + k % PER;
+}
+
 template <typename T, int EPI>
 __global__ __launch_bounds__(256) void matvec_dense_kernel(const T* __restrict__ B, int K, int N,
                                                            const float* __restrict__ x, float* __restrict__ out,
                                                            const float* __restrict__ aux) {
     using S = DnShape<T>;
-    constexpr int RB = S::RB, PER = S::PER, LPR = S::LPR, LOADS = S::LOADS, CS = S::CS;
+    constexpr int RB = S::RB, PER = S::PER, PIECES = S::PIECES, LOADS = S::LOADS;
     extern __shared__ __align__(16) unsigned char dsm[];
-    T* tile = reinterpret_cast<T*>(dsm);                                          // [2][64][CS]
-    float* xb = reinterpret_cast<float*>(dsm + (size_t)2 * DN_COLS * CS * sizeof(T));  // [2][RB]
+    uint4* tile = reinterpret_cast<uint4*>(dsm);                                  // [2][PIECES]
+    float* xb = reinterpret_cast<float*>(dsm + (size_t)2 * PIECES * 16);          // [2][RB]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j0 = blockIdx.x * DN_COLS;
-    const bool vec = ((size_t)N * sizeof(T)) % 16 == 0;
+    const int nkb = (K + PER - 1) / PER;
+    const uint4* __restrict__ P = reinterpret_cast<const uint4*>(B) + (size_t)blockIdx.x * nkb * DN_COLS;
     const int nblk = (K + RB - 1) / RB;
     constexpr int XL = (RB + 255) / 256;  // x values per thread per block
-    uint4 v[LOADS];
-    float xv[XL];
-    // block b's pieces into registers: piece e = tid + 256u is row e / LPR, columns
-    // (e % LPR) * PER .. + PER - 1; rows tid, tid + 256, ... of the block's x too
-    auto gload = [&](int b) {
+    // two register stages: block b + 2 loads while block b + 1 waits in registers for
+    // its LDS buffer and wave 0 runs the chains over block b
+    uint4 v0[LOADS], v1[LOADS];
+    float x0[XL], x1[XL];
+    // block b's pieces into registers: piece e = tid + 256u of the block is row piece
+    // b*RB/PER + e/64 of column e%64; rows tid, tid + 256, ... of the block's x too.
+    // Every load is issued (indices clamped into the panel and x; lstore puts the
+    // zeros past K), so that the wait before a store leaves the later stage in flight.
+    const size_t last_piece = (size_t)nkb * DN_COLS - 1;
+    auto gload = [&](uint4(&v)[LOADS], float(&xv)[XL], int b) {
 #pragma unroll
         for (int u = 0; u < LOADS; u++) {
-            const int e = tid + 256 * u, row = b * RB + e / LPR, col = j0 + (e % LPR) * PER;
-            if (row < K && vec && col + PER <= N) {
-                v[u] = *reinterpret_cast<const uint4*>(B + (size_t)row * N + col);
-            } else {
-                T el[PER];
-#pragma unroll
-                for (int k = 0; k < PER; k++) el[k] = (row < K && col + k < N) ? B[(size_t)row * N + col + k] : (T)0;
-                __builtin_memcpy(&v[u], el, 16);
-            }
+            const size_t e = (size_t)b * PIECES + tid + 256 * u;
+            v[u] = P[e < last_piece ? e : last_piece];
         }
 #pragma unroll
         for (int i = 0; i < XL; i++) {
-            const int rr = tid + 256 * i;
-            if (rr < RB) xv[i] = b * RB + rr < K ? x[b * RB + rr] : 0.0f;
+            const int rr = b * RB + tid + 256 * i;
+            xv[i] = x[rr < K ? rr : K - 1];
         }
     };
-    auto lstore = [&](int buf) {
-        T* tb = tile + (size_t)buf * DN_COLS * CS;
+    auto lstore = [&](const uint4(&v)[LOADS], const float(&xv)[XL], int b) {
+        const int buf = b & 1;
 #pragma unroll
         for (int u = 0; u < LOADS; u++) {
-            const int e = tid + 256 * u, r = e / LPR, c0 = (e % LPR) * PER;
-            T el[PER];
-            dn_unpack<T>(v[u], el);
-            // row r of column c sits at r ^ (PER * (piece & 7)): the pieces of one store
-            // instruction then fall in different LDS banks, and a column's rows stay
-            // in aligned runs of PER for the 16-byte reads
-            const int rs = r ^ (PER * ((e % LPR) & 7));
-#pragma unroll
-            for (int k = 0; k < PER; k++) tb[(size_t)(c0 + k) * CS + rs] = el[k];
+            const int e = tid + 256 * u;
+            tile[buf * PIECES + e] = b * (RB / PER) + e / DN_COLS < nkb ? v[u] : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < XL; i++) {
             const int rr = tid + 256 * i;
-            if (rr < RB) xb[buf * RB + rr] = xv[i];
+            if (rr < RB) xb[buf * RB + rr] = b * RB + rr < K ? xv[i] : 0.0f;
         }
     };
     float acc = 0.0f;
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int b = 0; b < nblk; b++) {
-        const int buf = b & 1;
-        if (b + 1 < nblk) gload(b + 1);
-        if (wave == 0) {
-            const T* col = tile + (size_t)buf * DN_COLS * CS + (size_t)lane * CS;
-            const float* xr = xb + buf * RB;
-            const int swz = PER * ((lane / PER) & 7);
-#pragma unroll 4
-            for (int p = 0; p < RB; p += PER) {
-                T el[PER];
-                dn_unpack<T>(*reinterpret_cast<const uint4*>(col + (p ^ swz)), el);
+    // wave 0's 64 chains over block b (rows past K are zeros in LDS, so the steps run
+    // to the block's last row piece rounded up to a group of G).  The LDS reads run
+    // one group ahead of the fmas (two register groups, indices clamped into the
+    // block so that every read is issued and each wait leaves the next group in
+    // flight).
+    auto chains = [&](int b) {
+        if (wave != 0) return;
+        constexpr int G = 4, NP = RB / PER, XQ = PER / 4;
+        const int rem = nkb - b * NP;
+        const int ns = rem < NP ? (rem + G - 1) / G * G : NP;
+        const uint4* col = tile + (b & 1) * PIECES + lane;
+        const float4* xr = reinterpret_cast<const float4*>(xb + (b & 1) * RB);
+        uint4 wa[G], wb[G];
+        float4 xa[G][XQ], xc[G][XQ];
+        auto rd = [&](int p, uint4(&w)[G], float4(&xq)[G][XQ]) {
+            p = p < NP - G ? p : NP - G;
 #pragma unroll
-                for (int k = 0; k < PER; k++) acc = __builtin_fmaf(xr[p + k], dense_w(el, k), acc);
+            for (int g = 0; g < G; g++) {
+                w[g] = col[(p + g) * DN_COLS];
+#pragma unroll
+                for (int q = 0; q < XQ; q++) xq[g][q] = xr[(p + g) * XQ + q];
             }
+        };
+        auto fm = [&](const uint4(&w)[G], const float4(&xq)[G][XQ]) {
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                T el[PER];
+                dn_unpack<T>(w[g], el);
+                float xs[PER];
+                __builtin_memcpy(xs, xq[g], sizeof(xs));
+#pragma unroll
+                for (int k = 0; k < PER; k++) acc = __builtin_fmaf(xs[k], dense_w(el, k), acc);
+            }
+        };
+        rd(0, wa, xa);
+        for (int p = 0; p < ns; p += 2 * G) {
+            rd(p + G, wb, xc);
+            __builtin_amdgcn_sched_barrier(0);  // keep the next group's reads ahead of the fmas
+            fm(wa, xa);
+            rd(p + 2 * G, wa, xa);
+            __builtin_amdgcn_sched_barrier(0);
+            if (p + G < ns) fm(wb, xc);
         }
-        if (b + 1 < nblk) lstore(buf ^ 1);
+    };
+    // block b is in LDS buffer b & 1 and block b + 1 in registers (nv, nx); (fv, fx)
+    // are free and take block b + 2
+    auto step = [&](int b, uint4(&nv)[LOADS], float(&nx)[XL], uint4(&fv)[LOADS], float(&fx)[XL]) {
+        gload(fv, fx, b + 2 < nblk ? b + 2 : nblk - 1);  // past the end: a re-read, never stored
+        chains(b);
+        if (b + 1 < nblk) lstore(nv, nx, b + 1);
         __syncthreads();
+    };
+    gload(v0, x0, 0);
+    gload(v1, x1, nblk > 1 ? 1 : 0);
+    lstore(v0, x0, 0);
+    __syncthreads();
+    for (int b = 0; b < nblk; b += 2) {
+        step(b, v1, x1, v0, x0);
+        if (b + 1 < nblk) step(b + 1, v0, x0, v1, x1);
     }
     const int j = j0 + lane;
     if (wave == 0 && j < N) {
@@ -386,7 +426,8 @@ __global__ __launch_bounds__(256) void gemm_quant_kernel(Acc W, int K, int N, in
     }
 }
 
-// dense [K][N] (f32, or f16 converted exactly): C = fma(A[i][p], B[p][j], C) in order of p.
+// dense [K][N] in the panel layout (f32, or f16 converted exactly): C = fma(A[i][p],
+// B[p][j], C) in order of p.
 template <typename T, int EPI>
 __global__ __launch_bounds__(256) void gemm_dense_kernel(const T* __restrict__ B, int K, int N, int m,
                                                          const float* __restrict__ A, float* __restrict__ Cm, int ldc,
@@ -413,7 +454,7 @@ __global__ __launch_bounds__(256) void gemm_dense_kernel(const T* __restrict__ B
         for (int c = 0; c < 8; c++) {
             const int e = t * 8 + c, kk = e >> 6, col = e & 63;
             const int k = k0 + kk, j = n0 + col;
-            ws[kk][col] = (k < K && j < N) ? dense_w(B, (size_t)k * N + j) : 0.0f;
+            ws[kk][col] = (k < K && j < N) ? dense_w(B, dense_index<T>(K, k, j)) : 0.0f;
         }
         __syncthreads();
         const int kmax = K - k0 < 32 ? K - k0 : 32;

@@ -85,7 +85,7 @@ struct DevLayer {
     float* rms2 = nullptr;
     float* bqkv = nullptr;
     Q8Dev qkv, o, gu, down;                        // JY_Q8_0
-    float *f_qkv = nullptr, *f_o = nullptr;        // JY_F32 [K][N]
+    float *f_qkv = nullptr, *f_o = nullptr;        // JY_F32 [K][N] in 64-column panels of pieces
     float *f_w1 = nullptr, *f_w3 = nullptr, *f_w2 = nullptr;
     DevW w[7];                                     // WT_MIXED: Wq Wk Wv Wo W1 W2 W3
 };
@@ -281,17 +281,49 @@ size_t wbytes(int type, size_t out, size_t in) {
     }
 }
 
-// one matrix of out x in weights (quantized [out][in]; f32 / f16 [in][out]) into HBM
-DevW put_w(jyhip_model* m, uint8_t* staging, const jy_wmat& src, int out, int in) {
+// A dense [K][N] matrix (jieyu's [in][out]) as ceil(N/64) panels, each holding 64
+// columns as 16-byte pieces [ceil(K/per)][64][per] (per = 16 / element size): piece
+// (kb, c) is column c's elements kb*per .. kb*per + per - 1.  Columns past N and
+// rows past K are zero.  The decode matvec's workgroup for panel p then streams one
+// contiguous run, and lane c of its chain wave reads whole pieces of its column.
+template <typename E>
+void dense_pack(const E* s, int K, int N, E* h) {
+    const int per = 16 / (int)sizeof(E), nkb = (K + per - 1) / per;
+    for (int k = 0; k < K; k++) {
+        const E* row = s + (size_t)k * N;
+        for (int j = 0; j < N; j++) h[(((size_t)(j / 64) * nkb + k / per) * 64 + j % 64) * per + k % per] = row[j];
+    }
+}
+
+void* dense_put(jyhip_model* m, const void* src, int K, int N, int es) {
+    if (!src) fail("missing dense tensor");
+    const int per = 16 / es, nkb = (K + per - 1) / per, np = (N + 63) / 64;
+    std::vector<uint8_t> h((size_t)np * nkb * 64 * 16, 0);
+    if (es == 4)
+        dense_pack(static_cast<const uint32_t*>(src), K, N, reinterpret_cast<uint32_t*>(h.data()));
+    else
+        dense_pack(static_cast<const uint16_t*>(src), K, N, reinterpret_cast<uint16_t*>(h.data()));
+    void* d = own(m, dalloc<uint8_t>(h.size(), false));
+    CK(hipMemcpy(d, h.data(), h.size(), hipMemcpyHostToDevice));
+    return d;
+}
+
+// one matrix of out x in weights (quantized [out][in]; f32 / f16 [in][out], in 64-column
+// panels unless `panels` is false: the embedding table keeps its [vocab][hidden] rows)
+DevW put_w(jyhip_model* m, uint8_t* staging, const jy_wmat& src, int out, int in, bool panels = true) {
     DevW w;
     w.type = src.type;
     w.in = in;
     w.out = out;
     const size_t nb = wbytes(src.type, out, in);
     if (src.type == JY_F32 || src.type == JY_F16) {
-        void* p = own(m, dalloc<uint8_t>(nb, false));
-        CK(hipMemcpy(p, src.data, nb, hipMemcpyHostToDevice));
-        w.dense = p;
+        if (panels) {
+            w.dense = dense_put(m, src.data, in, out, src.type == JY_F32 ? 4 : 2);
+        } else {
+            void* p = own(m, dalloc<uint8_t>(nb, false));
+            CK(hipMemcpy(p, src.data, nb, hipMemcpyHostToDevice));
+            w.dense = p;
+        }
     } else if (src.type == JY_Q8_0) {
         w.q8 = q8_alloc(m, out, in);
         q8_put(m, staging, src.data, out, in, w.q8, 0, 1);
@@ -325,7 +357,7 @@ void upload_mixed(jyhip_model* m, const jy_model_desc* d) {
     uint8_t* staging = dalloc<uint8_t>(stage, false);
     size_t total = 0;
     try {
-        m->embed_w = put_w(m, staging, d->embed, V, H);
+        m->embed_w = put_w(m, staging, d->embed, V, H, false);
         total += wbytes(d->embed.type, V, H);
         const bool dense_lm = d->lm_head.type == JY_F32 || d->lm_head.type == JY_F16;
         if (d->lm_head.data == d->embed.data && d->lm_head.type == d->embed.type && !dense_lm) {
@@ -428,23 +460,27 @@ void upload(jyhip_model* m, const jy_model_desc* d, int max_seq, int wtype) {
                           q8_bytes(V, H);
     } else {
         m->embed_f32 = f32_put(m, d->embed.data, (size_t)V * H);
-        m->lm_f32 = f32_put(m, d->lm_head.data, (size_t)H * V);  // [hidden][vocab]
+        m->lm_f32 = (float*)dense_put(m, d->lm_head.data, H, V, 4);  // [hidden][vocab]
         const size_t NQ = (size_t)qd + 2 * kvd;
         for (int l = 0; l < m->L; l++) {
             const jy_layer_weights& w = d->layers[l];
             DevLayer& D = m->layers[l];
             D.rms1 = f32_put(m, w.rms1_weight, H);
             D.rms2 = f32_put(m, w.rms2_weight, H);
-            D.f_qkv = (float*)own(m, dalloc<float>((size_t)H * NQ, false));  // [H][qd | kvd | kvd]
-            CK(hipMemcpy2D(D.f_qkv, NQ * 4, w.Wq.data, (size_t)qd * 4, (size_t)qd * 4, H, hipMemcpyHostToDevice));
-            CK(hipMemcpy2D(D.f_qkv + qd, NQ * 4, w.Wk.data, (size_t)kvd * 4, (size_t)kvd * 4, H,
-                           hipMemcpyHostToDevice));
-            CK(hipMemcpy2D(D.f_qkv + qd + kvd, NQ * 4, w.Wv.data, (size_t)kvd * 4, (size_t)kvd * 4, H,
-                           hipMemcpyHostToDevice));
-            D.f_o = f32_put(m, w.Wo.data, (size_t)qd * H);
-            D.f_w1 = f32_put(m, w.W1.data, (size_t)H * F);
-            D.f_w3 = f32_put(m, w.W3.data, (size_t)H * F);
-            D.f_w2 = f32_put(m, w.W2.data, (size_t)F * H);
+            {
+                std::vector<float> qkv((size_t)H * NQ);  // [H][qd | kvd | kvd]
+                const float* parts[3] = {static_cast<const float*>(w.Wq.data), static_cast<const float*>(w.Wk.data),
+                                         static_cast<const float*>(w.Wv.data)};
+                const int widths[3] = {qd, kvd, kvd};
+                for (int k = 0; k < H; k++)
+                    for (int i = 0, c = 0; i < 3; c += widths[i++])
+                        memcpy(&qkv[(size_t)k * NQ + c], parts[i] + (size_t)k * widths[i], (size_t)widths[i] * 4);
+                D.f_qkv = (float*)dense_put(m, qkv.data(), H, NQ, 4);
+            }
+            D.f_o = (float*)dense_put(m, w.Wo.data, qd, H, 4);
+            D.f_w1 = (float*)dense_put(m, w.W1.data, H, F, 4);
+            D.f_w3 = (float*)dense_put(m, w.W3.data, H, F, 4);
+            D.f_w2 = (float*)dense_put(m, w.W2.data, F, H, 4);
         }
         m->weight_bytes = ((size_t)m->L * ((size_t)H * NQ + (size_t)qd * H + 3 * (size_t)H * F) + (size_t)H * V) * 4;
     }

@@ -67,7 +67,8 @@ def test_wmat_matmul_reference_golden(jy):
 
 SHAPES = [(JT, n, k) for JT in (QM.JY_Q4_K, QM.JY_Q5_K, QM.JY_Q6_K)
           for (n, k) in ((4096, 4096), (14336, 4096), (4096, 14336), (1031, 768))] + \
-         [(QM.JY_F16, 1024, 4096), (QM.JY_F16, 4096, 1031), (QM.JY_Q8_0, 4096, 4096)]
+         [(QM.JY_F16, 1024, 4096), (QM.JY_F16, 4096, 1031), (QM.JY_Q8_0, 4096, 4096)] + \
+         [(QM.JY_F32, 1031, 1001), (QM.JY_F16, 70, 1003), (QM.JY_F32, 5, 3), (QM.JY_F16, 129, 7)]
 
 
 @pytest.mark.parametrize("t,n,k", SHAPES)
