@@ -148,7 +148,7 @@ void launch_rmsnorm(const float* X, float* Y, const float* w, int n, int rows, h
 // The chains are sequential in k, so the parallelism is one chain per output
 // column.  The matrix sits in HBM as 64-column panels of 16-byte pieces
 // [ceil(K/PER)][64][PER] (piece (kb, c) holds column c's rows kb*PER .. + PER - 1,
-// zero past K and N), and one workgroup owns one panel: all 256 threads stream
+// zero past K and N), and one workgroup owns one panel: four loader waves stream
 // blocks of RB rows of it (a contiguous run of pieces, plus the block's slice of x)
 // into a double-buffered LDS copy of the same order while wave 0 runs the 64
 // chains over the previous block, lane c reading column c's pieces (16 bytes per
@@ -158,11 +158,12 @@ __device__ __forceinline__ float dense_w(const float* B, size_t i) { return B[i]
 __device__ __forceinline__ float dense_w(const uint16_t* B, size_t i) { return half_to_float(B[i]); }
 
 static constexpr int DN_COLS = 64;
+static constexpr int DN_THREADS = 320;  // wave 0 runs the chains, waves 1..4 load
 template <typename T> struct DnShape {
     static constexpr int RB = sizeof(T) == 2 ? 512 : 256;  // rows per block (64 KiB of panel)
     static constexpr int PER = 16 / (int)sizeof(T);         // rows per 16-byte piece
     static constexpr int PIECES = RB / PER * DN_COLS;      // pieces per block
-    static constexpr int LOADS = PIECES / 256;              // pieces per thread per block
+    static constexpr int LOADS = PIECES / 256;              // pieces per loader thread per block
     static constexpr size_t lds() { return (size_t)2 * PIECES * 16 + (size_t)2 * RB * sizeof(float); }
 };
 
@@ -192,7 +193,7 @@ __device__ __forceinline__ size_t dense_index(int K, int k, int j) {
 }
 
 template <typename T, int EPI>
-__global__ __launch_bounds__(256) void matvec_dense_kernel(const T* __restrict__ B, int K, int N,
+__global__ __launch_bounds__(DN_THREADS) void matvec_dense_kernel(const T* __restrict__ B, int K, int N,
                                                            const float* __restrict__ x, float* __restrict__ out,
                                                            const float* __restrict__ aux) {
     using S = DnShape<T>;
@@ -200,7 +201,8 @@ __global__ __launch_bounds__(256) void matvec_dense_kernel(const T* __restrict__
     extern __shared__ __align__(16) unsigned char dsm[];
     uint4* tile = reinterpret_cast<uint4*>(dsm);                                  // [2][PIECES]
     float* xb = reinterpret_cast<float*>(dsm + (size_t)2 * PIECES * 16);          // [2][RB]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x - 64;  // loader thread 0..255 (waves 1..4)
     const int j0 = blockIdx.x * DN_COLS;
     const int nkb = (K + PER - 1) / PER;
     const uint4* __restrict__ P = reinterpret_cast<const uint4*>(B) + (size_t)blockIdx.x * nkb * DN_COLS;
@@ -210,8 +212,9 @@ __global__ __launch_bounds__(256) void matvec_dense_kernel(const T* __restrict__
     // its LDS buffer and wave 0 runs the chains over block b
     uint4 v0[LOADS], v1[LOADS];
     float x0[XL], x1[XL];
-    // block b's pieces into registers: piece e = tid + 256u of the block is row piece
-    // b*RB/PER + e/64 of column e%64; rows tid, tid + 256, ... of the block's x too.
+    // block b's pieces into a loader thread's registers: piece e = tid + 256u of the
+    // block is row piece b*RB/PER + e/64 of column e%64; rows tid, tid + 256, ... of
+    // the block's x too.
     // Every load is issued (indices clamped into the panel and x; lstore puts the
     // zeros past K), so that the wait before a store leaves the later stage in flight.
     const size_t last_piece = (size_t)nkb * DN_COLS - 1;
@@ -285,21 +288,32 @@ __global__ __launch_bounds__(256) void matvec_dense_kernel(const T* __restrict__
             if (p + G < ns) fm(wb, xc);
         }
     };
-    // block b is in LDS buffer b & 1 and block b + 1 in registers (nv, nx); (fv, fx)
-    // are free and take block b + 2
-    auto step = [&](int b, uint4(&nv)[LOADS], float(&nx)[XL], uint4(&fv)[LOADS], float(&fx)[XL]) {
-        gload(fv, fx, b + 2 < nblk ? b + 2 : nblk - 1);  // past the end: a re-read, never stored
-        chains(b);
-        if (b + 1 < nblk) lstore(nv, nx, b + 1);
+    // Phase b + 1 (between barriers b and b + 1, b = 0 .. nblk - 1): wave 0 runs the
+    // chains over block b in LDS buffer b & 1 while the loaders, holding block b + 1 in
+    // registers, issue the loads of block b + 2 into the other register set and then
+    // store block b + 1 into buffer (b + 1) & 1, which the chains left in phase b.
+    // Each side passes 1 + nblk barriers.
+    if (wave == 0) {
         __syncthreads();
-    };
-    gload(v0, x0, 0);
-    gload(v1, x1, nblk > 1 ? 1 : 0);
-    lstore(v0, x0, 0);
-    __syncthreads();
-    for (int b = 0; b < nblk; b += 2) {
-        step(b, v1, x1, v0, x0);
-        if (b + 1 < nblk) step(b + 1, v0, x0, v1, x1);
+        for (int b = 0; b < nblk; b++) {
+            chains(b);
+            __syncthreads();
+        }
+    } else {
+        gload(v0, x0, 0);
+        gload(v1, x1, nblk > 1 ? 1 : 0);
+        lstore(v0, x0, 0);
+        __syncthreads();
+        for (int b = 0; b < nblk; b += 2) {
+            gload(v0, x0, b + 2 < nblk ? b + 2 : nblk - 1);  // past the end: a re-read, never stored
+            if (b + 1 < nblk) lstore(v1, x1, b + 1);
+            __syncthreads();
+            if (b + 1 < nblk) {
+                gload(v1, x1, b + 3 < nblk ? b + 3 : nblk - 1);
+                if (b + 2 < nblk) lstore(v0, x0, b + 2);
+                __syncthreads();
+            }
+        }
     }
     const int j = j0 + lane;
     if (wave == 0 && j < N) {
@@ -313,7 +327,7 @@ __global__ __launch_bounds__(256) void matvec_dense_kernel(const T* __restrict__
 template <typename T>
 static void matvec_dense(const T* B, int K, int N, const float* x, float* out, const float* aux, Epi epi,
                          hipStream_t st) {
-    const dim3 grid((unsigned)((N + DN_COLS - 1) / DN_COLS)), block(256);
+    const dim3 grid((unsigned)((N + DN_COLS - 1) / DN_COLS)), block(DN_THREADS);
     const size_t lds = DnShape<T>::lds();
     switch (epi) {
     case EPI_STORE:
