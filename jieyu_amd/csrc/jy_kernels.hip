@@ -184,14 +184,6 @@ template <> __device__ __forceinline__ void dn_unpack<uint16_t>(const uint4& v, 
     }
 }
 
-// element (k, j) of a dense matrix in the panel layout with K rows
-template <typename T>
-__device__ __forceinline__ size_t dense_index(int K, int k, int j) {
-    constexpr int PER = 16 / (int)sizeof(T);
-    const int nkb = (K + PER - 1) / PER;
-    return (((size_t)(j / DN_COLS) * nkb + k / PER) * DN_COLS + j % DN_COLS) * PER + k % PER;
-}
-
 template <typename T, int EPI>
 __global__ __launch_bounds__(DN_THREADS) void matvec_dense_kernel(const T* __restrict__ B, int K, int N,
                                                            const float* __restrict__ x, float* __restrict__ out,
@@ -463,12 +455,26 @@ __global__ __launch_bounds__(256) void gemm_dense_kernel(const T* __restrict__ B
             const int k = k0 + lc + c;
             xs[lc + c][lt] = (tok < m && k < K) ? A[(size_t)tok * K + k] : 0.0f;
         }
-        // B rows k0..k0+31, columns n0..n0+63: thread loads 8 of them
+        // B rows k0..k0+31, columns n0..n0+63 of panel blockIdx.x: (32 / PER) x 64
+        // 16-byte pieces, piece pc = row piece pc / 64 of column pc % 64 (zeros past K
+        // come from the panel's padding; pieces past it are not read)
+        {
+            constexpr int PER = 16 / (int)sizeof(T), NPC = 32 / PER * 64 / 256;
+            const int nkb = (K + PER - 1) / PER;
+            const uint4* Pn = reinterpret_cast<const uint4*>(B) + (size_t)blockIdx.x * nkb * 64;
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const int e = t * 8 + c, kk = e >> 6, col = e & 63;
-            const int k = k0 + kk, j = n0 + col;
-            ws[kk][col] = (k < K && j < N) ? dense_w(B, dense_index<T>(K, k, j)) : 0.0f;
+            for (int i = 0; i < NPC; i++) {
+                const int pc = t + 256 * i, kb = k0 / PER + pc / 64, col = pc % 64;
+                T el[PER];
+                if (kb < nkb) {
+                    dn_unpack<T>(Pn[(size_t)kb * 64 + col], el);
+                } else {
+#pragma unroll
+                    for (int u = 0; u < PER; u++) el[u] = (T)0;
+                }
+#pragma unroll
+                for (int u = 0; u < PER; u++) ws[(pc / 64) * PER + u][col] = dense_w(el, u);
+            }
         }
         __syncthreads();
         const int kmax = K - k0 < 32 ? K - k0 : 32;
