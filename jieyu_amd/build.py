@@ -11,6 +11,7 @@ import shutil
 import subprocess
 import sys
 import tempfile
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -41,11 +42,11 @@ def _run(cmd):
     return r.stdout
 
 
-def build(verbose=False):
+def build(verbose=False, jobs=None):
     srcs = sorted(os.listdir(CSRC))
     tmp = tempfile.mkdtemp(prefix="jyamd_build_")
     try:
-        objs = []
+        objs, cmds = [], []
         for s in srcs:
             path = os.path.join(CSRC, s)
             obj = os.path.join(tmp, s + ".o")
@@ -61,8 +62,13 @@ def build(verbose=False):
                 continue
             if verbose:
                 print(" ".join(cmd))
-            _run(cmd)
+            cmds.append(cmd)
             objs.append(obj)
+        # one compiler per source file, at most `jobs` (default: the CPU count, capped at 8) at once
+        jobs = jobs or min(8, os.cpu_count() or 1)
+        with ThreadPoolExecutor(max_workers=jobs) as ex:
+            for f in [ex.submit(_run, c) for c in cmds]:
+                f.result()
         out_tmp = LIB + ".tmp"
         _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out_tmp, *objs, "-lgomp", "-lm"])
         os.replace(out_tmp, LIB)

@@ -92,6 +92,16 @@ __host__ __device__ __forceinline__ float silu_ref(float vx) {
     return vx / __builtin_fmaf(p, two_n, 1.0f);
 }
 
+// SiLU of the elements past the last full group of 8 of the flattened gate buffer
+// (libs/model_libs/silu/x86/x86_classic.txt:30-31): x / (1 + expf(-x)) with libm expf.
+__host__ __device__ __forceinline__ float silu_tail(float vx) { return vx / (1.0f + expf_libm(-vx)); }
+
+// silu of element e of a flattened gate buffer of n elements: the 8-wide form for the
+// first n/8*8, the libm form for the rest, as the reference's silu(gate, gate, n)
+__host__ __device__ __forceinline__ float silu_at(float vx, size_t e, size_t n) {
+    return e < n / 8 * 8 ? silu_ref(vx) : silu_tail(vx);
+}
+
 // int8 absmax quantisation step of kv_pack_q8 / the Q quantisation in attention
 // (libs/model_libs/attention/attention_q8.h:29-35): clamp to +-127, lrintf.
 __host__ __device__ __forceinline__ int8_t quant_i8(float v, float inv) {

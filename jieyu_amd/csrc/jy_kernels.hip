@@ -312,7 +312,7 @@ __global__ __launch_bounds__(DN_THREADS) void matvec_dense_kernel(const T* __res
         if (EPI == EPI_STORE) out[j] = acc;
         if (EPI == EPI_BIAS) out[j] = acc + aux[j];
         if (EPI == EPI_RESID) out[j] = out[j] + acc;
-        if (EPI == EPI_SWIGLU) out[j] = silu_ref(aux[j]) * acc;  // aux: the gate row; acc: up
+        if (EPI == EPI_SWIGLU) out[j] = silu_at(aux[j], j, N) * acc;  // aux: the gate row; acc: up
     }
 }
 
@@ -555,7 +555,7 @@ __global__ void silu_mul_kernel(const float* __restrict__ g, const float* __rest
     const size_t i = e / F, j = e % F;
     const float gv = interleaved ? g[i * 2 * F + 2 * j] : g[e];
     const float uv = interleaved ? g[i * 2 * F + 2 * j + 1] : u[e];
-    h[e] = silu_ref(gv) * uv;
+    h[e] = silu_at(gv, e, (size_t)m * F) * uv;
 }
 
 void launch_silu_mul(const float* g, const float* u, int interleaved, int m, int F, float* h, hipStream_t st) {

@@ -70,6 +70,10 @@ SPECS = {
     # all f16 ([in][out]), sizes that are not multiples of 32
     "f16": dict(hidden=320, heads=5, kv=1, hd=64, inter=872, vocab=900, theta=10000.0, bias=False,
                 layers=[{s: JY_F16 for s in SLOTS}] * 2, embed=JY_F16, lm=JY_F16, tied=False),
+    # all f16 with an FFN width that is not a multiple of 8: the last (rows * 1004) % 8
+    # gate values of each SwiGLU take silu's libm tail (silu/x86/x86_classic.txt:30-31)
+    "f16-tail": dict(hidden=256, heads=4, kv=1, hd=64, inter=1004, vocab=600, theta=10000.0, bias=False,
+                     layers=[{s: JY_F16 for s in SLOTS}] * 2, embed=JY_F16, lm=JY_F16, tied=False),
     # f32, f16 and Q8_0 side by side
     "f32-f16-q8": dict(hidden=256, heads=4, kv=2, hd=64, inter=768, vocab=800, theta=500000.0, bias=False,
                        layers=[dict(Wq=JY_F32, Wk=JY_F16, Wv=JY_Q8_0, Wo=JY_F16, W1=JY_Q8_0, W2=JY_F32, W3=JY_F16),

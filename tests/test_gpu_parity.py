@@ -85,6 +85,9 @@ SMALL = {
     "hd128-q8": dict(name="qwen2.5-7b", num_layers=1, hidden=1024, num_heads=8, num_kv_heads=2, head_dim=128,
                      intermediate=2048, vocab_size=2000),
     "tiny-f32": dict(name="tiny-f32", num_layers=2, vocab_size=4000),
+    # FFN width 1004: silu's libm tail on the last 4 gate values of a decode step and the
+    # last (rows * 1004) % 8 of a prompt (silu/x86/x86_classic.txt:30-31)
+    "f32-ffn-tail": dict(name="tiny-f32", num_layers=2, vocab_size=3000, intermediate=1004),
 }
 
 
