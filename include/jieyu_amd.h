@@ -77,6 +77,19 @@ JYHIP_API int jyhip_kv_read(const jyhip_kv* kv, int layer, int pos0, int npos, i
 JYHIP_API int jyhip_forward_cached(jyhip_model* model, jyhip_kv* kv, float* X, int seq, int start_pos,
                                    float* layer_out);
 
+/* Bytes of the static per-GPU workspace of jyhip_forward_cached_noalloc. */
+#define JYHIP_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* jyhip_forward_cached (layer_out aside) without any device allocation.  It has no
+ * counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, checks and results as jyhip_forward_cached with layer_out == NULL.
+ * Its workspace is one static array of JYHIP_NOALLOC_SCRATCH_BYTES in each GPU's memory,
+ * held until the process ends; a call whose rows and keys need more (a long prompt, a
+ * long context) fails with an error that names the size.  Every call on a GPU shares
+ * that GPU's array: calls that overlap on one GPU race. */
+JYHIP_API int jyhip_forward_cached_noalloc(jyhip_model* model, jyhip_kv* kv, float* X, int seq, int start_pos);
+
 /* generate / generate_cached (libs/model_libs/generate.h:9-112).  kv == NULL
  * uses a private max_seq cache.  Returns the sequence length written to
  * out_ids (prompt + generated), 0 for an empty / too long prompt, -1 on error.

@@ -63,6 +63,7 @@ def lib():
     _proto(L, "jyhip_kv_write", I, P, I, I, I, P, P, P, P)
     _proto(L, "jyhip_kv_read", I, P, I, I, I, P, P, P, P)
     _proto(L, "jyhip_forward_cached", I, P, P, P, I, I, P)
+    _proto(L, "jyhip_forward_cached_noalloc", I, P, P, P, I, I)
     _proto(L, "jyhip_generate", I, P, P, P, I, P, I, I, I, F, F, P, TOKEN_CB, P, P, C.POINTER(Stats))
     _proto(L, "jyhip_session_begin", P, P, P, P, I, P, I, I, I, F, F)
     _proto(L, "jyhip_session_resume", P, P, P, P, I, P, I, I, I, F, F)
@@ -182,6 +183,12 @@ class GpuModel:
         lo = np.zeros((self.num_layers, seq, self.hidden), np.float32) if layer_out else None
         _check(self._lib.jyhip_forward_cached(self.h, kv.h, _ptr(X), seq, start_pos, _ptr(lo)))
         return (X, lo) if layer_out else X
+
+    def forward_cached_noalloc(self, kv, X, start_pos):
+        """forward_cached over the GPU's static workspace (jyhip_forward_cached_noalloc)."""
+        X = np.array(X, np.float32, copy=True, order="C")
+        _check(self._lib.jyhip_forward_cached_noalloc(self.h, kv.h, _ptr(X), X.shape[0], start_pos))
+        return X
 
     def generate(self, prompt, max_new, max_seq=None, temperature=0.0, repetition_penalty=1.0, eos=None,
                  kv=None, callback=None, want_logits=False):

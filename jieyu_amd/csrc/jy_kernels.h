@@ -168,6 +168,9 @@ void launch_kv_import(const int8_t* k_ref, const float* ks_ref, const int8_t* v_
 void launch_kv_export(int8_t* k_ref, float* ks_ref, int8_t* v_ref, float* vs_ref, int pos0, int npos,
                       const KVDev& kv, int layer, hipStream_t st);
 
+// zeros over `bytes` (a multiple of 16, 16-byte aligned) of device memory, by a kernel
+void launch_zero_fill(void* p, size_t bytes, hipStream_t st);
+
 // argmax partials workspace for an EPI_ARGMAX matvec of `rows` rows
 int argmax_partials(int rows);
 

@@ -11,6 +11,8 @@
 //   attention          libs/model_libs/attention/x86/x86_classic.txt
 //   SiLU               libs/model_libs/silu/x86/x86_classic.txt
 //   greedy             libs/model_libs/generate.h:57-60
+#include <algorithm>
+
 #include "jy_layout.h"
 
 namespace jy {
@@ -752,6 +754,22 @@ void launch_kv_export(int8_t* k_ref, float* ks_ref, int8_t* v_ref, float* vs_ref
     const size_t n = (size_t)npos * kv.nkv * kv.hd;
     hipLaunchKernelGGL(kv_export_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, k_ref, ks_ref, v_ref,
                        vs_ref, pos0, npos, kv, layer);
+}
+
+// ---------------------------------------------------------------- clearing device memory
+
+// n16 16-byte words of zeros, grid-strided (a kernel, so a captured graph holds no memset node)
+__global__ __launch_bounds__(256) void zero_fill_kernel(uint4* __restrict__ p, size_t n16) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+        p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+void launch_zero_fill(void* p, size_t bytes, hipStream_t st) {
+    const size_t n16 = bytes / 16;
+    if (n16 == 0) return;
+    const unsigned grid = (unsigned)std::min<size_t>((n16 + 255) / 256, 2048);
+    hipLaunchKernelGGL(zero_fill_kernel, dim3(grid), dim3(256), 0, st, reinterpret_cast<uint4*>(p), n16);
 }
 
 }  // namespace jy

@@ -19,6 +19,11 @@
 
 using namespace jy;
 
+// The workspace of jyhip_forward_cached_noalloc: a fixed array in every GPU's memory,
+// held until the process ends.  In host code the name is only a stand-in for the
+// symbol, never a device address.
+static __device__ __align__(256) unsigned char scratch[JYHIP_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local std::string g_err;
@@ -65,12 +70,21 @@ void rope_table(int max_seq, int head_dim, float theta, std::vector<float>& c, s
 
 size_t q8_bytes(size_t rows, size_t cols) { return rows * (cols / 32) * 34; }
 
-// per-device kernel attributes (dynamic LDS limits), once per device and process
+// per device: the address of `scratch` on that device (hipGetSymbolAddress), the only
+// form in which host code hands the array to kernels or copies
+void* g_scratch[64] = {};
+
+// per-device set-up, once per device and process, with that device current: kernel
+// attributes (dynamic LDS limits) and the device address of `scratch`
 void init_device_kernels(int device) {
     static bool done[64] = {};
     if (device < 0 || device >= 64) fail("device index out of range");
     if (done[device]) return;
     ck(kernels_init(), "kernel attributes");
+    void* p = nullptr;
+    ck(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!p) fail("hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch[device] = p;
     done[device] = true;
 }
 
@@ -522,9 +536,8 @@ void release(jyhip_model* m) {
 // matmul (matmul_q.h:139-144).  Q8_0: six kernels per layer (RMSNorm + QKV + RoPE,
 // the two attention kernels with K/V packing, O + residual, RMSNorm + gate/up +
 // SwiGLU, down + residual).
-void run_decode_layers(jyhip_model* m, const KVDev& kv, const int* state, int pos0, float* layer_out_host,
-                       int max_keys, bool short_ctx = false) {
-    Workspace& w = m->ws;
+void run_decode_layers(jyhip_model* m, Workspace& w, const KVDev& kv, const int* state, int pos0,
+                       float* layer_out_host, int max_keys, bool short_ctx = false) {
     hipStream_t st = m->stream;
     const int H = m->H, NQ = m->qd + 2 * m->kvd, F = m->F;
     AttnArgs at;
@@ -605,9 +618,8 @@ void run_decode_layers(jyhip_model* m, const KVDev& kv, const int* state, int po
 
 // the prompt (seq > 1): the generic m > 1 matmul path (matmul_q.h:145-161) as tiled
 // GEMMs, RoPE + K/V packing of every row before attention.
-void run_prefill_layers(jyhip_model* m, const KVDev& kv, int seq, int start_pos, float* layer_out_host,
-                        int max_keys) {
-    Workspace& w = m->ws;
+void run_prefill_layers(jyhip_model* m, Workspace& w, const KVDev& kv, int seq, int start_pos,
+                        float* layer_out_host, int max_keys) {
     hipStream_t st = m->stream;
     const bool q8 = m->wtype == JY_Q8_0, mixed = m->wtype == WT_MIXED;
     const int H = m->H, NQ = m->qd + 2 * m->kvd, F = m->F;
@@ -679,18 +691,23 @@ void run_prefill_layers(jyhip_model* m, const KVDev& kv, int seq, int start_pos,
     CK(hipGetLastError());
 }
 
-void run_layers(jyhip_model* m, const KVDev& kv, int seq, int start_pos, const int* state, float* layer_out_host,
-                int max_keys) {
-    ensure_scores(m, (size_t)m->nh * max_keys * (size_t)std::max(1, std::min(seq, 64)));
+// attention score scratch (floats) a layer pass over `seq` rows attending up to max_keys keys takes
+size_t scores_need(const jyhip_model* m, int seq, int max_keys) {
+    return (size_t)m->nh * max_keys * (size_t)std::max(1, std::min(seq, 64));
+}
+
+// the layers over workspace w, whose buffers hold `seq` rows and scores_need(seq, max_keys) floats
+void run_layers(jyhip_model* m, Workspace& w, const KVDev& kv, int seq, int start_pos, const int* state,
+                float* layer_out_host, int max_keys) {
     if (seq == 1)
-        run_decode_layers(m, kv, state, start_pos, layer_out_host, max_keys);
+        run_decode_layers(m, w, kv, state, start_pos, layer_out_host, max_keys);
     else
-        run_prefill_layers(m, kv, seq, start_pos, layer_out_host, max_keys);
+        run_prefill_layers(m, w, kv, seq, start_pos, layer_out_host, max_keys);
 }
 
 // final RMSNorm of the last row + lm_head (+ greedy pick when fused) -> m->logits
 // final norm + lm_head (generate.h:48-49): fused into the Q8 matvec's prologue
-void final_and_head(jyhip_model* m, const float* xlast, bool argmax, int neos) {
+void final_and_head(jyhip_model* m, Workspace& w, const float* xlast, bool argmax, int neos) {
     if (m->wtype == JY_Q8_0) {
         MvArgs a;
         if (argmax) {
@@ -703,19 +720,20 @@ void final_and_head(jyhip_model* m, const float* xlast, bool argmax, int neos) {
         }
         launch_matvec_q8(m->lm_q8, xlast, m->final_rms, m->logits, argmax ? EPI_ARGMAX : EPI_STORE, a, m->stream);
     } else if (m->wtype == WT_MIXED) {
-        launch_rmsnorm(xlast, m->ws.xn, m->final_rms, m->H, 1, m->stream);
-        launch_mv(m->lm_w, m->ws.xn, m->logits, EPI_STORE, nullptr, m->stream);
+        launch_rmsnorm(xlast, w.xn, m->final_rms, m->H, 1, m->stream);
+        launch_mv(m->lm_w, w.xn, m->logits, EPI_STORE, nullptr, m->stream);
     } else {
-        launch_rmsnorm(xlast, m->ws.xn, m->final_rms, m->H, 1, m->stream);
-        launch_matvec_f32(m->lm_f32, m->H, m->V, m->ws.xn, m->logits, nullptr, EPI_STORE, m->stream);
+        launch_rmsnorm(xlast, w.xn, m->final_rms, m->H, 1, m->stream);
+        launch_matvec_f32(m->lm_f32, m->H, m->V, w.xn, m->logits, nullptr, EPI_STORE, m->stream);
     }
 }
 
 // greedy pick: fused into lm_head when possible, else the standalone kernel
 // (repetition penalty, f32 models)
-void head_and_pick(jyhip_model* m, const float* xlast, bool greedy, float rp, int prompt_len, int neos) {
+void head_and_pick(jyhip_model* m, Workspace& w, const float* xlast, bool greedy, float rp, int prompt_len,
+                   int neos) {
     const bool fused = greedy && rp == 1.0f && m->wtype == JY_Q8_0;
-    final_and_head(m, xlast, fused, neos);
+    final_and_head(m, w, xlast, fused, neos);
     if (greedy && !fused) launch_argmax(m->logits, m->V, m->ids, m->state, m->eos, neos, rp, prompt_len, m->stream);
 }
 
@@ -734,8 +752,8 @@ void decode_step(jyhip_model* m, const KVDev& kv, int max_keys, bool greedy, flo
                  bool short_ctx) {
     Workspace& w = m->ws;
     embed_rows(m, 0, m->state, 1, w.X);
-    run_decode_layers(m, kv, m->state, 0, nullptr, max_keys, short_ctx);
-    head_and_pick(m, w.X, greedy, rp, prompt_len, neos);
+    run_decode_layers(m, w, kv, m->state, 0, nullptr, max_keys, short_ctx);
+    head_and_pick(m, w, w.X, greedy, rp, prompt_len, neos);
 }
 
 // temperature sampling and the repetition penalty on the host, as generate.h:50-77
@@ -894,6 +912,7 @@ struct Session {
         hipStream_t st = m->stream;
         const int seq = plen - keep;
         ensure_ws(m, seq);
+        ensure_scores(m, scores_need(m, seq, max_keys));
         m->owner = this;
         CK(hipMemcpyAsync(m->ids, prompt, sizeof(int) * plen, hipMemcpyHostToDevice, st));
         const int st0[4] = {plen, 0, 0, 0};
@@ -903,8 +922,8 @@ struct Session {
         CK(hipEventRecord(ev[0], st));
         Workspace& w = m->ws;
         embed_rows(m, keep, nullptr, seq, w.X);
-        run_layers(m, kv->dev, seq, keep, nullptr, nullptr, max_keys);
-        head_and_pick(m, w.X + (size_t)(seq - 1) * m->H, greedy, rp, plen, neos);
+        run_layers(m, w, kv->dev, seq, keep, nullptr, nullptr, max_keys);
+        head_and_pick(m, w, w.X + (size_t)(seq - 1) * m->H, greedy, rp, plen, neos);
         CK(hipEventRecord(ev[1], st));
         CK(hipGetLastError());
         accept(greedy ? fetch_last() : pick_host());
@@ -1016,11 +1035,73 @@ int forward_impl(jyhip_model* m, jyhip_kv* kv, float* X, int seq, int start_pos,
     if ((size_t)start_pos + seq > (size_t)kv->dev.max_seq) fail("forward: KV cache capacity exceeded");
     if (start_pos + seq > m->max_seq) fail("forward: position beyond the RoPE table");
     hipStream_t st = m->stream;
+    const int max_keys = (start_pos + seq + 3) / 4 * 4;
     ensure_ws(m, seq);
+    ensure_scores(m, scores_need(m, seq, max_keys));
     Workspace& w = m->ws;
     CK(hipMemcpyAsync(w.X, X, sizeof(float) * seq * m->H, hipMemcpyHostToDevice, st));
+    run_layers(m, w, kv->dev, seq, start_pos, nullptr, layer_out, max_keys);
+    launch_rmsnorm(w.X, w.xn, m->final_rms, m->H, seq, st);  // forward.h:86-94
+    CK(hipGetLastError());
+    CK(hipMemcpyAsync(X, w.xn, sizeof(float) * seq * m->H, hipMemcpyDeviceToHost, st));
+    CK(hipStreamSynchronize(st));
+    kv->current_len = start_pos + seq;
+    return 0;
+}
+
+// The workspace buffers for `seq` rows and `scores_n` score floats laid out in
+// [base, base + *bytes), each buffer 256-byte aligned (the same buffers ensure_ws and
+// ensure_scores allocate one by one).
+Workspace ws_view(const jyhip_model* m, int seq, size_t scores_n, unsigned char* base, size_t* bytes) {
+    size_t off = 0;
+    auto take = [&](size_t nbytes) {
+        unsigned char* p = base + off;
+        off += (std::max<size_t>(nbytes, 1) + 255) / 256 * 256;
+        return p;
+    };
+    const size_t r = (size_t)seq;
+    Workspace w;
+    w.X = (float*)take(r * m->H * 4);
+    w.xn = (float*)take(r * m->H * 4);
+    w.qkv = (float*)take(r * (m->qd + 2 * m->kvd) * 4);
+    w.att = (float*)take(r * m->qd * 4);
+    w.g = (float*)take(r * 2 * m->F * 4);
+    w.u = (float*)take(r * m->F * 4);
+    w.h = (float*)take(r * m->F * 4);
+    w.q8 = (int8_t*)take(r * m->qd);
+    w.qsc = (float*)take(r * m->nh * 4);
+    w.scores = (float*)take(scores_n * 4);
+    w.scores_n = scores_n;
+    w.rows = seq;
+    *bytes = off;
+    return w;
+}
+
+// forward_cached over the GPU's static scratch: the checks and steps of forward_impl
+// (layer outputs aside) with no device allocation
+int forward_noalloc(jyhip_model* m, jyhip_kv* kv, float* X, int seq, int start_pos) {
+    if (!kv || !X) fail("forward: NULL kv or X");
+    if (kv->dev.num_layers < m->L || kv->dev.nkv != m->nkv || kv->dev.hd != m->hd)
+        fail("forward: KV cache shape does not match the model");
+    if (start_pos < 0) fail("forward: start_pos must not be negative");
+    if (seq <= 0) fail("forward: seq must be positive");
+    if ((size_t)start_pos + seq > (size_t)kv->dev.max_seq) fail("forward: KV cache capacity exceeded");
+    if (start_pos + seq > m->max_seq) fail("forward: position beyond the RoPE table");
+    unsigned char* base = static_cast<unsigned char*>(g_scratch[m->device]);
+    if (!base) fail("forward_cached_noalloc: the device's scratch address is not set up");
     const int max_keys = (start_pos + seq + 3) / 4 * 4;
-    run_layers(m, kv->dev, seq, start_pos, nullptr, layer_out, max_keys);
+    size_t need = 0;
+    Workspace w = ws_view(m, seq, scores_need(m, seq, max_keys), base, &need);
+    if (need > (size_t)JYHIP_NOALLOC_SCRATCH_BYTES)
+        fail("forward_cached_noalloc: " + std::to_string(seq) + " rows attending " + std::to_string(start_pos + seq) +
+             " keys need " + std::to_string(need) + " bytes of workspace, more than the " +
+             std::to_string((size_t)JYHIP_NOALLOC_SCRATCH_BYTES) + "-byte static scratch");
+    hipStream_t st = m->stream;
+    // the allocating path starts from zeroed buffers; so does this one, whatever an
+    // earlier call left in the shared array
+    launch_zero_fill(base, need, st);
+    CK(hipMemcpyAsync(w.X, X, sizeof(float) * seq * m->H, hipMemcpyHostToDevice, st));
+    run_layers(m, w, kv->dev, seq, start_pos, nullptr, nullptr, max_keys);
     launch_rmsnorm(w.X, w.xn, m->final_rms, m->H, seq, st);  // forward.h:86-94
     CK(hipGetLastError());
     CK(hipMemcpyAsync(X, w.xn, sizeof(float) * seq * m->H, hipMemcpyDeviceToHost, st));
@@ -1201,6 +1282,13 @@ JYHIP_API int jyhip_forward_cached(jyhip_model* m, jyhip_kv* kv, float* X, int s
     return guarded([&]() {
         if (!m) fail("model is NULL");
         return forward_impl(m, kv, X, seq, start_pos, layer_out);
+    }, -1);
+}
+
+JYHIP_API int jyhip_forward_cached_noalloc(jyhip_model* m, jyhip_kv* kv, float* X, int seq, int start_pos) {
+    return guarded([&]() {
+        if (!m) fail("model is NULL");
+        return forward_noalloc(m, kv, X, seq, start_pos);
     }, -1);
 }
 
