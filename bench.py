@@ -32,6 +32,13 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "batch-1 decode tokens/s (Q8, 8B shape) + achieved HBM GB/s vs peak"
+# arithmetic modes (jieyu_amd.MODE_*): exact reproduces the reference bit for bit; fast
+# splits the decode attention and matvec dots and runs prompt GEMMs on matrix cores
+# (hidden states within 1e-3 relative, greedy ids identical)
+MODES = {"exact": 0, "fast": 7}
+MODE_TEXT = {"exact": "bit-exact (reference arithmetic order)",
+             "fast": "fast: split-K attention and matvec dots, MFMA prompt GEMMs (tolerance 1e-3 relative, "
+                     "identical greedy ids)"}
 HBM_PEAK_GBS = 8000.0
 
 
@@ -70,10 +77,11 @@ def pmc_traffic(path=PMC_SUMMARY):
     return None
 
 
-def dominant_kernel_roofline(jy, d, iters=64):
-    """The decode step's gate/up launch (2F x hidden interleaved rows, RMSNorm prologue,
-    SwiGLU epilogue), timed in isolation with HIP events on its stream over enough
-    copies to defeat the 256 MiB infinity cache."""
+def dominant_kernel_roofline(jy, d, mode, iters=64):
+    """The decode step's gate/up launch (2F x hidden interleaved rows, RMSNorm, SwiGLU
+    epilogue) in the benchmark's mode, timed in isolation with HIP events on its stream
+    over enough copies to defeat the 256 MiB infinity cache."""
+    split = mode == "fast"
     rows, cols = 2 * d.intermediate, d.hidden
     nbytes = q8b(rows, cols)
     copies = max(2, int(np.ceil(1.2e9 / nbytes)))
@@ -85,19 +93,20 @@ def dominant_kernel_roofline(jy, d, iters=64):
     del x
     xin = np.random.default_rng(0).standard_normal(cols).astype(np.float32)
     m = jy.Q8Matrix(w, rows, cols, copies=copies)
-    us = m.time(xin, iters, variant=1)
+    us = m.time(xin, iters, variant=3 if split else 1)
     m.close()
     algo = nbytes + 2 * cols * 4 + (rows // 2) * 4  # weights, x, norm weights, SwiGLU output
     ach = algo / (us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(),
-            "kernel": "matvec_q8_kernel<EPI_SWIGLU, NORM> (gate/up, %d x %d)" % (rows, cols),
+            "kernel": ("matvec_q8_split_kernel<EPI_SWIGLU, NORM>" if split else "matvec_q8_kernel<EPI_SWIGLU, NORM>")
+                      + " (gate/up, %d x %d)" % (rows, cols),
             "bytes_per_launch": algo, "avg_launch_us": round(us, 3), "launches": iters, "copies": copies}
 
 
-def isolated_matvecs(jy, iters=64):
+def isolated_matvecs(jy, mode, iters=64):
     """The plain Q8 matvec at the isolated-kernel shapes (int8 ~ U[-127,127], scales
-    U(0.001,0.01), x ~ N(0,1), seed 1), rotating >1 GB of copies."""
+    U(0.001,0.01), x ~ N(0,1), seed 1) in the benchmark's mode, rotating >1 GB of copies."""
     syn = jy.lib()
     res = {}
     for rows, cols in ((4096, 4096), (14336, 4096), (4096, 14336)):
@@ -113,7 +122,7 @@ def isolated_matvecs(jy, iters=64):
         syn.jysyn_normal_fill(1, 13, 1.0, ptr(x), cols)
         copies = max(2, int(np.ceil(1.2e9 / blk.size)))
         m = jy.Q8Matrix(blk.reshape(-1), rows, cols, copies=copies)
-        us = m.time(x, iters)
+        us = m.time(x, iters, variant=2 if mode == "fast" else 0)
         m.close()
         algo = blk.size + cols * 4 + rows * 4
         res[f"{rows}x{cols}"] = {"us": round(us, 3), "GB/s": round(algo / (us * 1e-6) / 1e9, 1)}
@@ -163,7 +172,7 @@ def pack_kv_rows(x):
 OTHER_CONFIGS = (("tiny-f32", 16, 128, 0), ("qwen2.5-0.5b", 512, 256, 0), ("qwen2.5-7b", 1, 128, 32768))
 
 
-def other_config(jy, name, prompt_len, n_new, prefilled):
+def other_config(jy, name, prompt_len, n_new, prefilled, mode=0):
     """Decode rate of one more model workload through the same session path.  With
     `prefilled` > 0 the cache first holds that many positions of N(0,1) K/V (one draw,
     packed like the cache's own rows, written to every layer), and the session resumes
@@ -176,6 +185,7 @@ def other_config(jy, name, prompt_len, n_new, prefilled):
     d = syn.desc
     max_seq = (prefilled + prompt_len + n_new + 7) // 8 * 8
     g = jy.GpuModel(d, max_seq)
+    g.mode = mode
     gen_s = time.time() - t
     prompt = np.zeros(prefilled + prompt_len, np.int32)
     jy.lib().jysyn_uniform_int_fill(cfg.seed, 99, 0, d.vocab_size - 1, ptr(prompt), len(prompt))
@@ -285,6 +295,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernel", action="store_true")
     ap.add_argument("--no-other", action="store_true", help="skip the other model workloads")
+    ap.add_argument("--mode", choices=sorted(MODES), default="fast",
+                    help="arithmetic mode of the timed steps: fast (the tolerance forms) or exact (bit-exact)")
+    ap.add_argument("--other-mode-steps", type=int, default=16,
+                    help="steps then timed in the other mode, on the same session (0: skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB MiB (rocprofv3 counter scaling) and exit")
     args = ap.parse_args()
@@ -310,12 +324,14 @@ def main():
     d = syn.desc
     log(f"  {syn.weight_bytes / 1e9:.3f} GB of streamed weights in {time.time() - t:.1f} s; uploading ...")
     g = jy.GpuModel(d, args.max_seq)
-    log(f"  uploaded + repacked in {g.upload_ms / 1e3:.1f} s")
+    g.mode = MODES[args.mode]
+    log(f"  uploaded + repacked in {g.upload_ms / 1e3:.1f} s; mode {args.mode}")
 
     prompt = np.zeros(args.prompt_len, np.int32)
     jy.lib().jysyn_uniform_int_fill(cfg.seed, 99, 0, d.vocab_size - 1, ptr(prompt), len(prompt))
     K, W = args.steps, args.warmup
-    total_new = 1 + W + K
+    K2 = args.other_mode_steps
+    total_new = 1 + W + K + (2 + K2 if K2 > 0 else 0)
     assert args.prompt_len + total_new <= args.max_seq
     log(f"prefill {args.prompt_len} tokens ...")
     sess = g.session(prompt, total_new, max_seq=args.max_seq)
@@ -328,6 +344,19 @@ def main():
     t1 = time.perf_counter()
     st = sess.stats()
     ids = sess.ids()
+    other_mode = None
+    if K2 > 0:
+        # the same session, the other mode: two untimed steps (graph capture), then K2 timed
+        oname = "exact" if args.mode == "fast" else "fast"
+        g.mode = MODES[oname]
+        sess.step(2)
+        ta = time.perf_counter()
+        sess.step(K2)
+        tb = time.perf_counter()
+        g.mode = MODES[args.mode]
+        other_mode = {"mode": oname, "tokens_s": round(K2 / (tb - ta), 2),
+                      "ms_per_step": round((tb - ta) * 1e3 / K2, 4), "steps": K2}
+        log(f"  {oname} mode: {other_mode['tokens_s']} tok/s over {K2} steps")
     sess.close()
     assert made == K, f"produced {made} of {K} steps"
     wall_ms = (t1 - t0) * 1e3
@@ -343,9 +372,9 @@ def main():
     roof = iso = other = None
     if not args.no_kernel:
         log("dominant kernel in isolation ...")
-        roof = dominant_kernel_roofline(jy, d)
+        roof = dominant_kernel_roofline(jy, d, args.mode)
         log(f"  {roof['kernel']}: {roof['avg_launch_us']} us -> {roof['achieved']} GB/s")
-        iso = isolated_matvecs(jy)
+        iso = isolated_matvecs(jy, args.mode)
         log(f"  isolated matvec shapes: {iso}")
         other = isolated_other_types(jy)
         log(f"  other weight types: {other}")
@@ -364,7 +393,7 @@ def main():
     others = None
     if not args.no_other:
         log("other model workloads ...")
-        others = {name: other_config(jy, name, *rest) for name, *rest in OTHER_CONFIGS}
+        others = {name: other_config(jy, name, *rest, mode=MODES[args.mode]) for name, *rest in OTHER_CONFIGS}
 
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -374,12 +403,13 @@ def main():
         "config": {"workload": f"{args.config} shape, Q8_0 weights, int8 KV cache, batch-1 greedy decode after a "
                                f"{args.prompt_len}-token prompt (positions {p0}..{p0 + K - 1} timed)",
                    **shape, "prompt_len": args.prompt_len, "max_seq": args.max_seq,
-                   "mode": "bit-exact (reference arithmetic order)"},
+                   "mode": MODE_TEXT[args.mode]},
         "hbm_gbs": round(hbm_gbs, 1), "hbm_frac": round(hbm_gbs / HBM_PEAK_GBS, 4),
         "bytes_per_token_avg": int(bytes_total / K), "device_ms_per_step": round(dev_ms / K, 4),
         "prefill_ms": round(st.prefill_ms, 2), "prefill_tokens_s": round(args.prompt_len / (st.prefill_ms / 1e3), 1),
         "upload_s": round(st.upload_ms / 1e3, 2),
         "last_ids": ids[-8:].tolist(),
+        "other_mode": other_mode,
         "roofline": roof, "cpu_baseline": cpu, "isolated_q8_matvec": iso, "isolated_other_matvec": other,
         "other_configs": others,
     }

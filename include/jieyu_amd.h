@@ -53,6 +53,29 @@ JYHIP_API int jyhip_set_device(int device);
  * must all be JY_Q8_0 or all JY_F32. */
 JYHIP_API jyhip_model* jyhip_model_upload(const jy_model_desc* m, int max_seq);
 JYHIP_API void jyhip_model_free(jyhip_model* model);
+/* Arithmetic mode of a model's kernels (no counterpart in the reference).
+ * JYHIP_MODE_EXACT (the default) reproduces the reference's operation order and rounding
+ * bit for bit.  The other bits trade that for speed where the specification allows a
+ * tolerance (per-layer fp32 hidden states within 1e-3 relative, identical greedy ids):
+ *   JYHIP_MODE_SPLIT_ATTN  decode attention split across workgroups over the keys
+ *                          (flash-decoding): exact int8 quantisation and int32 q.k, the
+ *                          softmax sum and p.v accumulated per slice and merged;
+ *   JYHIP_MODE_SPLIT_MV    decode Q8_0 matvecs with each row's dot split across waves and
+ *                          the RMSNorm scale applied after the dot (linearity);
+ *   JYHIP_MODE_MFMA_PREFILL prompt GEMMs on bf16 matrix cores (int8 weights are exact in
+ *                          bf16; activations as a bf16 high + low pair; per-block scales
+ *                          applied in fp32).
+ * Int8 KV bytes and ids are the reference's wherever the fp32 values they come from are. */
+#define JYHIP_MODE_EXACT 0
+#define JYHIP_MODE_SPLIT_ATTN 1
+#define JYHIP_MODE_SPLIT_MV 2
+#define JYHIP_MODE_MFMA_PREFILL 4
+#define JYHIP_MODE_FAST (JYHIP_MODE_SPLIT_ATTN | JYHIP_MODE_SPLIT_MV | JYHIP_MODE_MFMA_PREFILL)
+/* Set the mode (a combination of the bits above) for later calls on the model; sessions
+ * capture their decode graphs again after a change.  Returns 0 / -1. */
+JYHIP_API int jyhip_model_set_mode(jyhip_model* model, int mode);
+JYHIP_API int jyhip_model_mode(const jyhip_model* model);
+
 /* Bytes of 2-D weights (incl. lm_head) one decode step streams. */
 JYHIP_API size_t jyhip_model_weight_bytes(const jyhip_model* model);
 JYHIP_API double jyhip_model_upload_ms(const jyhip_model* model);
@@ -137,10 +160,14 @@ typedef struct jyhip_q8mat jyhip_q8mat;
 JYHIP_API jyhip_q8mat* jyhip_q8_upload(const void* w, int rows, int cols, int copies);
 JYHIP_API void jyhip_q8_free(jyhip_q8mat* m);
 JYHIP_API int jyhip_q8_matvec(jyhip_q8mat* m, const float* x, float* y);
+/* jyhip_q8_matvec's kernel: JYHIP_MODE_EXACT (the default) or with JYHIP_MODE_SPLIT_MV the
+ * split-dot form.  Returns 0 / -1. */
+JYHIP_API int jyhip_q8_set_mode(jyhip_q8mat* m, int mode);
 /* Time `iters` launches (rotating copies) with HIP events on the launch stream:
  * *avg_us = mean kernel-to-kernel time per launch.  variant 0 is the plain
  * matvec; variant 1 is the decode step's gate/up launch of the same kernel
- * (RMSNorm prologue over x, SwiGLU epilogue over interleaved row pairs). */
+ * (RMSNorm over x, SwiGLU epilogue over interleaved row pairs); variants 2 and 3
+ * are the same two launches of the split-dot kernel (JYHIP_MODE_SPLIT_MV). */
 JYHIP_API int jyhip_q8_matvec_time(jyhip_q8mat* m, const float* x, int variant, int iters, double* avg_us);
 
 /* One weight matrix of any bound type in HBM: matmul_w (libs/model_libs/wmat_kernel.h:9-16)

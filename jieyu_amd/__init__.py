@@ -21,6 +21,14 @@ F = C.c_float
 
 TOKEN_CB = C.CFUNCTYPE(C.c_int, C.c_int, C.c_void_p)
 
+# arithmetic modes (include/jieyu_amd.h): exact reproduces the reference bit for bit; the
+# other bits are the tolerance forms of the decode attention, decode matvecs and prompt GEMMs
+MODE_EXACT = 0
+MODE_SPLIT_ATTN = 1
+MODE_SPLIT_MV = 2
+MODE_MFMA_PREFILL = 4
+MODE_FAST = MODE_SPLIT_ATTN | MODE_SPLIT_MV | MODE_MFMA_PREFILL
+
 
 class Stats(C.Structure):
     _fields_ = [("prefill_ms", C.c_double), ("decode_ms", C.c_double), ("prompt_len", C.c_int),
@@ -56,6 +64,8 @@ def lib():
     _proto(L, "jyhip_model_free", None, P)
     _proto(L, "jyhip_model_weight_bytes", C.c_size_t, P)
     _proto(L, "jyhip_model_upload_ms", C.c_double, P)
+    _proto(L, "jyhip_model_set_mode", I, P, I)
+    _proto(L, "jyhip_model_mode", I, P)
     _proto(L, "jyhip_kv_create", P, P, I)
     _proto(L, "jyhip_kv_free", None, P)
     _proto(L, "jyhip_kv_len", I, P)
@@ -76,6 +86,7 @@ def lib():
     _proto(L, "jyhip_q8_upload", P, P, I, I, I)
     _proto(L, "jyhip_q8_free", None, P)
     _proto(L, "jyhip_q8_matvec", I, P, P, P)
+    _proto(L, "jyhip_q8_set_mode", I, P, I)
     _proto(L, "jyhip_q8_matvec_time", I, P, P, I, I, C.POINTER(C.c_double))
     _proto(L, "jyhip_wmat_upload", P, C.POINTER(WMat), I, I, I)
     _proto(L, "jyhip_wmat_free", None, P)
@@ -172,6 +183,15 @@ class GpuModel:
     @property
     def upload_ms(self):
         return self._lib.jyhip_model_upload_ms(self.h)
+
+    @property
+    def mode(self):
+        """Arithmetic mode bits (MODE_EXACT, or MODE_SPLIT_ATTN | MODE_SPLIT_MV | MODE_MFMA_PREFILL)."""
+        return self._lib.jyhip_model_mode(self.h)
+
+    @mode.setter
+    def mode(self, bits):
+        _check(self._lib.jyhip_model_set_mode(self.h, int(bits)))
 
     def kv(self, max_seq=None):
         return KVCache(self, max_seq or self.max_seq)
@@ -294,8 +314,13 @@ class Q8Matrix:
         _check(self._lib.jyhip_q8_matvec(self.h, _ptr(x), _ptr(y)))
         return y
 
+    def set_mode(self, bits):
+        """MODE_EXACT or MODE_SPLIT_MV for matvec()."""
+        _check(self._lib.jyhip_q8_set_mode(self.h, int(bits)))
+
     def time(self, x, iters, variant=0):
-        """Mean µs per launch over `iters` launches; variant 1 = the decode gate/up launch."""
+        """Mean µs per launch over `iters` launches: variant 0 the plain matvec, 1 the decode
+        gate/up launch (RMSNorm + SwiGLU); 2 and 3 the same with the split-dot kernel."""
         x = np.ascontiguousarray(x, np.float32)
         us = C.c_double()
         _check(self._lib.jyhip_q8_matvec_time(self.h, _ptr(x), variant, iters, C.byref(us)))

@@ -1253,6 +1253,7 @@ void launch_attention(const AttnArgs& a, hipStream_t st) {
 }
 
 hipError_t matvec_init();
+hipError_t matvec_split_init();
 hipError_t quant_init();
 hipError_t dense_init();
 
@@ -1270,6 +1271,7 @@ hipError_t kernels_init() {
     if (e != hipSuccess) return e;
     e = quant_init();
     if (e == hipSuccess) e = dense_init();
+    if (e == hipSuccess) e = matvec_split_init();
     if (e != hipSuccess) return e;
     return matvec_init();
 }

@@ -110,6 +110,12 @@ void launch_rmsnorm(const float* X, float* Y, const float* w, int n, int rows, h
 // launches the one-workgroup pick over the per-workgroup maxima.
 void launch_matvec_q8(const Q8Dev& W, const float* x, const float* norm_w, float* out, Epi epi, const MvArgs& a,
                       hipStream_t st);
+// the same y = W x with each row's dot split over waves in a free order (the tolerance
+// mode), RMSNorm applied after the dot by linearity; same epilogues
+void launch_matvec_q8_split(const Q8Dev& W, const float* x, const float* norm_w, float* out, Epi epi,
+                            const MvArgs& a, hipStream_t st);
+// workgroups (argmax partials) of a split EPI_ARGMAX launch over `rows` rows
+int split_argmax_partials(int rows);
 // LDS the Q8 matvec takes for rows of `cols` (staged x, and the norm weights with
 // NORM), and what one workgroup may take (valid after kernels_init)
 size_t matvec_lds_bytes(int cols, bool norm);
@@ -157,6 +163,13 @@ struct AttnArgs {
 };
 void launch_attention(const AttnArgs& a, hipStream_t st);
 int att_short_keys();
+// decode attention split over the keys (jy_attention_split.hip): one token row (fused
+// q/k/v, nrows 1), `ns` slices (attn_split_slices of the longest length the launch may
+// see); part: attn_split_part_floats(nh, hd, ns) floats
+bool attn_split_supported(int nh, int nkv, int hd);
+int attn_split_slices(int keys);
+size_t attn_split_part_floats(int nh, int hd, int ns);
+void launch_attention_split(const AttnArgs& a, float* part, int ns, hipStream_t st);
 
 // greedy next token (with repetition penalty): ids[state[0]] = argmax; state[0]++
 void launch_argmax(const float* logits, int V, int* ids, int* state, const int* eos, int neos, float rep_penalty,

@@ -1,0 +1,97 @@
+// jy_matvec.h — pieces shared by the decode Q8_0 matvec kernels (the exact
+// 32-lane form in jy_matvec.hip, the split-dot form in jy_matvec_split.hip):
+// the activation vector's LDS layout and the per-row epilogues.
+#pragma once
+
+#include "jy_layout.h"
+
+namespace jy {
+
+// x in LDS, lane-pair major: element k sits at row (k & 31) >> 1 (the lane pair g that
+// reads it), column 2*(k >> 5) + (k & 1); XS = 2 * nbp + 4 floats per row
+__device__ __forceinline__ int xs_index(int k, int XS) {
+    return ((k & 31) >> 1) * XS + 2 * (k >> 5) + (k & 1);
+}
+
+// What a decode matvec does with the finished dot y of row `row` of a row group.  Every
+// lane of the row's 16-lane group holds y; the lane with g == 0 owns the row (own).
+// All lanes must call this together: the gate/up and q/k pairs are exchanged by a shuffle
+// with the partner row (lane ^ 16).
+//   STORE   out[row] = y
+//   BIAS    out[row] = y + aux[row]
+//   RESID   out[row] += y                       (transformer_layer.h:74-77, :86-89)
+//   SWIGLU  rows 2j, 2j+1 are gate_j, up_j:  out[j] = silu(gate) * up  (ffn.h:13-17)
+//   ROPE    q/k rows: (+ bias), then rope_at on the pair (2m, 2m+1) with the reference's
+//           store order inside each group of 8 pairs (rope/x86/x86_classic.txt:10-29);
+//           v rows stored as they are
+//   ARGMAX  out[row] = y, and the first maximum so far into (best_v, best_i)
+template <int EPI>
+__device__ __forceinline__ void mv_epilogue(float y, int row, bool own, int r, int rows, const MvArgs& a,
+                                            float* __restrict__ out, float& best_v, int& best_i) {
+    if (EPI == EPI_STORE) {
+        if (own) out[row] = y;
+    } else if (EPI == EPI_BIAS) {
+        if (own) out[row] = y + a.aux[row];
+    } else if (EPI == EPI_RESID) {
+        if (own) out[row] = out[row] + y;
+    } else if (EPI == EPI_SWIGLU) {
+        const float up = __shfl_xor(y, 16);
+        if (own && !(r & 1) && row + 1 < rows) out[row >> 1] = silu_ref(y) * up;
+    } else if (EPI == EPI_ROPE) {
+        const float yb = a.aux ? y + (own ? a.aux[row] : 0.0f) : y;
+        const float partner = __shfl_xor(yb, 16);
+        const int qk_rows = (a.nh + a.nkv) * a.hd;
+        if (own) {
+            if (row >= qk_rows) {
+                out[row] = yb;
+            } else if (!(r & 1)) {
+                const int hd = a.hd, half = hd >> 1;
+                const int head = row / hd, m = (row - head * hd) >> 1;
+                const int pos = a.state ? a.state[0] - 1 : a.pos0;
+                const float c = a.cos_t[(size_t)pos * half + m], s = a.sin_t[(size_t)pos * half + m];
+                const float y0 = __builtin_fmaf(yb, c, -(partner * s));
+                const float y1 = __builtin_fmaf(yb, s, partner * c);
+                int dst = m;
+                if (m < half / 8 * 8) {
+                    const int o = m & 7;
+                    dst = m - o + ((o == 2 || o == 3) ? o + 2 : (o == 4 || o == 5) ? o - 2 : o);
+                }
+                out[head * hd + 2 * dst] = y0;
+                out[head * hd + 2 * dst + 1] = y1;
+            }
+        }
+    } else if (EPI == EPI_ARGMAX) {
+        if (own) {
+            out[row] = y;
+            if (y > best_v || (y == best_v && row < best_i)) {
+                best_v = y;
+                best_i = row;
+            }
+        }
+    }
+}
+
+// ARGMAX: the workgroup's first maximum into the partials (rowv / rowi: one slot per row
+// of the workgroup's waves); argmax_finish_kernel scans them after the kernel, whose
+// boundary makes them visible device-wide (generate.h:57-60)
+__device__ __forceinline__ void mv_argmax_partial(float best_v, int best_i, int g, int r, int wave, int nwv,
+                                                  float* rowv, int* rowi, const MvArgs& a) {
+    if (g == 0) {
+        rowv[wave * 4 + r] = best_v;
+        rowi[wave * 4 + r] = best_i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float bv = rowv[0];
+        int bi = rowi[0];
+        for (int i = 1; i < nwv * 4; i++)
+            if (rowv[i] > bv || (rowv[i] == bv && rowi[i] < bi)) {
+                bv = rowv[i];
+                bi = rowi[i];
+            }
+        a.part_val[blockIdx.x] = bv;
+        a.part_idx[blockIdx.x] = bi;
+    }
+}
+
+}  // namespace jy

@@ -13,14 +13,9 @@
 // reference's rmsnorm), its weights prefetched while x is staged.
 #include <algorithm>
 
-#include "jy_layout.h"
+#include "jy_matvec.h"
 
 namespace jy {
-
-
-__device__ __forceinline__ int xs_index(int k, int XS) {
-    return ((k & 31) >> 1) * XS + 2 * (k >> 5) + (k & 1);
-}
 
 __device__ __forceinline__ void mv_chunk(const uint4& w, const uint4& dd, const float* xrow, int cc, float& a0,
                                          float& a1) {
@@ -332,74 +327,10 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
         const float y = t + dpp_f<0xB1>(t);
         const int row = rg * 4 + r;
         const bool own = active && g == 0 && row < W.rows;
-
-        if (EPI == EPI_STORE) {
-            if (own) out[row] = y;
-        } else if (EPI == EPI_BIAS) {
-            if (own) out[row] = y + a.aux[row];
-        } else if (EPI == EPI_RESID) {
-            if (own) out[row] = out[row] + y;
-        } else if (EPI == EPI_SWIGLU) {
-            // rows are interleaved gate/up pairs: h = silu(gate) * up (libs/model_libs/ffn/ffn.h:13-17)
-            const float up = __shfl_xor(y, 16);
-            if (own && !(r & 1) && row + 1 < W.rows) out[row >> 1] = silu_ref(y) * up;
-        } else if (EPI == EPI_ROPE) {
-            // q/k rows: bias, then rope_at on the pair (2m, 2m+1) with the reference's
-            // store order inside each group of 8 pairs (libs/model_libs/rope/x86/x86_classic.txt:10-29)
-            const float yb = a.aux ? y + (own ? a.aux[row] : 0.0f) : y;
-            const float partner = __shfl_xor(yb, 16);
-            const int qk_rows = (a.nh + a.nkv) * a.hd;
-            if (own) {
-                if (row >= qk_rows) {
-                    out[row] = yb;
-                } else if (!(r & 1)) {
-                    const int hd = a.hd, half = hd >> 1;
-                    const int head = row / hd, m = (row - head * hd) >> 1;
-                    const int pos = a.state ? a.state[0] - 1 : a.pos0;
-                    const float c = a.cos_t[(size_t)pos * half + m], s = a.sin_t[(size_t)pos * half + m];
-                    const float y0 = __builtin_fmaf(yb, c, -(partner * s));
-                    const float y1 = __builtin_fmaf(yb, s, partner * c);
-                    int dst = m;
-                    if (m < half / 8 * 8) {
-                        const int o = m & 7;
-                        dst = m - o + ((o == 2 || o == 3) ? o + 2 : (o == 4 || o == 5) ? o - 2 : o);
-                    }
-                    out[head * hd + 2 * dst] = y0;
-                    out[head * hd + 2 * dst + 1] = y1;
-                }
-            }
-        } else if (EPI == EPI_ARGMAX) {
-            if (own) {
-                out[row] = y;
-                if (y > best_v || (y == best_v && row < best_i)) {
-                    best_v = y;
-                    best_i = row;
-                }
-            }
-        }
+        mv_epilogue<EPI>(y, row, own, r, W.rows, a, out, best_v, best_i);
     }
 
-    if (EPI == EPI_ARGMAX) {
-        // first index of the strict maximum (generate.h:57-60): the workgroup's first
-        // maximum goes to the partials; argmax_finish_kernel scans them after this
-        // kernel (the kernel boundary makes them visible device-wide)
-        if (g == 0) {
-            rowv[wave * 4 + r] = best_v;
-            rowi[wave * 4 + r] = best_i;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            float bv = rowv[0];
-            int bi = rowi[0];
-            for (int i = 1; i < nwv * 4; i++)
-                if (rowv[i] > bv || (rowv[i] == bv && rowi[i] < bi)) {
-                    bv = rowv[i];
-                    bi = rowi[i];
-                }
-            a.part_val[blockIdx.x] = bv;
-            a.part_idx[blockIdx.x] = bi;
-        }
-    }
+    if (EPI == EPI_ARGMAX) mv_argmax_partial(best_v, best_i, g, r, wave, nwv, rowv, rowi, a);
 }
 
 // the greedy pick over the lm_head workgroups' partial maxima: lowest index among
@@ -454,6 +385,11 @@ __global__ __launch_bounds__(256) void argmax_finish_kernel(const float* __restr
     }
 }
 
+void launch_argmax_finish(const MvArgs& a, int np, hipStream_t st) {
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(256), 0, st, a.part_val, a.part_idx, np, a.ids, a.mstate,
+                       a.eos, a.neos);
+}
+
 static int g_cus = 256;
 
 // launch shape: 4 waves per workgroup, at most 4 workgroups per CU; each wave owns
@@ -487,9 +423,7 @@ static void mv_launch(const Q8Dev& W, const float* x, const float* nw, float* ou
         hipLaunchKernelGGL((matvec_q8_kernel<EPI, NORM, 2>), dim3(grid), dim3(256), lds, st, W, x, nw, out, a, per);
     else
         hipLaunchKernelGGL((matvec_q8_kernel<EPI, NORM, 1>), dim3(grid), dim3(256), lds, st, W, x, nw, out, a, per);
-    if (EPI == EPI_ARGMAX)
-        hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(256), 0, st, a.part_val, a.part_idx, grid, a.ids,
-                           a.mstate, a.eos, a.neos);
+    if (EPI == EPI_ARGMAX) launch_argmax_finish(a, grid, st);
 }
 
 template <bool NORM>

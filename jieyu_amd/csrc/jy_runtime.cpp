@@ -111,6 +111,8 @@ struct Workspace {
     float* qsc = nullptr;
     float* scores = nullptr;
     size_t scores_n = 0;
+    float* part = nullptr;  // split attention: per (query head, slice) o[hd], max, sum
+    size_t part_n = 0;
     unsigned gen = 0;  // bumped whenever a buffer above is replaced: graphs captured before are stale
 };
 
@@ -119,6 +121,7 @@ struct jyhip_model {
     int L = 0, H = 0, nh = 0, nkv = 0, hd = 0, F = 0, V = 0;
     int qd = 0, kvd = 0;
     int wtype = JY_Q8_0;
+    int mode = JYHIP_MODE_EXACT;
     bool bias = false;
     int max_seq = 0;
     float theta = 0.0f;
@@ -160,6 +163,7 @@ struct jyhip_wmat {
 };
 
 struct jyhip_q8mat {
+    int mode = JYHIP_MODE_EXACT;
     std::vector<Q8Dev> copies;
     float* x = nullptr;
     float* y = nullptr;
@@ -206,11 +210,15 @@ void ensure_ws(jyhip_model* m, int rows) {
     for (void* p : {(void*)w.X, (void*)w.xn, (void*)w.qkv, (void*)w.att, (void*)w.g, (void*)w.u, (void*)w.h,
                     (void*)w.q8, (void*)w.qsc})
         dfree(p);
-    float* const scores = w.scores;  // kept: sized by ensure_scores
+    float* const scores = w.scores;  // kept: sized by ensure_scores / ensure_part
     const size_t scores_n = w.scores_n;
+    float* const part = w.part;
+    const size_t part_n = w.part_n;
     w = Workspace{};
     w.scores = scores;
     w.scores_n = scores_n;
+    w.part = part;
+    w.part_n = part_n;
     const size_t r = (size_t)rows;
     w.X = dalloc<float>(r * m->H);
     w.xn = dalloc<float>(r * m->H);
@@ -232,6 +240,34 @@ void ensure_scores(jyhip_model* m, size_t n) {
     w.scores = dalloc<float>(n, false);
     w.scores_n = n;
     w.gen++;
+}
+
+void ensure_part(jyhip_model* m, size_t n) {
+    Workspace& w = m->ws;
+    if (w.part_n >= n) return;
+    dfree(w.part);
+    w.part = dalloc<float>(n, false);
+    w.part_n = n;
+    w.gen++;
+}
+
+// a decode Q8_0 matvec in the model's mode: the reference's 32-lane order, or the split dot
+void q8_matvec(const jyhip_model* m, const Q8Dev& W, const float* x, const float* norm_w, float* out, Epi epi,
+               const MvArgs& a, hipStream_t st) {
+    if (m->mode & JYHIP_MODE_SPLIT_MV)
+        launch_matvec_q8_split(W, x, norm_w, out, epi, a, st);
+    else
+        launch_matvec_q8(W, x, norm_w, out, epi, a, st);
+}
+
+// the decode attention runs split across workgroups (flash-decoding)
+bool split_attention(const jyhip_model* m) {
+    return (m->mode & JYHIP_MODE_SPLIT_ATTN) && m->wtype == JY_Q8_0 && attn_split_supported(m->nh, m->nkv, m->hd);
+}
+
+// slice partials (floats) a decode step attending up to max_keys keys takes
+size_t part_need(const jyhip_model* m, int max_keys) {
+    return split_attention(m) ? attn_split_part_floats(m->nh, m->hd, attn_split_slices(max_keys)) : 0;
 }
 
 bool known_type(int t) {
@@ -512,7 +548,7 @@ void upload(jyhip_model* m, const jy_model_desc* d, int max_seq, int wtype) {
     m->state = (int*)own(m, dalloc<int>(4));
     m->eos_cap = 64;
     m->eos = (int*)own(m, dalloc<int>(m->eos_cap));
-    const int np = argmax_partials(V);
+    const int np = std::max(argmax_partials(V), split_argmax_partials(V));
     m->part_val = (float*)own(m, dalloc<float>(np));
     m->part_idx = (int*)own(m, dalloc<int>(np));
 }
@@ -523,7 +559,7 @@ void release(jyhip_model* m) {
     for (void* p : m->owned) dfree(p);
     Workspace& w = m->ws;
     for (void* p : {(void*)w.X, (void*)w.xn, (void*)w.qkv, (void*)w.att, (void*)w.g, (void*)w.u, (void*)w.h,
-                    (void*)w.q8, (void*)w.qsc, (void*)w.scores})
+                    (void*)w.q8, (void*)w.qsc, (void*)w.scores, (void*)w.part})
         dfree(p);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
@@ -565,14 +601,17 @@ void run_decode_layers(jyhip_model* m, Workspace& w, const KVDev& kv, const int*
             qa.nh = m->nh;
             qa.nkv = m->nkv;
             qa.hd = m->hd;
-            launch_matvec_q8(D.qkv, w.X, D.rms1, w.qkv, EPI_ROPE, qa, st);
+            q8_matvec(m, D.qkv, w.X, D.rms1, w.qkv, EPI_ROPE, qa, st);
             at.fused = true;
             at.qkv = w.qkv;
-            launch_attention(at, st);
+            if (split_attention(m))
+                launch_attention_split(at, w.part, attn_split_slices(max_keys), st);
+            else
+                launch_attention(at, st);
             const MvArgs none;
-            launch_matvec_q8(D.o, w.att, nullptr, w.X, EPI_RESID, none, st);
-            launch_matvec_q8(D.gu, w.X, D.rms2, w.h, EPI_SWIGLU, none, st);
-            launch_matvec_q8(D.down, w.h, nullptr, w.X, EPI_RESID, none, st);
+            q8_matvec(m, D.o, w.att, nullptr, w.X, EPI_RESID, none, st);
+            q8_matvec(m, D.gu, w.X, D.rms2, w.h, EPI_SWIGLU, none, st);
+            q8_matvec(m, D.down, w.h, nullptr, w.X, EPI_RESID, none, st);
         } else if (m->wtype == WT_MIXED) {
             // one kernel per matrix, each in its own type's order
             const int qd = m->qd, kvd = m->kvd;
@@ -718,7 +757,7 @@ void final_and_head(jyhip_model* m, Workspace& w, const float* xlast, bool argma
             a.part_val = m->part_val;
             a.part_idx = m->part_idx;
         }
-        launch_matvec_q8(m->lm_q8, xlast, m->final_rms, m->logits, argmax ? EPI_ARGMAX : EPI_STORE, a, m->stream);
+        q8_matvec(m, m->lm_q8, xlast, m->final_rms, m->logits, argmax ? EPI_ARGMAX : EPI_STORE, a, m->stream);
     } else if (m->wtype == WT_MIXED) {
         launch_rmsnorm(xlast, w.xn, m->final_rms, m->H, 1, m->stream);
         launch_mv(m->lm_w, w.xn, m->logits, EPI_STORE, nullptr, m->stream);
@@ -811,6 +850,7 @@ struct Session {
     // attention kernel), [0] past it; each captured the first time a step call needs it
     hipGraphExec_t exec[2] = {nullptr, nullptr};
     unsigned exec_gen[2] = {0, 0};  // the workspace generation each graph was captured on
+    int exec_mode[2] = {0, 0};      // the model's mode each graph was captured in
     hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
     double decode_ms = 0.0;
     int decoded = 0;
@@ -913,6 +953,7 @@ struct Session {
         const int seq = plen - keep;
         ensure_ws(m, seq);
         ensure_scores(m, scores_need(m, seq, max_keys));
+        ensure_part(m, part_need(m, max_keys));
         m->owner = this;
         CK(hipMemcpyAsync(m->ids, prompt, sizeof(int) * plen, hipMemcpyHostToDevice, st));
         const int st0[4] = {plen, 0, 0, 0};
@@ -948,6 +989,7 @@ struct Session {
         (void)hipGraphDestroy(graph);
         ck(ie, "hipGraphInstantiate");
         exec_gen[which] = m->ws.gen;
+        exec_mode[which] = m->mode;
     }
 
     // the graph for a step over a sequence of `length` tokens (it attends `length` keys)
@@ -961,8 +1003,9 @@ struct Session {
             fail("session: a later generation has started on this model; this one can no longer step");
         // a graph captured before the workspace was replaced (a longer prompt or chunk
         // since) would address freed buffers: capture it again
+        ensure_part(m, part_need(m, max_keys));  // the mode may have changed since begin
         for (int i = 0; i < 2; i++)
-            if (exec[i] && exec_gen[i] != m->ws.gen) {
+            if (exec[i] && (exec_gen[i] != m->ws.gen || exec_mode[i] != m->mode)) {
                 (void)hipGraphExecDestroy(exec[i]);
                 exec[i] = nullptr;
             }
@@ -1038,6 +1081,7 @@ int forward_impl(jyhip_model* m, jyhip_kv* kv, float* X, int seq, int start_pos,
     const int max_keys = (start_pos + seq + 3) / 4 * 4;
     ensure_ws(m, seq);
     ensure_scores(m, scores_need(m, seq, max_keys));
+    ensure_part(m, part_need(m, max_keys));
     Workspace& w = m->ws;
     CK(hipMemcpyAsync(w.X, X, sizeof(float) * seq * m->H, hipMemcpyHostToDevice, st));
     run_layers(m, w, kv->dev, seq, start_pos, nullptr, layer_out, max_keys);
@@ -1052,7 +1096,8 @@ int forward_impl(jyhip_model* m, jyhip_kv* kv, float* X, int seq, int start_pos,
 // The workspace buffers for `seq` rows and `scores_n` score floats laid out in
 // [base, base + *bytes), each buffer 256-byte aligned (the same buffers ensure_ws and
 // ensure_scores allocate one by one).
-Workspace ws_view(const jyhip_model* m, int seq, size_t scores_n, unsigned char* base, size_t* bytes) {
+Workspace ws_view(const jyhip_model* m, int seq, int max_keys, size_t scores_n, unsigned char* base,
+                  size_t* bytes) {
     size_t off = 0;
     auto take = [&](size_t nbytes) {
         unsigned char* p = base + off;
@@ -1072,6 +1117,8 @@ Workspace ws_view(const jyhip_model* m, int seq, size_t scores_n, unsigned char*
     w.qsc = (float*)take(r * m->nh * 4);
     w.scores = (float*)take(scores_n * 4);
     w.scores_n = scores_n;
+    w.part_n = part_need(m, max_keys);
+    w.part = (float*)take(w.part_n * 4);
     w.rows = seq;
     *bytes = off;
     return w;
@@ -1091,7 +1138,7 @@ int forward_noalloc(jyhip_model* m, jyhip_kv* kv, float* X, int seq, int start_p
     if (!base) fail("forward_cached_noalloc: the device's scratch address is not set up");
     const int max_keys = (start_pos + seq + 3) / 4 * 4;
     size_t need = 0;
-    Workspace w = ws_view(m, seq, scores_need(m, seq, max_keys), base, &need);
+    Workspace w = ws_view(m, seq, max_keys, scores_need(m, seq, max_keys), base, &need);
     if (need > (size_t)JYHIP_NOALLOC_SCRATCH_BYTES)
         fail("forward_cached_noalloc: " + std::to_string(seq) + " rows attending " + std::to_string(start_pos + seq) +
              " keys need " + std::to_string(need) + " bytes of workspace, more than the " +
@@ -1167,6 +1214,17 @@ JYHIP_API jyhip_model* jyhip_model_upload(const jy_model_desc* d, int max_seq) {
 JYHIP_API void jyhip_model_free(jyhip_model* m) { release(m); }
 
 JYHIP_API size_t jyhip_model_weight_bytes(const jyhip_model* m) { return m ? m->weight_bytes : 0; }
+
+JYHIP_API int jyhip_model_set_mode(jyhip_model* m, int mode) {
+    return guarded([&]() {
+        if (!m) fail("model is NULL");
+        if (mode & ~JYHIP_MODE_FAST) fail("unknown mode bits");
+        m->mode = mode;
+        return 0;
+    }, -1);
+}
+
+JYHIP_API int jyhip_model_mode(const jyhip_model* m) { return m ? m->mode : -1; }
 
 JYHIP_API double jyhip_model_upload_ms(const jyhip_model* m) { return m ? m->upload_ms : 0.0; }
 
@@ -1432,7 +1490,10 @@ JYHIP_API int jyhip_q8_matvec(jyhip_q8mat* q, const float* x, float* y) {
         if (!q || !x || !y) fail("NULL argument");
         const Q8Dev& d = q->copies[0];
         CK(hipMemcpyAsync(q->x, x, sizeof(float) * d.cols, hipMemcpyHostToDevice, q->stream));
-        launch_matvec_q8(d, q->x, nullptr, q->y, EPI_STORE, MvArgs(), q->stream);
+        if (q->mode & JYHIP_MODE_SPLIT_MV)
+            launch_matvec_q8_split(d, q->x, nullptr, q->y, EPI_STORE, MvArgs(), q->stream);
+        else
+            launch_matvec_q8(d, q->x, nullptr, q->y, EPI_STORE, MvArgs(), q->stream);
         CK(hipGetLastError());
         CK(hipMemcpyAsync(y, q->y, sizeof(float) * d.rows, hipMemcpyDeviceToHost, q->stream));
         CK(hipStreamSynchronize(q->stream));
@@ -1440,15 +1501,31 @@ JYHIP_API int jyhip_q8_matvec(jyhip_q8mat* q, const float* x, float* y) {
     }, -1);
 }
 
+JYHIP_API int jyhip_q8_set_mode(jyhip_q8mat* q, int mode) {
+    return guarded([&]() {
+        if (!q) fail("matrix is NULL");
+        if (mode & ~JYHIP_MODE_FAST) fail("unknown mode bits");
+        q->mode = mode;
+        return 0;
+    }, -1);
+}
+
 JYHIP_API int jyhip_q8_matvec_time(jyhip_q8mat* q, const float* x, int variant, int iters, double* avg_us) {
     return guarded([&]() {
-        if (!q || !x || !avg_us || iters <= 0 || variant < 0 || variant > 1) fail("bad argument");
+        if (!q || !x || !avg_us || iters <= 0 || variant < 0 || variant > 3) fail("bad argument");
         const Q8Dev& d0 = q->copies[0];
-        if (variant == 1 && d0.rows % 2) fail("the gate/up variant needs interleaved row pairs");
+        if ((variant & 1) && d0.rows % 2) fail("the gate/up variant needs interleaved row pairs");
+        const bool split = variant >= 2;
+        auto mv = [&](const Q8Dev& W, const float* nw, Epi epi) {
+            if (split)
+                launch_matvec_q8_split(W, q->x, nw, q->y, epi, MvArgs(), q->stream);
+            else
+                launch_matvec_q8(W, q->x, nw, q->y, epi, MvArgs(), q->stream);
+        };
         CK(hipMemcpyAsync(q->x, x, sizeof(float) * d0.cols, hipMemcpyHostToDevice, q->stream));
         const float* nw = nullptr;
         Epi epi = EPI_STORE;
-        if (variant == 1) {  // decode's gate/up launch: RMSNorm prologue (unit weights), SwiGLU epilogue
+        if (variant & 1) {  // decode's gate/up launch: RMSNorm (unit weights), SwiGLU epilogue
             if (!q->nw) {
                 std::vector<float> ones(d0.cols, 1.0f);
                 q->nw = dalloc<float>(d0.cols);
@@ -1457,14 +1534,12 @@ JYHIP_API int jyhip_q8_matvec_time(jyhip_q8mat* q, const float* x, int variant, 
             nw = q->nw;
             epi = EPI_SWIGLU;
         }
-        for (size_t c = 0; c < q->copies.size(); c++)  // warm: one pass over every copy
-            launch_matvec_q8(q->copies[c], q->x, nw, q->y, epi, MvArgs(), q->stream);
+        for (size_t c = 0; c < q->copies.size(); c++) mv(q->copies[c], nw, epi);  // warm: every copy once
         hipEvent_t a, b;
         CK(hipEventCreate(&a));
         CK(hipEventCreate(&b));
         CK(hipEventRecord(a, q->stream));
-        for (int i = 0; i < iters; i++)
-            launch_matvec_q8(q->copies[(size_t)i % q->copies.size()], q->x, nw, q->y, epi, MvArgs(), q->stream);
+        for (int i = 0; i < iters; i++) mv(q->copies[(size_t)i % q->copies.size()], nw, epi);
         CK(hipEventRecord(b, q->stream));
         CK(hipEventSynchronize(b));
         float ms = 0.0f;
