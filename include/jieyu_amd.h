@@ -71,6 +71,11 @@ JYHIP_API void jyhip_model_free(jyhip_model* model);
 #define JYHIP_MODE_SPLIT_MV 2
 #define JYHIP_MODE_MFMA_PREFILL 4
 #define JYHIP_MODE_FAST (JYHIP_MODE_SPLIT_ATTN | JYHIP_MODE_SPLIT_MV | JYHIP_MODE_MFMA_PREFILL)
+/* With both split bits: each decode row of every layer (and, in a session's greedy step, the
+ * head) as one persistent kernel whose workgroups hand activations to each other through
+ * grid barriers, instead of about six kernels per layer.  Same arithmetic as the split
+ * forms; opt-in (measured slower than the separate kernels at the benchmark shapes). */
+#define JYHIP_MODE_PERSIST 8
 /* Set the mode (a combination of the bits above) for later calls on the model; sessions
  * capture their decode graphs again after a change.  Returns 0 / -1. */
 JYHIP_API int jyhip_model_set_mode(jyhip_model* model, int mode);

@@ -28,6 +28,7 @@ MODE_SPLIT_ATTN = 1
 MODE_SPLIT_MV = 2
 MODE_MFMA_PREFILL = 4
 MODE_FAST = MODE_SPLIT_ATTN | MODE_SPLIT_MV | MODE_MFMA_PREFILL
+MODE_PERSIST = 8  # with the split bits: the decode step as one persistent kernel (opt-in)
 
 
 class Stats(C.Structure):

@@ -1254,6 +1254,7 @@ void launch_attention(const AttnArgs& a, hipStream_t st) {
 
 hipError_t matvec_init();
 hipError_t matvec_split_init();
+hipError_t persist_init();
 hipError_t quant_init();
 hipError_t dense_init();
 
@@ -1272,6 +1273,7 @@ hipError_t kernels_init() {
     e = quant_init();
     if (e == hipSuccess) e = dense_init();
     if (e == hipSuccess) e = matvec_split_init();
+    if (e == hipSuccess) e = persist_init();
     if (e != hipSuccess) return e;
     return matvec_init();
 }

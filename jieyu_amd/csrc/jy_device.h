@@ -145,6 +145,23 @@ __device__ __forceinline__ void lds_barrier() {
 #endif
 }
 
+// Activation loads and stores: COH (one kernel whose workgroups hand each other data,
+// possibly on other XCDs, whose L2 caches are not coherent with each other) reads and
+// writes through to the agent-coherent level (sc1 on gfx950); otherwise plain accesses
+// (the data was written by an earlier kernel: the kernel boundary makes it visible).
+template <bool COH>
+__device__ __forceinline__ float act_ld(const float* p) {
+    if (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return *p;
+}
+template <bool COH>
+__device__ __forceinline__ void act_st(float* p, float v) {
+    if (COH)
+        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        *p = v;
+}
+
 // maximum over the 64 lanes of a wave, in every lane (fmaxf: order-independent for
 // the non-negative / finite values it is used on)
 __device__ __forceinline__ float wave_max64(float v) {

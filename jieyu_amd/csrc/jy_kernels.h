@@ -171,6 +171,55 @@ int attn_split_slices(int keys);
 size_t attn_split_part_floats(int nh, int hd, int ns);
 void launch_attention_split(const AttnArgs& a, float* part, int ns, hipStream_t st);
 
+// ---- the persistent decode kernel (jy_decode_persist.hip), tolerance mode
+// One Q8_0 matrix as the persistent kernel streams it: its layout and the plan of its
+// wave streams (SK waves per row group, U-chunk buffers, `per` passes per workgroup).
+struct PMat {
+    const uint8_t* qs = nullptr;
+    const uint16_t* d = nullptr;
+    int rows = 0, cols = 0, nch = 0, nchp = 0, nbp = 0;
+    int SK = 1, U = 1, per = 0;
+};
+struct PLayer {
+    PMat qkv, o, gu, down;
+    const float* rms1 = nullptr;
+    const float* rms2 = nullptr;
+    const float* bqkv = nullptr;
+};
+struct PersistArgs {
+    const PLayer* layers = nullptr;  // device array [L]
+    int L = 0, H = 0, F = 0;
+    PMat lm;
+    const float* final_rms = nullptr;
+    const float* cos_t = nullptr;
+    const float* sin_t = nullptr;
+    AttnArgs att;  // one fused decode row: qkv, kv, state or start_pos, out (the attention output)
+    float* X = nullptr;
+    float* qkv = nullptr;
+    float* h = nullptr;
+    float* part = nullptr;  // attention slices: attn_split_part_floats(nh, hd, ns)
+    int ns = 1;
+    unsigned* flags = nullptr;  // [workgroups] barrier flags, then [nkv] slice counters: zero at launch
+    unsigned* acnt = nullptr;
+    int* err = nullptr;         // set when a barrier wait gave up
+    float* layer_x = nullptr;   // optional [L][H]: X after every layer
+    int head = 0;               // 1: final RMSNorm + lm_head + greedy pick into ids / mstate
+    float* logits = nullptr;
+    float* part_val = nullptr;  // [workgroups]
+    int* part_idx = nullptr;
+    int* ids = nullptr;
+    int* mstate = nullptr;
+    const int* eos = nullptr;
+    int neos = 0;
+};
+bool persist_supported(int nh, int nkv, int hd);
+int persist_workgroups();
+int persist_slices(int nkv, int max_keys);
+size_t persist_lds_bytes(int max_nbp, int hd);
+bool persist_resident(int hd, size_t lds);
+void persist_plan(PMat& M, int nwg);
+void launch_decode_persist(const PersistArgs& A, size_t lds, hipStream_t st);
+
 // greedy next token (with repetition penalty): ids[state[0]] = argmax; state[0]++
 void launch_argmax(const float* logits, int V, int* ids, int* state, const int* eos, int neos, float rep_penalty,
                    int prompt_len, hipStream_t st);

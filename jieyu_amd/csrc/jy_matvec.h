@@ -25,25 +25,27 @@ __device__ __forceinline__ int xs_index(int k, int XS) {
 //           store order inside each group of 8 pairs (rope/x86/x86_classic.txt:10-29);
 //           v rows stored as they are
 //   ARGMAX  out[row] = y, and the first maximum so far into (best_v, best_i)
-template <int EPI>
+// With COH the activations are read and written through to the agent-coherent level
+// (act_ld / act_st), for a kernel whose workgroups hand them to each other.
+template <int EPI, bool COH = false>
 __device__ __forceinline__ void mv_epilogue(float y, int row, bool own, int r, int rows, const MvArgs& a,
                                             float* __restrict__ out, float& best_v, int& best_i) {
     if (EPI == EPI_STORE) {
-        if (own) out[row] = y;
+        if (own) act_st<COH>(out + row, y);
     } else if (EPI == EPI_BIAS) {
-        if (own) out[row] = y + a.aux[row];
+        if (own) act_st<COH>(out + row, y + a.aux[row]);
     } else if (EPI == EPI_RESID) {
-        if (own) out[row] = out[row] + y;
+        if (own) act_st<COH>(out + row, act_ld<COH>(out + row) + y);
     } else if (EPI == EPI_SWIGLU) {
         const float up = __shfl_xor(y, 16);
-        if (own && !(r & 1) && row + 1 < rows) out[row >> 1] = silu_ref(y) * up;
+        if (own && !(r & 1) && row + 1 < rows) act_st<COH>(out + (row >> 1), silu_ref(y) * up);
     } else if (EPI == EPI_ROPE) {
         const float yb = a.aux ? y + (own ? a.aux[row] : 0.0f) : y;
         const float partner = __shfl_xor(yb, 16);
         const int qk_rows = (a.nh + a.nkv) * a.hd;
         if (own) {
             if (row >= qk_rows) {
-                out[row] = yb;
+                act_st<COH>(out + row, yb);
             } else if (!(r & 1)) {
                 const int hd = a.hd, half = hd >> 1;
                 const int head = row / hd, m = (row - head * hd) >> 1;
@@ -56,13 +58,13 @@ __device__ __forceinline__ void mv_epilogue(float y, int row, bool own, int r, i
                     const int o = m & 7;
                     dst = m - o + ((o == 2 || o == 3) ? o + 2 : (o == 4 || o == 5) ? o - 2 : o);
                 }
-                out[head * hd + 2 * dst] = y0;
-                out[head * hd + 2 * dst + 1] = y1;
+                act_st<COH>(out + head * hd + 2 * dst, y0);
+                act_st<COH>(out + head * hd + 2 * dst + 1, y1);
             }
         }
     } else if (EPI == EPI_ARGMAX) {
         if (own) {
-            out[row] = y;
+            act_st<COH>(out + row, y);
             if (y > best_v || (y == best_v && row < best_i)) {
                 best_v = y;
                 best_i = row;

@@ -44,7 +44,8 @@ __device__ __forceinline__ float split_chunk_dot(const uint4& w, const uint4& dd
 
 // Wave w of a workgroup: slice ks = w % SK of row group rs = w / SK of each of the
 // workgroup's passes; pass p covers row groups (p * gridDim.x + blockIdx.x) * RPW + rs.
-// cps chunks per slice (nchp / SK, a multiple of U).
+// cps = nchp / SK chunks per slice, streamed in steps of U chunks; the last step of a
+// slice may be partial (its spare loads land on in-bounds chunks that are not used).
 template <int EPI, bool NORM, int SK, int U>
 __global__ __launch_bounds__(256) void matvec_q8_split_kernel(Q8Dev W, const float* __restrict__ x,
                                                               const float* __restrict__ nw, float* __restrict__ out,
@@ -62,7 +63,7 @@ __global__ __launch_bounds__(256) void matvec_q8_split_kernel(Q8Dev W, const flo
     const int K = W.cols, nch = W.nch, nchp = W.nchp, XS = 2 * W.nbp + 4;
     const int groups = (W.rows + 3) >> 2;
     const int cps = nchp / SK, c_lo = ks * cps;
-    const int steps_per_row = cps / U;
+    const int steps_per_row = (cps + U - 1) / U;
 
     // the weight stream: (row group of pass p, chunk c_lo + i), i < cps, pass after pass
     const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(W.qs, (short)0, 0x7fffffff, 0x00020000);
@@ -79,7 +80,7 @@ __global__ __launch_bounds__(256) void matvec_q8_split_kernel(Q8Dev W, const flo
             db[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(drs, doff, (c + u) * 64, 0));
         }
         li += U;
-        if (li == cps) {
+        if (li >= cps) {
             li = 0;
             lp++;
         }
@@ -185,10 +186,10 @@ __global__ __launch_bounds__(256) void matvec_q8_split_kernel(Q8Dev W, const flo
             const int p = s / steps_per_row;
 #pragma unroll
             for (int u = 0; u < U; u++)
-                if (c_lo + ci + u < nch) acc = split_chunk_dot(wA[u], dA[u], xrow, c_lo + ci + u, acc);
+                if (ci + u < cps && c_lo + ci + u < nch) acc = split_chunk_dot(wA[u], dA[u], xrow, c_lo + ci + u, acc);
             load(wA, dA);
             ci += U;
-            if (ci == cps) {
+            if (ci >= cps) {
                 finish(p);
                 ci = 0;
             }
@@ -197,10 +198,10 @@ __global__ __launch_bounds__(256) void matvec_q8_split_kernel(Q8Dev W, const flo
             const int p = (s + 1) / steps_per_row;
 #pragma unroll
             for (int u = 0; u < U; u++)
-                if (c_lo + ci + u < nch) acc = split_chunk_dot(wB[u], dB[u], xrow, c_lo + ci + u, acc);
+                if (ci + u < cps && c_lo + ci + u < nch) acc = split_chunk_dot(wB[u], dB[u], xrow, c_lo + ci + u, acc);
             load(wB, dB);
             ci += U;
-            if (ci == cps) {
+            if (ci >= cps) {
                 finish(p);
                 ci = 0;
             }
@@ -216,28 +217,43 @@ struct SplitShape {
     int SK, U, grid, per;
 };
 
-// split and buffer depth by shape: enough waves to keep the matrix's bytes in flight
-// (at least two per SIMD), each slice a whole number of buffers
-static SplitShape split_shape(const Q8Dev& W) {
+// the deepest buffer of U in {8, 7, 4, 2, 1} chunks that divides a slice of cps chunks
+static int split_u(int cps) {
+    for (int u : {8, 7, 4, 2})
+        if (cps % u == 0) return u;
+    return 1;
+}
+
+static SplitShape shape_of(const Q8Dev& W, int sk, int wpc) {
     const int groups = (W.rows + 3) / 4;
-    SplitShape s{1, 1, 1, 1};
-    int sk = 1;
-    while (sk < 4 && groups * sk < 8 * g_split_cus && W.nchp % (sk * 2) == 0) sk *= 2;
-    s.SK = sk;
-    const int cps = W.nchp / sk;
-    s.U = cps % 4 == 0 ? 4 : cps % 2 == 0 ? 2 : 1;
+    SplitShape s{sk, split_u(W.nchp / sk), 1, 1};
     const int rpw = 4 / sk;
     const int passes = (groups + rpw - 1) / rpw;
-    const int max_wg = 4 * g_split_cus;
+    const int max_wg = wpc * g_split_cus;
     s.per = (passes + max_wg - 1) / max_wg;
     s.grid = (passes + s.per - 1) / s.per;
     return s;
 }
 
+// split and buffer depth by shape: enough waves to keep the matrix's bytes in flight
+// (at least two per SIMD), each slice a whole number of buffers
+static SplitShape split_shape(const Q8Dev& W) {
+    const int groups = (W.rows + 3) / 4;
+    int sk = 1;
+    while (sk < 4 && groups * sk < 8 * g_split_cus && W.nchp % (sk * 2) == 0) sk *= 2;
+    return shape_of(W, sk, 4);
+}
+
 template <int EPI, bool NORM, int SK>
 static void split_launch_u(const Q8Dev& W, const SplitShape& sh, const float* x, const float* nw, float* out,
                            const MvArgs& a, size_t lds, hipStream_t st) {
-    if (sh.U == 4)
+    if (sh.U == 8)
+        hipLaunchKernelGGL((matvec_q8_split_kernel<EPI, NORM, SK, 8>), dim3(sh.grid), dim3(256), lds, st, W, x, nw,
+                           out, a, sh.per);
+    else if (sh.U == 7)
+        hipLaunchKernelGGL((matvec_q8_split_kernel<EPI, NORM, SK, 7>), dim3(sh.grid), dim3(256), lds, st, W, x, nw,
+                           out, a, sh.per);
+    else if (sh.U == 4)
         hipLaunchKernelGGL((matvec_q8_split_kernel<EPI, NORM, SK, 4>), dim3(sh.grid), dim3(256), lds, st, W, x, nw,
                            out, a, sh.per);
     else if (sh.U == 2)
@@ -293,7 +309,9 @@ int split_argmax_partials(int rows) {
 template <int EPI, bool NORM, int SK>
 static hipError_t split_attr_sk() {
     hipError_t e = hipSuccess;
-    for (const void* f : {reinterpret_cast<const void*>(&matvec_q8_split_kernel<EPI, NORM, SK, 4>),
+    for (const void* f : {reinterpret_cast<const void*>(&matvec_q8_split_kernel<EPI, NORM, SK, 8>),
+                          reinterpret_cast<const void*>(&matvec_q8_split_kernel<EPI, NORM, SK, 7>),
+                          reinterpret_cast<const void*>(&matvec_q8_split_kernel<EPI, NORM, SK, 4>),
                           reinterpret_cast<const void*>(&matvec_q8_split_kernel<EPI, NORM, SK, 2>),
                           reinterpret_cast<const void*>(&matvec_q8_split_kernel<EPI, NORM, SK, 1>)})
         if (e == hipSuccess) e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 4096);

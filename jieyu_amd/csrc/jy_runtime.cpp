@@ -146,6 +146,13 @@ struct jyhip_model {
     int eos_cap = 0;
     float* part_val = nullptr;  // lm_head argmax partials
     int* part_idx = nullptr;
+    // the persistent decode kernel (Q8_0 models whose shapes it runs with one workgroup per CU)
+    PLayer* pk_layers = nullptr;  // device [L]: each matrix's stream plan
+    PMat pk_lm;
+    unsigned* pk_flags = nullptr;  // barrier flags of the workgroups, then the attention slice counters
+    size_t pk_flag_bytes = 0;
+    int* pk_err = nullptr;         // set by the kernel when a barrier wait gave up
+    size_t pk_lds = 0;
     std::vector<void*> owned;
 };
 
@@ -268,6 +275,74 @@ bool split_attention(const jyhip_model* m) {
 // slice partials (floats) a decode step attending up to max_keys keys takes
 size_t part_need(const jyhip_model* m, int max_keys) {
     return split_attention(m) ? attn_split_part_floats(m->nh, m->hd, attn_split_slices(max_keys)) : 0;
+}
+
+// the decode step runs as the persistent kernel: asked for, its shapes supported, and the
+// mode has both split forms it is built from
+bool use_persist(const jyhip_model* m) {
+    return m->pk_layers && (m->mode & JYHIP_MODE_PERSIST) && (m->mode & JYHIP_MODE_SPLIT_MV) &&
+           (m->mode & JYHIP_MODE_SPLIT_ATTN);
+}
+
+// one decode row (position state[0]-1, or pos0 without state) of every layer in the
+// persistent kernel over workspace w; with head, also the final norm, lm_head and the greedy
+// pick; with layer_x (device [L][H]) X after every layer
+void launch_persist(jyhip_model* m, Workspace& w, const KVDev& kv, const int* state, int pos0, int max_keys,
+                    float* layer_x, bool head, int neos) {
+    PersistArgs A;
+    A.layers = m->pk_layers;
+    A.L = m->L;
+    A.H = m->H;
+    A.F = m->F;
+    A.lm = m->pk_lm;
+    A.final_rms = m->final_rms;
+    A.cos_t = m->cos_t;
+    A.sin_t = m->sin_t;
+    A.att.fused = true;
+    A.att.qkv = w.qkv;
+    A.att.nrows = 1;
+    A.att.row0 = 0;
+    A.att.start_pos = pos0;
+    A.att.state = state;
+    A.att.nh = m->nh;
+    A.att.nkv = m->nkv;
+    A.att.hd = m->hd;
+    A.att.kv = kv;
+    A.att.max_keys = max_keys;
+    A.att.out = w.att;
+    A.X = w.X;
+    A.qkv = w.qkv;
+    A.h = w.h;
+    A.part = w.part;
+    A.ns = persist_slices(m->nkv, max_keys);
+    A.flags = m->pk_flags;
+    A.acnt = m->pk_flags + persist_workgroups();
+    A.err = m->pk_err;
+    A.layer_x = layer_x;
+    A.head = head ? 1 : 0;
+    if (head) {
+        A.logits = m->logits;
+        A.part_val = m->part_val;
+        A.part_idx = m->part_idx;
+        A.ids = m->ids;
+        A.mstate = m->state;
+        A.eos = m->eos;
+        A.neos = neos;
+    }
+    launch_zero_fill(m->pk_flags, m->pk_flag_bytes, m->stream);  // flags and counters start at zero
+    launch_decode_persist(A, m->pk_lds, m->stream);
+}
+
+// after the stream is synchronised: a persistent step whose barrier wait gave up is an error
+void check_persist(jyhip_model* m) {
+    if (!m->pk_err) return;
+    int e = 0;
+    CK(hipMemcpy(&e, m->pk_err, sizeof(int), hipMemcpyDeviceToHost));
+    if (e) {
+        launch_zero_fill(m->pk_err, 16, m->stream);
+        CK(hipStreamSynchronize(m->stream));
+        fail("decode step: the persistent kernel's workgroups did not all meet at a barrier (not all resident?)");
+    }
 }
 
 bool known_type(int t) {
@@ -436,6 +511,51 @@ void upload_mixed(jyhip_model* m, const jy_model_desc* d) {
     m->weight_bytes = total;
 }
 
+PMat pmat(const Q8Dev& q, int nwg) {
+    PMat p;
+    p.qs = q.qs;
+    p.d = q.d;
+    p.rows = q.rows;
+    p.cols = q.cols;
+    p.nch = q.nch;
+    p.nchp = q.nchp;
+    p.nbp = q.nbp;
+    persist_plan(p, nwg);
+    return p;
+}
+
+// the persistent decode kernel's per-model state: every matrix's stream plan on the device,
+// the barrier flags and the error word; left unset (the separate kernels run instead) for
+// shapes it does not take or when one workgroup per CU would not stay resident
+void build_persist(jyhip_model* m) {
+    if (m->wtype != JY_Q8_0 || !persist_supported(m->nh, m->nkv, m->hd)) return;
+    const int nwg = persist_workgroups();
+    std::vector<PLayer> h(m->L);
+    int max_nbp = 0;
+    for (int l = 0; l < m->L; l++) {
+        const DevLayer& D = m->layers[l];
+        h[l].qkv = pmat(D.qkv, nwg);
+        h[l].o = pmat(D.o, nwg);
+        h[l].gu = pmat(D.gu, nwg);
+        h[l].down = pmat(D.down, nwg);
+        h[l].rms1 = D.rms1;
+        h[l].rms2 = D.rms2;
+        h[l].bqkv = D.bqkv;
+        max_nbp = std::max({max_nbp, D.qkv.nbp, D.o.nbp, D.gu.nbp, D.down.nbp});
+    }
+    PMat lm = pmat(m->lm_q8, nwg);
+    max_nbp = std::max(max_nbp, lm.nbp);
+    const size_t lds = persist_lds_bytes(max_nbp, m->hd);
+    if (!persist_resident(m->hd, lds)) return;
+    m->pk_layers = (PLayer*)own(m, dalloc<PLayer>(m->L));
+    CK(hipMemcpy(m->pk_layers, h.data(), sizeof(PLayer) * m->L, hipMemcpyHostToDevice));
+    m->pk_lm = lm;
+    m->pk_flag_bytes = (size_t)(nwg + m->nkv + 3) / 4 * 16;
+    m->pk_flags = (unsigned*)own(m, dalloc<uint8_t>(m->pk_flag_bytes));
+    m->pk_err = (int*)own(m, dalloc<int>(4));
+    m->pk_lds = lds;
+}
+
 void upload(jyhip_model* m, const jy_model_desc* d, int max_seq, int wtype) {
     m->L = d->num_layers;
     m->H = d->hidden;
@@ -543,12 +663,14 @@ void upload(jyhip_model* m, const jy_model_desc* d, int max_seq, int wtype) {
             CK(hipMemcpy(D.bqkv + qd, w.bk, (size_t)kvd * 4, hipMemcpyHostToDevice));
             CK(hipMemcpy(D.bqkv + qd + kvd, w.bv, (size_t)kvd * 4, hipMemcpyHostToDevice));
         }
+    build_persist(m);
     m->logits = (float*)own(m, dalloc<float>(V));
     m->ids = (int*)own(m, dalloc<int>((size_t)max_seq + 1));
     m->state = (int*)own(m, dalloc<int>(4));
     m->eos_cap = 64;
     m->eos = (int*)own(m, dalloc<int>(m->eos_cap));
-    const int np = std::max(argmax_partials(V), split_argmax_partials(V));
+    // one partial maximum per lm_head workgroup of any of the decode forms
+    const int np = std::max({argmax_partials(V), split_argmax_partials(V), persist_workgroups()});
     m->part_val = (float*)own(m, dalloc<float>(np));
     m->part_idx = (int*)own(m, dalloc<int>(np));
 }
@@ -575,6 +697,29 @@ void release(jyhip_model* m) {
 void run_decode_layers(jyhip_model* m, Workspace& w, const KVDev& kv, const int* state, int pos0,
                        float* layer_out_host, int max_keys, bool short_ctx = false) {
     hipStream_t st = m->stream;
+    if (use_persist(m)) {
+        float* lx = nullptr;
+        if (layer_out_host) lx = dalloc<float>((size_t)m->L * m->H, false);
+        try {
+            launch_persist(m, w, kv, state, pos0, max_keys, lx, false, 0);
+            CK(hipGetLastError());
+            if (lx) {
+                CK(hipMemcpyAsync(layer_out_host, lx, sizeof(float) * m->L * m->H, hipMemcpyDeviceToHost, st));
+                CK(hipStreamSynchronize(st));
+            }
+        } catch (...) {
+            if (lx) {
+                (void)hipStreamSynchronize(st);
+                dfree(lx);
+            }
+            throw;
+        }
+        if (lx) {
+            dfree(lx);
+            check_persist(m);
+        }
+        return;
+    }
     const int H = m->H, NQ = m->qd + 2 * m->kvd, F = m->F;
     AttnArgs at;
     at.nrows = 1;
@@ -791,6 +936,12 @@ void decode_step(jyhip_model* m, const KVDev& kv, int max_keys, bool greedy, flo
                  bool short_ctx) {
     Workspace& w = m->ws;
     embed_rows(m, 0, m->state, 1, w.X);
+    if (use_persist(m)) {
+        const bool fused = greedy && rp == 1.0f;  // the kernel's own lm_head and greedy pick
+        launch_persist(m, w, kv, m->state, 0, max_keys, nullptr, fused, neos);
+        if (!fused) head_and_pick(m, w, w.X, greedy, rp, prompt_len, neos);
+        return;
+    }
     run_decode_layers(m, w, kv, m->state, 0, nullptr, max_keys, short_ctx);
     head_and_pick(m, w, w.X, greedy, rp, prompt_len, neos);
 }
@@ -1028,6 +1179,7 @@ struct Session {
         }
         CK(hipEventRecord(ev[3], st));
         CK(hipStreamSynchronize(st));
+        check_persist(m);
         float ms = 0.0f;
         CK(hipEventElapsedTime(&ms, ev[2], ev[3]));
         decode_ms += ms;
@@ -1089,6 +1241,7 @@ int forward_impl(jyhip_model* m, jyhip_kv* kv, float* X, int seq, int start_pos,
     CK(hipGetLastError());
     CK(hipMemcpyAsync(X, w.xn, sizeof(float) * seq * m->H, hipMemcpyDeviceToHost, st));
     CK(hipStreamSynchronize(st));
+    check_persist(m);
     kv->current_len = start_pos + seq;
     return 0;
 }
@@ -1153,6 +1306,7 @@ int forward_noalloc(jyhip_model* m, jyhip_kv* kv, float* X, int seq, int start_p
     CK(hipGetLastError());
     CK(hipMemcpyAsync(X, w.xn, sizeof(float) * seq * m->H, hipMemcpyDeviceToHost, st));
     CK(hipStreamSynchronize(st));
+    check_persist(m);
     kv->current_len = start_pos + seq;
     return 0;
 }
@@ -1218,7 +1372,7 @@ JYHIP_API size_t jyhip_model_weight_bytes(const jyhip_model* m) { return m ? m->
 JYHIP_API int jyhip_model_set_mode(jyhip_model* m, int mode) {
     return guarded([&]() {
         if (!m) fail("model is NULL");
-        if (mode & ~JYHIP_MODE_FAST) fail("unknown mode bits");
+        if (mode & ~(JYHIP_MODE_FAST | JYHIP_MODE_PERSIST)) fail("unknown mode bits");
         m->mode = mode;
         return 0;
     }, -1);

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import ptr, rope_tables
+from conftest import kv_views, prefill_kv, ptr, rope_tables
 
 pytestmark = pytest.mark.gpu
 
@@ -60,14 +60,6 @@ def layer_errs(got, want):
     return [rel_err(got[l], want[l]) for l in range(got.shape[0])]
 
 
-def kv_arrays(okv, L, max_seq, nkv, hd):
-    k = np.ctypeslib.as_array(C.cast(okv.k, C.POINTER(C.c_int8)), (L, max_seq, nkv, hd))
-    v = np.ctypeslib.as_array(C.cast(okv.v, C.POINTER(C.c_int8)), (L, max_seq, nkv, hd))
-    ks = np.ctypeslib.as_array(C.cast(okv.ks, C.POINTER(C.c_float)), (L, max_seq, nkv))
-    vs = np.ctypeslib.as_array(C.cast(okv.vs, C.POINTER(C.c_float)), (L, max_seq, nkv))
-    return k, v, ks, vs
-
-
 # the isolated-kernel workload (int8 ~ U[-127,127], scales U(0.001,0.01), x ~ N(0,1), seed 1)
 # and ragged shapes: rows not a multiple of 4, K with padded chunks (896: 28 blocks)
 @pytest.mark.parametrize("rows,cols", [(4096, 4096), (14336, 4096), (4096, 14336), (13, 96), (517, 896),
@@ -96,7 +88,10 @@ def test_split_matvec_within_tolerance(jy, oracle_lib, rows, cols):
     assert rel_err(y, ref) <= TOL
 
 
-@pytest.mark.parametrize("mode_name", ["SPLIT_ATTN", "SPLIT_MV", "FAST"])
+MODES = {"SPLIT_ATTN": 1, "SPLIT_MV": 2, "FAST": 7, "PERSIST": 7 | 8}
+
+
+@pytest.mark.parametrize("mode_name", list(MODES))
 @pytest.mark.parametrize("key", list(MODELS))
 def test_forward_cached_within_tolerance(jy, oracle_lib, key, mode_name):
     """A prompt chunk then decode steps through forward_cached: every layer's output within
@@ -110,7 +105,7 @@ def test_forward_cached_within_tolerance(jy, oracle_lib, key, mode_name):
     okv = oracle.JyoKV()
     assert oracle_lib.jyo_kv_init(C.byref(okv), L, max_seq, nkv, hd) == 0
     g = jy.GpuModel(d, max_seq)
-    g.mode = getattr(jy, "MODE_" + mode_name)
+    g.mode = MODES[mode_name]
     kv = g.kv(max_seq)
     rng = np.random.default_rng(7)
     start = 0
@@ -126,7 +121,7 @@ def test_forward_cached_within_tolerance(jy, oracle_lib, key, mode_name):
         worst = max(worst, max(errs))
         assert max(errs) <= TOL, f"seq={seq} start={start}: relative errors {errs}"
         start += seq
-    ok8, ov8, oks, ovs = kv_arrays(okv, L, max_seq, nkv, hd)
+    ok8, ov8, oks, ovs = kv_views(okv, L, max_seq, nkv, hd)
     k, ks, v, vs = kv.read(0, 0, start)
     if not g.mode & jy.MODE_SPLIT_MV:
         assert np.array_equal(k, ok8[0, :start]) and np.array_equal(v, ov8[0, :start])
@@ -144,10 +139,11 @@ def test_forward_cached_within_tolerance(jy, oracle_lib, key, mode_name):
     s.close()
 
 
+@pytest.mark.parametrize("mode_name", ["FAST", "PERSIST"])
 @pytest.mark.parametrize("key", list(MODELS))
-def test_generate_fast_ids_match_oracle(jy, oracle_lib, key):
-    """Greedy ids of a whole generation in the fastest mode equal the oracle's."""
-    say(f"generate {key} in MODE_FAST")
+def test_generate_fast_ids_match_oracle(jy, oracle_lib, key, mode_name):
+    """Greedy ids of a whole generation in the tolerance modes equal the oracle's."""
+    say(f"generate {key} in MODE_{mode_name}")
     s = make(oracle_lib, key)
     d = s.desc
     prompt = np.zeros(13, np.int32)
@@ -158,7 +154,7 @@ def test_generate_fast_ids_match_oracle(jy, oracle_lib, key):
     n = oracle_lib.jyo_generate(C.byref(d), ptr(prompt), len(prompt), None, 0, ptr(cos), ptr(sin), max_seq, max_new,
                                 0.0, 1.0, ptr(ref), None, None)
     g = jy.GpuModel(d, max_seq)
-    g.mode = jy.MODE_FAST
+    g.mode = MODES[mode_name]
     ids, _ = g.generate(prompt, max_new)
     g.close()
     s.close()
@@ -166,29 +162,7 @@ def test_generate_fast_ids_match_oracle(jy, oracle_lib, key):
 
 
 def prefill_cache(oracle_lib, d, pre, max_seq, kv):
-    L, nkv, hd = d.num_layers, d.num_kv_heads, d.head_dim
-    okv = oracle.JyoKV()
-    assert oracle_lib.jyo_kv_init(C.byref(okv), L, max_seq, nkv, hd) == 0
-    ok8, ov8, oks, ovs = kv_arrays(okv, L, max_seq, nkv, hd)
-    for l in range(L):
-        kf = np.zeros(pre * nkv * hd, np.float32)
-        vf = np.zeros_like(kf)
-        oracle_lib.jysyn_normal_fill(9, 1000 + 2 * l, 1.0, ptr(kf), kf.size)
-        oracle_lib.jysyn_normal_fill(9, 1001 + 2 * l, 1.0, ptr(vf), vf.size)
-        k8 = np.zeros(kf.size, np.int8)
-        v8 = np.zeros(kf.size, np.int8)
-        ks = np.zeros(pre * nkv, np.float32)
-        vs = np.zeros_like(ks)
-        oracle_lib.jyo_kv_pack(ptr(kf), ptr(k8), ptr(ks), nkv, hd, pre)
-        oracle_lib.jyo_kv_pack(ptr(vf), ptr(v8), ptr(vs), nkv, hd, pre)
-        ok8[l, :pre] = k8.reshape(pre, nkv, hd)
-        ov8[l, :pre] = v8.reshape(pre, nkv, hd)
-        oks[l, :pre] = ks.reshape(pre, nkv)
-        ovs[l, :pre] = vs.reshape(pre, nkv)
-        kv.write(l, 0, k8.reshape(pre, nkv, hd), ks.reshape(pre, nkv), v8.reshape(pre, nkv, hd),
-                 vs.reshape(pre, nkv))
-    kv.set_len(pre)
-    return okv
+    return prefill_kv(oracle_lib, d, pre, max_seq, kv)
 
 
 # slices of 16 keys (40), one tile per slice (700 .. 20000), two tiles per slice past
@@ -217,7 +191,7 @@ def test_split_attention_long_context(jy, oracle_lib, pre):
         Xg, log = g.forward_cached(kv, X, pre + i, layer_out=True)
         errs = layer_errs(log, lo) + [rel_err(Xg, Xo)]
         assert max(errs) <= TOL, f"step {i}: relative errors {errs}"
-    ok8, ov8, _, _ = kv_arrays(okv, L, max_seq, nkv, hd)
+    ok8, ov8, _, _ = kv_views(okv, L, max_seq, nkv, hd)
     k, _, v, _ = kv.read(0, pre, 4)
     assert np.array_equal(k, ok8[0, pre:pre + 4]) and np.array_equal(v, ov8[0, pre:pre + 4])
     oracle_lib.jyo_kv_free(C.byref(okv))
@@ -226,8 +200,9 @@ def test_split_attention_long_context(jy, oracle_lib, pre):
     s.close()
 
 
+@pytest.mark.parametrize("mode_name", ["FAST", "PERSIST"])
 @pytest.mark.parametrize("pre,n_new", [(700, 24), (6000, 12)])
-def test_fast_resume_over_long_cache(jy, oracle_lib, pre, n_new):
+def test_fast_resume_over_long_cache(jy, oracle_lib, pre, n_new, mode_name):
     """The graph-replayed decode step in MODE_FAST over a pre-filled cache: greedy ids equal
     the oracle driven token by token (embedding row, forward_cached, lm_head, first maximum)."""
     say(f"MODE_FAST session resume over a {pre}-position cache")
@@ -237,7 +212,7 @@ def test_fast_resume_over_long_cache(jy, oracle_lib, pre, n_new):
     max_seq = pre + n_new + 8
     cos, sin = rope_tables(oracle_lib, max_seq, hd, d.rope_theta)
     g = jy.GpuModel(d, max_seq)
-    g.mode = jy.MODE_FAST
+    g.mode = MODES[mode_name]
     kv = g.kv(max_seq)
     okv = prefill_cache(oracle_lib, d, pre, max_seq, kv)
     ids = np.zeros(pre + 1, np.int32)
@@ -279,7 +254,7 @@ def test_mode_switch_recaptures(jy, oracle_lib):
     g = jy.GpuModel(d, 64)
     ss = g.session(prompt, 30)
     ss.step(5)
-    g.mode = jy.MODE_FAST
+    g.mode = jy.MODE_FAST | jy.MODE_PERSIST
     ss.step(10)
     g.mode = jy.MODE_EXACT
     ss.step(30)
