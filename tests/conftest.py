@@ -62,3 +62,48 @@ def q8_random_uniform(olib, rows, cols, seed):
     blk[:, 0:2] = dh.view(np.uint8).reshape(nb, 2)
     blk[:, 2:] = q.astype(np.int8).view(np.uint8).reshape(nb, 32)
     return blk.reshape(-1)
+
+
+def kv_views(okv, L, max_seq, nkv, hd):
+    """numpy views of an oracle cache (jyo_kv): int8 K, V [L][max_seq][nkv][hd], fp32 scales."""
+    import ctypes as C_
+    k = np.ctypeslib.as_array(C_.cast(okv.k, C_.POINTER(C_.c_int8)), (L, max_seq, nkv, hd))
+    v = np.ctypeslib.as_array(C_.cast(okv.v, C_.POINTER(C_.c_int8)), (L, max_seq, nkv, hd))
+    ks = np.ctypeslib.as_array(C_.cast(okv.ks, C_.POINTER(C_.c_float)), (L, max_seq, nkv))
+    vs = np.ctypeslib.as_array(C_.cast(okv.vs, C_.POINTER(C_.c_float)), (L, max_seq, nkv))
+    return k, v, ks, vs
+
+
+def prefill_kv(olib, d, pre, max_seq, kv, one_draw=False):
+    """Fill positions [0, pre) of every layer of the GPU cache `kv` and of a new oracle cache
+    (returned) with N(0,1) K and V packed by the oracle's kv_pack_q8 (the long-context
+    workload's setup).  one_draw: the same draw in every layer (the benchmark's setup)."""
+    import ctypes as C_
+    import oracle as O_
+    L, nkv, hd = d.num_layers, d.num_kv_heads, d.head_dim
+    okv = O_.JyoKV()
+    assert olib.jyo_kv_init(C_.byref(okv), L, max_seq, nkv, hd) == 0
+    ok8, ov8, oks, ovs = kv_views(okv, L, max_seq, nkv, hd)
+    packed = None
+    for l in range(L):
+        if packed is None or not one_draw:
+            kf = np.zeros(pre * nkv * hd, np.float32)
+            vf = np.zeros_like(kf)
+            olib.jysyn_normal_fill(9, 1000 + (0 if one_draw else 2 * l), 1.0, ptr(kf), kf.size)
+            olib.jysyn_normal_fill(9, 1001 + (0 if one_draw else 2 * l), 1.0, ptr(vf), vf.size)
+            k8 = np.zeros(kf.size, np.int8)
+            v8 = np.zeros(kf.size, np.int8)
+            ks = np.zeros(pre * nkv, np.float32)
+            vs = np.zeros_like(ks)
+            olib.jyo_kv_pack(ptr(kf), ptr(k8), ptr(ks), nkv, hd, pre)
+            olib.jyo_kv_pack(ptr(vf), ptr(v8), ptr(vs), nkv, hd, pre)
+            del kf, vf
+            packed = (k8.reshape(pre, nkv, hd), ks.reshape(pre, nkv), v8.reshape(pre, nkv, hd), vs.reshape(pre, nkv))
+        k8, ks, v8, vs = packed
+        ok8[l, :pre] = k8
+        ov8[l, :pre] = v8
+        oks[l, :pre] = ks
+        ovs[l, :pre] = vs
+        kv.write(l, 0, k8, ks, v8, vs)
+    kv.set_len(pre)
+    return okv

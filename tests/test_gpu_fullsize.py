@@ -1,0 +1,200 @@
+"""The benchmark models at full size on the GPU, against the reference and the oracle.
+
+* Greedy ids of the Llama-3-8B, Qwen2.5-0.5B (its 512-token prompt, through the prompt
+  GEMM tiles) and Qwen2.5-7B shapes equal the ids jieyu's own decode loop produced for the
+  same seeded models and prompts (tests/golden/fullsize.json, written by
+  tests/golden/make_fullsize_golden.py from the compiled reference).
+* Decode steps at the benchmark positions through forward_cached: Llama-3-8B over a cache
+  filled to 1024 positions, Qwen2.5-7B over 32768; per-layer hidden states bit-exact with
+  the oracle in the exact mode, within 1e-3 relative (max|gpu - oracle| <= 1e-3 *
+  max|oracle| per layer) in the fast mode.
+* Greedy decoding after the 32768-position cache (jyhip_session_resume) equals the oracle
+  driven token by token, in both modes.
+The pre-filled caches hold packed N(0, 1) K and V, as the long-context benchmark sets up.
+"""
+import ctypes as C
+import json
+import os
+
+import numpy as np
+import pytest
+
+from conftest import prefill_kv, ptr, rope_tables
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+TOL = 1e-3
+MODES = {"exact": 0, "fast": 7}
+
+
+def say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def jy():
+    import jieyu_amd
+    if jieyu_amd.device_count() < 1:
+        pytest.fail("no HIP device visible")
+    return jieyu_amd
+
+
+@pytest.fixture(scope="module")
+def golden():
+    with open(os.path.join(HERE, "golden", "fullsize.json")) as f:
+        return json.load(f)["cases"]
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+def rel_err(got, want):
+    return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
+
+
+class Full:
+    """One benchmark model, built on the host and uploaded once for a group of tests."""
+
+    def __init__(self, jy, olib, name, max_seq):
+        from jieyu_amd.model import Synth, synth_config
+        say(f"building the {name} model")
+        self.cfg = synth_config(name)
+        self.syn = Synth(olib, self.cfg)
+        self.d = self.syn.desc
+        self.g = jy.GpuModel(self.d, max_seq)
+        self.max_seq = max_seq
+
+    def prompt(self, olib, n):
+        p = np.zeros(n, np.int32)
+        olib.jysyn_uniform_int_fill(self.cfg.seed, 99, 0, self.d.vocab_size - 1, ptr(p), n)
+        return p
+
+    def close(self):
+        self.g.close()
+        self.syn.close()
+
+
+def check_generate(jy, olib, full, case):
+    prompt = full.prompt(olib, case["prompt_len"])
+    assert prompt.tolist() == case["ids"][:case["prompt_len"]]
+    for mode in MODES:
+        full.g.mode = MODES[mode]
+        say(f"  {mode} mode: {case['prompt_len']}-token prompt, {case['max_new']} greedy tokens")
+        ids, _ = full.g.generate(prompt, case["max_new"], max_seq=case["max_seq"])
+        assert ids.tolist() == case["ids"], f"{mode}: gpu {ids[len(prompt):].tolist()} vs reference " \
+                                            f"{case['ids'][len(prompt):]}"
+
+
+def check_decode_layers(jy, olib, full, pre, steps):
+    """forward_cached steps at positions pre, pre+1, ... over a cache pre-filled to pre."""
+    d = full.d
+    L, H = d.num_layers, d.hidden
+    cos, sin = rope_tables(olib, full.max_seq, d.head_dim, d.rope_theta)
+    kv = full.g.kv(full.max_seq)
+    okv = prefill_kv(olib, d, pre, full.max_seq, kv, one_draw=True)
+    rng = np.random.default_rng(pre)
+    xs = [rng.standard_normal((1, H)).astype(np.float32) for _ in range(steps)]
+    want = []
+    for i, X in enumerate(xs):
+        Xo = X.copy()
+        lo = np.zeros((L, 1, H), np.float32)
+        assert olib.jyo_forward_cached(C.byref(d), ptr(Xo), ptr(cos), ptr(sin), 1, pre + i, C.byref(okv),
+                                       ptr(lo)) == 0
+        want.append((Xo, lo))
+    for mode in MODES:
+        full.g.mode = MODES[mode]
+        kv.set_len(pre)
+        for i, X in enumerate(xs):
+            Xg, log = full.g.forward_cached(kv, X, pre + i, layer_out=True)
+            Xo, lo = want[i]
+            if mode == "exact":
+                assert bits_equal(log, lo) and bits_equal(Xg, Xo), f"exact, step at {pre + i}"
+            else:
+                errs = [rel_err(log[l], lo[l]) for l in range(L)] + [rel_err(Xg, Xo)]
+                assert max(errs) <= TOL, f"fast, step at {pre + i}: worst layer error {max(errs):.3g}"
+                say(f"  fast mode at {pre + i}: worst per-layer relative error {max(errs):.3g}")
+    olib.jyo_kv_free(C.byref(okv))
+    kv.close()
+
+
+class TestLlama3_8B:
+    @pytest.fixture(scope="class")
+    def full(self, jy, oracle_lib):
+        f = Full(jy, oracle_lib, "llama3-8b", 1104)
+        yield f
+        f.close()
+
+    def test_generate_matches_reference(self, jy, oracle_lib, full, golden):
+        say("llama3-8b: greedy ids vs the reference")
+        check_generate(jy, oracle_lib, full, golden["llama3-8b-full"])
+
+    def test_decode_at_1024(self, jy, oracle_lib, full):
+        say("llama3-8b: decode steps at 1024..1025 vs the oracle, per layer")
+        check_decode_layers(jy, oracle_lib, full, 1024, 2)
+
+
+class TestQwen05B:
+    @pytest.fixture(scope="class")
+    def full(self, jy, oracle_lib):
+        f = Full(jy, oracle_lib, "qwen2.5-0.5b", 600)
+        yield f
+        f.close()
+
+    def test_512_prompt_matches_reference(self, jy, oracle_lib, full, golden):
+        say("qwen2.5-0.5b: 512-token prompt + 64 greedy tokens vs the reference")
+        check_generate(jy, oracle_lib, full, golden["qwen2.5-0.5b-full-512"])
+
+
+class TestQwen7B:
+    PRE = 32768
+
+    @pytest.fixture(scope="class")
+    def full(self, jy, oracle_lib):
+        f = Full(jy, oracle_lib, "qwen2.5-7b", self.PRE + 24)
+        yield f
+        f.close()
+
+    def test_generate_matches_reference(self, jy, oracle_lib, full, golden):
+        say("qwen2.5-7b: greedy ids vs the reference")
+        check_generate(jy, oracle_lib, full, golden["qwen2.5-7b-full"])
+
+    def test_decode_at_32768(self, jy, oracle_lib, full):
+        say("qwen2.5-7b: decode steps at 32768..32769 vs the oracle, per layer")
+        check_decode_layers(jy, oracle_lib, full, self.PRE, 2)
+
+    def test_resume_after_32768(self, jy, oracle_lib, full):
+        """jyhip_session_resume over the pre-filled cache: the graph-replayed greedy steps give
+        the oracle's tokens (embedding row, forward_cached, lm_head, first maximum)."""
+        say("qwen2.5-7b: greedy decoding after a 32768-position cache vs the oracle")
+        d = full.d
+        H, V = d.hidden, d.vocab_size
+        n_new = 8
+        cos, sin = rope_tables(oracle_lib, full.max_seq, d.head_dim, d.rope_theta)
+        kv = full.g.kv(full.max_seq)
+        okv = prefill_kv(oracle_lib, d, self.PRE, full.max_seq, kv, one_draw=True)
+        ids = full.prompt(oracle_lib, self.PRE + 1)
+        want = []
+        tok = int(ids[-1])
+        for i in range(n_new):
+            X = np.zeros((1, H), np.float32)
+            oracle_lib.jyo_embed_row(C.byref(d.embed), tok, H, ptr(X))
+            assert oracle_lib.jyo_forward_cached(C.byref(d), ptr(X), ptr(cos), ptr(sin), 1, self.PRE + i,
+                                                 C.byref(okv), None) == 0
+            logits = np.zeros(V, np.float32)
+            oracle_lib.jyo_matmul_w(C.byref(d.lm_head), 1, V, H, ptr(X), ptr(logits))
+            tok = int(np.argmax(logits))
+            want.append(tok)
+        for mode in MODES:
+            full.g.mode = MODES[mode]
+            kv.set_len(self.PRE)
+            s = full.g.session(ids, n_new, max_seq=full.max_seq, kv=kv, resume=True)
+            s.step(n_new)
+            got = s.ids()[self.PRE + 1:].tolist()
+            s.close()
+            assert got == want, f"{mode}: gpu {got} vs oracle {want}"
+        oracle_lib.jyo_kv_free(C.byref(okv))
+        kv.close()

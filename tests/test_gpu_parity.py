@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import ptr, q8_random_normal, q8_random_uniform, rope_tables
+from conftest import prefill_kv, ptr, q8_random_normal, q8_random_uniform, rope_tables
 
 pytestmark = pytest.mark.gpu
 
@@ -179,35 +179,7 @@ def test_forward_cached_layers_and_kv(jy, oracle_lib):
 
 
 def prefill_cache(oracle_lib, d, pre, max_seq, kv):
-    """Pack N(0,1) K/V for positions [0, pre) of every layer into the GPU cache `kv` and
-    into a new oracle cache (returned), as the long-context workload sets up its cache."""
-    L, nkv, hd = d.num_layers, d.num_kv_heads, d.head_dim
-    okv = oracle.JyoKV()
-    assert oracle_lib.jyo_kv_init(C.byref(okv), L, max_seq, nkv, hd) == 0
-    ok8 = np.ctypeslib.as_array(C.cast(okv.k, C.POINTER(C.c_int8)), (L * max_seq * nkv * hd,))
-    ov8 = np.ctypeslib.as_array(C.cast(okv.v, C.POINTER(C.c_int8)), (L * max_seq * nkv * hd,))
-    oks = np.ctypeslib.as_array(C.cast(okv.ks, C.POINTER(C.c_float)), (L * max_seq * nkv,))
-    ovs = np.ctypeslib.as_array(C.cast(okv.vs, C.POINTER(C.c_float)), (L * max_seq * nkv,))
-    for l in range(L):
-        kf = np.zeros(pre * nkv * hd, np.float32)
-        vf = np.zeros_like(kf)
-        oracle_lib.jysyn_normal_fill(9, 1000 + 2 * l, 1.0, ptr(kf), kf.size)
-        oracle_lib.jysyn_normal_fill(9, 1001 + 2 * l, 1.0, ptr(vf), vf.size)
-        k8 = np.zeros(kf.size, np.int8)
-        v8 = np.zeros(kf.size, np.int8)
-        ks = np.zeros(pre * nkv, np.float32)
-        vs = np.zeros_like(ks)
-        oracle_lib.jyo_kv_pack(ptr(kf), ptr(k8), ptr(ks), nkv, hd, pre)
-        oracle_lib.jyo_kv_pack(ptr(vf), ptr(v8), ptr(vs), nkv, hd, pre)
-        base = l * max_seq
-        ok8[base * nkv * hd:(base + pre) * nkv * hd] = k8
-        ov8[base * nkv * hd:(base + pre) * nkv * hd] = v8
-        oks[base * nkv:(base + pre) * nkv] = ks
-        ovs[base * nkv:(base + pre) * nkv] = vs
-        kv.write(l, 0, k8.reshape(pre, nkv, hd), ks.reshape(pre, nkv), v8.reshape(pre, nkv, hd),
-                 vs.reshape(pre, nkv))
-    kv.set_len(pre)
-    return okv
+    return prefill_kv(oracle_lib, d, pre, max_seq, kv)
 
 
 # 766: 767 / 768 keys (scores inside the softmax/PV kernel) then 769 (two kernels);
