@@ -62,9 +62,8 @@ JYHIP_API void jyhip_model_free(jyhip_model* model);
  *                          softmax sum and p.v accumulated per slice and merged;
  *   JYHIP_MODE_SPLIT_MV    decode Q8_0 matvecs with each row's dot split across waves and
  *                          the RMSNorm scale applied after the dot (linearity);
- *   JYHIP_MODE_MFMA_PREFILL prompt GEMMs on bf16 matrix cores (int8 weights are exact in
- *                          bf16; activations as a bf16 high + low pair; per-block scales
- *                          applied in fp32).
+ *   JYHIP_MODE_MFMA_PREFILL reserved for prompt GEMMs on matrix cores; accepted, and the
+ *                          prompt GEMMs run the exact tiles.
  * Int8 KV bytes and ids are the reference's wherever the fp32 values they come from are. */
 #define JYHIP_MODE_EXACT 0
 #define JYHIP_MODE_SPLIT_ATTN 1

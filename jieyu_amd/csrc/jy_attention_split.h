@@ -19,59 +19,88 @@ __host__ __device__ __forceinline__ int split_chunk(int nk, int ns) {
     return c < SPL_MIN_CHUNK ? SPL_MIN_CHUNK : c;
 }
 
+// query heads per kv head as a kernel instance computes them: 1, 2, 4 or 8 (the heads
+// past the real count carry a zero query and are never written out)
+__host__ __device__ constexpr int split_heads(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8; }
+
+// sum over the 64 lanes of a wave, in every lane, in a fixed order: rows of 16 by DPP,
+// then the four row sums
 __device__ __forceinline__ float wave_sum64(float v) {
-    // fixed butterfly order: the same bits whatever the launch
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 4);
-    v += __shfl_xor(v, 8);
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
+    v += dpp_f<0xB1>(v);   // quad_perm 1,0,3,2
+    v += dpp_f<0x4E>(v);   // quad_perm 2,3,0,1
+    v += dpp_f<0x124>(v);  // row_ror 4
+    v += dpp_f<0x128>(v);  // row_ror 8
+    return (read_lane(v, 0) + read_lane(v, 16)) + (read_lane(v, 32) + read_lane(v, 48));
 }
 
 // e^x from the hardware exp2 (v_exp_f32): about 1 ulp plus the rounding of x*log2(e),
 // a relative error under 1e-6 for the |x| <= 20 that carry weight here
 __device__ __forceinline__ float exp_hw(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 
-// LDS of one slice (a struct so that a kernel can place it in static or dynamic LDS)
-template <int P>
+// Sum of each group of LP adjacent lanes (LP 4 or 8) into the group's last lane, by DPP row
+// shifts within rows of 16 lanes (exact: integer adds)
+template <int LP>
+__device__ __forceinline__ int piece_sum_last(int d) {
+    d += __builtin_amdgcn_update_dpp(0, d, 0x111, 0xf, 0xf, true);  // row_shr 1
+    d += __builtin_amdgcn_update_dpp(0, d, 0x112, 0xf, 0xf, true);  // row_shr 2
+    if (LP > 4) d += __builtin_amdgcn_update_dpp(0, d, 0x114, 0xf, 0xf, true);  // row_shr 4
+    return d;
+}
+
+// LDS of one slice (a struct so that a kernel can place it in static or dynamic LDS).
+// The tile arrays and the final per-subset sums of p.v share their space.
+template <int P, int GT>
 struct SplitLds {
-    static constexpr int HD = P * 16, NW = SPL_THREADS / 64, KS = SPL_THREADS / HD;
-    int8_t q8[SPL_GMAX][HD] __attribute__((aligned(16)));
-    int8_t vt[SPL_THREADS][HD + 16] __attribute__((aligned(16)));  // V tile, rows padded
+    static constexpr int HD = P * 16, NW = SPL_THREADS / 64;
+    static constexpr int DG = HD / 4, NKS = SPL_THREADS / DG;  // p.v: 4 dims per thread, key subsets
+    struct Tile {
+        int8_t vt[SPL_THREADS][HD];  // V rows of the tile
+        int dots[SPL_THREADS][GT];   // int32 q.k of each key and query head
+        float pw[GT][SPL_THREADS];   // e_j * vs_j
+    };
+    union {
+        Tile t;
+        float accs[NKS][GT][HD];  // after the last tile: each key subset's o
+    } u __attribute__((aligned(16)));
+    int8_t q8[GT][HD] __attribute__((aligned(16)));
     int8_t knew[HD] __attribute__((aligned(16)));
     int8_t vnew[HD] __attribute__((aligned(16)));
-    float qsc[SPL_GMAX];
-    float pw[SPL_GMAX][SPL_THREADS];  // e_j * vs_j of the tile
-    float redm[NW][SPL_GMAX], reds[NW][SPL_GMAX];
+    float qsc[GT];
+    float redm[NW][GT], reds[NW][GT];
     float kvs_new[2];
-    float accs[KS - 1][SPL_GMAX][HD];
 };
 
 // One (kv head, slice of keys) unit of the split attention, by the whole workgroup
 // (SPL_THREADS threads): writes the slice's (o[hd], max, sum) for each query head of the
 // group to part.  Returns false (having done nothing) for a slice past the live length.
-// P = hd / 16: 16-byte pieces per key row.
-template <int P, bool COH>
+// P = hd / 16: 16-byte pieces per key row; GT = split_heads(nh / nkv).
+//
+// Per tile of 256 keys:
+//  1. the K and V rows arrive as 16-byte pieces, P adjacent lanes per key (every load
+//     instruction of a wave reads 64 / P whole rows, contiguous); each lane takes the
+//     int32 dot of its piece with each query head's piece, and a DPP sum puts the key's
+//     dot in the group's last lane, which stores it; the V pieces go to the LDS tile;
+//  2. one key per thread: scores, the tile maximum per head, the weights and their sums;
+//  3. p.v: each thread accumulates 4 output dims over every NKS-th quad of keys.
+template <int P, int GT, bool COH>
 __device__ __forceinline__ bool attn_slice(const AttnArgs& a, int ns, float* __restrict__ part, int kvh, int s,
-                                           SplitLds<P>& L) {
-    constexpr int HD = P * 16;
-    constexpr int NW = SPL_THREADS / 64;
-    constexpr int KS = SPL_THREADS / HD;  // key subsets of the p.v phase (4 for hd 64, 2 for hd 128)
+                                           SplitLds<P, GT>& L) {
+    using Lds = SplitLds<P, GT>;
+    constexpr int HD = Lds::HD, NW = Lds::NW, DG = Lds::DG, NKS = Lds::NKS;
+    auto& vt = L.u.t.vt;
+    auto& dots = L.u.t.dots;
+    auto& pw = L.u.t.pw;
+    auto& accs = L.u.accs;
     auto& q8 = L.q8;
     auto& qsc = L.qsc;
-    auto& vt = L.vt;
-    auto& pw = L.pw;
     auto& redm = L.redm;
     auto& reds = L.reds;
     auto& knew = L.knew;
     auto& vnew = L.vnew;
     auto& kvs_new = L.kvs_new;
-    auto& accs = L.accs;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nh = a.nh, nkv = a.nkv, G = nh / nkv;
+    const int nh = a.nh, nkv = a.nkv, G = nh / nkv;  // G <= GT
     const int pos = a.state ? a.state[0] - 1 : a.start_pos + a.row0;
     const int nk = pos + 1;
     const int chunk = split_chunk(nk, ns);
@@ -87,20 +116,31 @@ __device__ __forceinline__ bool attn_slice(const AttnArgs& a, int ns, float* __r
     const float* row = a.qkv;  // one token row: q [nh*hd] | k [nkv*hd] | v [nkv*hd]
 
     // every load that depends only on the position goes out first: this tile's K and V
-    // rows and scales (the token's own key comes from the workgroup's copy instead) and
-    // the fp32 vectors this wave quantises (items wave, wave+4, wave+8: the group's query
-    // heads, then with the new position its k and v)
-    auto load_row = [&](const int8_t* base, int j, int4* r) {
+    // pieces (load round u: keys u*KPR .. u*KPR+KPR-1 of the tile, this thread holding
+    // piece pc of key u*KPR + kr) and the scales of this thread's key (the token's own
+    // key comes from the workgroup's copy instead), then the fp32 vectors this wave
+    // quantises (items wave, wave+4, wave+8: the group's query heads, then with the new
+    // position its k and v)
+    constexpr int KPR = SPL_THREADS / P;
+    const int pc = tid % P, kr = tid / P;
+    int4 kp[P], vp[P];
 #pragma unroll
-        for (int c = 0; c < P; c++) r[c] = *reinterpret_cast<const int4*>(base + (size_t)j * HD + 16 * c);
+    for (int u = 0; u < P; u++) kp[u] = vp[u] = make_int4(0, 0, 0, 0);
+    auto load_tile = [&](int t0) {
+#pragma unroll
+        for (int u = 0; u < P; u++) {
+            const int j = t0 + u * KPR + kr;
+            if (j < j1 && j != pos) {
+                kp[u] = *reinterpret_cast<const int4*>(K + (size_t)j * HD + 16 * pc);
+                vp[u] = *reinterpret_cast<const int4*>(V + (size_t)j * HD + 16 * pc);
+            }
+        }
     };
-    int4 kr[P], vr[P];
-    float ksj = 0.0f, vsj = 0.0f;
+    load_tile(j0);
+    float ksj = 0.0f, vsj = 0.0f;  // the scales of key t0 + tid, this thread's in the softmax
     {
         const int j = j0 + tid;
         if (j < j1 && j != pos) {
-            load_row(K, j, kr);
-            load_row(V, j, vr);
             ksj = KSc[j];
             vsj = VSc[j];
         }
@@ -138,6 +178,9 @@ __device__ __forceinline__ bool attn_slice(const AttnArgs& a, int ns, float* __r
             }
         }
     }
+    // heads past the group's real count: zero query (finite scores, never written out)
+    for (int i = G * HD + tid; i < GT * HD; i += SPL_THREADS) (&q8[0][0])[i] = 0;
+    if (tid < GT - G) qsc[G + tid] = 0.0f;
     __syncthreads();
     if (holds_new) {
         // kv_pack_q8 of the new position: appended by the one workgroup that holds it
@@ -152,130 +195,164 @@ __device__ __forceinline__ bool attn_slice(const AttnArgs& a, int ns, float* __r
     }
 
     const float scale = 1.0f / sqrtf((float)HD);
-    float m_run[SPL_GMAX], l_run[SPL_GMAX], acc[SPL_GMAX];
+    float m_run[GT], l_run[GT], acc[GT][4];
 #pragma unroll
-    for (int g = 0; g < SPL_GMAX; g++) {
+    for (int g = 0; g < GT; g++) {
         m_run[g] = -__builtin_inff();
         l_run[g] = 0.0f;
-        acc[g] = 0.0f;
+        acc[g][0] = acc[g][1] = acc[g][2] = acc[g][3] = 0.0f;
     }
-    // p.v mapping: thread = (output dim d, key subset kq)
-    const int d = tid % HD, kq = tid / HD;
+    // p.v mapping: thread = (dims 4*dg .. 4*dg+3, key subset ks)
+    const int dg = tid % DG, ks = tid / DG;
 
     for (int t0 = j0; t0 < j1; t0 += SPL_THREADS) {
         const int j = t0 + tid;
         const bool live = j < j1;
-        if (live && j == pos) {
-#pragma unroll
-            for (int c = 0; c < P; c++) {
-                kr[c] = *reinterpret_cast<const int4*>(knew + 16 * c);
-                vr[c] = *reinterpret_cast<const int4*>(vnew + 16 * c);
-            }
+        if (j == pos) {
             ksj = kvs_new[0];
             vsj = kvs_new[1];
         }
-        // V row into the tile (dim-major reads later)
+        // 1. V pieces into the tile; each key's exact int32 q.k for every head of the group
 #pragma unroll
-        for (int c = 0; c < P; c++) *reinterpret_cast<int4*>(&vt[tid][16 * c]) = live ? vr[c] : make_int4(0, 0, 0, 0);
-        // exact int32 dots against every query head of the group
-        float sc[SPL_GMAX];
+        for (int u = 0; u < P; u++) {
+            const int kt = u * KPR + kr;  // key in the tile
+            if (t0 + kt == pos) {
+                kp[u] = *reinterpret_cast<const int4*>(knew + 16 * pc);
+                vp[u] = *reinterpret_cast<const int4*>(vnew + 16 * pc);
+            }
+            *reinterpret_cast<int4*>(&vt[kt][16 * pc]) = vp[u];
+            int dd[GT];
 #pragma unroll
-        for (int g = 0; g < SPL_GMAX; g++) {
-            sc[g] = -__builtin_inff();
-            if (g < G && live) {
-                int dot = 0;
+            for (int g = 0; g < GT; g++) {
+                const int4 q4 = *reinterpret_cast<const int4*>(&q8[g][16 * pc]);
+                int x = __builtin_amdgcn_sdot4(q4.x, kp[u].x, 0, false);
+                x = __builtin_amdgcn_sdot4(q4.y, kp[u].y, x, false);
+                x = __builtin_amdgcn_sdot4(q4.z, kp[u].z, x, false);
+                x = __builtin_amdgcn_sdot4(q4.w, kp[u].w, x, false);
+                dd[g] = piece_sum_last<P>(x);
+            }
+            if (pc == P - 1) {
+                if constexpr (GT >= 4) {
 #pragma unroll
-                for (int c = 0; c < P; c++) {
-                    const int4 q4 = *reinterpret_cast<const int4*>(&q8[g][16 * c]);
-                    dot = __builtin_amdgcn_sdot4(q4.x, kr[c].x, dot, false);
-                    dot = __builtin_amdgcn_sdot4(q4.y, kr[c].y, dot, false);
-                    dot = __builtin_amdgcn_sdot4(q4.z, kr[c].z, dot, false);
-                    dot = __builtin_amdgcn_sdot4(q4.w, kr[c].w, dot, false);
+                    for (int g = 0; g < GT; g += 4)
+                        *reinterpret_cast<int4*>(&dots[kt][g]) = make_int4(dd[g], dd[g + 1], dd[g + 2], dd[g + 3]);
+                } else {
+#pragma unroll
+                    for (int g = 0; g < GT; g++) dots[kt][g] = dd[g];
                 }
-                sc[g] = (float)dot * ((ksj * qsc[g]) * scale);
             }
         }
-        // the next tile's rows are independent of this one's math: request them now
+        // the next tile's pieces and scales are independent of this one's math: request them now
         const int jn = j + SPL_THREADS;
         const bool next = jn < j1 && jn != pos;
-        if (next) {
-            load_row(K, jn, kr);
-            load_row(V, jn, vr);
-        }
+        if (t0 + SPL_THREADS < j1) load_tile(t0 + SPL_THREADS);
         const float ks_next = next ? KSc[jn] : 0.0f;
         const float vs_next = next ? VSc[jn] : 0.0f;
-        // tile maximum per head: waves, then the workgroup
+        __syncthreads();  // the tile's dots and V
+
+        // 2. scores of this thread's key; tile maximum per head: waves, then the workgroup
+        float sc[GT];
+        {
+            int dv[GT];
+            if constexpr (GT >= 4) {
 #pragma unroll
-        for (int g = 0; g < SPL_GMAX; g++)
-            if (g < G) {
-                const float mw = wave_max64(sc[g]);
-                if (lane == 0) redm[wave][g] = mw;
+                for (int g = 0; g < GT; g += 4) {
+                    const int4 t = *reinterpret_cast<const int4*>(&dots[tid][g]);
+                    dv[g] = t.x;
+                    dv[g + 1] = t.y;
+                    dv[g + 2] = t.z;
+                    dv[g + 3] = t.w;
+                }
+            } else {
+#pragma unroll
+                for (int g = 0; g < GT; g++) dv[g] = dots[tid][g];
             }
+#pragma unroll
+            for (int g = 0; g < GT; g++) sc[g] = live ? (float)dv[g] * ((ksj * qsc[g]) * scale) : -__builtin_inff();
+        }
+#pragma unroll
+        for (int g = 0; g < GT; g++) {
+            const float mw = wave_max64(sc[g]);
+            if (lane == 0) redm[wave][g] = mw;
+        }
         __syncthreads();
         // running maximum, the rescale of what came before, this tile's weights and sums
-        float e[SPL_GMAX];
 #pragma unroll
-        for (int g = 0; g < SPL_GMAX; g++)
-            if (g < G) {
-                float mt = redm[0][g];
+        for (int g = 0; g < GT; g++) {
+            float mt = redm[0][g];
 #pragma unroll
-                for (int w = 1; w < NW; w++) mt = fmaxf(mt, redm[w][g]);
-                const float mn = fmaxf(m_run[g], mt);
-                const float al = m_run[g] == -__builtin_inff() ? 0.0f : exp_hw(m_run[g] - mn);
-                m_run[g] = mn;
-                e[g] = live ? exp_hw(sc[g] - mn) : 0.0f;
-                pw[g][tid] = e[g] * vsj;
-                l_run[g] *= al;
-                acc[g] *= al;
-                const float sw = wave_sum64(e[g]);
-                if (lane == 0) reds[wave][g] = sw;
-            }
+            for (int w = 1; w < NW; w++) mt = fmaxf(mt, redm[w][g]);
+            const float mn = fmaxf(m_run[g], mt);
+            const float al = m_run[g] == -__builtin_inff() ? 0.0f : exp_hw(m_run[g] - mn);
+            m_run[g] = mn;
+            const float e = live ? exp_hw(sc[g] - mn) : 0.0f;
+            pw[g][tid] = e * vsj;
+            l_run[g] *= al;
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[g][c] *= al;
+            const float sw = wave_sum64(e);
+            if (lane == 0) reds[wave][g] = sw;
+        }
         __syncthreads();
 #pragma unroll
-        for (int g = 0; g < SPL_GMAX; g++)
-            if (g < G) {
-                float st = reds[0][g];
+        for (int g = 0; g < GT; g++) {
+            float st = reds[0][g];
 #pragma unroll
-                for (int w = 1; w < NW; w++) st += reds[w][g];
-                l_run[g] += st;
-            }
-        // o[g][d] += sum over this subset's keys (every KS-th key of the tile) of (e * vs) * v
+            for (int w = 1; w < NW; w++) st += reds[w][g];
+            l_run[g] += st;
+        }
+        // 3. o[g][4dg + c] += sum over this subset's quads of keys of (e * vs) * v; the keys of
+        // a quad past the tile's live ones carry zero weight
         const int tn = min(SPL_THREADS, j1 - t0);
-        for (int t = kq; t < tn; t += KS) {
-            const float vv = (float)vt[t][d];
+        for (int q = ks; 4 * q < tn; q += NKS) {
+            // the int8 values as v + 128 in unsigned bytes, converted and less 128 (exact).  The
+            // direct (float)(int8) of a byte field compiled (hipcc 7.2, gfx950) to
+            // v_cvt_f32_u32_sdwa with sext(), which converts a negative byte as 2^32 + v.
+            unsigned v4[4];
 #pragma unroll
-            for (int g = 0; g < SPL_GMAX; g++)
-                if (g < G) acc[g] = __builtin_fmaf(pw[g][t], vv, acc[g]);
+            for (int i = 0; i < 4; i++) v4[i] = *reinterpret_cast<const unsigned*>(&vt[4 * q + i][4 * dg]) ^ 0x80808080u;
+            float4 p4[GT];
+#pragma unroll
+            for (int g = 0; g < GT; g++) p4[g] = *reinterpret_cast<const float4*>(&pw[g][4 * q]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const float vv = (float)((v4[i] >> (8 * c)) & 0xffu) - 128.0f;
+#pragma unroll
+                    for (int g = 0; g < GT; g++) {
+                        const float pg = i == 0 ? p4[g].x : i == 1 ? p4[g].y : i == 2 ? p4[g].z : p4[g].w;
+                        acc[g][c] = __builtin_fmaf(pg, vv, acc[g][c]);
+                    }
+                }
+            }
         }
         ksj = ks_next;
         vsj = vs_next;
-        if (t0 + SPL_THREADS < j1) __syncthreads();  // vt / pw / red are rewritten by the next tile
+        __syncthreads();  // the tile arrays are rewritten by the next tile or the subset sums
     }
 
-    // the key subsets' partial sums, in subset order
-    if (kq > 0) {
+    // the key subsets' sums, added in subset order
 #pragma unroll
-        for (int g = 0; g < SPL_GMAX; g++)
-            if (g < G) accs[kq - 1][g][d] = acc[g];
-    }
+    for (int g = 0; g < GT; g++)
+        *reinterpret_cast<float4*>(&accs[ks][g][4 * dg]) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
     __syncthreads();
-    if (kq == 0) {
+    const int W = HD + 2;
+    for (int o = tid; o < G * HD; o += SPL_THREADS) {
+        const int g = o / HD, d = o - g * HD;
+        float t = accs[0][g][d];
 #pragma unroll
-        for (int q = 1; q < KS; q++)
+        for (int q = 1; q < NKS; q++) t += accs[q][g][d];
+        float* out = part + ((size_t)(kvh * G + g) * ns + s) * W;
+        act_st<COH>(out + d, t);
+        if (d == 0) {
 #pragma unroll
-            for (int g = 0; g < SPL_GMAX; g++)
-                if (g < G) acc[g] += accs[q - 1][g][d];
-        const int W = HD + 2;
-#pragma unroll
-        for (int g = 0; g < SPL_GMAX; g++)
-            if (g < G) {
-                float* o = part + ((size_t)(kvh * G + g) * ns + s) * W;
-                act_st<COH>(o + d, acc[g]);
-                if (d == 0) {
-                    act_st<COH>(o + HD, m_run[g]);
-                    act_st<COH>(o + HD + 1, l_run[g]);
+            for (int gg = 0; gg < GT; gg++)
+                if (gg == g) {
+                    act_st<COH>(out + HD, m_run[gg]);
+                    act_st<COH>(out + HD + 1, l_run[gg]);
                 }
-            }
+        }
     }
     return true;
 }

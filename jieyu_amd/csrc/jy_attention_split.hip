@@ -11,9 +11,9 @@
 //
 // Two kernels per layer.
 //  1. attn_split_kernel: one workgroup per (kv head, slice of keys).  It quantises the
-//     group's query heads, walks its keys in tiles of one key per thread (K and V rows
-//     straight into registers), and keeps a running (max, sum, o[hd]) per query head
-//     of the group, rescaled per tile.  The workgroup whose slice holds the token's own
+//     group's query heads, walks its keys in tiles of 256 (K and V rows in 16-byte pieces
+//     across adjacent lanes, V through LDS to the p.v stage), and keeps a running
+//     (max, sum, o[hd]) per query head of the group, rescaled per tile.  The workgroup whose slice holds the token's own
 //     position quantises its k and v, appends them to the cache and uses its own copy.
 //  2. attn_combine_kernel: one workgroup per query head merges the slices:
 //     M = max m_s, L = sum l_s e^(m_s - M), o = sum o_s e^(m_s - M) / L.
@@ -26,11 +26,11 @@
 
 namespace jy {
 
-// P = hd / 16: 16-byte pieces per key row
-template <int P>
+// P = hd / 16: 16-byte pieces per key row; GT = split_heads(query heads per kv head)
+template <int P, int GT>
 __global__ __launch_bounds__(SPL_THREADS) void attn_split_kernel(AttnArgs a, int ns, float* __restrict__ part) {
-    __shared__ SplitLds<P> lds;
-    attn_slice<P, false>(a, ns, part, blockIdx.x, blockIdx.y, lds);
+    __shared__ SplitLds<P, GT> lds;
+    attn_slice<P, GT, false>(a, ns, part, blockIdx.x, blockIdx.y, lds);
 }
 
 // one workgroup of 256 threads per query head merges the live slices: every slice's
@@ -91,10 +91,18 @@ size_t attn_split_part_floats(int nh, int hd, int ns) { return (size_t)nh * ns *
 
 void launch_attention_split(const AttnArgs& a, float* part, int ns, hipStream_t st) {
     const dim3 grid(a.nkv, ns), block(SPL_THREADS);
-    if (a.hd == 64)
-        hipLaunchKernelGGL(attn_split_kernel<4>, grid, block, 0, st, a, ns, part);
-    else
-        hipLaunchKernelGGL(attn_split_kernel<8>, grid, block, 0, st, a, ns, part);
+    auto k = attn_split_kernel<8, 8>;
+    switch (split_heads(a.nh / a.nkv) * (a.hd == 64 ? -1 : 1)) {
+        case -1: k = attn_split_kernel<4, 1>; break;
+        case -2: k = attn_split_kernel<4, 2>; break;
+        case -4: k = attn_split_kernel<4, 4>; break;
+        case -8: k = attn_split_kernel<4, 8>; break;
+        case 1: k = attn_split_kernel<8, 1>; break;
+        case 2: k = attn_split_kernel<8, 2>; break;
+        case 4: k = attn_split_kernel<8, 4>; break;
+        default: break;
+    }
+    hipLaunchKernelGGL(k, grid, block, 0, st, a, ns, part);
     hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nh), dim3(256), 0, st, a, ns, part);
 }
 

@@ -383,8 +383,8 @@ __global__ __launch_bounds__(PK_THREADS, 1) void decode_persist_kernel(PersistAr
             const int unit = blockIdx.x;
             if (unit < at.nkv * A.ns) {
                 const int kvh = unit / A.ns, s = unit - kvh * A.ns;
-                SplitLds<P>& L = *reinterpret_cast<SplitLds<P>*>(smem);
-                if (attn_slice<P, true>(at, A.ns, A.part, kvh, s, L)) {
+                SplitLds<P, SPL_GMAX>& L = *reinterpret_cast<SplitLds<P, SPL_GMAX>*>(smem);
+                if (attn_slice<P, SPL_GMAX, true>(at, A.ns, A.part, kvh, s, L)) {
                     __builtin_amdgcn_s_waitcnt(0);  // the slice's partial sums are complete
                     __syncthreads();
                     if (tid == 0) {
@@ -397,7 +397,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void decode_persist_kernel(PersistAr
                     }
                     __syncthreads();
                     if (last) {
-                        float* ml = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + sizeof(SplitLds<P>));
+                        float* ml = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + sizeof(SplitLds<P, SPL_GMAX>));
                         pk_combine<P>(at, A.ns, A.part, kvh, ml, ml + 2 * SPL_GMAX * 256);
                     }
                 }
@@ -509,7 +509,7 @@ int persist_slices(int nkv, int max_keys) { return std::max(1, std::min(attn_spl
 // the lm_head) or the attention's tile plus its merge arrays
 size_t persist_lds_bytes(int max_nbp, int hd) {
     const size_t xs = (size_t)16 * (2 * max_nbp + 4) * sizeof(float);
-    const size_t at = (hd == 64 ? sizeof(SplitLds<4>) : sizeof(SplitLds<8>)) + (size_t)3 * SPL_GMAX * 256 * 4;
+    const size_t at = (hd == 64 ? sizeof(SplitLds<4, SPL_GMAX>) : sizeof(SplitLds<8, SPL_GMAX>)) + (size_t)3 * SPL_GMAX * 256 * 4;
     return std::max(xs, at);
 }
 

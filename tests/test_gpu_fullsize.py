@@ -3,13 +3,19 @@
 * Greedy ids of the Llama-3-8B, Qwen2.5-0.5B (its 512-token prompt, through the prompt
   GEMM tiles) and Qwen2.5-7B shapes equal the ids jieyu's own decode loop produced for the
   same seeded models and prompts (tests/golden/fullsize.json, written by
-  tests/golden/make_fullsize_golden.py from the compiled reference).
+  tests/golden/make_fullsize_golden.py from the compiled reference): in the exact mode
+  every id; in the fast mode every id up to a near tie, where the token the fast mode
+  picked must score within NEAR_TIE * max|logit| of the reference's pick by the exact
+  logits of that step (the fast mode's logits differ from the exact ones by its rounding,
+  about 1e-3 of max|logit| after 32 layers, so a closer tie may go either way; the ids
+  after a tie follow a different prefix and are not compared).
 * Decode steps at the benchmark positions through forward_cached: Llama-3-8B over a cache
   filled to 1024 positions, Qwen2.5-7B over 32768; per-layer hidden states bit-exact with
   the oracle in the exact mode, within 1e-3 relative (max|gpu - oracle| <= 1e-3 *
   max|oracle| per layer) in the fast mode.
 * Greedy decoding after the 32768-position cache (jyhip_session_resume) equals the oracle
-  driven token by token, in both modes.
+  driven token by token: every id in the exact mode, up to a near tie (as above, by the
+  oracle's logits) in the fast mode.
 The pre-filled caches hold packed N(0, 1) K and V, as the long-context benchmark sets up.
 """
 import ctypes as C
@@ -25,6 +31,7 @@ pytestmark = pytest.mark.gpu
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 TOL = 1e-3
+NEAR_TIE = 2e-3
 MODES = {"exact": 0, "fast": 7}
 
 
@@ -78,15 +85,42 @@ class Full:
         self.syn.close()
 
 
+def check_near_tie(got, want, n0, exact_logits):
+    """got (fast mode) against want (exact): equal, or equal up to index i where the exact
+    logits of that step (exact_logits(i)) rate got[i] within NEAR_TIE * max|logit| of want[i]."""
+    if got == want:
+        return
+    assert len(got) == len(want), f"lengths {len(got)} vs {len(want)}"
+    i = next(k for k in range(len(got)) if got[k] != want[k])
+    assert i >= n0, f"prompt ids differ at {i}"
+    lg = exact_logits(i)
+    assert int(np.argmax(lg)) == want[i]
+    gap = float(lg[want[i]] - lg[got[i]])
+    bound = NEAR_TIE * float(np.abs(lg).max())
+    say(f"  fast mode: near tie at generated token {i - n0}: exact logits {lg[want[i]]:.6f} (reference's pick) "
+        f"vs {lg[got[i]]:.6f} (fast mode's), gap {gap:.3g}, bound {bound:.3g}")
+    assert gap <= bound, f"fast mode picked {got[i]} at {i}: exact-logit gap {gap:.3g} > {bound:.3g}"
+
+
 def check_generate(jy, olib, full, case):
     prompt = full.prompt(olib, case["prompt_len"])
-    assert prompt.tolist() == case["ids"][:case["prompt_len"]]
+    n0 = case["prompt_len"]
+    assert prompt.tolist() == case["ids"][:n0]
     for mode in MODES:
         full.g.mode = MODES[mode]
-        say(f"  {mode} mode: {case['prompt_len']}-token prompt, {case['max_new']} greedy tokens")
+        say(f"  {mode} mode: {n0}-token prompt, {case['max_new']} greedy tokens")
         ids, _ = full.g.generate(prompt, case["max_new"], max_seq=case["max_seq"])
-        assert ids.tolist() == case["ids"], f"{mode}: gpu {ids[len(prompt):].tolist()} vs reference " \
-                                            f"{case['ids'][len(prompt):]}"
+        if mode == "exact":
+            assert ids.tolist() == case["ids"], f"exact: gpu {ids[n0:].tolist()} vs reference {case['ids'][n0:]}"
+            continue
+
+        def exact_logits(i):
+            full.g.mode = MODES["exact"]
+            _, _, lg = full.g.generate(prompt, i - n0 + 1, max_seq=case["max_seq"], want_logits=True)
+            full.g.mode = MODES[mode]
+            return lg
+
+        check_near_tie(ids.tolist(), case["ids"], n0, exact_logits)
 
 
 def check_decode_layers(jy, olib, full, pre, steps):
@@ -177,7 +211,7 @@ class TestQwen7B:
         kv = full.g.kv(full.max_seq)
         okv = prefill_kv(oracle_lib, d, self.PRE, full.max_seq, kv, one_draw=True)
         ids = full.prompt(oracle_lib, self.PRE + 1)
-        want = []
+        want, want_logits = [], []
         tok = int(ids[-1])
         for i in range(n_new):
             X = np.zeros((1, H), np.float32)
@@ -188,6 +222,7 @@ class TestQwen7B:
             oracle_lib.jyo_matmul_w(C.byref(d.lm_head), 1, V, H, ptr(X), ptr(logits))
             tok = int(np.argmax(logits))
             want.append(tok)
+            want_logits.append(logits)
         for mode in MODES:
             full.g.mode = MODES[mode]
             kv.set_len(self.PRE)
@@ -195,6 +230,9 @@ class TestQwen7B:
             s.step(n_new)
             got = s.ids()[self.PRE + 1:].tolist()
             s.close()
-            assert got == want, f"{mode}: gpu {got} vs oracle {want}"
+            if mode == "exact":
+                assert got == want, f"exact: gpu {got} vs oracle {want}"
+            else:
+                check_near_tie(got, want, 0, lambda i: want_logits[i])
         oracle_lib.jyo_kv_free(C.byref(okv))
         kv.close()
