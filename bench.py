@@ -37,8 +37,9 @@ METRIC = "batch-1 decode tokens/s (Q8, 8B shape) + achieved HBM GB/s vs peak"
 # ids identical except at near ties closer than the mode's rounding)
 MODES = {"exact": 0, "fast": 7}
 MODE_TEXT = {"exact": "bit-exact (reference arithmetic order)",
-             "fast": "fast: split-K attention and matvec dots (tolerance 1e-3 relative per layer; greedy ids "
-                     "identical except at near ties within 2e-3 of max|logit|)"}
+             "fast": "fast: split-K attention and matvec dots, matrix-core (fp16 hi/lo MFMA) prompt GEMMs "
+                     "(tolerance 1e-3 relative per layer; greedy ids identical except at near ties within 2e-3 "
+                     "of max|logit|)"}
 HBM_PEAK_GBS = 8000.0
 
 

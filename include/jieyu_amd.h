@@ -59,11 +59,17 @@ JYHIP_API void jyhip_model_free(jyhip_model* model);
  * tolerance (per-layer fp32 hidden states within 1e-3 relative, identical greedy ids):
  *   JYHIP_MODE_SPLIT_ATTN  decode attention split across workgroups over the keys
  *                          (flash-decoding): exact int8 quantisation and int32 q.k, the
- *                          softmax sum and p.v accumulated per slice and merged;
+ *                          softmax sum and p.v accumulated per slice and merged; prompt
+ *                          rows in the same arithmetic, one workgroup per kv head and row;
  *   JYHIP_MODE_SPLIT_MV    decode Q8_0 matvecs with each row's dot split across waves and
  *                          the RMSNorm scale applied after the dot (linearity);
- *   JYHIP_MODE_MFMA_PREFILL reserved for prompt GEMMs on matrix cores; accepted, and the
- *                          prompt GEMMs run the exact tiles.
+ *   JYHIP_MODE_MFMA_PREFILL Q8_0 prompt GEMMs (m > 1) on the matrix cores: each activation
+ *                          row scaled by a power of two and split into fp16 high + low parts
+ *                          (22 significant bits), int8 weights exact in fp16, one fp32 MFMA
+ *                          sum per 32-weight block times its scale.  Enabling it builds a
+ *                          second copy of every layer's Q8_0 matrices in the matrix-core
+ *                          operand order (about 1.13 bytes per weight; kept until the model
+ *                          is freed); other weight types keep the exact tiles.
  * Int8 KV bytes and ids are the reference's wherever the fp32 values they come from are. */
 #define JYHIP_MODE_EXACT 0
 #define JYHIP_MODE_SPLIT_ATTN 1
@@ -165,7 +171,8 @@ JYHIP_API jyhip_q8mat* jyhip_q8_upload(const void* w, int rows, int cols, int co
 JYHIP_API void jyhip_q8_free(jyhip_q8mat* m);
 JYHIP_API int jyhip_q8_matvec(jyhip_q8mat* m, const float* x, float* y);
 /* jyhip_q8_matvec's kernel: JYHIP_MODE_EXACT (the default) or with JYHIP_MODE_SPLIT_MV the
- * split-dot form.  Returns 0 / -1. */
+ * split-dot form; with JYHIP_MODE_MFMA_PREFILL jyhip_q8_gemm runs the matrix-core kernel
+ * (the first such call builds its copies of the matrix).  Returns 0 / -1. */
 JYHIP_API int jyhip_q8_set_mode(jyhip_q8mat* m, int mode);
 /* Time `iters` launches (rotating copies) with HIP events on the launch stream:
  * *avg_us = mean kernel-to-kernel time per launch.  variant 0 is the plain
@@ -173,6 +180,13 @@ JYHIP_API int jyhip_q8_set_mode(jyhip_q8mat* m, int mode);
  * (RMSNorm over x, SwiGLU epilogue over interleaved row pairs); variants 2 and 3
  * are the same two launches of the split-dot kernel (JYHIP_MODE_SPLIT_MV). */
 JYHIP_API int jyhip_q8_matvec_time(jyhip_q8mat* m, const float* x, int variant, int iters, double* avg_us);
+/* C[mr][rows] = A[mr][cols] W^T (row-major fp32) through the prompt GEMM of the
+ * matrix's mode: the exact tiles, or with JYHIP_MODE_MFMA_PREFILL the matrix-core kernel
+ * (the generic m > 1 matmul of libs/matmul_libs/matmul_q.h:145-161).  Returns 0 / -1. */
+JYHIP_API int jyhip_q8_gemm(jyhip_q8mat* m, int mr, const float* A, float* C);
+/* Mean device time in microseconds of `iters` such GEMMs (A uploaded once, the launches
+ * cycling through the matrix's copies), the activation split included.  Returns 0 / -1. */
+JYHIP_API int jyhip_q8_gemm_time(jyhip_q8mat* m, int mr, const float* A, int iters, double* avg_us);
 
 /* One weight matrix of any bound type in HBM: matmul_w (libs/model_libs/wmat_kernel.h:9-16)
  * with B = w, n output rows, k inputs (f32 / f16 [k][n]; Q8_0 / k-quants [n][k/block]).

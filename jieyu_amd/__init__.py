@@ -89,6 +89,8 @@ def lib():
     _proto(L, "jyhip_q8_matvec", I, P, P, P)
     _proto(L, "jyhip_q8_set_mode", I, P, I)
     _proto(L, "jyhip_q8_matvec_time", I, P, P, I, I, C.POINTER(C.c_double))
+    _proto(L, "jyhip_q8_gemm", I, P, I, P, P)
+    _proto(L, "jyhip_q8_gemm_time", I, P, I, P, I, C.POINTER(C.c_double))
     _proto(L, "jyhip_wmat_upload", P, C.POINTER(WMat), I, I, I)
     _proto(L, "jyhip_wmat_free", None, P)
     _proto(L, "jyhip_wmat_matmul", I, P, I, P, P)
@@ -316,8 +318,23 @@ class Q8Matrix:
         return y
 
     def set_mode(self, bits):
-        """MODE_EXACT or MODE_SPLIT_MV for matvec()."""
+        """MODE_EXACT, MODE_SPLIT_MV for matvec(), MODE_MFMA_PREFILL for gemm()."""
         _check(self._lib.jyhip_q8_set_mode(self.h, int(bits)))
+
+    def gemm(self, A):
+        """C[m][rows] = A[m][cols] W^T by the prompt GEMM of the matrix's mode."""
+        A = np.ascontiguousarray(A, np.float32)
+        assert A.ndim == 2 and A.shape[1] == self.cols
+        out = np.zeros((A.shape[0], self.rows), np.float32)
+        _check(self._lib.jyhip_q8_gemm(self.h, A.shape[0], _ptr(A), _ptr(out)))
+        return out
+
+    def gemm_time(self, A, iters):
+        """Mean µs per prompt GEMM of A (the activation split included)."""
+        A = np.ascontiguousarray(A, np.float32)
+        us = C.c_double()
+        _check(self._lib.jyhip_q8_gemm_time(self.h, A.shape[0], _ptr(A), iters, C.byref(us)))
+        return us.value
 
     def time(self, x, iters, variant=0):
         """Mean µs per launch over `iters` launches: variant 0 the plain matvec, 1 the decode

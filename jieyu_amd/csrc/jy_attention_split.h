@@ -74,6 +74,11 @@ struct SplitLds {
 // (SPL_THREADS threads): writes the slice's (o[hd], max, sum) for each query head of the
 // group to part.  Returns false (having done nothing) for a slice past the live length.
 // P = hd / 16: 16-byte pieces per key row; GT = split_heads(nh / nkv).
+// Decode (a.fused): one token row; the workgroup quantises q, and with the slice that
+// holds the token's position its k and v, which it appends to the cache.  Prompt rows
+// (!a.fused): row `prow` of the launch at position start_pos + row0 + prow, q8 / qsc from
+// the RoPE + packing pass and every key already in the cache; with part == nullptr the
+// slice is the row's whole key range and o / sum goes straight to a.out.
 //
 // Per tile of 256 keys:
 //  1. the K and V rows arrive as 16-byte pieces, P adjacent lanes per key (every load
@@ -84,7 +89,7 @@ struct SplitLds {
 //  3. p.v: each thread accumulates 4 output dims over every NKS-th quad of keys.
 template <int P, int GT, bool COH>
 __device__ __forceinline__ bool attn_slice(const AttnArgs& a, int ns, float* __restrict__ part, int kvh, int s,
-                                           SplitLds<P, GT>& L) {
+                                           SplitLds<P, GT>& L, int prow = 0) {
     using Lds = SplitLds<P, GT>;
     constexpr int HD = Lds::HD, NW = Lds::NW, DG = Lds::DG, NKS = Lds::NKS;
     auto& vt = L.u.t.vt;
@@ -101,13 +106,15 @@ __device__ __forceinline__ bool attn_slice(const AttnArgs& a, int ns, float* __r
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nh = a.nh, nkv = a.nkv, G = nh / nkv;  // G <= GT
-    const int pos = a.state ? a.state[0] - 1 : a.start_pos + a.row0;
+    const bool fused = a.fused;
+    const int pos = a.state ? a.state[0] - 1 : a.start_pos + a.row0 + prow;
     const int nk = pos + 1;
     const int chunk = split_chunk(nk, ns);
     const int j0 = s * chunk;
     if (j0 >= nk) return false;  // whole workgroup: a slice past the live length
     const int j1 = min(nk, j0 + chunk);
-    const bool holds_new = j1 == nk;  // this slice ends at the token's own position
+    const bool holds_new = fused && j1 == nk;  // this slice ends at the token's own position
+    const int own = fused ? pos : -1;          // the key taken from the workgroup's copy
     const size_t head = (size_t)a.layer * nkv + kvh;
     int8_t* K = a.kv.k + head * a.kv.max_seq * HD;
     int8_t* V = a.kv.v + head * a.kv.max_seq * HD;
@@ -130,7 +137,7 @@ __device__ __forceinline__ bool attn_slice(const AttnArgs& a, int ns, float* __r
 #pragma unroll
         for (int u = 0; u < P; u++) {
             const int j = t0 + u * KPR + kr;
-            if (j < j1 && j != pos) {
+            if (j < j1 && j != own) {
                 kp[u] = *reinterpret_cast<const int4*>(K + (size_t)j * HD + 16 * pc);
                 vp[u] = *reinterpret_cast<const int4*>(V + (size_t)j * HD + 16 * pc);
             }
@@ -140,12 +147,12 @@ __device__ __forceinline__ bool attn_slice(const AttnArgs& a, int ns, float* __r
     float ksj = 0.0f, vsj = 0.0f;  // the scales of key t0 + tid, this thread's in the softmax
     {
         const int j = j0 + tid;
-        if (j < j1 && j != pos) {
+        if (j < j1 && j != own) {
             ksj = KSc[j];
             vsj = VSc[j];
         }
     }
-    const int nitems = G + (holds_new ? 2 : 0);
+    const int nitems = fused ? G + (holds_new ? 2 : 0) : 0;
     constexpr int PER = HD / 64;  // elements per lane of one vector
     float qv[3][PER];
 #pragma unroll
@@ -178,6 +185,13 @@ __device__ __forceinline__ bool attn_slice(const AttnArgs& a, int ns, float* __r
             }
         }
     }
+    if (!fused) {  // the row's quantised query heads of this group, as the packing pass left them
+        const size_t qrow = (size_t)(a.row0 + prow) * nh + (size_t)kvh * G;
+        const int4* src = reinterpret_cast<const int4*>(a.q8 + qrow * HD);
+        for (int i = tid; i < G * HD / 16; i += SPL_THREADS)
+            reinterpret_cast<int4*>(&q8[0][0])[i] = src[i];
+        if (tid < G) qsc[tid] = a.qsc[qrow + tid];
+    }
     // heads past the group's real count: zero query (finite scores, never written out)
     for (int i = G * HD + tid; i < GT * HD; i += SPL_THREADS) (&q8[0][0])[i] = 0;
     if (tid < GT - G) qsc[G + tid] = 0.0f;
@@ -208,7 +222,7 @@ __device__ __forceinline__ bool attn_slice(const AttnArgs& a, int ns, float* __r
     for (int t0 = j0; t0 < j1; t0 += SPL_THREADS) {
         const int j = t0 + tid;
         const bool live = j < j1;
-        if (j == pos) {
+        if (j == own) {
             ksj = kvs_new[0];
             vsj = kvs_new[1];
         }
@@ -216,7 +230,7 @@ __device__ __forceinline__ bool attn_slice(const AttnArgs& a, int ns, float* __r
 #pragma unroll
         for (int u = 0; u < P; u++) {
             const int kt = u * KPR + kr;  // key in the tile
-            if (t0 + kt == pos) {
+            if (t0 + kt == own) {
                 kp[u] = *reinterpret_cast<const int4*>(knew + 16 * pc);
                 vp[u] = *reinterpret_cast<const int4*>(vnew + 16 * pc);
             }
@@ -244,7 +258,7 @@ __device__ __forceinline__ bool attn_slice(const AttnArgs& a, int ns, float* __r
         }
         // the next tile's pieces and scales are independent of this one's math: request them now
         const int jn = j + SPL_THREADS;
-        const bool next = jn < j1 && jn != pos;
+        const bool next = jn < j1 && jn != own;
         if (t0 + SPL_THREADS < j1) load_tile(t0 + SPL_THREADS);
         const float ks_next = next ? KSc[jn] : 0.0f;
         const float vs_next = next ? VSc[jn] : 0.0f;
@@ -343,6 +357,14 @@ __device__ __forceinline__ bool attn_slice(const AttnArgs& a, int ns, float* __r
         float t = accs[0][g][d];
 #pragma unroll
         for (int q = 1; q < NKS; q++) t += accs[q][g][d];
+        if (!part) {  // the whole key range: the normalised output
+            float lg = 0.0f;
+#pragma unroll
+            for (int gg = 0; gg < GT; gg++)
+                if (gg == g) lg = l_run[gg];
+            a.out[((size_t)(a.row0 + prow) * nh + kvh * G + g) * HD + d] = t / lg;
+            continue;
+        }
         float* out = part + ((size_t)(kvh * G + g) * ns + s) * W;
         act_st<COH>(out + d, t);
         if (d == 0) {

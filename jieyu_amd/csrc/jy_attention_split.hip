@@ -33,6 +33,14 @@ __global__ __launch_bounds__(SPL_THREADS) void attn_split_kernel(AttnArgs a, int
     attn_slice<P, GT, false>(a, ns, part, blockIdx.x, blockIdx.y, lds);
 }
 
+// prompt rows: one workgroup per (kv head, row), the row's whole key range as one slice,
+// the normalised output straight to a.out; rows in descending order (the longest first)
+template <int P, int GT>
+__global__ __launch_bounds__(SPL_THREADS) void attn_prefill_kernel(AttnArgs a) {
+    __shared__ SplitLds<P, GT> lds;
+    attn_slice<P, GT, false>(a, 1, nullptr, blockIdx.x, 0, lds, a.nrows - 1 - (int)blockIdx.y);
+}
+
 // one workgroup of 256 threads per query head merges the live slices: every slice's
 // (max, sum) loaded at once, the weights e^(m_s - M) one per thread, then o over the
 // slices in two interleaved halves per output dim, summed in a fixed order
@@ -104,6 +112,22 @@ void launch_attention_split(const AttnArgs& a, float* part, int ns, hipStream_t 
     }
     hipLaunchKernelGGL(k, grid, block, 0, st, a, ns, part);
     hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nh), dim3(256), 0, st, a, ns, part);
+}
+
+void launch_attention_prefill_split(const AttnArgs& a, hipStream_t st) {
+    const dim3 grid(a.nkv, a.nrows), block(SPL_THREADS);
+    auto k = attn_prefill_kernel<8, 8>;
+    switch (split_heads(a.nh / a.nkv) * (a.hd == 64 ? -1 : 1)) {
+        case -1: k = attn_prefill_kernel<4, 1>; break;
+        case -2: k = attn_prefill_kernel<4, 2>; break;
+        case -4: k = attn_prefill_kernel<4, 4>; break;
+        case -8: k = attn_prefill_kernel<4, 8>; break;
+        case 1: k = attn_prefill_kernel<8, 1>; break;
+        case 2: k = attn_prefill_kernel<8, 2>; break;
+        case 4: k = attn_prefill_kernel<8, 4>; break;
+        default: break;
+    }
+    hipLaunchKernelGGL(k, grid, block, 0, st, a);
 }
 
 }  // namespace jy

@@ -1,0 +1,274 @@
+// jy_gemm_mfma.hip — prompt (m > 1) GEMMs of Q8_0 matrices on the matrix cores, the
+// tolerance mode's form of the generic matmul path (libs/matmul_libs/matmul_q.h:145-161:
+// C[i][n] = sum_k A[i][k] * q[n][k] * d[n][k/32]).
+//
+// Numbers.  The int8 weights are exact in fp16.  Each activation row is scaled by a power
+// of two that puts its largest magnitude in [2^13, 2^14) and split into an fp16 high part
+// and an fp16 low part (the rounding remainder), 22 significant bits together.  One
+// v_mfma_f32_16x16x32_f16 per part gives a 32-weight block's sum sum_k a[k] q[k] in fp32
+// (every product exact, fp32 additions); the block's fp16 scale multiplies that sum in an
+// fp32 fma into the running result, and the epilogue undoes the row's power of two.  So
+// the differences from the reference's fp32 loop are the order of the fp32 additions and
+// the 2^-22 relative split of the activations.
+//
+// Layout.  The matrix is kept a second time for these kernels (built when the mode is
+// enabled): for every tile of 16 rows and every block, the 512 bytes the 64 lanes of an
+// MFMA's B operand read, lane l = c + 16 G (row c of the tile, k = 8G .. 8G+7 of the
+// block) holding 8 bytes; and the block scales as fp32, four blocks of a row together.
+// The A operand takes lane l = r + 16 G for row r and the same k = 8G .. 8G+7: whatever
+// order the instruction gives the four lane groups' k, A and B agree on it.
+//
+// Tiling.  A workgroup of 4 waves computes 128 rows (tokens) x 128 columns (matrix rows),
+// each wave 64 x 64: 4 x 4 tiles of 16 x 16, acc in the MFMA C layout (lane l holds rows
+// 4 (l/16) .. +3 of column l % 16).  Operands come straight from global memory (L2): per
+// block a wave loads its 4 row tiles' high and low parts (16 B per lane each) and its 4
+// column tiles' weights (8 B per lane), one block ahead of the MFMAs that use them.
+#include "jy_layout.h"
+
+namespace jy {
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+static constexpr int GM_TILE = 128;  // workgroup tile: rows and columns
+
+// ---------------------------------------------------------------- the matrix copy
+
+// one thread per (16-row tile t, block b, lane l): the 8 weights of row 16t + (l % 16),
+// k = 32b + 8(l/16) .. +7, from the lane-pair layout (slot r*16 + g of chunk b/8 holds
+// weights 2g, 2g+1 of each of its 8 blocks at bytes 2j, 2j+1); the scales of blocks
+// 4*b4 .. 4*b4+3 of each row by the threads with l < 16 and b % 4 == 0
+__global__ void mfma_repack_kernel(Q8Dev W, Q8MfmaDev M) {
+    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t total = (size_t)M.tiles * M.nb * 64;
+    if (id >= total) return;
+    const int l = (int)(id % 64);
+    const size_t tb = id / 64;
+    const int b = (int)(tb % M.nb), t = (int)(tb / M.nb);
+    const int n = 16 * t + (l % 16), G = l / 16;
+    uint32_t w0 = 0, w1 = 0;
+    if (n < W.rows) {
+        const int rg = n >> 2, r = n & 3, ch = b >> 3, j = b & 7;
+        const uint8_t* chunk = W.qs + ((size_t)rg * W.nchp + ch) * 1024;
+        uint32_t v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint8_t* s = chunk + (size_t)(r * 16 + 4 * G + i) * 16 + 2 * j;
+            v[i] = (uint32_t)s[0] | ((uint32_t)s[1] << 8);
+        }
+        w0 = v[0] | (v[1] << 16);
+        w1 = v[2] | (v[3] << 16);
+    }
+    uint2* dst = reinterpret_cast<uint2*>(M.q + (tb * 64 + l) * 8);
+    *dst = make_uint2(w0, w1);
+    if (l < 16 && (b & 3) == 0) {
+        float4 dv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (n < W.rows) {
+            const int rg = n >> 2, r = n & 3;
+            float t4[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int bb = b + i;
+                float s = 0.0f;
+                if (bb < W.nb) {
+                    const uint16_t h = W.d[((size_t)rg * W.nchp + (bb >> 3)) * 32 + r * 8 + (bb & 7)];
+                    s = (float)__builtin_bit_cast(_Float16, h);
+                }
+                t4[i] = s;
+            }
+            dv = make_float4(t4[0], t4[1], t4[2], t4[3]);
+        }
+        reinterpret_cast<float4*>(M.d)[((size_t)t * M.nb4 + (b >> 2)) * 16 + l] = dv;
+    }
+}
+
+void launch_mfma_repack(const Q8Dev& W, const Q8MfmaDev& M, hipStream_t st) {
+    const size_t total = (size_t)M.tiles * M.nb * 64;
+    hipLaunchKernelGGL(mfma_repack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, W, M);
+}
+
+// ---------------------------------------------------------------- the activation split
+
+// one workgroup per row of the padded activations [mp][K]: rows past m are zero
+__global__ __launch_bounds__(256) void mfma_split_kernel(const float* __restrict__ A, int m, int K,
+                                                         _Float16* __restrict__ hi, _Float16* __restrict__ lo,
+                                                         float* __restrict__ unscale) {
+    __shared__ float red[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float* a = A + (size_t)row * K;
+    const bool live = row < m;
+    float amax = 0.0f;
+    if (live)
+        for (int k = tid; k < K; k += 256) amax = fmaxf(amax, fabsf(a[k]));
+    amax = wave_max64(amax);
+    if ((tid & 63) == 0) red[tid >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // 2^s with amax * 2^s in [2^13, 2^14); s kept within float's normal exponents
+    int ex = 0;
+    if (amax > 0.0f) frexpf(amax, &ex);
+    const int s = amax > 0.0f ? min(max(14 - ex, -100), 100) : 0;
+    const float up = ldexpf(1.0f, s);
+    if (tid == 0) unscale[row] = ldexpf(1.0f, -s);
+    _Float16* h = hi + (size_t)row * K;
+    _Float16* w = lo + (size_t)row * K;
+    for (int k = tid; k < K; k += 256) {
+        const float v = live ? a[k] * up : 0.0f;
+        const _Float16 vh = (_Float16)v;
+        h[k] = vh;
+        w[k] = (_Float16)(v - (float)vh);
+    }
+}
+
+void launch_mfma_split(const float* A, int m, int mp, int K, _Float16* hi, _Float16* lo, float* unscale,
+                       hipStream_t st) {
+    hipLaunchKernelGGL(mfma_split_kernel, dim3(mp), dim3(256), 0, st, A, m, K, hi, lo, unscale);
+}
+
+// ---------------------------------------------------------------- the GEMM
+
+// 8 int8 weights (two dwords) -> 8 fp16 values, exact: each byte biased by 128 into the
+// mantissa of 1024 (0x6400 | u = 1024 + u), then less 1152
+__device__ __forceinline__ h8_t q8_to_h8(uint32_t w0, uint32_t w1) {
+    w0 ^= 0x80808080u;
+    w1 ^= 0x80808080u;
+    const uint32_t e = 0x64646464u;
+    const uint32_t p0 = __builtin_amdgcn_perm(e, w0, 0x04010400u), p1 = __builtin_amdgcn_perm(e, w0, 0x04030402u);
+    const uint32_t p2 = __builtin_amdgcn_perm(e, w1, 0x04010400u), p3 = __builtin_amdgcn_perm(e, w1, 0x04030402u);
+    const h2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const h2_t r0 = __builtin_bit_cast(h2_t, p0) - off, r1 = __builtin_bit_cast(h2_t, p1) - off;
+    const h2_t r2 = __builtin_bit_cast(h2_t, p2) - off, r3 = __builtin_bit_cast(h2_t, p3) - off;
+    return h8_t{r0.x, r0.y, r1.x, r1.y, r2.x, r2.y, r3.x, r3.y};
+}
+
+struct GmOps {
+    h8_t ah[4], al[4];  // the wave's 4 row tiles, high and low parts
+    uint2 q[4];         // the wave's 4 column tiles' weights
+};
+
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(Q8MfmaDev W, int m, int K, const _Float16* __restrict__ ahi,
+                                                           const _Float16* __restrict__ alo,
+                                                           const float* __restrict__ unscale, float* __restrict__ C,
+                                                           int ldc, const float* __restrict__ aux) {
+    const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int c = l & 15, G = l >> 4;
+    const int row0 = blockIdx.x * GM_TILE + wm * 64;     // the wave's first token row
+    const int tile0 = blockIdx.y * (GM_TILE / 16) + wn * 4;  // the wave's first 16-column tile
+    const int nb = W.nb;
+    // per lane: token rows row0 + 16 mt + c, k offset 8 G within each block
+    const _Float16* ph[4];
+    const _Float16* pl[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++) {
+        const size_t off = (size_t)(row0 + 16 * mt + c) * K + 8 * G;
+        ph[mt] = ahi + off;
+        pl[mt] = alo + off;
+    }
+    bool tv[4];
+    const uint2* pq[4];
+    const float4* pd[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) {
+        const int t = tile0 + nt;
+        tv[nt] = t < W.tiles;
+        const int tt = tv[nt] ? t : 0;
+        pq[nt] = reinterpret_cast<const uint2*>(W.q) + (size_t)tt * nb * 64 + l;
+        pd[nt] = reinterpret_cast<const float4*>(W.d) + (size_t)tt * W.nb4 * 16 + c;
+    }
+    auto load = [&](GmOps& o, int b) {
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++) {
+            o.ah[mt] = *reinterpret_cast<const h8_t*>(ph[mt] + (size_t)b * 32);
+            o.al[mt] = *reinterpret_cast<const h8_t*>(pl[mt] + (size_t)b * 32);
+        }
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) o.q[nt] = tv[nt] ? pq[nt][(size_t)b * 64] : make_uint2(0u, 0u);
+    };
+
+    f4_t acc[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // one block: its operands in `use`; the next block's loads go to `fill` first
+    float4 dq[4];
+    auto step = [&](GmOps& use, GmOps& fill, int b) {
+        if ((b & 3) == 0) {
+#pragma unroll
+            for (int nt = 0; nt < 4; nt++) dq[nt] = tv[nt] ? pd[nt][(size_t)(b >> 2) * 16] : make_float4(0, 0, 0, 0);
+        }
+        if (b + 1 < nb) load(fill, b + 1);
+        const int bj = b & 3;
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) {
+            if (!tv[nt]) continue;  // wave-uniform: a column tile past the matrix
+            const h8_t bq = q8_to_h8(use.q[nt].x, use.q[nt].y);
+            const float dj = bj == 0 ? dq[nt].x : bj == 1 ? dq[nt].y : bj == 2 ? dq[nt].z : dq[nt].w;
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++) {
+                f4_t t = __builtin_amdgcn_mfma_f32_16x16x32_f16(use.ah[mt], bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(use.al[mt], bq, t, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[mt][nt][i] = __builtin_fmaf(dj, t[i], acc[mt][nt][i]);
+            }
+        }
+    };
+    GmOps ops0, ops1;
+    load(ops0, 0);
+    for (int b = 0; b < nb; b += 2) {
+        step(ops0, ops1, b);
+        if (b + 1 < nb) step(ops1, ops0, b + 1);
+    }
+
+    // epilogue: acc[mt][nt][i] is C[row0 + 16 mt + 4 G + i][16 (tile0 + nt) + c] before the row's unscale
+    const int N = W.rows;
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) {
+        const int col = 16 * (tile0 + nt) + c;
+        if (!tv[nt] || col >= N) continue;
+        const float bias = EPI == EPI_BIAS ? aux[col] : 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int row = row0 + 16 * mt + 4 * G + i;
+                if (row >= m) continue;
+                const float y = acc[mt][nt][i] * unscale[row];
+                float* dst = C + (size_t)row * ldc + col;
+                if (EPI == EPI_RESID)
+                    *dst += y;
+                else
+                    *dst = y + bias;
+            }
+    }
+}
+
+int mfma_rows_padded(int m) { return (m + GM_TILE - 1) / GM_TILE * GM_TILE; }
+
+void launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
+                         float* C, int ldc, const float* aux, Epi epi, hipStream_t st) {
+    // x: token tiles (the fastest in dispatch order: the workgroups that read one column
+    // tile's weights run together), y: column tiles
+    const dim3 grid((unsigned)(mfma_rows_padded(m) / GM_TILE), (unsigned)((W.tiles + GM_TILE / 16 - 1) / (GM_TILE / 16)));
+    const int K = W.nb * 32;
+    switch (epi) {
+        case EPI_BIAS:
+            hipLaunchKernelGGL(gemm_q8_mfma_kernel<EPI_BIAS>, grid, dim3(256), 0, st, W, m, K, hi, lo, unscale, C, ldc,
+                               aux);
+            break;
+        case EPI_RESID:
+            hipLaunchKernelGGL(gemm_q8_mfma_kernel<EPI_RESID>, grid, dim3(256), 0, st, W, m, K, hi, lo, unscale, C,
+                               ldc, aux);
+            break;
+        default:
+            hipLaunchKernelGGL(gemm_q8_mfma_kernel<EPI_STORE>, grid, dim3(256), 0, st, W, m, K, hi, lo, unscale, C,
+                               ldc, aux);
+            break;
+    }
+}
+
+}  // namespace jy

@@ -24,6 +24,15 @@ struct Q8Dev {
     int U = 0;     // decode matvec register-buffer depth (chunks per buffer, two buffers)
 };
 
+// A Q8_0 matrix as the matrix-core prompt GEMM reads it (jy_gemm_mfma.hip): per tile of
+// 16 rows and block of 32 weights, 512 bytes in MFMA B-operand lane order (q), and the
+// block scales as fp32, four blocks of a row together (d).  Rows past `rows` are zero.
+struct Q8MfmaDev {
+    int8_t* q = nullptr;  // [tiles][nb][64 lanes][8]
+    float* d = nullptr;   // [tiles][nb4][16 rows][4]
+    int rows = 0, cols = 0, nb = 0, nb4 = 0, tiles = 0;
+};
+
 // A Q4_K / Q5_K / Q6_K matrix of rows x cols (cols a multiple of 256), repacked so
 // that one 256-weight super-block of four rows is read by one wave, thread
 // t = ri*16 + g (row ri of the group, lane pair g) owning weights 32c + 2g + u
@@ -129,6 +138,16 @@ void launch_matvec_f16(const uint16_t* B, int K, int N, const float* x, float* o
                        hipStream_t st);
 // prefill GEMMs, C[m][N] (+ epilogue: EPI_STORE / EPI_BIAS / EPI_RESID)
 void launch_gemm_q8(const Q8Dev& W, int m, const float* A, float* C, const float* aux, Epi epi, hipStream_t st);
+// the matrix-core form (jy_gemm_mfma.hip): the copy of W it reads (built once), the split
+// of the activations A [m][K] into fp16 high / low parts over mfma_rows_padded(m) rows
+// (rows past m zero) with each row's power-of-two unscale, and C[m][ldc] (+ epilogue:
+// EPI_STORE / EPI_BIAS / EPI_RESID) from them
+void launch_mfma_repack(const Q8Dev& W, const Q8MfmaDev& M, hipStream_t st);
+int mfma_rows_padded(int m);
+void launch_mfma_split(const float* A, int m, int mp, int K, _Float16* hi, _Float16* lo, float* unscale,
+                       hipStream_t st);
+void launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
+                         float* C, int ldc, const float* aux, Epi epi, hipStream_t st);
 void launch_gemm_f32(const float* B, int K, int N, int m, const float* A, float* C, const float* aux, Epi epi,
                      hipStream_t st);
 // h[i][j] = silu(gu[i][2j]) * gu[i][2j+1]  (or silu(g) * u with separate buffers)
@@ -170,6 +189,9 @@ bool attn_split_supported(int nh, int nkv, int hd);
 int attn_split_slices(int keys);
 size_t attn_split_part_floats(int nh, int hd, int ns);
 void launch_attention_split(const AttnArgs& a, float* part, int ns, hipStream_t st);
+// prompt rows in the same arithmetic (q8 / qsc from launch_rope_pack, keys in the cache,
+// a.nrows rows from a.row0): one workgroup per (kv head, row), output to a.out
+void launch_attention_prefill_split(const AttnArgs& a, hipStream_t st);
 
 // ---- the persistent decode kernel (jy_decode_persist.hip), tolerance mode
 // One Q8_0 matrix as the persistent kernel streams it: its layout and the plan of its

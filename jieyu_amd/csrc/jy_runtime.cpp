@@ -99,6 +99,7 @@ struct DevLayer {
     float* rms2 = nullptr;
     float* bqkv = nullptr;
     Q8Dev qkv, o, gu, down;                        // JY_Q8_0
+    Q8MfmaDev mqkv, mo, mgu, mdown;                // their matrix-core GEMM copies (MFMA prefill mode)
     float *f_qkv = nullptr, *f_o = nullptr;        // JY_F32 [K][N] in 64-column panels of pieces
     float *f_w1 = nullptr, *f_w3 = nullptr, *f_w2 = nullptr;
     DevW w[7];                                     // WT_MIXED: Wq Wk Wv Wo W1 W2 W3
@@ -113,6 +114,11 @@ struct Workspace {
     size_t scores_n = 0;
     float* part = nullptr;  // split attention: per (query head, slice) o[hd], max, sum
     size_t part_n = 0;
+    // matrix-core prompt GEMMs: the activations' fp16 high / low parts and row unscales
+    _Float16 *ah = nullptr, *al = nullptr;
+    float* aus = nullptr;
+    size_t a_cap = 0;  // halves per part
+    int a_rows = 0;    // rows of aus
     unsigned gen = 0;  // bumped whenever a buffer above is replaced: graphs captured before are stale
 };
 
@@ -122,6 +128,7 @@ struct jyhip_model {
     int qd = 0, kvd = 0;
     int wtype = JY_Q8_0;
     int mode = JYHIP_MODE_EXACT;
+    bool mfma_built = false;  // the layers' Q8MfmaDev copies exist
     bool bias = false;
     int max_seq = 0;
     float theta = 0.0f;
@@ -172,6 +179,8 @@ struct jyhip_wmat {
 struct jyhip_q8mat {
     int mode = JYHIP_MODE_EXACT;
     std::vector<Q8Dev> copies;
+    std::vector<Q8MfmaDev> mcopies;  // the matrix-core GEMM's copies (built with JYHIP_MODE_MFMA_PREFILL)
+    std::vector<void*> mowned;
     float* x = nullptr;
     float* y = nullptr;
     float* nw = nullptr;  // unit RMSNorm weights for the gate/up timing variant
@@ -221,11 +230,17 @@ void ensure_ws(jyhip_model* m, int rows) {
     const size_t scores_n = w.scores_n;
     float* const part = w.part;
     const size_t part_n = w.part_n;
+    const Workspace split = w;  // the MFMA split buffers are kept too (ensure_split)
     w = Workspace{};
     w.scores = scores;
     w.scores_n = scores_n;
     w.part = part;
     w.part_n = part_n;
+    w.ah = split.ah;
+    w.al = split.al;
+    w.aus = split.aus;
+    w.a_cap = split.a_cap;
+    w.a_rows = split.a_rows;
     const size_t r = (size_t)rows;
     w.X = dalloc<float>(r * m->H);
     w.xn = dalloc<float>(r * m->H);
@@ -247,6 +262,62 @@ void ensure_scores(jyhip_model* m, size_t n) {
     w.scores = dalloc<float>(n, false);
     w.scores_n = n;
     w.gen++;
+}
+
+// the matrix-core GEMMs' split buffers: `halves` per part, `rows` unscales
+void ensure_split(jyhip_model* m, size_t halves, int rows) {
+    Workspace& w = m->ws;
+    if (w.a_cap >= halves && w.a_rows >= rows) return;
+    dfree(w.ah);
+    dfree(w.al);
+    dfree(w.aus);
+    w.ah = w.al = nullptr;
+    w.aus = nullptr;
+    w.a_cap = 0;
+    w.a_rows = 0;
+    w.ah = reinterpret_cast<_Float16*>(dalloc<uint16_t>(halves, false));
+    w.al = reinterpret_cast<_Float16*>(dalloc<uint16_t>(halves, false));
+    w.aus = dalloc<float>((size_t)rows, false);
+    w.a_cap = halves;
+    w.a_rows = rows;
+}
+
+// a matrix's copy for the matrix-core GEMM (allocation recorded in `owned`)
+Q8MfmaDev mfma_copy(std::vector<void*>& owned, const Q8Dev& W, hipStream_t st) {
+    Q8MfmaDev M;
+    M.rows = W.rows;
+    M.cols = W.cols;
+    M.nb = W.nb;
+    M.nb4 = (W.nb + 3) / 4;
+    M.tiles = (W.rows + 15) / 16;
+    M.q = reinterpret_cast<int8_t*>(dalloc<uint8_t>((size_t)M.tiles * M.nb * 512, false));
+    owned.push_back(M.q);
+    M.d = dalloc<float>((size_t)M.tiles * M.nb4 * 64, false);
+    owned.push_back(M.d);
+    launch_mfma_repack(W, M, st);
+    CK(hipGetLastError());
+    return M;
+}
+
+// the layers' matrix-core copies, built once when a Q8_0 model first enables MFMA prefill
+void build_mfma(jyhip_model* m) {
+    if (m->mfma_built || m->wtype != JY_Q8_0) return;
+    for (DevLayer& D : m->layers) {
+        D.mqkv = mfma_copy(m->owned, D.qkv, m->stream);
+        D.mo = mfma_copy(m->owned, D.o, m->stream);
+        D.mgu = mfma_copy(m->owned, D.gu, m->stream);
+        D.mdown = mfma_copy(m->owned, D.down, m->stream);
+    }
+    CK(hipStreamSynchronize(m->stream));
+    m->mfma_built = true;
+}
+
+// whether a prompt pass runs its Q8_0 GEMMs on the matrix cores, and the split size it needs
+bool use_mfma(const jyhip_model* m) {
+    return m->wtype == JY_Q8_0 && (m->mode & JYHIP_MODE_MFMA_PREFILL) && m->mfma_built;
+}
+size_t mfma_split_halves(const jyhip_model* m, int seq) {
+    return (size_t)mfma_rows_padded(seq) * std::max({m->H, m->qd, m->F});
 }
 
 void ensure_part(jyhip_model* m, size_t n) {
@@ -681,7 +752,8 @@ void release(jyhip_model* m) {
     for (void* p : m->owned) dfree(p);
     Workspace& w = m->ws;
     for (void* p : {(void*)w.X, (void*)w.xn, (void*)w.qkv, (void*)w.att, (void*)w.g, (void*)w.u, (void*)w.h,
-                    (void*)w.q8, (void*)w.qsc, (void*)w.scores, (void*)w.part})
+                    (void*)w.q8, (void*)w.qsc, (void*)w.scores, (void*)w.part, (void*)w.ah, (void*)w.al,
+                    (void*)w.aus})
         dfree(p);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
@@ -822,6 +894,25 @@ void run_prefill_layers(jyhip_model* m, Workspace& w, const KVDev& kv, int seq, 
     at.scratch = w.scores;
     at.max_keys = max_keys;
     at.out = w.att;
+    // Q8_0 GEMMs: the exact tiles, or (MFMA prefill mode) the activations split into fp16
+    // high / low parts and the matrix-core kernel
+    const bool mf = q8 && use_mfma(m);
+    // attention of the prompt rows: the tolerance mode's split form (one workgroup per kv
+    // head and row) or the exact kernels over chunks of rows
+    const bool split_rows = (m->mode & JYHIP_MODE_SPLIT_ATTN) && attn_split_supported(m->nh, m->nkv, m->hd);
+    const int mp = mfma_rows_padded(seq);
+    if (mf && (w.a_cap < mfma_split_halves(m, seq) || w.a_rows < mp)) {
+        if (&w != &m->ws) fail("prefill: the workspace has no room for the matrix-core split buffers");
+        ensure_split(m, mfma_split_halves(m, seq), mp);
+    }
+    auto gemm_q8 = [&](const Q8Dev& W, const Q8MfmaDev& M, const float* A, float* Cm, const float* aux, Epi epi) {
+        if (mf) {
+            launch_mfma_split(A, seq, mp, W.cols, w.ah, w.al, w.aus, st);
+            launch_gemm_q8_mfma(M, seq, w.ah, w.al, w.aus, Cm, W.rows, aux, epi, st);
+        } else {
+            launch_gemm_q8(W, seq, A, Cm, aux, epi, st);
+        }
+    };
     for (int l = 0; l < m->L; l++) {
         const DevLayer& D = m->layers[l];
         launch_rmsnorm(w.X, w.xn, D.rms1, H, seq, st);
@@ -832,22 +923,28 @@ void run_prefill_layers(jyhip_model* m, Workspace& w, const KVDev& kv, int seq, 
             launch_gemm(D.w[1], seq, w.xn, w.qkv + qd, NQ, D.bqkv ? D.bqkv + qd : nullptr, qkv_epi, st);
             launch_gemm(D.w[2], seq, w.xn, w.qkv + qd + kvd, NQ, D.bqkv ? D.bqkv + qd + kvd : nullptr, qkv_epi, st);
         } else if (q8) {
-            launch_gemm_q8(D.qkv, seq, w.xn, w.qkv, D.bqkv, qkv_epi, st);
+            gemm_q8(D.qkv, D.mqkv, w.xn, w.qkv, D.bqkv, qkv_epi);
         } else {
             launch_gemm_f32(D.f_qkv, H, NQ, seq, w.xn, w.qkv, D.bqkv, qkv_epi, st);
         }
         launch_rope_pack(w.qkv, seq, start_pos, nullptr, m->nh, m->nkv, m->hd, m->cos_t, m->sin_t, kv, l, w.q8,
                          w.qsc, st);
         at.layer = l;
-        for (int r0 = 0; r0 < seq; r0 += chunk) {
-            at.row0 = r0;
-            at.nrows = std::min(chunk, seq - r0);
-            launch_attention(at, st);
+        if (split_rows) {
+            at.row0 = 0;
+            at.nrows = seq;
+            launch_attention_prefill_split(at, st);
+        } else {
+            for (int r0 = 0; r0 < seq; r0 += chunk) {
+                at.row0 = r0;
+                at.nrows = std::min(chunk, seq - r0);
+                launch_attention(at, st);
+            }
         }
         if (mixed)
             launch_gemm(D.w[3], seq, w.att, w.X, H, nullptr, EPI_RESID, st);
         else if (q8)
-            launch_gemm_q8(D.o, seq, w.att, w.X, nullptr, EPI_RESID, st);
+            gemm_q8(D.o, D.mo, w.att, w.X, nullptr, EPI_RESID);
         else
             launch_gemm_f32(D.f_o, m->qd, H, seq, w.att, w.X, nullptr, EPI_RESID, st);
         launch_rmsnorm(w.X, w.xn, D.rms2, H, seq, st);
@@ -857,9 +954,9 @@ void run_prefill_layers(jyhip_model* m, Workspace& w, const KVDev& kv, int seq, 
             launch_silu_mul(w.g, w.u, 0, seq, F, w.h, st);
             launch_gemm(D.w[5], seq, w.h, w.X, H, nullptr, EPI_RESID, st);
         } else if (q8) {
-            launch_gemm_q8(D.gu, seq, w.xn, w.g, nullptr, EPI_STORE, st);
+            gemm_q8(D.gu, D.mgu, w.xn, w.g, nullptr, EPI_STORE);
             launch_silu_mul(w.g, nullptr, 1, seq, F, w.h, st);
-            launch_gemm_q8(D.down, seq, w.h, w.X, nullptr, EPI_RESID, st);
+            gemm_q8(D.down, D.mdown, w.h, w.X, nullptr, EPI_RESID);
         } else {
             launch_gemm_f32(D.f_w1, H, F, seq, w.xn, w.g, nullptr, EPI_STORE, st);
             launch_gemm_f32(D.f_w3, H, F, seq, w.xn, w.u, nullptr, EPI_STORE, st);
@@ -1272,6 +1369,13 @@ Workspace ws_view(const jyhip_model* m, int seq, int max_keys, size_t scores_n, 
     w.scores_n = scores_n;
     w.part_n = part_need(m, max_keys);
     w.part = (float*)take(w.part_n * 4);
+    if (seq > 1 && use_mfma(m)) {
+        w.a_cap = mfma_split_halves(m, seq);
+        w.a_rows = mfma_rows_padded(seq);
+        w.ah = (_Float16*)take(w.a_cap * 2);
+        w.al = (_Float16*)take(w.a_cap * 2);
+        w.aus = (float*)take((size_t)w.a_rows * 4);
+    }
     w.rows = seq;
     *bytes = off;
     return w;
@@ -1373,6 +1477,10 @@ JYHIP_API int jyhip_model_set_mode(jyhip_model* m, int mode) {
     return guarded([&]() {
         if (!m) fail("model is NULL");
         if (mode & ~(JYHIP_MODE_FAST | JYHIP_MODE_PERSIST)) fail("unknown mode bits");
+        if (mode & JYHIP_MODE_MFMA_PREFILL) {
+            CK(hipSetDevice(m->device));
+            build_mfma(m);
+        }
         m->mode = mode;
         return 0;
     }, -1);
@@ -1632,6 +1740,7 @@ JYHIP_API void jyhip_q8_free(jyhip_q8mat* q) {
         dfree(d.qs);
         dfree(d.d);
     }
+    for (void* p : q->mowned) dfree(p);
     dfree(q->x);
     dfree(q->y);
     dfree(q->nw);
@@ -1659,7 +1768,92 @@ JYHIP_API int jyhip_q8_set_mode(jyhip_q8mat* q, int mode) {
     return guarded([&]() {
         if (!q) fail("matrix is NULL");
         if (mode & ~JYHIP_MODE_FAST) fail("unknown mode bits");
+        if ((mode & JYHIP_MODE_MFMA_PREFILL) && q->mcopies.empty()) {
+            for (const Q8Dev& d : q->copies) q->mcopies.push_back(mfma_copy(q->mowned, d, q->stream));
+            CK(hipStreamSynchronize(q->stream));
+        }
         q->mode = mode;
+        return 0;
+    }, -1);
+}
+
+}  // extern "C"
+
+namespace {
+// C[mr][rows] = A[mr][cols] W^T for copy c in the matrix's mode, device buffers given;
+// the MFMA form splits A into hi / lo first
+void q8_gemm_launch(jyhip_q8mat* q, size_t c, int mr, const float* A, float* Cd, _Float16* hi, _Float16* lo,
+                    float* us) {
+    const Q8Dev& d = q->copies[c];
+    if (q->mode & JYHIP_MODE_MFMA_PREFILL) {
+        launch_mfma_split(A, mr, mfma_rows_padded(mr), d.cols, hi, lo, us, q->stream);
+        launch_gemm_q8_mfma(q->mcopies[c], mr, hi, lo, us, Cd, d.rows, nullptr, EPI_STORE, q->stream);
+    } else {
+        launch_gemm_q8(d, mr, A, Cd, nullptr, EPI_STORE, q->stream);
+    }
+}
+
+// run f(A_dev, C_dev, hi, lo, us) with device buffers for mr rows of A uploaded from host
+template <class F>
+void with_gemm_buffers(jyhip_q8mat* q, int mr, const float* A, F&& f) {
+    const Q8Dev& d = q->copies[0];
+    const size_t mp = (size_t)mfma_rows_padded(mr);
+    float* Ad = nullptr;
+    float* Cd = nullptr;
+    uint16_t *hi = nullptr, *lo = nullptr;
+    float* us = nullptr;
+    try {
+        Ad = dalloc<float>((size_t)mr * d.cols, false);
+        Cd = dalloc<float>((size_t)mr * d.rows, false);
+        hi = dalloc<uint16_t>(mp * d.cols, false);
+        lo = dalloc<uint16_t>(mp * d.cols, false);
+        us = dalloc<float>(mp, false);
+        CK(hipMemcpyAsync(Ad, A, sizeof(float) * mr * d.cols, hipMemcpyHostToDevice, q->stream));
+        f(Ad, Cd, reinterpret_cast<_Float16*>(hi), reinterpret_cast<_Float16*>(lo), us);
+    } catch (...) {
+        (void)hipStreamSynchronize(q->stream);
+        for (void* p : {(void*)Ad, (void*)Cd, (void*)hi, (void*)lo, (void*)us}) dfree(p);
+        throw;
+    }
+    (void)hipStreamSynchronize(q->stream);
+    for (void* p : {(void*)Ad, (void*)Cd, (void*)hi, (void*)lo, (void*)us}) dfree(p);
+}
+}  // namespace
+
+extern "C" {
+
+JYHIP_API int jyhip_q8_gemm(jyhip_q8mat* q, int mr, const float* A, float* Cout) {
+    return guarded([&]() {
+        if (!q || !A || !Cout || mr <= 0) fail("bad argument");
+        with_gemm_buffers(q, mr, A, [&](float* Ad, float* Cd, _Float16* hi, _Float16* lo, float* us) {
+            q8_gemm_launch(q, 0, mr, Ad, Cd, hi, lo, us);
+            CK(hipGetLastError());
+            CK(hipMemcpyAsync(Cout, Cd, sizeof(float) * mr * q->copies[0].rows, hipMemcpyDeviceToHost, q->stream));
+            CK(hipStreamSynchronize(q->stream));
+        });
+        return 0;
+    }, -1);
+}
+
+JYHIP_API int jyhip_q8_gemm_time(jyhip_q8mat* q, int mr, const float* A, int iters, double* avg_us) {
+    return guarded([&]() {
+        if (!q || !A || !avg_us || mr <= 0 || iters <= 0) fail("bad argument");
+        with_gemm_buffers(q, mr, A, [&](float* Ad, float* Cd, _Float16* hi, _Float16* lo, float* us) {
+            for (size_t c = 0; c < q->copies.size(); c++) q8_gemm_launch(q, c, mr, Ad, Cd, hi, lo, us);
+            hipEvent_t a, b;
+            CK(hipEventCreate(&a));
+            CK(hipEventCreate(&b));
+            CK(hipEventRecord(a, q->stream));
+            for (int i = 0; i < iters; i++) q8_gemm_launch(q, (size_t)i % q->copies.size(), mr, Ad, Cd, hi, lo, us);
+            CK(hipEventRecord(b, q->stream));
+            CK(hipEventSynchronize(b));
+            float ms = 0.0f;
+            CK(hipEventElapsedTime(&ms, a, b));
+            (void)hipEventDestroy(a);
+            (void)hipEventDestroy(b);
+            CK(hipGetLastError());
+            *avg_us = 1000.0 * ms / iters;
+        });
         return 0;
     }, -1);
 }

@@ -4,9 +4,10 @@ The specification allows floating-point reordering within 1e-3 relative on per-l
 fp32 hidden states, with identical greedy token ids.  Here "within 1e-3 relative" is
 checked per layer output as max|gpu - oracle| <= 1e-3 * max|oracle| (an element-wise
 ratio is meaningless at values near zero).  Int8 KV bytes are checked exactly where the
-fp32 values they quantise are the reference's: without the split matvec the first
-layer's K and V come from the exact QKV matvec of the unchanged inputs.  With it their
-scales may differ in the last bits and a value on a rounding boundary by one step.
+fp32 values they quantise are the reference's: without the split matvec and the
+matrix-core prompt GEMMs the first layer's K and V come from the exact QKV products of the
+unchanged inputs.  With either their scales may differ in the last bits and a value on a
+rounding boundary by one step.
 """
 import ctypes as C
 
@@ -88,7 +89,47 @@ def test_split_matvec_within_tolerance(jy, oracle_lib, rows, cols):
     assert rel_err(y, ref) <= TOL
 
 
-MODES = {"SPLIT_ATTN": 1, "SPLIT_MV": 2, "FAST": 7, "PERSIST": 7 | 8}
+def dequant(w, rows, cols):
+    q = w.reshape(rows, cols // 32, 34)
+    d = q[:, :, :2].copy().view(np.float16).astype(np.float64)[:, :, 0]
+    return (q[:, :, 2:].view(np.int8).astype(np.float64) * d[:, :, None]).reshape(rows, cols)
+
+
+# prompt GEMMs: ragged token counts (not multiples of the 128-row tile), rows not multiples of
+# 16, blocks not multiples of 4 (1184 = 37 blocks), the benchmark's 4096 x 4096 at 1024 tokens;
+# activation rows spread over 10^-3 .. 10^3 with one zero row
+@pytest.mark.parametrize("m,rows,cols", [(2, 13, 96), (37, 300, 1184), (200, 517, 896), (130, 1000, 4864),
+                                         (1024, 4096, 4096)])
+def test_mfma_gemm_within_tolerance(jy, oracle_lib, m, rows, cols):
+    """The matrix-core prompt GEMM (fp16 high/low split of the activations, fp16 weights,
+    fp32 block sums times the block scales) within 1e-5 of sum |a| |w| of the float64
+    product, element by element; the exact tiles bit-equal to the oracle's matmul."""
+    from conftest import q8_random_uniform
+    say(f"mfma gemm m={m} {rows}x{cols}")
+    w = q8_random_uniform(oracle_lib, rows, cols, seed=3)
+    A = np.zeros((m, cols), np.float32)
+    oracle_lib.jysyn_normal_fill(3, 17, 1.0, ptr(A), A.size)
+    A *= (10.0 ** (np.arange(m) % 7 - 3)).astype(np.float32)[:, None]
+    A[m // 2] = 0.0
+    M = jy.Q8Matrix(w, rows, cols)
+    M.set_mode(jy.MODE_MFMA_PREFILL)
+    got = M.gemm(A)
+    M.set_mode(jy.MODE_EXACT)
+    tiles = M.gemm(A) if m * rows * cols <= 1 << 28 else None
+    M.close()
+    wf = dequant(w, rows, cols)
+    A64 = A.astype(np.float64)
+    exact = A64 @ wf.T
+    bound = 1e-5 * (np.abs(A64) @ np.abs(wf).T)
+    assert np.all(np.abs(got - exact) <= bound), f"worst excess {np.max(np.abs(got - exact) - bound):.3g}"
+    assert np.all(got[m // 2] == 0.0)
+    if tiles is not None:
+        ref = np.zeros((m, rows), np.float32)
+        oracle_lib.jyo_matmul_q8(ptr(A), ptr(w), ptr(ref), m, rows, cols)
+        assert np.array_equal(tiles.view(np.uint32), ref.view(np.uint32))
+
+
+MODES = {"SPLIT_ATTN": 1, "SPLIT_MV": 2, "MFMA_PREFILL": 4, "FAST": 7, "PERSIST": 7 | 8}
 
 
 @pytest.mark.parametrize("mode_name", list(MODES))
@@ -123,7 +164,7 @@ def test_forward_cached_within_tolerance(jy, oracle_lib, key, mode_name):
         start += seq
     ok8, ov8, oks, ovs = kv_views(okv, L, max_seq, nkv, hd)
     k, ks, v, vs = kv.read(0, 0, start)
-    if not g.mode & jy.MODE_SPLIT_MV:
+    if not g.mode & (jy.MODE_SPLIT_MV | jy.MODE_MFMA_PREFILL):
         assert np.array_equal(k, ok8[0, :start]) and np.array_equal(v, ov8[0, :start])
         assert np.array_equal(ks, oks[0, :start]) and np.array_equal(vs, ovs[0, :start])
     else:
