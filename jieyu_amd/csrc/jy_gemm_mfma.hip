@@ -20,9 +20,10 @@
 //
 // Tiling.  A workgroup of 4 waves computes 128 rows (tokens) x 128 columns (matrix rows),
 // each wave 64 x 64: 4 x 4 tiles of 16 x 16, acc in the MFMA C layout (lane l holds rows
-// 4 (l/16) .. +3 of column l % 16).  Operands come straight from global memory (L2): per
-// block a wave loads its 4 row tiles' high and low parts (16 B per lane each) and its 4
-// column tiles' weights (8 B per lane), one block ahead of the MFMAs that use them.
+// 4 (l/16) .. +3 of column l % 16).  Per block the workgroup stages the tile's activation
+// parts and its weights (converted to fp16 once) in LDS, double-buffered, with the global
+// loads two blocks ahead in registers: block b+2's loads are in flight while the waves run
+// block b's MFMAs from LDS and stage block b+1.
 #include "jy_layout.h"
 
 namespace jy {
@@ -142,50 +143,72 @@ __device__ __forceinline__ h8_t q8_to_h8(uint32_t w0, uint32_t w1) {
     return h8_t{r0.x, r0.y, r1.x, r1.y, r2.x, r2.y, r3.x, r3.y};
 }
 
-struct GmOps {
-    h8_t ah[4], al[4];  // the wave's 4 row tiles, high and low parts
-    uint2 q[4];         // the wave's 4 column tiles' weights
+// LDS of one block stage, in MFMA operand order: for each of the 8 row tiles (high and
+// low parts) and 8 column tiles (weights as fp16), the 64 lanes' 16-byte operands at
+// lane * 16, so that every operand read and every staging write is one contiguous 1 KiB
+// per wave instruction (no bank conflicts); and the 128 columns' block scales
+struct GmStage {
+    h8_t ah[8][64];
+    h8_t al[8][64];
+    h8_t bq[8][64];
+    float d[GM_TILE];
+};
+
+// Block b of the workgroup's tile into registers (global loads only): thread t stages
+// operand positions p = t and t + 256 (row tile p/64, lane p%64: token row 16 (p/64) +
+// (p%16), k 8 ((p%64)/16) .. +7) of the high and low parts; lanes 2 (t%32), +1 of column
+// tile t/32 (8 weight bytes each); with t < 128 column t's scale
+struct GmRegs {
+    uint4 h0, h1, l0, l1;
+    uint2 q0, q1;
+    float d;
 };
 
 template <int EPI>
-__global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(Q8MfmaDev W, int m, int K, const _Float16* __restrict__ ahi,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_q8_mfma_kernel(Q8MfmaDev W, int m, int K, const _Float16* __restrict__ ahi,
                                                            const _Float16* __restrict__ alo,
                                                            const float* __restrict__ unscale, float* __restrict__ C,
                                                            int ldc, const float* __restrict__ aux) {
+    __shared__ GmStage st[2];
     const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
     const int c = l & 15, G = l >> 4;
-    const int row0 = blockIdx.x * GM_TILE + wm * 64;     // the wave's first token row
-    const int tile0 = blockIdx.y * (GM_TILE / 16) + wn * 4;  // the wave's first 16-column tile
+    const int rowt = blockIdx.x * GM_TILE;               // the workgroup's first token row
+    const int tilet = blockIdx.y * (GM_TILE / 16);      // its first 16-column tile
     const int nb = W.nb;
-    // per lane: token rows row0 + 16 mt + c, k offset 8 G within each block
-    const _Float16* ph[4];
-    const _Float16* pl[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; mt++) {
-        const size_t off = (size_t)(row0 + 16 * mt + c) * K + 8 * G;
-        ph[mt] = ahi + off;
-        pl[mt] = alo + off;
-    }
-    bool tv[4];
-    const uint2* pq[4];
-    const float4* pd[4];
-#pragma unroll
-    for (int nt = 0; nt < 4; nt++) {
-        const int t = tile0 + nt;
-        tv[nt] = t < W.tiles;
-        const int tt = tv[nt] ? t : 0;
-        pq[nt] = reinterpret_cast<const uint2*>(W.q) + (size_t)tt * nb * 64 + l;
-        pd[nt] = reinterpret_cast<const float4*>(W.d) + (size_t)tt * W.nb4 * 16 + c;
-    }
-    auto load = [&](GmOps& o, int b) {
-#pragma unroll
-        for (int mt = 0; mt < 4; mt++) {
-            o.ah[mt] = *reinterpret_cast<const h8_t*>(ph[mt] + (size_t)b * 32);
-            o.al[mt] = *reinterpret_cast<const h8_t*>(pl[mt] + (size_t)b * 32);
+
+    // staging roles
+    const size_t a0 = (size_t)(rowt + 16 * (tid >> 6) + c) * K + 8 * G;        // position t
+    const size_t a1 = (size_t)(rowt + 16 * ((tid + 256) >> 6) + c) * K + 8 * G;  // position t + 256
+    const int qt = tid >> 5, qpart = tid & 31;  // column tile (of 8) and lane pair
+    const bool qlive = tilet + qt < W.tiles;
+    const uint2* gq = reinterpret_cast<const uint2*>(W.q) + ((size_t)(qlive ? tilet + qt : 0) * nb) * 64 + 2 * qpart;
+    const int dtile = tilet + (tid >> 4);
+    const bool dlive = tid < GM_TILE && dtile < W.tiles;
+    const float* gd = W.d + ((size_t)(dlive ? dtile : 0) * W.nb4 * 16 + (tid & 15)) * 4;
+
+    auto fetch = [&](GmRegs& r, int b) {
+        const size_t kb = (size_t)b * 32;
+        r.h0 = *reinterpret_cast<const uint4*>(ahi + a0 + kb);
+        r.h1 = *reinterpret_cast<const uint4*>(ahi + a1 + kb);
+        r.l0 = *reinterpret_cast<const uint4*>(alo + a0 + kb);
+        r.l1 = *reinterpret_cast<const uint4*>(alo + a1 + kb);
+        if (qlive) {
+            r.q0 = gq[(size_t)b * 64];
+            r.q1 = gq[(size_t)b * 64 + 1];
+        } else {
+            r.q0 = r.q1 = make_uint2(0u, 0u);
         }
-#pragma unroll
-        for (int nt = 0; nt < 4; nt++) o.q[nt] = tv[nt] ? pq[nt][(size_t)b * 64] : make_uint2(0u, 0u);
+        r.d = dlive ? gd[(size_t)(b >> 2) * 64 + (b & 3)] : 0.0f;
+    };
+    auto stage = [&](const GmRegs& r, GmStage& S) {
+        (&S.ah[0][0])[tid] = __builtin_bit_cast(h8_t, r.h0);
+        (&S.ah[0][0])[tid + 256] = __builtin_bit_cast(h8_t, r.h1);
+        (&S.al[0][0])[tid] = __builtin_bit_cast(h8_t, r.l0);
+        (&S.al[0][0])[tid + 256] = __builtin_bit_cast(h8_t, r.l1);
+        S.bq[qt][2 * qpart] = q8_to_h8(r.q0.x, r.q0.y);
+        S.bq[qt][2 * qpart + 1] = q8_to_h8(r.q1.x, r.q1.y);
+        if (tid < GM_TILE) S.d[tid] = r.d;
     };
 
     f4_t acc[4][4];
@@ -194,48 +217,79 @@ __global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(Q8MfmaDev W, int m, i
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // one block: its operands in `use`; the next block's loads go to `fill` first
-    float4 dq[4];
-    auto step = [&](GmOps& use, GmOps& fill, int b) {
-        if ((b & 3) == 0) {
+    bool ntv[4];
 #pragma unroll
-            for (int nt = 0; nt < 4; nt++) dq[nt] = tv[nt] ? pd[nt][(size_t)(b >> 2) * 16] : make_float4(0, 0, 0, 0);
+    for (int nt = 0; nt < 4; nt++) ntv[nt] = tilet + wn * 4 + nt < W.tiles;
+
+    // block b's MFMAs from LDS stage b % 2
+    auto compute = [&](int b) {
+        const GmStage& S = st[b & 1];
+        h8_t ah[4], al[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++) {
+            ah[mt] = S.ah[wm * 4 + mt][l];
+            al[mt] = S.al[wm * 4 + mt][l];
         }
-        if (b + 1 < nb) load(fill, b + 1);
-        const int bj = b & 3;
+        // two column tiles at a time: their 8 tiles' block sums (16 independent MFMAs back
+        // to back), then the scaling
 #pragma unroll
-        for (int nt = 0; nt < 4; nt++) {
-            if (!tv[nt]) continue;  // wave-uniform: a column tile past the matrix
-            const h8_t bq = q8_to_h8(use.q[nt].x, use.q[nt].y);
-            const float dj = bj == 0 ? dq[nt].x : bj == 1 ? dq[nt].y : bj == 2 ? dq[nt].z : dq[nt].w;
+        for (int n0 = 0; n0 < 4; n0 += 2) {
+            f4_t t[4][2];
+            float dj[2];
 #pragma unroll
-            for (int mt = 0; mt < 4; mt++) {
-                f4_t t = __builtin_amdgcn_mfma_f32_16x16x32_f16(use.ah[mt], bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(use.al[mt], bq, t, 0, 0, 0);
+            for (int u = 0; u < 2; u++) {
+                const h8_t bq = S.bq[wn * 4 + n0 + u][l];
+                dj[u] = S.d[wn * 64 + (n0 + u) * 16 + c];
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[mt][nt][i] = __builtin_fmaf(dj, t[i], acc[mt][nt][i]);
+                for (int mt = 0; mt < 4; mt++)
+                    t[mt][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
             }
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const h8_t bq = S.bq[wn * 4 + n0 + u][l];
+#pragma unroll
+                for (int mt = 0; mt < 4; mt++)
+                    t[mt][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], bq, t[mt][u], 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        acc[mt][n0 + u][i] = __builtin_fmaf(dj[u], t[mt][u][i], acc[mt][n0 + u][i]);
         }
     };
-    GmOps ops0, ops1;
-    load(ops0, 0);
+    // registers: ra holds the block after the one being computed (in flight since the
+    // previous iteration), rb takes the loads of the block two ahead
+    GmRegs ra, rb;
+    fetch(ra, 0);
+    if (nb > 1) fetch(rb, 1);
+    stage(ra, st[0]);
+    __syncthreads();
+    auto iter = [&](int b, GmRegs& next, GmRegs& ahead) {
+        if (b + 2 < nb) fetch(ahead, b + 2);
+        compute(b);
+        if (b + 1 < nb) stage(next, st[(b + 1) & 1]);
+        __syncthreads();
+    };
     for (int b = 0; b < nb; b += 2) {
-        step(ops0, ops1, b);
-        if (b + 1 < nb) step(ops1, ops0, b + 1);
+        iter(b, rb, ra);
+        if (b + 1 < nb) iter(b + 1, ra, rb);
     }
 
-    // epilogue: acc[mt][nt][i] is C[row0 + 16 mt + 4 G + i][16 (tile0 + nt) + c] before the row's unscale
+    // epilogue: acc[mt][nt][i] is C[row][col] before the row's unscale
     const int N = W.rows;
 #pragma unroll
     for (int nt = 0; nt < 4; nt++) {
-        const int col = 16 * (tile0 + nt) + c;
-        if (!tv[nt] || col >= N) continue;
+        const int col = 16 * (tilet + wn * 4 + nt) + c;
+        if (!ntv[nt] || col >= N) continue;
         const float bias = EPI == EPI_BIAS ? aux[col] : 0.0f;
 #pragma unroll
         for (int mt = 0; mt < 4; mt++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int row = row0 + 16 * mt + 4 * G + i;
+                const int row = rowt + wm * 64 + 16 * mt + 4 * G + i;
                 if (row >= m) continue;
                 const float y = acc[mt][nt][i] * unscale[row];
                 float* dst = C + (size_t)row * ldc + col;
