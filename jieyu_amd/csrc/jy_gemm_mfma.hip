@@ -147,11 +147,12 @@ __device__ __forceinline__ h8_t q8_to_h8(uint32_t w0, uint32_t w1) {
 // low parts) and 8 column tiles (weights as fp16), the 64 lanes' 16-byte operands at
 // lane * 16, so that every operand read and every staging write is one contiguous 1 KiB
 // per wave instruction (no bank conflicts); and the 128 columns' block scales
+template <int NT>
 struct GmStage {
     h8_t ah[8][64];
     h8_t al[8][64];
-    h8_t bq[8][64];
-    float d[GM_TILE];
+    h8_t bq[2 * NT][64];
+    float d[32 * NT];
 };
 
 // Block b of the workgroup's tile into registers (global loads only): thread t stages
@@ -164,27 +165,29 @@ struct GmRegs {
     float d;
 };
 
-template <int EPI>
+// NT column tiles per wave: a workgroup covers 128 tokens x 32 NT columns
+template <int EPI, int NT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_q8_mfma_kernel(Q8MfmaDev W, int m, int K, const _Float16* __restrict__ ahi,
                                                            const _Float16* __restrict__ alo,
                                                            const float* __restrict__ unscale, float* __restrict__ C,
                                                            int ldc, const float* __restrict__ aux) {
-    __shared__ GmStage st[2];
+    __shared__ GmStage<NT> st[2];
     const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
     const int c = l & 15, G = l >> 4;
     const int rowt = blockIdx.x * GM_TILE;               // the workgroup's first token row
-    const int tilet = blockIdx.y * (GM_TILE / 16);      // its first 16-column tile
+    const int tilet = blockIdx.y * 2 * NT;              // its first 16-column tile
     const int nb = W.nb;
 
     // staging roles
     const size_t a0 = (size_t)(rowt + 16 * (tid >> 6) + c) * K + 8 * G;        // position t
     const size_t a1 = (size_t)(rowt + 16 * ((tid + 256) >> 6) + c) * K + 8 * G;  // position t + 256
-    const int qt = tid >> 5, qpart = tid & 31;  // column tile (of 8) and lane pair
-    const bool qlive = tilet + qt < W.tiles;
+    const int qt = tid >> 5, qpart = tid & 31;  // column tile (of 2 NT) and lane pair
+    const bool qstage = qt < 2 * NT;
+    const bool qlive = qstage && tilet + qt < W.tiles;
     const uint2* gq = reinterpret_cast<const uint2*>(W.q) + ((size_t)(qlive ? tilet + qt : 0) * nb) * 64 + 2 * qpart;
     const int dtile = tilet + (tid >> 4);
-    const bool dlive = tid < GM_TILE && dtile < W.tiles;
+    const bool dlive = tid < 32 * NT && dtile < W.tiles;
     const float* gd = W.d + ((size_t)(dlive ? dtile : 0) * W.nb4 * 16 + (tid & 15)) * 4;
 
     auto fetch = [&](GmRegs& r, int b) {
@@ -201,29 +204,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
         r.d = dlive ? gd[(size_t)(b >> 2) * 64 + (b & 3)] : 0.0f;
     };
-    auto stage = [&](const GmRegs& r, GmStage& S) {
+    auto stage = [&](const GmRegs& r, GmStage<NT>& S) {
         (&S.ah[0][0])[tid] = __builtin_bit_cast(h8_t, r.h0);
         (&S.ah[0][0])[tid + 256] = __builtin_bit_cast(h8_t, r.h1);
         (&S.al[0][0])[tid] = __builtin_bit_cast(h8_t, r.l0);
         (&S.al[0][0])[tid + 256] = __builtin_bit_cast(h8_t, r.l1);
-        S.bq[qt][2 * qpart] = q8_to_h8(r.q0.x, r.q0.y);
-        S.bq[qt][2 * qpart + 1] = q8_to_h8(r.q1.x, r.q1.y);
-        if (tid < GM_TILE) S.d[tid] = r.d;
+        if (qstage) {
+            S.bq[qt][2 * qpart] = q8_to_h8(r.q0.x, r.q0.y);
+            S.bq[qt][2 * qpart + 1] = q8_to_h8(r.q1.x, r.q1.y);
+        }
+        if (tid < 32 * NT) S.d[tid] = r.d;
     };
 
-    f4_t acc[4][4];
+    f4_t acc[4][NT];
 #pragma unroll
     for (int mt = 0; mt < 4; mt++)
 #pragma unroll
-        for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int nt = 0; nt < NT; nt++) acc[mt][nt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    bool ntv[4];
+    bool ntv[NT];
 #pragma unroll
-    for (int nt = 0; nt < 4; nt++) ntv[nt] = tilet + wn * 4 + nt < W.tiles;
+    for (int nt = 0; nt < NT; nt++) ntv[nt] = tilet + wn * NT + nt < W.tiles;
 
     // block b's MFMAs from LDS stage b % 2
     auto compute = [&](int b) {
-        const GmStage& S = st[b & 1];
+        const GmStage<NT>& S = st[b & 1];
         h8_t ah[4], al[4];
 #pragma unroll
         for (int mt = 0; mt < 4; mt++) {
@@ -233,20 +238,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // two column tiles at a time: their 8 tiles' block sums (16 independent MFMAs back
         // to back), then the scaling
 #pragma unroll
-        for (int n0 = 0; n0 < 4; n0 += 2) {
+        for (int n0 = 0; n0 < NT; n0 += 2) {
             f4_t t[4][2];
             float dj[2];
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const h8_t bq = S.bq[wn * 4 + n0 + u][l];
-                dj[u] = S.d[wn * 64 + (n0 + u) * 16 + c];
+                const h8_t bq = S.bq[wn * NT + n0 + u][l];
+                dj[u] = S.d[(wn * NT + n0 + u) * 16 + c];
 #pragma unroll
                 for (int mt = 0; mt < 4; mt++)
                     t[mt][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
             }
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const h8_t bq = S.bq[wn * 4 + n0 + u][l];
+                const h8_t bq = S.bq[wn * NT + n0 + u][l];
 #pragma unroll
                 for (int mt = 0; mt < 4; mt++)
                     t[mt][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], bq, t[mt][u], 0, 0, 0);
@@ -281,8 +286,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // epilogue: acc[mt][nt][i] is C[row][col] before the row's unscale
     const int N = W.rows;
 #pragma unroll
-    for (int nt = 0; nt < 4; nt++) {
-        const int col = 16 * (tilet + wn * 4 + nt) + c;
+    for (int nt = 0; nt < NT; nt++) {
+        const int col = 16 * (tilet + wn * NT + nt) + c;
         if (!ntv[nt] || col >= N) continue;
         const float bias = EPI == EPI_BIAS ? aux[col] : 0.0f;
 #pragma unroll
@@ -303,26 +308,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
 int mfma_rows_padded(int m) { return (m + GM_TILE - 1) / GM_TILE * GM_TILE; }
 
-void launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
-                         float* C, int ldc, const float* aux, Epi epi, hipStream_t st) {
+template <int NT>
+static void gemm_mfma_launch(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
+                             float* C, int ldc, const float* aux, Epi epi, hipStream_t st) {
     // x: token tiles (the fastest in dispatch order: the workgroups that read one column
     // tile's weights run together), y: column tiles
-    const dim3 grid((unsigned)(mfma_rows_padded(m) / GM_TILE), (unsigned)((W.tiles + GM_TILE / 16 - 1) / (GM_TILE / 16)));
+    const dim3 grid((unsigned)(mfma_rows_padded(m) / GM_TILE), (unsigned)((W.tiles + 2 * NT - 1) / (2 * NT)));
     const int K = W.nb * 32;
     switch (epi) {
         case EPI_BIAS:
-            hipLaunchKernelGGL(gemm_q8_mfma_kernel<EPI_BIAS>, grid, dim3(256), 0, st, W, m, K, hi, lo, unscale, C, ldc,
-                               aux);
+            hipLaunchKernelGGL((gemm_q8_mfma_kernel<EPI_BIAS, NT>), grid, dim3(256), 0, st, W, m, K, hi, lo, unscale, C,
+                               ldc, aux);
             break;
         case EPI_RESID:
-            hipLaunchKernelGGL(gemm_q8_mfma_kernel<EPI_RESID>, grid, dim3(256), 0, st, W, m, K, hi, lo, unscale, C,
-                               ldc, aux);
+            hipLaunchKernelGGL((gemm_q8_mfma_kernel<EPI_RESID, NT>), grid, dim3(256), 0, st, W, m, K, hi, lo, unscale,
+                               C, ldc, aux);
             break;
         default:
-            hipLaunchKernelGGL(gemm_q8_mfma_kernel<EPI_STORE>, grid, dim3(256), 0, st, W, m, K, hi, lo, unscale, C,
-                               ldc, aux);
+            hipLaunchKernelGGL((gemm_q8_mfma_kernel<EPI_STORE, NT>), grid, dim3(256), 0, st, W, m, K, hi, lo, unscale,
+                               C, ldc, aux);
             break;
     }
+}
+
+static int g_gemm_cus = 0;
+
+// the wide tile (64 columns per wave), or the narrow one (32 columns per wave: twice the
+// workgroups) when the wide tile would leave CUs with one workgroup or none (measured at
+// 1024 tokens: 4096-row matrices 160 -> 154 us, 14336-column 561 -> 546 us; the 6144-row
+// QKV, 384 wide workgroups, is faster wide: 185 vs 273 us)
+void launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
+                         float* C, int ldc, const float* aux, Epi epi, hipStream_t st) {
+    if (!g_gemm_cus) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+            g_gemm_cus = cus;
+        else
+            g_gemm_cus = 256;
+    }
+    const long wide = (long)(mfma_rows_padded(m) / GM_TILE) * ((W.tiles + 7) / 8);
+    if (wide > g_gemm_cus)
+        gemm_mfma_launch<4>(W, m, hi, lo, unscale, C, ldc, aux, epi, st);
+    else
+        gemm_mfma_launch<2>(W, m, hi, lo, unscale, C, ldc, aux, epi, st);
 }
 
 }  // namespace jy
