@@ -41,6 +41,7 @@ MODE_TEXT = {"exact": "bit-exact (reference arithmetic order)",
                      "(tolerance 1e-3 relative per layer; greedy ids identical except at near ties within 2e-3 "
                      "of max|logit|)"}
 HBM_PEAK_GBS = 8000.0
+F16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak
 
 
 def log(msg):
@@ -103,6 +104,51 @@ def dominant_kernel_roofline(jy, d, mode, iters=64):
             "kernel": ("matvec_q8_split_kernel<EPI_SWIGLU, NORM>" if split else "matvec_q8_kernel<EPI_SWIGLU, NORM>")
                       + " (gate/up, %d x %d)" % (rows, cols),
             "bytes_per_launch": algo, "avg_launch_us": round(us, 3), "launches": iters, "copies": copies}
+
+
+def prompt_gemm_flops(d, n):
+    """Useful flops of the prompt GEMMs (QKV, O, gate/up, down: 2 per weight per row) for n rows."""
+    H, F, L = d.hidden, d.intermediate, d.num_layers
+    qd, kvd = d.num_heads * d.head_dim, d.num_kv_heads * d.head_dim
+    return 2.0 * n * L * (H * (qd + 2 * kvd) + qd * H + H * 2 * F + F * H)
+
+
+def prefill_mfma(d, n, ms, mode):
+    """Matrix-core use over a whole prompt pass (attention and the other kernels included,
+    so a floor on the GEMMs' own rate): useful GEMM TFLOP/s, and the MFMA flops executed
+    (twice the useful ones: the activations' fp16 high and low parts) as a fraction of the
+    dense fp16 peak."""
+    if not MODES[mode] & 4:
+        return None
+    useful = prompt_gemm_flops(d, n) / (ms * 1e-3) / 1e12
+    return {"gemm_tflops": round(useful, 1), "mfma_executed_tflops": round(2 * useful, 1),
+            "peak_tflops": F16_MFMA_PEAK_TFLOPS, "mfma_frac": round(2 * useful / F16_MFMA_PEAK_TFLOPS, 4)}
+
+
+def isolated_prompt_gemm(jy, d, n, iters=8):
+    """The matrix-core prompt GEMM of the model's gate/up matrix (2F x H, uniform int8 and
+    scales, seed 1) on n rows of N(0,1) activations, the activation split included: its
+    rate against the dense fp16 MFMA peak (executed flops: twice the useful ones)."""
+    rows, cols = 2 * d.intermediate, d.hidden
+    syn = jy.lib()
+    nb = rows * (cols // 32)
+    q = np.zeros(nb * 32, np.int32)
+    syn.jysyn_uniform_int_fill(1, 11, -127, 127, ptr(q), q.size)
+    dsc = np.zeros(nb, np.float32)
+    syn.jysyn_uniform_fill(1, 12, 0.001, 0.01, ptr(dsc), dsc.size)
+    blk = np.zeros((nb, 34), np.uint8)
+    blk[:, 0:2] = dsc.astype(np.float16).view(np.uint8).reshape(nb, 2)
+    blk[:, 2:] = q.astype(np.int8).view(np.uint8).reshape(nb, 32)
+    A = np.zeros((n, cols), np.float32)
+    syn.jysyn_normal_fill(1, 14, 1.0, ptr(A), A.size)
+    m = jy.Q8Matrix(blk.reshape(-1), rows, cols)
+    m.set_mode(jy.MODE_MFMA_PREFILL)
+    us = m.gemm_time(A, iters)
+    m.close()
+    useful = 2.0 * n * rows * cols / (us * 1e-6) / 1e12
+    return {"bound": "mfma", "kernel": "gemm_q8_mfma_kernel (gate/up, %d x %d, %d rows)" % (rows, cols, n),
+            "us": round(us, 1), "gemm_tflops": round(useful, 1), "mfma_executed_tflops": round(2 * useful, 1),
+            "peak_tflops": F16_MFMA_PEAK_TFLOPS, "mfma_frac": round(2 * useful / F16_MFMA_PEAK_TFLOPS, 4)}
 
 
 def isolated_matvecs(jy, mode, iters=64):
@@ -221,6 +267,7 @@ def other_config(jy, name, prompt_len, n_new, prefilled, mode=0):
         res["prefilled_kv_positions"] = prefilled
     else:
         res["prefill_tokens_s"] = round(prompt_len / (pre_ms / 1e3), 1)
+        res["prefill_mfma"] = prefill_mfma(d, prompt_len, pre_ms, "fast" if mode & 4 else "exact")
     if kv is not None:
         kv.close()
     g.close()
@@ -370,7 +417,7 @@ def main():
     log(f"  {K} steps: {wall_ms:.1f} ms wall ({dev_ms:.1f} ms device) -> {tok_s:.1f} tok/s, "
         f"{hbm_gbs:.0f} GB/s = {100 * hbm_gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s")
 
-    roof = iso = other = None
+    roof = iso = other = pgemm = None
     if not args.no_kernel:
         log("dominant kernel in isolation ...")
         roof = dominant_kernel_roofline(jy, d, args.mode)
@@ -379,6 +426,9 @@ def main():
         log(f"  isolated matvec shapes: {iso}")
         other = isolated_other_types(jy)
         log(f"  other weight types: {other}")
+        if MODES[args.mode] & 4:
+            pgemm = isolated_prompt_gemm(jy, d, args.prompt_len)
+            log(f"  prompt GEMM: {pgemm}")
 
     cpu = None
     if not args.no_cpu:
@@ -408,6 +458,7 @@ def main():
         "hbm_gbs": round(hbm_gbs, 1), "hbm_frac": round(hbm_gbs / HBM_PEAK_GBS, 4),
         "bytes_per_token_avg": int(bytes_total / K), "device_ms_per_step": round(dev_ms / K, 4),
         "prefill_ms": round(st.prefill_ms, 2), "prefill_tokens_s": round(args.prompt_len / (st.prefill_ms / 1e3), 1),
+        "prefill_mfma": prefill_mfma(d, args.prompt_len, st.prefill_ms, args.mode), "isolated_prompt_gemm": pgemm,
         "upload_s": round(st.upload_ms / 1e3, 2),
         "last_ids": ids[-8:].tolist(),
         "other_mode": other_mode,

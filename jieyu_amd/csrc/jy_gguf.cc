@@ -13,11 +13,26 @@
 //                     an existing file the way json_file::WriteJsonKey does
 //   vocab.json, merges.txt  from tokenizer.ggml.tokens / .merges
 // Errors are std::runtime_error with the reference's texts.
+//
+// How: the header is parsed into a plan (hyper-parameters, the list of output tensors
+// with their layouts) and every check, including the source ranges and dequantization
+// support of each tensor, runs before the first file is written, so a failed conversion
+// writes nothing.  The source is then memory-mapped; quantized rows are copied out of
+// the mapping, dense tensors dequantized from it block run by block run, and transposed
+// weights produced in panels of whole-block input columns (each panel dequantizes only
+// the blocks it covers from every source row).
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <filesystem>
 #include <fstream>
+#include <set>
 #include <stdexcept>
 
 #include "jy_text.h"
@@ -423,32 +438,24 @@ uint16_t f2bf(float v) {  // converter.h:81-86: + 0x8000 unless inf / nan
     return (uint16_t)(b >> 16);
 }
 
-// write_as (converter.h:88-100)
-void write_as(std::ostream& f, const float* v, uint64_t n, uint8_t dtype) {
+// float values in a model.bf dtype, little-endian, appended to `out`
+void encode_values(const float* v, size_t n, uint8_t dtype, vector<unsigned char>& out) {
+    const size_t at = out.size();
     if (dtype == BF_F32) {
-        f.write(reinterpret_cast<const char*>(v), (std::streamsize)(n * 4));
+        out.resize(at + n * 4);
+        memcpy(out.data() + at, v, n * 4);
         return;
     }
-    vector<unsigned char> out((size_t)n * 2);
-    for (uint64_t i = 0; i < n; i++) {
+    out.resize(at + n * 2);
+    unsigned char* o = out.data() + at;
+    for (size_t i = 0; i < n; i++) {
         const uint16_t h = dtype == BF_F16 ? f2h(v[i]) : f2bf(v[i]);
-        out[2 * i] = (unsigned char)(h & 0xFF);
-        out[2 * i + 1] = (unsigned char)(h >> 8);
+        o[2 * i] = (unsigned char)h;
+        o[2 * i + 1] = (unsigned char)(h >> 8);
     }
-    f.write(reinterpret_cast<const char*>(out.data()), (std::streamsize)out.size());
 }
 
 size_t bf_elem_bytes(uint8_t d) { return d == BF_F32 || d == BF_I32 ? 4 : (d == BF_F16 || d == BF_BF16) ? 2 : d == BF_I8 ? 1 : 0; }
-
-// One model.bf tensor written from the GGUF file (bfile::StreamTensor)
-struct Sink {
-    string name;
-    uint8_t dtype = BF_F32;
-    vector<uint32_t> shape;
-    uint64_t nbytes = 0;
-    const GTensor* src = nullptr;
-    bool raw = false, transpose = false, permute = false;
-};
 
 // GGUF stores q / k rows with each head's RoPE pairs split into halves; jieyu's
 // rope_at takes adjacent pairs, so output row r of a head reads source row
@@ -458,90 +465,56 @@ uint64_t perm_row(uint64_t r, int hd) {
     return h * hd + ((k & 1) ? hd / 2 + k / 2 : k / 2);
 }
 
-bool read_at(std::ifstream& in, uint64_t off, unsigned char* p, uint64_t n) {
-    in.seekg((std::streamoff)off);
-    in.read(reinterpret_cast<char*>(p), (std::streamsize)n);
-    return (uint64_t)in.gcount() == n;
-}
-
-// the tensor's bytes in model.bf order (make_sink / make_raw_sink, gguf_convert.h:115-229)
-bool emit(const GFile& g, const Sink& s, int hd, std::ostream& f) {
-    std::ifstream in(g.path, std::ios::binary);
-    if (!in) return false;
-    const GTensor& t = *s.src;
-    const uint64_t base = g.data_off + t.offset;
-    const auto [be, bb] = gblock(t.type);
-    {
-        if (s.raw) {  // quantized rows copied, q / k rows permuted
-            const uint64_t k = t.shape[0], n = t.shape[1], rb = k / be * bb;
-            vector<unsigned char> row((size_t)rb);
-            for (uint64_t j = 0; j < n; j++) {
-                if (!read_at(in, base + (s.permute ? perm_row(j, hd) : j) * rb, row.data(), rb)) return false;
-                f.write(reinterpret_cast<const char*>(row.data()), (std::streamsize)rb);
-            }
-            return (bool)f;
-        }
-        const uint64_t total = t.n_elem, in_dim = t.shape[0], out_dim = t.shape.size() > 1 ? t.shape[1] : 0;
-        vector<unsigned char> raw;
-        vector<float> tmp;
-        if (s.permute && !s.transpose) {  // a q / k bias (1-D)
-            raw.resize((size_t)t.nbytes);
-            if (!read_at(in, base, raw.data(), raw.size())) return false;
-            tmp.resize((size_t)total);
-            dequant(t.type, raw.data(), tmp.data(), total);
-            vector<float> o((size_t)total);
-            for (uint64_t i = 0; i < total; i++) o[i] = tmp[perm_row(i, hd)];
-            write_as(f, o.data(), total, s.dtype);
-            return (bool)f;
-        }
-        if (!s.transpose) {  // in order, ~4 MiB of source at a time
-            const uint64_t chunk = ((4u << 20) / bb) * be;
-            for (uint64_t done = 0; done < total;) {
-                const uint64_t n = std::min(chunk, total - done), bytes = n / be * bb;
-                raw.resize((size_t)bytes);
-                if (!read_at(in, base + done / be * bb, raw.data(), bytes)) return false;
-                tmp.resize((size_t)n);
-                dequant(t.type, raw.data(), tmp.data(), n);
-                write_as(f, tmp.data(), n, s.dtype);
-                done += n;
-            }
-            return (bool)f;
-        }
-        // [out][in] -> [in][out]: output tiles of `tile` input columns (<= 128 MiB of
-        // floats), each filled from whole-head runs of source rows (~8 MiB)
-        uint64_t tile = std::max<uint64_t>(1, (128u << 20) / (4 * out_dim));
-        tile = std::min(tile, in_dim);
-        uint64_t rb = (8u << 20) / (4 * in_dim) / (uint64_t)hd * (uint64_t)hd;
-        rb = std::min(std::max(rb, (uint64_t)hd), out_dim);
-        vector<float> dst;
-        for (uint64_t t0 = 0; t0 < in_dim; t0 += tile) {
-            const uint64_t t1 = std::min(in_dim, t0 + tile);
-            dst.assign((size_t)((t1 - t0) * out_dim), 0.0f);
-            for (uint64_t j0 = 0; j0 < out_dim; j0 += rb) {
-                const uint64_t j1 = std::min(out_dim, j0 + rb), n = (j1 - j0) * in_dim, bytes = n / be * bb;
-                raw.resize((size_t)bytes);
-                if (!read_at(in, base + (j0 * in_dim) / be * bb, raw.data(), bytes)) return false;
-                tmp.resize((size_t)n);
-                dequant(t.type, raw.data(), tmp.data(), n);
-                for (uint64_t j = j0; j < j1; j++) {
-                    const uint64_t r2 = s.permute ? perm_row(j, hd) : j;
-                    const float* srow = tmp.data() + (r2 - j0) * in_dim;
-                    for (uint64_t c = t0; c < t1; c++) dst[(size_t)((c - t0) * out_dim + j)] = srow[c];
-                }
-            }
-            write_as(f, dst.data(), dst.size(), s.dtype);
-        }
-        return (bool)f;
+bool dequant_known(uint32_t t) {
+    switch (t) {
+        case G_F32: case G_F16: case G_BF16: case G_Q8_0: case G_Q4_0: case G_Q4_1: case G_Q5_0: case G_Q5_1:
+        case G_Q4_K: case G_Q5_K: case G_Q6_K: return true;
+        default: return false;
     }
 }
 
-void put32(unsigned char* p, uint32_t v) {
-    for (int k = 0; k < 4; k++) p[k] = (unsigned char)(v >> (8 * k));
-}
-void put64(unsigned char* p, uint64_t v) {
-    for (int k = 0; k < 8; k++) p[k] = (unsigned char)(v >> (8 * k));
-}
-uint64_t up64(uint64_t v) { return (v + 63) / 64 * 64; }
+// The source file mapped read-only: every tensor's bytes are a pointer into it.
+class Mapped {
+public:
+    explicit Mapped(const string& path) {
+        fd_ = ::open(path.c_str(), O_RDONLY);
+        if (fd_ < 0) throw runtime_error("gguf: 打不开 " + path);
+        struct stat st;
+        if (fstat(fd_, &st) != 0) throw runtime_error("gguf: 打不开 " + path);
+        size_ = (uint64_t)st.st_size;
+        if (size_) {
+            void* p = mmap(nullptr, (size_t)size_, PROT_READ, MAP_PRIVATE, fd_, 0);
+            if (p == MAP_FAILED) throw runtime_error("gguf: 打不开 " + path);
+            base_ = static_cast<const unsigned char*>(p);
+        }
+    }
+    ~Mapped() {
+        if (base_) munmap(const_cast<unsigned char*>(base_), (size_t)size_);
+        if (fd_ >= 0) ::close(fd_);
+    }
+    Mapped(const Mapped&) = delete;
+    Mapped& operator=(const Mapped&) = delete;
+    const unsigned char* data() const { return base_; }
+    uint64_t size() const { return size_; }
+
+private:
+    int fd_ = -1;
+    const unsigned char* base_ = nullptr;
+    uint64_t size_ = 0;
+};
+
+// One tensor of the output: where its values come from and how they are laid out.
+//   raw        quantized 2-D blocks kept: source row j (or perm_row(j) for q / k) per row
+//   transposed a 2-D weight dequantized, GGUF's [out rows][in] written as [in][out]
+//   pairs      q / k: rows (or a bias's elements) back in adjacent RoPE pair order
+struct OutTensor {
+    string name;
+    const GTensor* src = nullptr;
+    uint8_t dtype = BF_F32;
+    vector<uint32_t> shape;
+    uint64_t bytes = 0;
+    bool raw = false, transposed = false, pairs = false;
+};
 
 uint64_t bf_tensor_bytes(uint8_t d, uint64_t elems) {
     if (d == BF_Q4K || d == BF_Q5K || d == BF_Q6K)
@@ -551,62 +524,122 @@ uint64_t bf_tensor_bytes(uint8_t d, uint64_t elems) {
     return eb ? elems * eb : ~0ull;
 }
 
-// write_bfile_stream (bfile.h:276-341): 64-byte header, 104-byte entries, data at
-// 64-byte aligned offsets after the table
-void write_bfile(const string& path, const GgufResult& r, const GFile& g, const vector<Sink>& ts) {
-    const uint64_t dir_bytes = ts.size() * 104, header = up64(64 + dir_bytes);
-    if (header > 0xFFFFFFFFull) throw runtime_error("bfile: 张量太多");
-    vector<uint64_t> offs(ts.size());
-    uint64_t cur = 0;
-    for (size_t i = 0; i < ts.size(); i++) {  // check_tensor_meta (bfile.h:258-273)
-        const Sink& s = ts[i];
-        if (s.name.empty() || s.name.size() > 63) throw runtime_error("bfile: 张量名长度必须 1..63: " + s.name);
-        if (s.shape.size() > 4) throw runtime_error("bfile: 维度超过 4: " + s.name);
-        if (s.dtype > BF_Q8_0) throw runtime_error("bfile: 不认识的 dtype: " + s.name);
-        uint64_t elems = 1;
-        for (uint32_t d : s.shape) elems *= d;
-        if (bf_tensor_bytes(s.dtype, elems) != s.nbytes) throw runtime_error("bfile: shape 与数据长度不符: " + s.name);
-        offs[i] = cur;
-        cur = up64(cur + s.nbytes);
+constexpr size_t kFlushBytes = 16u << 20;  // output buffered in pieces of about this size
+
+void flush_if(std::ostream& f, vector<unsigned char>& buf, bool all) {
+    if (buf.empty() || (!all && buf.size() < kFlushBytes)) return;
+    f.write(reinterpret_cast<const char*>(buf.data()), (std::streamsize)buf.size());
+    buf.clear();
+}
+
+// a tensor's bytes in model.bf order, read from the mapped source (bounds checked when
+// the conversion was planned)
+void write_tensor(const unsigned char* file, uint64_t data_off, const OutTensor& o, int hd, std::ostream& f) {
+    const GTensor& t = *o.src;
+    const unsigned char* src = file + data_off + t.offset;
+    const auto [be, bb] = gblock(t.type);
+    vector<unsigned char> buf;
+    buf.reserve(kFlushBytes + (1u << 20));
+    if (o.raw) {
+        const uint64_t rows = t.shape[1], row_bytes = t.shape[0] / be * bb;
+        for (uint64_t j = 0; j < rows; j++) {
+            const unsigned char* r = src + (o.pairs ? perm_row(j, hd) : j) * row_bytes;
+            buf.insert(buf.end(), r, r + row_bytes);
+            flush_if(f, buf, false);
+        }
+        flush_if(f, buf, true);
+        return;
     }
-    std::ofstream f(path, std::ios::binary | std::ios::trunc);
-    if (!f) throw runtime_error("bfile: 无法写入 " + path);
-    unsigned char head[64] = {};
-    memcpy(head, "JYAIBF", 6);
-    put64(head + 6, r.hidden);
-    put64(head + 14, r.layers);
-    head[22] = 1;  // mode
+    vector<float> vals;
+    if (!o.transposed) {
+        if (o.pairs) {  // a q / k bias: whole, then reordered
+            vector<float> v((size_t)t.n_elem);
+            dequant(t.type, src, v.data(), t.n_elem);
+            vals.resize(v.size());
+            for (uint64_t i = 0; i < t.n_elem; i++) vals[(size_t)i] = v[(size_t)perm_row(i, hd)];
+            encode_values(vals.data(), vals.size(), o.dtype, buf);
+            flush_if(f, buf, true);
+            return;
+        }
+        // in source order, a run of whole blocks at a time
+        const uint64_t run = std::max<uint64_t>(1, (1u << 20) / be) * be;
+        for (uint64_t e0 = 0; e0 < t.n_elem; e0 += run) {
+            const uint64_t n = std::min(run, t.n_elem - e0);
+            vals.resize((size_t)n);
+            dequant(t.type, src + e0 / be * bb, vals.data(), n);
+            encode_values(vals.data(), (size_t)n, o.dtype, buf);
+            flush_if(f, buf, false);
+        }
+        flush_if(f, buf, true);
+        return;
+    }
+    // transposed: output row c (input column c) holds every source row's element c.  The
+    // output goes out in panels of `width` input columns (whole quant blocks); a panel is
+    // filled by dequantizing, for each source row, only the blocks it covers.
+    const uint64_t in_dim = t.shape[0], out_dim = t.shape[1], row_bytes = in_dim / be * bb;
+    uint64_t width = (32u << 20) / (4 * std::max<uint64_t>(out_dim, 1)) / be * be;
+    width = std::min(std::max<uint64_t>(width, be), in_dim);
+    vector<float> panel, piece((size_t)width);
+    for (uint64_t c0 = 0; c0 < in_dim; c0 += width) {
+        const uint64_t w = std::min(width, in_dim - c0);
+        panel.resize((size_t)(w * out_dim));
+        for (uint64_t j = 0; j < out_dim; j++) {
+            const unsigned char* r = src + (o.pairs ? perm_row(j, hd) : j) * row_bytes + c0 / be * bb;
+            dequant(t.type, r, piece.data(), w);
+            for (uint64_t c = 0; c < w; c++) panel[(size_t)(c * out_dim + j)] = piece[(size_t)c];
+        }
+        encode_values(panel.data(), panel.size(), o.dtype, buf);
+        flush_if(f, buf, true);
+    }
+}
+
+void put_le(unsigned char* p, uint64_t v, int n) {
+    for (int k = 0; k < n; k++) p[k] = (unsigned char)(v >> (8 * k));
+}
+uint64_t align64(uint64_t v) { return (v + 63) & ~uint64_t(63); }
+
+// model.bf, bfile v2 (libs/model_libs/bfile.h:276-341): a 64-byte header, a 104-byte
+// entry per tensor, the data at 64-byte aligned offsets after the (aligned) table.
+// The tensor entries were checked when the conversion was planned.
+void write_model_bf(const string& path, const GgufResult& r, const Mapped& file, uint64_t data_off,
+                    const vector<OutTensor>& ts) {
+    const uint64_t table = align64(64 + 104 * (uint64_t)ts.size());
+    vector<unsigned char> head((size_t)table, 0);
+    memcpy(head.data(), "JYAIBF", 6);
+    put_le(&head[6], r.hidden, 8);
+    put_le(&head[14], r.layers, 8);
+    head[22] = 1;
     head[23] = (unsigned char)r.num_heads;
     head[24] = (unsigned char)r.num_kv_heads;
     head[25] = (unsigned char)r.head_dim;
-    put32(head + 26, r.intermediate);
-    put64(head + 30, r.vocab);
-    put32(head + 38, 2);
-    put32(head + 42, (uint32_t)ts.size());
-    put32(head + 46, (uint32_t)header);
-    put32(head + 50, 104);
-    f.write(reinterpret_cast<const char*>(head), 64);
+    put_le(&head[26], r.intermediate, 4);
+    put_le(&head[30], r.vocab, 8);
+    put_le(&head[38], 2, 4);
+    put_le(&head[42], ts.size(), 4);
+    put_le(&head[46], table, 4);
+    put_le(&head[50], 104, 4);
+    vector<uint64_t> at(ts.size());
+    uint64_t pos = 0;
     for (size_t i = 0; i < ts.size(); i++) {
-        unsigned char e[104] = {};
+        at[i] = pos;
+        pos = align64(pos + ts[i].bytes);
+        unsigned char* e = &head[64 + 104 * i];
         memcpy(e, ts[i].name.data(), ts[i].name.size());
         e[64] = ts[i].dtype;
         e[65] = (unsigned char)ts[i].shape.size();
-        for (size_t d = 0; d < ts[i].shape.size(); d++) put32(e + 68 + 4 * d, ts[i].shape[d]);
-        put64(e + 88, offs[i]);
-        put64(e + 96, ts[i].nbytes);
-        f.write(reinterpret_cast<const char*>(e), 104);
+        for (size_t d = 0; d < ts[i].shape.size(); d++) put_le(e + 68 + 4 * d, ts[i].shape[d], 4);
+        put_le(e + 88, at[i], 8);
+        put_le(e + 96, ts[i].bytes, 8);
     }
-    const vector<char> pad((size_t)(header - 64 - dir_bytes), 0);
-    f.write(pad.data(), (std::streamsize)pad.size());
-    uint64_t written = 0;
+    std::ofstream f(path, std::ios::binary | std::ios::trunc);
+    if (!f) throw runtime_error("bfile: 无法写入 " + path);
+    f.write(reinterpret_cast<const char*>(head.data()), (std::streamsize)head.size());
+    uint64_t done = 0;
+    static const char zeros[64] = {};
     for (size_t i = 0; i < ts.size(); i++) {
-        if (offs[i] > written) {
-            const vector<char> z((size_t)(offs[i] - written), 0);
-            f.write(z.data(), (std::streamsize)z.size());
-            written = offs[i];
-        }
-        if (!emit(g, ts[i], r.head_dim, f)) throw runtime_error("bfile: 写张量失败: " + ts[i].name);
-        written += ts[i].nbytes;
+        f.write(zeros, (std::streamsize)(at[i] - done));  // < 64 bytes of alignment
+        write_tensor(file.data(), data_off, ts[i], r.head_dim, f);
+        done = at[i] + ts[i].bytes;
     }
     f.flush();
     if (!f) throw runtime_error("bfile: 写入失败 " + path);
@@ -704,60 +737,52 @@ void json_write(string& out, const JValue& v, int level) {
     }
 }
 
-// json_file::SetJsonWay + WriteJsonKey (libs/json_libs/json.h:20-47, :146-176, :240-313)
-// for the flat keys the converter writes: an existing file is loaded and updated,
-// a missing or blank one starts empty, an unreadable one is left alone (every
-// write is refused); the whole document is rewritten after each key.
-class InfoFile {
-public:
-    explicit InfoFile(const string& path) : path_(path) {
-        string text;
-        JValue v;
-        if (read_file(resolve_path(path_), text) && json_parse(text, v)) {
-            root_ = std::move(v);  // kept as parsed, whatever its kind
-            ok_ = true;
-        } else if (text.find_first_not_of(" \t\r\n") == string::npos) {
-            root_.kind = JValue::Object;  // missing or blank: a new object
-            ok_ = true;
-        }
+// model_info.json as json_file::SetJsonWay + WriteJsonKey leave it (libs/json_libs/
+// json.h:20-47, :146-176, :240-313) after a run of flat key writes: an existing document
+// keeps its other members and their order (a key already present is updated in place, a
+// new one appended); a missing or blank file starts as an empty object; a file that does
+// not parse is left as it is.  Values are typed as make_value (json_parser.h:291-320)
+// types them.
+JValue info_value(const string& value) {
+    JValue v;
+    if (json_number(value)) {
+        v.kind = JValue::Number;
+        v.raw = value;
+    } else if (value == "true" || value == "false") {
+        v.kind = JValue::Bool;
+        v.raw = value;
+    } else if (value == "null") {
+        v.kind = JValue::Null;
+    } else if (value.empty() || (value[0] != '{' && value[0] != '[') || !json_parse(value, v)) {
+        v = JValue();
+        v.kind = JValue::String;
+        v.text = value;
     }
-    void set(const string& key, const string& value) {
-        if (!ok_) return;
-        JValue v;  // make_value (json_parser.h:291-320)
-        if (json_number(value)) {
-            v.kind = JValue::Number;
-            v.raw = value;
-        } else if (value == "true" || value == "false") {
-            v.kind = JValue::Bool;
-            v.raw = value;
-        } else if (value == "null") {
-            v.kind = JValue::Null;
-        } else if (!value.empty() && (value[0] == '{' || value[0] == '[') && json_parse(value, v)) {
-        } else {
-            v = JValue();
-            v.kind = JValue::String;
-            v.text = value;
-        }
-        bool found = false;
-        for (auto& m : root_.members)
-            if (m.first == key) {
-                m.second = v;
-                found = true;
-                break;
-            }
-        if (!found) root_.members.emplace_back(key, v);
-        string out;
-        json_write(out, root_, 0);
-        out.push_back('\n');
-        std::ofstream f(resolve_path(path_), std::ios::binary);
-        f.write(out.data(), (std::streamsize)out.size());
-    }
+    return v;
+}
 
-private:
-    string path_;
-    JValue root_;
-    bool ok_ = false;
-};
+void merge_info(const string& path, const vector<std::pair<string, string>>& entries) {
+    const string file = resolve_path(path);
+    string text;
+    JValue doc;
+    if (!(read_file(file, text) && json_parse(text, doc))) {
+        if (text.find_first_not_of(" \t\r\n") != string::npos) return;  // unparsable: untouched
+        doc = JValue();
+        doc.kind = JValue::Object;
+    }
+    for (const auto& [key, value] : entries) {
+        auto it = std::find_if(doc.members.begin(), doc.members.end(), [&](const auto& m) { return m.first == key; });
+        if (it != doc.members.end())
+            it->second = info_value(value);
+        else
+            doc.members.emplace_back(key, info_value(value));
+    }
+    string out;
+    json_write(out, doc, 0);
+    out.push_back('\n');
+    std::ofstream f(file, std::ios::binary | std::ios::trunc);
+    f.write(out.data(), (std::streamsize)out.size());
+}
 
 // ---------------------------------------------------------------- names
 
@@ -816,211 +841,253 @@ const char* dtype_name(uint8_t d) {
     }
 }
 
-string jesc(const string& s) {  // vocab.json keys: only '"' and '\\' escaped (gguf_convert.h:56-65)
-    string o;
-    for (const char c : s) {
-        if (c == '"')
-            o += "\\\"";
-        else if (c == '\\')
-            o += "\\\\";
-        else
-            o += c;
-    }
-    return o;
-}
-
-long long meta_int(const GFile& g, const string& k, long long d) {
-    const Meta* m = g.meta(k);
-    return m ? m->as_int(d) : d;
-}
-
-double meta_float(const GFile& g, const string& k, double d) {
-    const Meta* m = g.meta(k);
-    return m ? m->as_float(d) : d;
-}
-
 }  // namespace
 
-// ggufc::convert (libs/gguf_libs/gguf_convert.h:260-421)
-GgufResult gguf_convert(const std::string& src, const std::string& out_dir, uint8_t out_dtype, bool quant,
-                        bool verbose) {
-    const GFile g = gguf_open(src);
-    GgufResult r;
-    const Meta* am = g.meta("general.architecture");
-    r.arch = am && !am->s.empty() ? am->s : string("llama");
-    const string pre = r.arch + ".";
-    if (verbose) printf("GGUF v%u  %s  tensors %zu\n", g.version, r.arch.c_str(), g.tensors.size());
+namespace {
 
-    long long hidden = meta_int(g, pre + "embedding_length", 0), nl = meta_int(g, pre + "block_count", 0);
-    const long long inter = meta_int(g, pre + "feed_forward_length", 0), nh = meta_int(g, pre + "attention.head_count", 0);
-    const long long nkv = meta_int(g, pre + "attention.head_count_kv", nh);
-    long long hd = meta_int(g, pre + "attention.key_length", 0);
-    const double rope = meta_float(g, pre + "rope.freq_base", 10000.0);
-    const long long ctx = meta_int(g, pre + "context_length", 1024);
+// ---------------------------------------------------------------- the plan
 
-    const GTensor* emb = g.find("token_embd.weight");
+// Hyper-parameters from the header (llama.cpp's `<arch>.` keys), with the embedding's
+// shape, the token list and the block names standing in for missing ones, and the
+// checks model_info.json's fields need (gguf_convert.h:260-421 gives the texts)
+void read_hyper(const GFile& g, GgufResult& r) {
+    auto num = [&](const string& key, long long fallback) {
+        const Meta* m = g.meta(r.arch + "." + key);
+        return m ? m->as_int(fallback) : fallback;
+    };
+    long long hidden = num("embedding_length", 0), blocks = num("block_count", 0);
+    const long long ffn = num("feed_forward_length", 0), heads = num("attention.head_count", 0);
+    const long long kv_heads = num("attention.head_count_kv", heads);
+    long long head_dim = num("attention.key_length", 0);
+    const Meta* fb = g.meta(r.arch + ".rope.freq_base");
+    const double theta = fb ? fb->as_float(10000.0) : 10000.0;
+    const long long ctx = num("context_length", 1024);
+
     long long vocab = 0;
-    if (emb && emb->shape.size() >= 2) {
-        if (hidden <= 0) hidden = (long long)emb->shape[0];
-        vocab = (long long)emb->shape[1];
+    if (const GTensor* e = g.find("token_embd.weight"); e && e->shape.size() >= 2) {
+        if (hidden <= 0) hidden = (long long)e->shape[0];
+        vocab = (long long)e->shape[1];
     }
     if (vocab <= 0)
         if (const Meta* tk = g.meta("tokenizer.ggml.tokens")) vocab = (long long)tk->n;
-    if (nl <= 0)
+    if (blocks <= 0)
         for (const GTensor& t : g.tensors)
-            if (t.name.size() > 4 && t.name.compare(0, 4, "blk.") == 0) nl = std::max(nl, atoll(t.name.c_str() + 4) + 1);
-    if (hidden <= 0 || vocab <= 0 || nl <= 0 || inter <= 0)
-        throw runtime_error("gguf: 超参不全（hidden / layers / intermediate / vocab）");
-    if (nh <= 0) throw runtime_error("gguf: 没有 attention.head_count");
-    if (hd <= 0) hd = hidden / nh;
-    if (nh > 255 || nkv > 255 || hd > 255) throw runtime_error("gguf: num_heads / num_kv_heads / head_dim 必须落在 1..255");
-    if (nkv <= 0 || nh % nkv != 0) throw runtime_error("gguf: num_heads 必须能被 num_kv_heads 整除");
-    if (hidden != nh * hd) printf("[警告] hidden(%lld) != num_heads*head_dim(%lld)\n", hidden, nh * hd);
-    for (const GTensor& t : g.tensors)
-        if (t.shape.size() == 2 && t.shape[0] % gblock(t.type).first != 0)
-            throw runtime_error("gguf: " + t.name + " 的行长不是量化块的整数倍");
+            if (t.name.rfind("blk.", 0) == 0 && t.name.size() > 4) blocks = std::max(blocks, atoll(t.name.c_str() + 4) + 1);
 
-    // the sinks, in GGUF tensor order
-    auto dense = [&](const GTensor& t, const string& name, bool tr, bool pm, uint8_t dt) {
-        Sink s;
-        s.name = name;
-        s.dtype = dt;
-        s.src = &t;
-        s.transpose = tr;
-        s.permute = pm;
+    if (hidden <= 0 || vocab <= 0 || blocks <= 0 || ffn <= 0)
+        throw runtime_error("gguf: 超参不全（hidden / layers / intermediate / vocab）");
+    if (heads <= 0) throw runtime_error("gguf: 没有 attention.head_count");
+    if (head_dim <= 0) head_dim = hidden / heads;
+    if (heads > 255 || kv_heads > 255 || head_dim > 255)
+        throw runtime_error("gguf: num_heads / num_kv_heads / head_dim 必须落在 1..255");
+    if (kv_heads <= 0 || heads % kv_heads) throw runtime_error("gguf: num_heads 必须能被 num_kv_heads 整除");
+    if (hidden != heads * head_dim) printf("[警告] hidden(%lld) != num_heads*head_dim(%lld)\n", hidden, heads * head_dim);
+
+    r.hidden = (uint64_t)hidden;
+    r.layers = (uint64_t)blocks;
+    r.num_heads = (int)(uint8_t)heads;
+    r.num_kv_heads = (int)(uint8_t)kv_heads;
+    r.head_dim = (int)(uint8_t)head_dim;
+    r.intermediate = (uint32_t)ffn;
+    r.vocab = (uint64_t)vocab;
+    r.rope_theta = (long long)std::fabs(theta);
+    r.max_position = ctx;
+}
+
+// every output tensor, in GGUF tensor order, then the tied head when the file has no
+// output.weight; the counters of the report
+vector<OutTensor> plan_tensors(const GFile& g, uint8_t out_dtype, bool quant, GgufResult& r,
+                               vector<string>& skipped) {
+    for (const GTensor& t : g.tensors)
+        if (t.shape.size() == 2 && t.shape[0] % gblock(t.type).first)
+            throw runtime_error("gguf: " + t.name + " 的行长不是量化块的整数倍");
+    vector<OutTensor> out;
+    auto add_dense = [&](const GTensor& t, const string& name, bool transposed, bool pairs, uint8_t dtype) {
+        OutTensor o;
+        o.name = name;
+        o.src = &t;
+        o.dtype = dtype;
+        o.transposed = transposed;
+        o.pairs = pairs;
         if (t.shape.size() == 1)
-            s.shape = {(uint32_t)t.shape[0]};
-        else if (tr)
-            s.shape = {(uint32_t)t.shape[0], (uint32_t)t.shape[1]};
-        else
-            s.shape = {(uint32_t)(t.shape.size() > 1 ? t.shape[1] : 0), (uint32_t)t.shape[0]};
-        uint64_t e = 1;
-        for (uint32_t d : s.shape) e *= d;
-        s.nbytes = e * bf_elem_bytes(dt);
-        return s;
+            o.shape = {(uint32_t)t.shape[0]};
+        else if (transposed)  // [in][out]
+            o.shape = {(uint32_t)t.shape[0], (uint32_t)t.shape[1]};
+        else  // the embedding: [vocab][hidden]
+            o.shape = {(uint32_t)(t.shape.size() > 1 ? t.shape[1] : 0), (uint32_t)t.shape[0]};
+        o.bytes = bf_elem_bytes(dtype);
+        for (uint32_t d : o.shape) o.bytes *= d;
+        out.push_back(std::move(o));
+        if (transposed) r.transposed++;
     };
-    vector<Sink> sinks;
-    vector<string> skipped;
     for (const GTensor& t : g.tensors) {
         const string hf = hf_name(t.name);
         if (hf.empty()) {
             skipped.push_back(t.name);
             continue;
         }
-        const bool is_emb = t.name == "token_embd.weight", tr = t.shape.size() == 2 && !is_emb;
-        const bool pm = t.name.find(".attn_q.") != string::npos || t.name.find(".attn_k.") != string::npos;
-        const int qc = t.shape.size() == 2 ? quant_code(t.type) : -1;
-        if (quant && qc >= 0) {  // make_raw_sink (gguf_convert.h:201-229)
-            Sink s;
-            s.name = hf;
-            s.dtype = (uint8_t)qc;
-            s.src = &t;
-            s.raw = true;
-            s.permute = pm;
-            s.shape = {(uint32_t)t.shape[1], (uint32_t)t.shape[0]};
-            s.nbytes = t.shape[1] * (t.shape[0] / gblock(t.type).first) * gblock(t.type).second;
-            sinks.push_back(s);
+        const bool two_d = t.shape.size() == 2, embedding = t.name == "token_embd.weight";
+        const bool pairs = t.name.find(".attn_q.") != string::npos || t.name.find(".attn_k.") != string::npos;
+        const int code = two_d ? quant_code(t.type) : -1;
+        if (quant && code >= 0) {
+            OutTensor o;
+            o.name = hf;
+            o.src = &t;
+            o.dtype = (uint8_t)code;
+            o.raw = true;
+            o.pairs = pairs;
+            o.shape = {(uint32_t)t.shape[1], (uint32_t)t.shape[0]};
+            o.bytes = t.nbytes;
+            out.push_back(std::move(o));
             r.quant++;
         } else {
-            sinks.push_back(dense(t, hf, tr, pm, t.shape.size() == 2 ? out_dtype : (uint8_t)BF_F32));
-            if (tr) r.transposed++;
+            add_dense(t, hf, two_d && !embedding, pairs, two_d ? out_dtype : (uint8_t)BF_F32);
         }
-        if (pm) r.permuted++;
+        if (pairs) r.permuted++;
     }
     if (!g.find("output.weight")) {
-        if (!emb) throw runtime_error("gguf: 既没有 output.weight 也没有 token_embd.weight");
+        const GTensor* e = g.find("token_embd.weight");
+        if (!e) throw runtime_error("gguf: 既没有 output.weight 也没有 token_embd.weight");
         r.tied_lm_head = true;
-        if (!(quant && quant_code(emb->type) >= 0)) {
-            sinks.push_back(dense(*emb, "lm_head.weight", true, false, out_dtype));
-            r.transposed++;
-        }
+        if (!(quant && quant_code(e->type) >= 0)) add_dense(*e, "lm_head.weight", true, false, out_dtype);
     }
+    return out;
+}
+
+// what would stop model.bf from being written, found before anything is: the entry
+// checks of bfile's writer (check_tensor_meta, bfile.h:258-273), then per tensor in output
+// order a source range past the end of the file or a type with no dequantization
+void check_tensors(const GFile& g, const vector<OutTensor>& ts) {
+    if (align64(64 + 104 * (uint64_t)ts.size()) > 0xFFFFFFFFull) throw runtime_error("bfile: 张量太多");
+    for (const OutTensor& o : ts) {
+        if (o.name.empty() || o.name.size() > 63) throw runtime_error("bfile: 张量名长度必须 1..63: " + o.name);
+        if (o.shape.size() > 4) throw runtime_error("bfile: 维度超过 4: " + o.name);
+        if (o.dtype > BF_Q8_0) throw runtime_error("bfile: 不认识的 dtype: " + o.name);
+        uint64_t elems = 1;
+        for (uint32_t d : o.shape) elems *= d;
+        if (bf_tensor_bytes(o.dtype, elems) != o.bytes) throw runtime_error("bfile: shape 与数据长度不符: " + o.name);
+    }
+    for (const OutTensor& o : ts) {
+        const uint64_t start = g.data_off + o.src->offset;
+        if (start > g.file_size || o.src->nbytes > g.file_size - start)
+            throw runtime_error("bfile: 写张量失败: " + o.name);
+        if (!o.raw && !dequant_known(o.src->type))
+            throw runtime_error(string("gguf: 还没写这种量化的反量化 ") + gtype_name(o.src->type));
+    }
+}
+
+// model_info.json's keys, in the order jieyu's converter writes them
+vector<std::pair<string, string>> info_entries(const GFile& g, const GgufResult& r, const string& src,
+                                               uint8_t out_dtype, bool quant) {
+    vector<std::pair<string, string>> e = {
+        {"hidden_size", std::to_string(r.hidden)},
+        {"layer_count", std::to_string(r.layers)},
+        {"mode", "1"},
+        {"num_heads", std::to_string(r.num_heads)},
+        {"num_kv_heads", std::to_string(r.num_kv_heads)},
+        {"head_dim", std::to_string(r.head_dim)},
+        {"intermediate_size", std::to_string(r.intermediate)},
+        {"vocab_size", std::to_string(r.vocab)},
+        {"rope_theta", std::to_string(r.rope_theta)},
+        {"max_position_embeddings", std::to_string(r.max_position)},
+        {"dtype", quant ? string("quant") : string(dtype_name(out_dtype))},
+        {"add_bos_token", "0"},
+        {"rope_style", "adjacent_after_permute"},
+        {"source_arch", r.arch},
+        {"source_file", fs::path(src).filename().string()},
+    };
+    if (const Meta* nm = g.meta("general.name"); nm && !nm->s.empty()) e.emplace_back("source_name", nm->s);
+    const Meta* tk = g.meta("tokenizer.ggml.tokens");
+    if (!tk) return e;
+    const std::set<string> vocab(tk->strs.begin(), tk->strs.end());
+    // the chat markers: the first of each list the vocabulary holds
+    const std::pair<const char*, vector<const char*>> markers[] = {
+        {"message_start", {"<|im_start|>", "<|start_header_id|>"}},
+        {"message_end", {"<|im_end|>", "<|eot_id|>", "<|end_of_turn|>"}},
+        {"text_end", {"<|endoftext|>", "<|end_of_text|>", "</s>"}},
+    };
+    for (const auto& [key, cands] : markers)
+        for (const char* c : cands)
+            if (vocab.count(c)) {
+                e.emplace_back(key, c);
+                break;
+            }
+    // DeepSeek's template: markers spelled with U+FF5C (fullwidth vertical line) and
+    // U+2581 (lower one eighth block)
+    const string bar = "\xEF\xBD\x9C", low = "\xE2\x96\x81";
+    auto marker = [&](const string& inner) { return "<" + bar + inner + bar + ">"; };
+    const string user = marker("User"), assistant = marker("Assistant");
+    if (vocab.count(user) && vocab.count(assistant)) {
+        e.emplace_back("template", "deepseek");
+        e.emplace_back("bos_text", marker("begin" + low + "of" + low + "sentence"));
+        e.emplace_back("user_start", user);
+        e.emplace_back("assistant_start", assistant);
+        e.emplace_back("turn_end", marker("end" + low + "of" + low + "sentence"));
+    }
+    return e;
+}
+
+}  // namespace
+
+// GGUF file -> model directory, as jieyu's converter (ggufc::convert,
+// libs/gguf_libs/gguf_convert.h:260-421) leaves it.  Everything that can fail is checked
+// before the first file is written, so a failed conversion writes nothing.
+GgufResult gguf_convert(const std::string& src, const std::string& out_dir, uint8_t out_dtype, bool quant,
+                        bool verbose) {
+    const GFile g = gguf_open(src);
+    GgufResult r;
+    const Meta* arch = g.meta("general.architecture");
+    r.arch = arch && !arch->s.empty() ? arch->s : string("llama");
+    if (verbose) printf("GGUF v%u  %s  tensors %zu\n", g.version, r.arch.c_str(), g.tensors.size());
+    read_hyper(g, r);
+    vector<string> skipped;
+    const vector<OutTensor> tensors = plan_tensors(g, out_dtype, quant, r, skipped);
     if (verbose && !skipped.empty()) {
         printf("  skipped %zu unknown tensors:", skipped.size());
         for (size_t i = 0; i < skipped.size() && i < 6; i++) printf(" %s", skipped[i].c_str());
         printf(skipped.size() > 6 ? " ...\n" : "\n");
     }
+    check_tensors(g, tensors);
+    const Meta* tokens = g.meta("tokenizer.ggml.tokens");
+    if (!tokens || tokens->strs.empty()) throw runtime_error("gguf: 没有 tokenizer.ggml.tokens，抽不出词表");
+    r.eos_id = (int)(g.meta("tokenizer.ggml.eos_token_id") ? g.meta("tokenizer.ggml.eos_token_id")->as_int(-1) : -1);
+    if (r.eos_id < 0)
+        r.eos_id = (int)(g.meta("tokenizer.ggml.bos_token_id") ? g.meta("tokenizer.ggml.bos_token_id")->as_int(-1) : -1);
 
-    r.hidden = (uint64_t)hidden;
-    r.layers = (uint64_t)nl;
-    r.num_heads = (int)(uint8_t)nh;
-    r.num_kv_heads = (int)(uint8_t)nkv;
-    r.head_dim = (int)(uint8_t)hd;
-    r.intermediate = (uint32_t)inter;
-    r.vocab = (uint64_t)vocab;
-    r.rope_theta = (long long)(rope < 0 ? -rope : rope);
-    r.max_position = ctx;
-
+    // the files
     fs::create_directories(out_dir);
-    const string bf = (fs::path(out_dir) / "model.bf").string();
-    write_bfile(bf, r, g, sinks);
-    r.tensor_count = sinks.size();
-    r.file_size = fs::file_size(bf);
-
+    const fs::path dir(out_dir);
     {
-        InfoFile info((fs::path(out_dir) / "model_info.json").string());
-        info.set("hidden_size", std::to_string(r.hidden));
-        info.set("layer_count", std::to_string(r.layers));
-        info.set("mode", "1");
-        info.set("num_heads", std::to_string(r.num_heads));
-        info.set("num_kv_heads", std::to_string(r.num_kv_heads));
-        info.set("head_dim", std::to_string(r.head_dim));
-        info.set("intermediate_size", std::to_string(r.intermediate));
-        info.set("vocab_size", std::to_string(r.vocab));
-        info.set("rope_theta", std::to_string(r.rope_theta));
-        info.set("max_position_embeddings", std::to_string(r.max_position));
-        info.set("dtype", quant ? string("quant") : string(dtype_name(out_dtype)));
-        info.set("add_bos_token", "0");
-        info.set("rope_style", "adjacent_after_permute");
-        info.set("source_arch", r.arch);
-        info.set("source_file", fs::path(src).filename().string());
-        if (const Meta* nm = g.meta("general.name"))
-            if (!nm->s.empty()) info.set("source_name", nm->s);
-        if (const Meta* tk = g.meta("tokenizer.ggml.tokens")) {
-            auto has = [&](const string& s) { return std::find(tk->strs.begin(), tk->strs.end(), s) != tk->strs.end(); };
-            auto pick = [&](const char* key, std::initializer_list<const char*> cands) {
-                for (const char* c : cands)
-                    if (has(c)) {
-                        info.set(key, c);
-                        return;
-                    }
-            };
-            pick("message_start", {"<|im_start|>", "<|start_header_id|>"});
-            pick("message_end", {"<|im_end|>", "<|eot_id|>", "<|end_of_turn|>"});
-            pick("text_end", {"<|endoftext|>", "<|end_of_text|>", "</s>"});
-            // DeepSeek's markers use U+FF5C (fullwidth vertical line) and U+2581 (lower one eighth block)
-            const string bar = "\xEF\xBD\x9C", sp = "\xE2\x96\x81";
-            const string user = "<" + bar + "User" + bar + ">", asst = "<" + bar + "Assistant" + bar + ">";
-            if (has(user) && has(asst)) {
-                info.set("template", "deepseek");
-                info.set("bos_text", "<" + bar + "begin" + sp + "of" + sp + "sentence" + bar + ">");
-                info.set("user_start", user);
-                info.set("assistant_start", asst);
-                info.set("turn_end", "<" + bar + "end" + sp + "of" + sp + "sentence" + bar + ">");
-            }
+        const Mapped file(src);
+        write_model_bf((dir / "model.bf").string(), r, file, g.data_off, tensors);
+    }
+    r.tensor_count = tensors.size();
+    r.file_size = fs::file_size(dir / "model.bf");
+    merge_info((dir / "model_info.json").string(), info_entries(g, r, src, out_dtype, quant));
+
+    // vocab.json: {"piece": id, ...} one per line, only '"' and '\\' escaped;
+    // merges.txt: the version line, then the merge rules (gguf_convert.h:231-258)
+    string vocab = "{\n";
+    for (size_t i = 0; i < tokens->strs.size(); i++) {
+        if (i) vocab += ",\n";
+        vocab += "  \"";
+        for (const char c : tokens->strs[i]) {
+            if (c == '"' || c == '\\') vocab.push_back('\\');
+            vocab.push_back(c);
         }
+        vocab += "\": " + std::to_string(i);
     }
-
-    // write_tokenizer (gguf_convert.h:231-258)
-    const Meta* tk = g.meta("tokenizer.ggml.tokens");
-    if (!tk || tk->strs.empty()) throw runtime_error("gguf: 没有 tokenizer.ggml.tokens，抽不出词表");
-    r.eos_id = (int)meta_int(g, "tokenizer.ggml.eos_token_id", -1);
-    if (r.eos_id < 0) r.eos_id = (int)meta_int(g, "tokenizer.ggml.bos_token_id", -1);
-    {
-        std::ofstream v((fs::path(out_dir) / "vocab.json").string(), std::ios::binary | std::ios::trunc);
-        if (!v) throw runtime_error("gguf: 写不了 vocab.json");
-        v << "{\n";
-        for (size_t i = 0; i < tk->strs.size(); i++) v << (i ? ",\n" : "") << "  \"" << jesc(tk->strs[i]) << "\": " << i;
-        v << "\n}\n";
+    vocab += "\n}\n";
+    string merges = "#version: 0.2\n";
+    if (const Meta* mg = g.meta("tokenizer.ggml.merges"))
+        for (const string& m : mg->strs) merges += m + "\n";
+    for (const auto& [name, text] : {std::pair<const char*, const string*>{"vocab.json", &vocab},
+                                     std::pair<const char*, const string*>{"merges.txt", &merges}}) {
+        std::ofstream f((dir / name).string(), std::ios::binary | std::ios::trunc);
+        if (!f) throw runtime_error(string("gguf: 写不了 ") + name);
+        f.write(text->data(), (std::streamsize)text->size());
     }
-    {
-        std::ofstream m((fs::path(out_dir) / "merges.txt").string(), std::ios::binary | std::ios::trunc);
-        if (!m) throw runtime_error("gguf: 写不了 merges.txt");
-        m << "#version: 0.2\n";
-        if (const Meta* mg = g.meta("tokenizer.ggml.merges"))
-            for (const string& s : mg->strs) m << s << "\n";
-    }
-    if (verbose) printf("  vocab %zu tokens, eos=%d\n", tk->strs.size(), r.eos_id);
+    if (verbose) printf("  vocab %zu tokens, eos=%d\n", tokens->strs.size(), r.eos_id);
     return r;
 }
 

@@ -4,7 +4,8 @@
 The GGUF inputs are rebuilt from tests/golden/gguf_models.py; tests/golden/gguf.json
 holds, per case, what the reference converter wrote (sha256 and size of model.bf,
 model_info.json, vocab.json, merges.txt), its report, or its error text
-(make_gguf_golden.py).  Where oracle/_ref is built the reference also runs on the
+(make_gguf_golden.py).  A failed conversion here writes no file at all (the reference
+may leave the files it wrote before the failure; only its error text is compared).  Where oracle/_ref is built the reference also runs on the
 same files here and the outputs are compared byte for byte.  CPU only: the
 converter is host code.
 """
@@ -76,7 +77,10 @@ def test_errors_match_reference(tmp_path, gold, name):
     want = gold["errors"][name]
     assert rc == want["rc"]
     assert err == want["error"]
-    assert digest(out) == want["files"]  # what was written before the failure, byte for byte
+    if rc == 0:
+        assert digest(out) == want["files"]
+    else:  # everything is checked before the first file is written: a failure leaves nothing
+        assert digest(out) == {}
 
 
 def test_converted_model_binds(tmp_path):
