@@ -62,7 +62,9 @@ JYHIP_API void jyhip_model_free(jyhip_model* model);
  *                          softmax sum and p.v accumulated per slice and merged; prompt
  *                          rows in the same arithmetic, one workgroup per kv head and row;
  *   JYHIP_MODE_SPLIT_MV    decode Q8_0 matvecs with each row's dot split across waves and
- *                          the RMSNorm scale applied after the dot (linearity);
+ *                          the RMSNorm scale applied after the dot (linearity); opt-in: it
+ *                          measured slower than the exact matvec (8B shape after 1024
+ *                          tokens: 419 -> 358 tokens/s), so JYHIP_MODE_FAST leaves it out;
  *   JYHIP_MODE_MFMA_PREFILL Q8_0 prompt GEMMs (m > 1) on the matrix cores: each activation
  *                          row scaled by a power of two and split into fp16 high + low parts
  *                          (22 significant bits), int8 weights exact in fp16, one fp32 MFMA
@@ -75,12 +77,13 @@ JYHIP_API void jyhip_model_free(jyhip_model* model);
 #define JYHIP_MODE_SPLIT_ATTN 1
 #define JYHIP_MODE_SPLIT_MV 2
 #define JYHIP_MODE_MFMA_PREFILL 4
-#define JYHIP_MODE_FAST (JYHIP_MODE_SPLIT_ATTN | JYHIP_MODE_SPLIT_MV | JYHIP_MODE_MFMA_PREFILL)
+#define JYHIP_MODE_FAST (JYHIP_MODE_SPLIT_ATTN | JYHIP_MODE_MFMA_PREFILL)
 /* With both split bits: each decode row of every layer (and, in a session's greedy step, the
  * head) as one persistent kernel whose workgroups hand activations to each other through
  * grid barriers, instead of about six kernels per layer.  Same arithmetic as the split
  * forms; opt-in (measured slower than the separate kernels at the benchmark shapes). */
 #define JYHIP_MODE_PERSIST 8
+#define JYHIP_MODE_ALL (JYHIP_MODE_SPLIT_ATTN | JYHIP_MODE_SPLIT_MV | JYHIP_MODE_MFMA_PREFILL | JYHIP_MODE_PERSIST)
 /* Set the mode (a combination of the bits above) for later calls on the model; sessions
  * capture their decode graphs again after a change.  Returns 0 / -1. */
 JYHIP_API int jyhip_model_set_mode(jyhip_model* model, int mode);

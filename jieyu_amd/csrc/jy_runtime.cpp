@@ -1476,7 +1476,7 @@ JYHIP_API size_t jyhip_model_weight_bytes(const jyhip_model* m) { return m ? m->
 JYHIP_API int jyhip_model_set_mode(jyhip_model* m, int mode) {
     return guarded([&]() {
         if (!m) fail("model is NULL");
-        if (mode & ~(JYHIP_MODE_FAST | JYHIP_MODE_PERSIST)) fail("unknown mode bits");
+        if (mode & ~JYHIP_MODE_ALL) fail("unknown mode bits");
         if (mode & JYHIP_MODE_MFMA_PREFILL) {
             CK(hipSetDevice(m->device));
             build_mfma(m);
@@ -1767,7 +1767,7 @@ JYHIP_API int jyhip_q8_matvec(jyhip_q8mat* q, const float* x, float* y) {
 JYHIP_API int jyhip_q8_set_mode(jyhip_q8mat* q, int mode) {
     return guarded([&]() {
         if (!q) fail("matrix is NULL");
-        if (mode & ~JYHIP_MODE_FAST) fail("unknown mode bits");
+        if (mode & ~(JYHIP_MODE_ALL & ~JYHIP_MODE_PERSIST)) fail("unknown mode bits");
         if ((mode & JYHIP_MODE_MFMA_PREFILL) && q->mcopies.empty()) {
             for (const Q8Dev& d : q->copies) q->mcopies.push_back(mfma_copy(q->mowned, d, q->stream));
             CK(hipStreamSynchronize(q->stream));

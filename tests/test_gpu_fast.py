@@ -130,7 +130,7 @@ def test_mfma_gemm_within_tolerance(jy, oracle_lib, m, rows, cols):
         assert np.array_equal(tiles.view(np.uint32), ref.view(np.uint32))
 
 
-MODES = {"SPLIT_ATTN": 1, "SPLIT_MV": 2, "MFMA_PREFILL": 4, "FAST": 7, "PERSIST": 7 | 8}
+MODES = {"SPLIT_ATTN": 1, "SPLIT_MV": 2, "MFMA_PREFILL": 4, "FAST": 5, "ALL": 7, "PERSIST": 7 | 8}
 
 
 @pytest.mark.parametrize("mode_name", list(MODES))
@@ -296,7 +296,7 @@ def test_mode_switch_recaptures(jy, oracle_lib):
     g = jy.GpuModel(d, 64)
     ss = g.session(prompt, 30)
     ss.step(5)
-    g.mode = jy.MODE_FAST | jy.MODE_PERSIST
+    g.mode = jy.MODE_SPLIT_ATTN | jy.MODE_SPLIT_MV | jy.MODE_PERSIST
     ss.step(10)
     g.mode = jy.MODE_EXACT
     ss.step(30)

@@ -4,11 +4,20 @@
   GEMM tiles) and Qwen2.5-7B shapes equal the ids jieyu's own decode loop produced for the
   same seeded models and prompts (tests/golden/fullsize.json, written by
   tests/golden/make_fullsize_golden.py from the compiled reference): in the exact mode
-  every id; in the fast mode every id up to a near tie, where the token the fast mode
-  picked must score within NEAR_TIE * max|logit| of the reference's pick by the exact
-  logits of that step (the fast mode's logits differ from the exact ones by its rounding,
-  about 1e-3 of max|logit| after 32 layers, so a closer tie may go either way; the ids
-  after a tie follow a different prefix and are not compared).
+  every id; in the fast mode every id up to a near tie.  At a tie the fast mode's logits of
+  that step (same prefix) must be within LOGIT_TOL * max|logit| (3e-2) of the exact ones, and the
+  exact-logit gap between the two picks no larger than twice their largest difference: the
+  flip is then what the measured rounding explains.  (These random-init models amplify a
+  change of rounding: GEMMs 5x closer to float64 than the reference's own fp32 sums still
+  move the logits by about 1e-3 of max|logit| after 32 layers.)  The ids after a tie follow
+  a different prefix and are not compared.
+* Each layer on its own (the same input for the GPU's layer and the oracle's): a 16-row
+  prompt and one decode row of Llama-3-8B through forward_cached, and at layers 0, 1, 15
+  and 31 the oracle running that one layer on the GPU's input to it; bit-exact in the exact
+  mode, within 1e-3 relative in the fast mode.  (Over the whole stack the fast mode's
+  deviations compound: a change of rounding that moves a q / k / v value across an int8
+  rounding boundary moves that element by 1/127 of its head's range, so the random-init
+  8B model ends ~1e-2 from the exact run after 32 layers of 48 prompt rows.)
 * Decode steps at the benchmark positions through forward_cached: Llama-3-8B over a cache
   filled to 1024 positions, Qwen2.5-7B over 32768; per-layer hidden states bit-exact with
   the oracle in the exact mode, within 1e-3 relative (max|gpu - oracle| <= 1e-3 *
@@ -25,14 +34,16 @@ import os
 import numpy as np
 import pytest
 
+import oracle
+
 from conftest import prefill_kv, ptr, rope_tables
 
 pytestmark = pytest.mark.gpu
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 TOL = 1e-3
-NEAR_TIE = 2e-3
-MODES = {"exact": 0, "fast": 7}
+LOGIT_TOL = 3e-2  # the whole stack's compounded deviation (about 1e-2 of the hidden states after 32 layers)
+MODES = {"exact": 0, "fast": 5}
 
 
 def say(msg):
@@ -85,9 +96,11 @@ class Full:
         self.syn.close()
 
 
-def check_near_tie(got, want, n0, exact_logits):
-    """got (fast mode) against want (exact): equal, or equal up to index i where the exact
-    logits of that step (exact_logits(i)) rate got[i] within NEAR_TIE * max|logit| of want[i]."""
+def check_near_tie(got, want, n0, exact_logits, fast_logits=None):
+    """got (fast mode) against want (exact): equal, or equal up to index i where the step's
+    fast logits (fast_logits(i), same prefix) are within LOGIT_TOL of the exact ones
+    (exact_logits(i)) and the exact-logit gap of the two picks is within twice their largest
+    difference.  Without fast logits the gap is bounded by LOGIT_TOL * max|logit|."""
     if got == want:
         return
     assert len(got) == len(want), f"lengths {len(got)} vs {len(want)}"
@@ -95,11 +108,19 @@ def check_near_tie(got, want, n0, exact_logits):
     assert i >= n0, f"prompt ids differ at {i}"
     lg = exact_logits(i)
     assert int(np.argmax(lg)) == want[i]
+    scale = float(np.abs(lg).max())
     gap = float(lg[want[i]] - lg[got[i]])
-    bound = NEAR_TIE * float(np.abs(lg).max())
-    say(f"  fast mode: near tie at generated token {i - n0}: exact logits {lg[want[i]]:.6f} (reference's pick) "
-        f"vs {lg[got[i]]:.6f} (fast mode's), gap {gap:.3g}, bound {bound:.3g}")
-    assert gap <= bound, f"fast mode picked {got[i]} at {i}: exact-logit gap {gap:.3g} > {bound:.3g}"
+    if fast_logits is not None:
+        lf = fast_logits(i)
+        assert int(np.argmax(lf)) == got[i]
+        diff = float(np.abs(lf - lg).max())
+        say(f"  fast mode: near tie at generated token {i - n0}: exact-logit gap {gap:.3g}, fast vs exact "
+            f"logits max|diff| {diff:.3g} ({diff / scale:.2g} of max|logit|)")
+        assert diff <= LOGIT_TOL * scale, f"fast logits off by {diff:.3g} at {i}"
+        assert gap <= 2 * diff, f"fast mode picked {got[i]} at {i}: gap {gap:.3g} > 2 x {diff:.3g}"
+    else:
+        say(f"  fast mode: near tie at generated token {i - n0}: exact-logit gap {gap:.3g}")
+        assert gap <= LOGIT_TOL * scale, f"fast mode picked {got[i]} at {i}: gap {gap:.3g}"
 
 
 def check_generate(jy, olib, full, case):
@@ -114,13 +135,14 @@ def check_generate(jy, olib, full, case):
             assert ids.tolist() == case["ids"], f"exact: gpu {ids[n0:].tolist()} vs reference {case['ids'][n0:]}"
             continue
 
-        def exact_logits(i):
-            full.g.mode = MODES["exact"]
-            _, _, lg = full.g.generate(prompt, i - n0 + 1, max_seq=case["max_seq"], want_logits=True)
-            full.g.mode = MODES[mode]
-            return lg
+        def logits_in(m):
+            def at(i):
+                full.g.mode = MODES[m]
+                _, _, lg = full.g.generate(prompt, i - n0 + 1, max_seq=case["max_seq"], want_logits=True)
+                return lg
+            return at
 
-        check_near_tie(ids.tolist(), case["ids"], n0, exact_logits)
+        check_near_tie(ids.tolist(), case["ids"], n0, logits_in("exact"), logits_in(mode))
 
 
 def check_decode_layers(jy, olib, full, pre, steps):
@@ -155,6 +177,57 @@ def check_decode_layers(jy, olib, full, pre, steps):
     kv.close()
 
 
+def one_layer(desc, l):
+    """A descriptor of layer l alone (the weights stay where they are)."""
+    from jieyu_amd.model import LayerWeights, ModelDesc
+    d1 = ModelDesc()
+    C.memmove(C.byref(d1), C.byref(desc), C.sizeof(ModelDesc))
+    d1.num_layers = 1
+    d1.layers = C.cast(C.addressof(desc.layers.contents) + l * C.sizeof(LayerWeights), C.POINTER(LayerWeights))
+    return d1
+
+
+def check_layers_alone(jy, olib, full, layers, rows=16):
+    d = full.d
+    H = d.hidden
+    cos, sin = rope_tables(olib, full.max_seq, d.head_dim, d.rope_theta)
+    rng = np.random.default_rng(11)
+    X = rng.standard_normal((rows, H)).astype(np.float32)
+    x1 = rng.standard_normal((1, H)).astype(np.float32)
+    for mode in MODES:
+        full.g.mode = MODES[mode]
+        kv = full.g.kv(full.max_seq)
+        _, lo = full.g.forward_cached(kv, X, 0, layer_out=True)
+        _, lo1 = full.g.forward_cached(kv, x1, rows, layer_out=True)
+        kv.close()
+        got = np.concatenate([lo, lo1], axis=1)  # [L][rows + 1][H]
+        worst = 0.0
+        for l in layers:
+            inp = np.concatenate([X, x1]) if l == 0 else got[l - 1].copy()
+            okv = oracle.JyoKV()
+            assert olib.jyo_kv_init(C.byref(okv), 1, full.max_seq, d.num_kv_heads, d.head_dim) == 0
+            d1 = one_layer(d, l)
+            # the prompt rows as one chunk, then the decode row (the m = 1 path), as the GPU ran them
+            out = np.zeros((1, rows + 1, H), np.float32)
+            xa = np.ascontiguousarray(inp[:rows])
+            xb = np.ascontiguousarray(inp[rows:])
+            oa = np.zeros((1, rows, H), np.float32)
+            ob = np.zeros((1, 1, H), np.float32)
+            assert olib.jyo_forward_cached(C.byref(d1), ptr(xa), ptr(cos), ptr(sin), rows, 0, C.byref(okv),
+                                           ptr(oa)) == 0
+            assert olib.jyo_forward_cached(C.byref(d1), ptr(xb), ptr(cos), ptr(sin), 1, rows, C.byref(okv),
+                                           ptr(ob)) == 0
+            out[0, :rows], out[0, rows] = oa[0], ob[0, 0]
+            olib.jyo_kv_free(C.byref(okv))
+            if mode == "exact":
+                assert bits_equal(got[l], out[0]), f"exact, layer {l}"
+            else:
+                err = rel_err(got[l], out[0])
+                worst = max(worst, err)
+                assert err <= TOL, f"fast, layer {l} alone: relative error {err:.3g}"
+        say(f"  {mode} mode: layers {layers} alone, worst relative error {worst:.3g}")
+
+
 class TestLlama3_8B:
     @pytest.fixture(scope="class")
     def full(self, jy, oracle_lib):
@@ -165,6 +238,10 @@ class TestLlama3_8B:
     def test_generate_matches_reference(self, jy, oracle_lib, full, golden):
         say("llama3-8b: greedy ids vs the reference")
         check_generate(jy, oracle_lib, full, golden["llama3-8b-full"])
+
+    def test_layers_alone(self, jy, oracle_lib, full):
+        say("llama3-8b: layers 0, 1, 15, 31 alone (16 prompt rows + 1 decode row) vs the oracle")
+        check_layers_alone(jy, oracle_lib, full, (0, 1, 15, 31))
 
     def test_decode_at_1024(self, jy, oracle_lib, full):
         say("llama3-8b: decode steps at 1024..1025 vs the oracle, per layer")
