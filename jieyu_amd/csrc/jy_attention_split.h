@@ -379,4 +379,52 @@ __device__ __forceinline__ bool attn_slice(const AttnArgs& a, int ns, float* __r
     return true;
 }
 
+// Merge of the live slices of kv head kvh's G query heads into a.out, by one workgroup of
+// SPL_THREADS threads (in the persistent decode kernel, the last slice workgroup of that kv
+// head to finish): each slice's
+// weight e^(m_s - M) and L = sum_s e^(m_s - M) l_s per head, then o = sum_s w_s o_s / L with
+// SB slices' loads in flight per output.  LDS: ml [2 G live], wsl [G live] floats.  With
+// COH the partials are read from the agent-coherent level (they were written by other
+// workgroups) and the output written through to it.
+template <int P, bool COH>
+__device__ __forceinline__ void combine_group(const AttnArgs& a, int ns, const float* part, int kvh, float* ml,
+                                              float* wsl) {
+    constexpr int HD = P * 16;
+    const int tid = threadIdx.x, G = a.nh / a.nkv, W = HD + 2;
+    const int pos = a.state ? a.state[0] - 1 : a.start_pos + a.row0;
+    const int nk = pos + 1;
+    const int chunk = split_chunk(nk, ns);
+    const int live = (nk + chunk - 1) / chunk;
+    for (int i = tid; i < G * live; i += SPL_THREADS) {
+        const int gg = i / live, s = i - gg * live;
+        const float* o = part + ((size_t)(kvh * G + gg) * ns + s) * W;
+        ml[2 * i] = act_ld<COH>(o + HD);
+        ml[2 * i + 1] = act_ld<COH>(o + HD + 1);
+    }
+    __syncthreads();
+    for (int i = tid; i < G * live; i += SPL_THREADS) {
+        const int gg = i / live;
+        float M = -__builtin_inff();
+        for (int s = 0; s < live; s++) M = fmaxf(M, ml[2 * (gg * live + s)]);
+        wsl[i] = exp_hw(ml[2 * i] - M);
+    }
+    __syncthreads();
+    constexpr int SB = 16;
+    for (int i = tid; i < G * HD; i += SPL_THREADS) {
+        const int gg = i / HD, d = i - gg * HD;
+        float L = 0.0f, o = 0.0f;
+        const float* pb = part + (size_t)(kvh * G + gg) * ns * W;
+        for (int s0 = 0; s0 < live; s0 += SB) {
+            float ov[SB];
+#pragma unroll
+            for (int u = 0; u < SB; u++) ov[u] = s0 + u < live ? act_ld<COH>(pb + (size_t)(s0 + u) * W + d) : 0.0f;
+#pragma unroll
+            for (int u = 0; u < SB; u++)
+                if (s0 + u < live) o = __builtin_fmaf(wsl[gg * live + s0 + u], ov[u], o);
+        }
+        for (int q = 0; q < live; q++) L = __builtin_fmaf(wsl[gg * live + q], ml[2 * (gg * live + q) + 1], L);
+        act_st<COH>(a.out + (size_t)(kvh * G + gg) * HD + d, o / L);
+    }
+}
+
 }  // namespace jy

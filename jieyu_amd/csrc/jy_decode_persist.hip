@@ -288,50 +288,6 @@ __device__ __forceinline__ void pk_matvec(const PMat& M, const float* xs, float 
 
 // ---------------------------------------------------------------- attention phase
 
-// the last slice of kv head kvh to finish merges the group's slices into att (the
-// separate form's attn_combine_kernel, for the G query heads of one kv head)
-template <int P>
-__device__ __forceinline__ void pk_combine(const AttnArgs& a, int ns, const float* part, int kvh, float* ml,
-                                           float* wsl) {
-    constexpr int HD = P * 16;
-    const int tid = threadIdx.x, G = a.nh / a.nkv, W = HD + 2;
-    const int pos = a.state ? a.state[0] - 1 : a.start_pos + a.row0;
-    const int nk = pos + 1;
-    const int chunk = split_chunk(nk, ns);
-    const int live = (nk + chunk - 1) / chunk;
-    // (max, sum) of every (head, slice), then the weights e^(m - M) and the sums L per head
-    for (int i = tid; i < G * live; i += PK_THREADS) {
-        const int gg = i / live, s = i - gg * live;
-        const float* o = part + ((size_t)(kvh * G + gg) * ns + s) * W;
-        ml[2 * i] = act_ld<true>(o + HD);
-        ml[2 * i + 1] = act_ld<true>(o + HD + 1);
-    }
-    lds_barrier();
-    for (int i = tid; i < G * live; i += PK_THREADS) {
-        const int gg = i / live;
-        float M = -__builtin_inff();
-        for (int s = 0; s < live; s++) M = fmaxf(M, ml[2 * (gg * live + s)]);
-        wsl[i] = exp_hw(ml[2 * i] - M);
-    }
-    lds_barrier();
-    constexpr int SB = 16;  // slices' loads in flight per output
-    for (int i = tid; i < G * HD; i += PK_THREADS) {
-        const int gg = i / HD, d = i - gg * HD;
-        float L = 0.0f, o = 0.0f;
-        const float* pb = part + (size_t)(kvh * G + gg) * ns * W;
-        for (int s0 = 0; s0 < live; s0 += SB) {
-            float ov[SB];
-#pragma unroll
-            for (int u = 0; u < SB; u++) ov[u] = s0 + u < live ? act_ld<true>(pb + (size_t)(s0 + u) * W + d) : 0.0f;
-#pragma unroll
-            for (int u = 0; u < SB; u++)
-                if (s0 + u < live) o = __builtin_fmaf(wsl[gg * live + s0 + u], ov[u], o);
-        }
-        for (int q = 0; q < live; q++) L = __builtin_fmaf(wsl[gg * live + q], ml[2 * (gg * live + q) + 1], L);
-        act_st<true>(a.out + (size_t)(kvh * G + gg) * HD + d, o / L);
-    }
-}
-
 // ---------------------------------------------------------------- the kernel
 
 template <int P>
@@ -398,7 +354,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void decode_persist_kernel(PersistAr
                     __syncthreads();
                     if (last) {
                         float* ml = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + sizeof(SplitLds<P, SPL_GMAX>));
-                        pk_combine<P>(at, A.ns, A.part, kvh, ml, ml + 2 * SPL_GMAX * 256);
+                        combine_group<P, true>(at, A.ns, A.part, kvh, ml, ml + 2 * SPL_GMAX * 256);
                     }
                 }
             }
