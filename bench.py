@@ -33,12 +33,15 @@ sys.path.insert(0, ROOT)
 
 METRIC = "batch-1 decode tokens/s (Q8, 8B shape) + achieved HBM GB/s vs peak"
 # arithmetic modes (jieyu_amd.MODE_*): exact reproduces the reference bit for bit; fast
-# splits the decode attention over the keys and runs prompt GEMMs on the matrix cores
+# splits the decode attention over the keys (and the dots of matrices under 2048 rows) and
+# runs prompt GEMMs on the matrix cores
 # (hidden states within 1e-3 relative; greedy ids identical except at near ties closer than
 # the mode's rounding)
-MODES = {"exact": 0, "fast": 5}
+MODES = {"exact": 0, "fast": 7}
+SPLIT_MV_ROWS = 2048  # the fast mode's decode matvecs use the split-dot form below this many rows
 MODE_TEXT = {"exact": "bit-exact (reference arithmetic order)",
-             "fast": "fast: split-K (flash-decoding) attention, matrix-core (fp16 hi/lo MFMA) prompt GEMMs "
+             "fast": "fast: split-K (flash-decoding) attention, split-dot matvecs under 2048 rows, matrix-core "
+                     "(fp16 hi/lo MFMA) prompt GEMMs "
                      "(each layer within 1e-3 relative of the reference given the same input; deviations "
                      "compound over the stack through the int8 requantization of q/k/v; greedy ids identical "
                      "up to the first near tie)"}
@@ -85,7 +88,7 @@ def dominant_kernel_roofline(jy, d, mode, iters=64):
     """The decode step's gate/up launch (2F x hidden interleaved rows, RMSNorm, SwiGLU
     epilogue) in the benchmark's mode, timed in isolation with HIP events on its stream
     over enough copies to defeat the 256 MiB infinity cache."""
-    split = bool(MODES[mode] & 2)  # the split-dot matvec only where the mode has it
+    split = bool(MODES[mode] & 2) and 2 * d.intermediate < SPLIT_MV_ROWS  # the kernel the step uses
     rows, cols = 2 * d.intermediate, d.hidden
     nbytes = q8b(rows, cols)
     copies = max(2, int(np.ceil(1.2e9 / nbytes)))
@@ -171,7 +174,7 @@ def isolated_matvecs(jy, mode, iters=64):
         syn.jysyn_normal_fill(1, 13, 1.0, ptr(x), cols)
         copies = max(2, int(np.ceil(1.2e9 / blk.size)))
         m = jy.Q8Matrix(blk.reshape(-1), rows, cols, copies=copies)
-        us = m.time(x, iters, variant=2 if MODES[mode] & 2 else 0)
+        us = m.time(x, iters, variant=2 if MODES[mode] & 2 and rows < SPLIT_MV_ROWS else 0)
         m.close()
         algo = blk.size + cols * 4 + rows * 4
         res[f"{rows}x{cols}"] = {"us": round(us, 3), "GB/s": round(algo / (us * 1e-6) / 1e9, 1)}

@@ -61,10 +61,11 @@ JYHIP_API void jyhip_model_free(jyhip_model* model);
  *                          (flash-decoding): exact int8 quantisation and int32 q.k, the
  *                          softmax sum and p.v accumulated per slice and merged; prompt
  *                          rows in the same arithmetic, one workgroup per kv head and row;
- *   JYHIP_MODE_SPLIT_MV    decode Q8_0 matvecs with each row's dot split across waves and
- *                          the RMSNorm scale applied after the dot (linearity); opt-in: it
- *                          measured slower than the exact matvec (8B shape after 1024
- *                          tokens: 419 -> 358 tokens/s), so JYHIP_MODE_FAST leaves it out;
+ *   JYHIP_MODE_SPLIT_MV    decode Q8_0 matvecs of fewer than JYHIP_SPLIT_MV_ROWS rows with
+ *                          each row's dot split across waves and the RMSNorm scale applied
+ *                          after the dot (linearity); larger matrices keep the exact kernel,
+ *                          which measured faster there (e.g. 4096 x 14336: 15.7 vs 18.9 us;
+ *                          896 x 4864: 7.2 vs 5.1 us the other way);
  *   JYHIP_MODE_MFMA_PREFILL Q8_0 prompt GEMMs (m > 1) on the matrix cores: each activation
  *                          row scaled by a power of two and split into fp16 high + low parts
  *                          (22 significant bits), int8 weights exact in fp16, one fp32 MFMA
@@ -77,7 +78,8 @@ JYHIP_API void jyhip_model_free(jyhip_model* model);
 #define JYHIP_MODE_SPLIT_ATTN 1
 #define JYHIP_MODE_SPLIT_MV 2
 #define JYHIP_MODE_MFMA_PREFILL 4
-#define JYHIP_MODE_FAST (JYHIP_MODE_SPLIT_ATTN | JYHIP_MODE_MFMA_PREFILL)
+#define JYHIP_MODE_FAST (JYHIP_MODE_SPLIT_ATTN | JYHIP_MODE_SPLIT_MV | JYHIP_MODE_MFMA_PREFILL)
+#define JYHIP_SPLIT_MV_ROWS 2048
 /* With both split bits: each decode row of every layer (and, in a session's greedy step, the
  * head) as one persistent kernel whose workgroups hand activations to each other through
  * grid barriers, instead of about six kernels per layer.  Same arithmetic as the split
@@ -174,7 +176,7 @@ JYHIP_API jyhip_q8mat* jyhip_q8_upload(const void* w, int rows, int cols, int co
 JYHIP_API void jyhip_q8_free(jyhip_q8mat* m);
 JYHIP_API int jyhip_q8_matvec(jyhip_q8mat* m, const float* x, float* y);
 /* jyhip_q8_matvec's kernel: JYHIP_MODE_EXACT (the default) or with JYHIP_MODE_SPLIT_MV the
- * split-dot form; with JYHIP_MODE_MFMA_PREFILL jyhip_q8_gemm runs the matrix-core kernel
+ * split-dot form at any size; with JYHIP_MODE_MFMA_PREFILL jyhip_q8_gemm runs the matrix-core kernel
  * (the first such call builds its copies of the matrix).  Returns 0 / -1. */
 JYHIP_API int jyhip_q8_set_mode(jyhip_q8mat* m, int mode);
 /* Time `iters` launches (rotating copies) with HIP events on the launch stream:

@@ -27,7 +27,8 @@ MODE_EXACT = 0
 MODE_SPLIT_ATTN = 1
 MODE_SPLIT_MV = 2
 MODE_MFMA_PREFILL = 4
-MODE_FAST = MODE_SPLIT_ATTN | MODE_MFMA_PREFILL  # the split matvec measured slower: opt-in
+MODE_FAST = MODE_SPLIT_ATTN | MODE_SPLIT_MV | MODE_MFMA_PREFILL
+SPLIT_MV_ROWS = 2048  # a model's decode matvecs use the split-dot form below this many rows
 MODE_PERSIST = 8  # with the split bits: the decode step as one persistent kernel (opt-in)
 
 

@@ -332,7 +332,7 @@ void ensure_part(jyhip_model* m, size_t n) {
 // a decode Q8_0 matvec in the model's mode: the reference's 32-lane order, or the split dot
 void q8_matvec(const jyhip_model* m, const Q8Dev& W, const float* x, const float* norm_w, float* out, Epi epi,
                const MvArgs& a, hipStream_t st) {
-    if (m->mode & JYHIP_MODE_SPLIT_MV)
+    if ((m->mode & JYHIP_MODE_SPLIT_MV) && W.rows < JYHIP_SPLIT_MV_ROWS)
         launch_matvec_q8_split(W, x, norm_w, out, epi, a, st);
     else
         launch_matvec_q8(W, x, norm_w, out, epi, a, st);

@@ -130,7 +130,7 @@ def test_mfma_gemm_within_tolerance(jy, oracle_lib, m, rows, cols):
         assert np.array_equal(tiles.view(np.uint32), ref.view(np.uint32))
 
 
-MODES = {"SPLIT_ATTN": 1, "SPLIT_MV": 2, "MFMA_PREFILL": 4, "FAST": 5, "ALL": 7, "PERSIST": 7 | 8}
+MODES = {"SPLIT_ATTN": 1, "SPLIT_MV": 2, "MFMA_PREFILL": 4, "FAST": 7, "PERSIST": 7 | 8}
 
 
 @pytest.mark.parametrize("mode_name", list(MODES))
