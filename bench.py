@@ -397,6 +397,7 @@ def main():
     made = sess.step(K)
     t1 = time.perf_counter()
     st = sess.stats()
+    pre_mfma = prefill_mfma(d, args.prompt_len, st.prefill_ms, args.mode)  # while the descriptor is alive
     ids = sess.ids()
     other_mode = None
     if K2 > 0:
@@ -464,7 +465,7 @@ def main():
         "hbm_gbs": round(hbm_gbs, 1), "hbm_frac": round(hbm_gbs / HBM_PEAK_GBS, 4),
         "bytes_per_token_avg": int(bytes_total / K), "device_ms_per_step": round(dev_ms / K, 4),
         "prefill_ms": round(st.prefill_ms, 2), "prefill_tokens_s": round(args.prompt_len / (st.prefill_ms / 1e3), 1),
-        "prefill_mfma": prefill_mfma(d, args.prompt_len, st.prefill_ms, args.mode), "isolated_prompt_gemm": pgemm,
+        "prefill_mfma": pre_mfma, "isolated_prompt_gemm": pgemm,
         "upload_s": round(st.upload_ms / 1e3, 2),
         "last_ids": ids[-8:].tolist(),
         "other_mode": other_mode,
