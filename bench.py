@@ -294,46 +294,87 @@ def copy_calibration(mb):
     print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "launches": 8}), flush=True)
 
 
-def cpu_baseline(desc, prompt, n_new, gpu_model):
-    """jieyu's decode loop built from the reference sources (or the C oracle where that
-    build is absent) on this host; rate as the reference's -tokenspeed report defines
-    it: (n-1) / (t_last - t_first) (libs/model_libs/pipeline.h:356-372)."""
+def host_cpu():
+    """The host CPU: model name, logical CPUs (all and usable by this process), ISA flags
+    that matter to the reference's kernels."""
+    model, flags = None, set()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if model is None and line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+            elif not flags and line.startswith("flags"):
+                flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    want = ("sse4_2", "avx", "avx2", "fma", "f16c", "avx512f", "avx512bw", "avx512vl", "avx512_vnni",
+            "avx512_bf16", "avx512_fp16", "amx_tile", "amx_bf16", "amx_int8")
+    return {"model": model, "nproc": os.cpu_count(), "usable": len(os.sched_getaffinity(0)),
+            "isa": [f for f in want if f in flags]}
+
+
+def cpu_baseline(desc, prefilled, n_steps, timed=None):
+    """jieyu's decode step built from the reference sources (or the C oracle where that build
+    is absent) on this host, at the benchmark's positions: the KV cache holds `prefilled`
+    positions (random int8 K/V and scales: the values do not change the work), then n_steps
+    greedy steps, each the embedding row, forward_cached over one row, the lm_head and the
+    first maximum (generate.h:9-89's per-token loop).  Rate = steps / their summed time."""
     import oracle
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    max_seq = len(prompt) + n_new + 1
+    L, H, V = desc.num_layers, desc.hidden, desc.vocab_size
+    nkv, hd = desc.num_kv_heads, desc.head_dim
+    max_seq = prefilled + n_steps + 1
     olib = oracle.load_oracle()
-    half = desc.head_dim // 2
+    half = hd // 2
     cos = np.zeros(max_seq * half, np.float32)
     sin = np.zeros_like(cos)
-    olib.jyo_rope_table(max_seq, desc.head_dim, desc.rope_theta, ptr(cos), ptr(sin))
-    out = np.zeros(max_seq + 1, np.int32)
-    stamps = np.zeros(n_new + 1, np.float64)
-    t0 = time.monotonic()
+    olib.jyo_rope_table(max_seq, hd, desc.rope_theta, ptr(cos), ptr(sin))
+    rng = np.random.default_rng(7)
+    n8, ns = L * nkv * max_seq * hd, L * nkv * max_seq
     if oracle.ref_available():
-        kind = "reference"
-        ref = oracle.load_ref()
-        n = ref.jyref_generate(C.byref(desc), ptr(prompt), len(prompt), None, 0, ptr(cos), ptr(sin), max_seq, n_new,
-                               0.0, 1.0, ptr(out), None, ptr(stamps), len(stamps))
+        kind, lib = "reference", oracle.load_ref()
+        kv = lib.jyref_kv_create(L, max_seq, nkv, hd)
+        arrays = [(lib.jyref_kv_k(kv), C.c_int8, n8), (lib.jyref_kv_v(kv), C.c_int8, n8),
+                  (lib.jyref_kv_ks(kv), C.c_float, ns), (lib.jyref_kv_vs(kv), C.c_float, ns)]
+        lib.jyref_kv_set_len(kv, prefilled)
+        row = lambda tok, X: lib.jyref_wmat_row(C.byref(desc.embed), tok, H, ptr(X))
+        fwd = lambda X, pos: lib.jyref_forward_cached(C.byref(desc), ptr(cos), ptr(sin), ptr(X), 1, pos, kv, None)
+        head = lambda X, lg: lib.jyref_matmul_w(C.byref(desc.lm_head), 1, V, H, ptr(X), ptr(lg))
+        free = lambda: lib.jyref_kv_free(kv)
     else:
         kind = "port"
-        n = olib.jyo_generate(C.byref(desc), ptr(prompt), len(prompt), None, 0, ptr(cos), ptr(sin), max_seq, n_new,
-                              0.0, 1.0, ptr(out), None, None)
-        stamps[:] = 0.0
-    wall = time.monotonic() - t0
-    made = n - len(prompt)
-    if kind == "reference" and made > 1:
-        rate = (made - 1) / (stamps[made - 1] - stamps[0])
-        prefill = len(prompt) / (stamps[0] - t0)
-    else:
-        rate = made / wall if wall > 0 else 0.0
-        prefill = None
-    gpu_ids, _ = gpu_model.generate(prompt, n_new, max_seq=max_seq)
-    same = bool(np.array_equal(gpu_ids, out[:n]))
-    return {"value": round(rate, 4), "unit": "tokens/s", "cores": threads, "kind": kind,
-            "sample": f"{len(prompt)}-token prompt then {made} greedy tokens on the same model "
-                      f"(decode rate = (n-1)/(t_last-t_first)); wall {wall:.1f} s",
-            "prefill_tokens_s": None if prefill is None else round(prefill, 3),
-            "gpu_tokens_identical": same}
+        kvs = oracle.JyoKV()
+        assert olib.jyo_kv_init(C.byref(kvs), L, max_seq, nkv, hd) == 0
+        arrays = [(kvs.k, C.c_int8, n8), (kvs.v, C.c_int8, n8), (kvs.ks, C.c_float, ns), (kvs.vs, C.c_float, ns)]
+        kvs.current_len = prefilled
+        row = lambda tok, X: olib.jyo_embed_row(C.byref(desc.embed), tok, H, ptr(X))
+        fwd = lambda X, pos: olib.jyo_forward_cached(C.byref(desc), ptr(X), ptr(cos), ptr(sin), 1, pos,
+                                                      C.byref(kvs), None)
+        head = lambda X, lg: olib.jyo_matmul_w(C.byref(desc.lm_head), 1, V, H, ptr(X), ptr(lg))
+        free = lambda: olib.jyo_kv_free(C.byref(kvs))
+    for addr, ctype, n in arrays:
+        a = np.ctypeslib.as_array((ctype * n).from_address(C.cast(addr, C.c_void_p).value))
+        if ctype is C.c_int8:
+            a[:] = rng.integers(-127, 128, n, dtype=np.int8)
+        else:
+            a[:] = rng.uniform(0.01, 0.02, n).astype(np.float32)
+    X = np.zeros(H, np.float32)
+    logits = np.zeros(V, np.float32)
+    tok, times = 1, []
+    for i in range(n_steps):
+        t = time.monotonic()
+        row(tok, X)
+        assert fwd(X, prefilled + i) == 0
+        head(X, logits)
+        tok = int(np.argmax(logits))
+        times.append(time.monotonic() - t)
+    free()
+    kept = times[1:] if len(times) > 1 else times  # the first step pays the page-ins
+    return {"value": round(len(kept) / sum(kept), 4), "unit": "tokens/s", "cores": threads, "kind": kind,
+            "sample": f"{n_steps} greedy decode steps at positions {prefilled}..{prefilled + n_steps - 1} over a "
+                      f"cache holding {prefilled} positions, the first untimed"
+                      + (f"; the benchmark times positions {timed[0]}..{timed[1]}, so the rate is extrapolated "
+                         f"over their (small) growth in attention work" if timed else ""),
+            "step_s": [round(x, 3) for x in times], "cpu": host_cpu()}
 
 
 def main():
@@ -344,8 +385,8 @@ def main():
     ap.add_argument("--config", default="llama3-8b")
     ap.add_argument("--prompt-len", type=int, default=1024)
     ap.add_argument("--max-seq", type=int, default=4096)
-    ap.add_argument("--cpu-prompt", type=int, default=8)
-    ap.add_argument("--cpu-tokens", type=int, default=96)
+    ap.add_argument("--cpu-steps", type=int, default=12,
+                    help="reference decode steps timed on the host at the benchmark's positions")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernel", action="store_true")
     ap.add_argument("--no-other", action="store_true", help="skip the other model workloads")
@@ -439,10 +480,10 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        log(f"CPU baseline: {args.cpu_prompt}-token prompt + {args.cpu_tokens} tokens ...")
-        cpu = cpu_baseline(d, prompt[:args.cpu_prompt].copy(), args.cpu_tokens, g)
-        log(f"  {cpu['kind']}: {cpu['value']} tok/s on {cpu['cores']} threads; GPU identical: "
-            f"{cpu['gpu_tokens_identical']}")
+        log(f"CPU baseline: {args.cpu_steps} decode steps over a {args.prompt_len}-position cache ...")
+        cpu = cpu_baseline(d, args.prompt_len, args.cpu_steps, (p0, p0 + K - 1))
+        log(f"  {cpu['kind']}: {cpu['value']} tok/s on {cpu['cores']} threads ({cpu['cpu']['model']}, "
+            f"{cpu['cpu']['usable']} of {cpu['cpu']['nproc']} CPUs usable)")
     shape = {"num_layers": d.num_layers, "hidden": d.hidden, "heads": d.num_heads, "kv_heads": d.num_kv_heads,
              "head_dim": d.head_dim, "ffn": d.intermediate, "vocab": d.vocab_size, "rope_theta": d.rope_theta}
     g.close()
