@@ -22,26 +22,28 @@
 // uses as many slices as that length needs.
 #include <algorithm>
 
-#include "jy_attention_split.h"
+#include "jy_attention_mfma.h"
 
 namespace jy {
 
-// P = hd / 16: 16-byte pieces per key row; GT = split_heads(query heads per kv head).
-// (A one-kernel form, whose last slice workgroup of each kv head merged the slices, measured
-// slower than this kernel plus attn_combine_kernel: 8B decode after 1024 tokens 386 vs 427
-// tokens/s; the persistent decode kernel keeps that merge, combine_group.)
-template <int P, int GT>
-__global__ __launch_bounds__(SPL_THREADS) void attn_split_kernel(AttnArgs a, int ns, float* __restrict__ part) {
-    __shared__ SplitLds<P, GT> lds;
-    attn_slice<P, GT, false>(a, ns, part, blockIdx.x, blockIdx.y, lds);
+// P = hd / 16: 16-byte pieces per key row; GT = split_heads(query heads per kv head); NW
+// waves per workgroup.  One workgroup per (kv head, slice); with one slice (part ==
+// nullptr) the normalised output goes straight to a.out and no merge kernel follows.
+// (A form whose last slice workgroup of each kv head merged the slices measured slower than
+// the separate merge kernel: 8B decode after 1024 tokens 386 vs 427 tokens/s.)
+template <int P, int GT, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4, 4))) void attn_split_kernel(
+    AttnArgs a, int ns, float* __restrict__ part) {
+    __shared__ MslLds<P * 16, NW> lds;
+    attn_slice_mfma<P, GT, NW, false>(a, ns, part, blockIdx.x, blockIdx.y, lds);
 }
 
 // prompt rows: one workgroup per (kv head, row), the row's whole key range as one slice,
 // the normalised output straight to a.out; rows in descending order (the longest first)
 template <int P, int GT>
-__global__ __launch_bounds__(SPL_THREADS) void attn_prefill_kernel(AttnArgs a) {
-    __shared__ SplitLds<P, GT> lds;
-    attn_slice<P, GT, false>(a, 1, nullptr, blockIdx.x, 0, lds, a.nrows - 1 - (int)blockIdx.y);
+__global__ __launch_bounds__(SPL_THREADS) __attribute__((amdgpu_waves_per_eu(4, 4))) void attn_prefill_kernel(AttnArgs a) {
+    __shared__ MslLds<P * 16, 4> lds;
+    attn_slice_mfma<P, GT, 4, false>(a, 1, nullptr, blockIdx.x, 0, lds, a.nrows - 1 - (int)blockIdx.y);
 }
 
 // The merge for many slices: one workgroup per (query head, 32 output dims).  Every
@@ -94,26 +96,32 @@ bool attn_split_supported(int nh, int nkv, int hd) {
     return nkv > 0 && nh % nkv == 0 && nh / nkv <= SPL_GMAX && (hd == 64 || hd == 128);
 }
 
-int attn_split_slices(int keys) { return std::max(1, std::min(256, (keys + 127) / 128)); }
+// slices of about MSL_SLICE_KEYS keys (one step per wave: a second step of a wave waits a
+// whole memory round trip, which measured slower than more workgroups and the merge
+// kernel: 16 waves x 64 keys per kv head at 1024 keys 14.1 us, 4 waves x 32 keys per slice
+// 7.0 us + 4.6 us merge)
+static constexpr int MSL_SLICE_KEYS = 128, MSL_NW = 4;
+
+int attn_split_slices(int keys) { return std::max(1, std::min(256, (keys + MSL_SLICE_KEYS - 1) / MSL_SLICE_KEYS)); }
 
 size_t attn_split_part_floats(int nh, int hd, int ns) { return (size_t)nh * ns * (hd + 2); }
 
-// the slices, then the merge over (head, 32 dims)
+// the slices, then (more than one) the merge over (head, 32 dims)
 void launch_attention_split(const AttnArgs& a, float* part, int ns, hipStream_t st) {
-    const dim3 grid(a.nkv, ns), block(SPL_THREADS);
-    auto k = attn_split_kernel<8, 8>;
+    const dim3 grid(a.nkv, ns), block(64 * MSL_NW);
+    auto k = attn_split_kernel<8, 8, MSL_NW>;
     switch (split_heads(a.nh / a.nkv) * (a.hd == 64 ? -1 : 1)) {
-        case -1: k = attn_split_kernel<4, 1>; break;
-        case -2: k = attn_split_kernel<4, 2>; break;
-        case -4: k = attn_split_kernel<4, 4>; break;
-        case -8: k = attn_split_kernel<4, 8>; break;
-        case 1: k = attn_split_kernel<8, 1>; break;
-        case 2: k = attn_split_kernel<8, 2>; break;
-        case 4: k = attn_split_kernel<8, 4>; break;
+        case -1: k = attn_split_kernel<4, 1, MSL_NW>; break;
+        case -2: k = attn_split_kernel<4, 2, MSL_NW>; break;
+        case -4: k = attn_split_kernel<4, 4, MSL_NW>; break;
+        case -8: k = attn_split_kernel<4, 8, MSL_NW>; break;
+        case 1: k = attn_split_kernel<8, 1, MSL_NW>; break;
+        case 2: k = attn_split_kernel<8, 2, MSL_NW>; break;
+        case 4: k = attn_split_kernel<8, 4, MSL_NW>; break;
         default: break;
     }
-    hipLaunchKernelGGL(k, grid, block, 0, st, a, ns, part);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nh, a.hd / 32), dim3(256), 0, st, a, ns, part);
+    hipLaunchKernelGGL(k, grid, block, 0, st, a, ns, ns > 1 ? part : nullptr);
+    if (ns > 1) hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nh, a.hd / 32), dim3(256), 0, st, a, ns, part);
 }
 
 void launch_attention_prefill_split(const AttnArgs& a, hipStream_t st) {

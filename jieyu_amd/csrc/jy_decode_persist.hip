@@ -458,8 +458,11 @@ bool persist_supported(int nh, int nkv, int hd) { return g_pk_cus > 0 && attn_sp
 
 int persist_workgroups() { return g_pk_cus; }
 
-// slices of the attention: the split form's count for max_keys, at most one workgroup per slice
-int persist_slices(int nkv, int max_keys) { return std::max(1, std::min(attn_split_slices(max_keys), g_pk_cus / nkv)); }
+// slices of the attention: about 128 keys each (a 256-key tile per slice workgroup half
+// used at most), at most one workgroup per slice
+int persist_slices(int nkv, int max_keys) {
+    return std::max(1, std::min(std::min(256, (max_keys + 127) / 128), g_pk_cus / nkv));
+}
 
 // LDS of one launch: the largest staged vector (widest input of the layer's matrices and
 // the lm_head) or the attention's tile plus its merge arrays

@@ -343,9 +343,12 @@ bool split_attention(const jyhip_model* m) {
     return (m->mode & JYHIP_MODE_SPLIT_ATTN) && m->wtype == JY_Q8_0 && attn_split_supported(m->nh, m->nkv, m->hd);
 }
 
-// slice partials (floats) a decode step attending up to max_keys keys takes
+// slice partials (floats) a decode step attending up to max_keys keys takes: the separate
+// kernels' slice count or the persistent kernel's, whichever is larger (either may run)
 size_t part_need(const jyhip_model* m, int max_keys) {
-    return split_attention(m) ? attn_split_part_floats(m->nh, m->hd, attn_split_slices(max_keys)) : 0;
+    if (!split_attention(m)) return 0;
+    const int ns = std::max(attn_split_slices(max_keys), persist_slices(m->nkv, max_keys));
+    return attn_split_part_floats(m->nh, m->hd, ns);
 }
 
 // the decode step runs as the persistent kernel: asked for, its shapes supported, and the
