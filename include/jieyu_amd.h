@@ -62,10 +62,10 @@ JYHIP_API void jyhip_model_free(jyhip_model* model);
  *                          softmax sum and p.v accumulated per slice and merged; prompt
  *                          rows in the same arithmetic, one workgroup per kv head and row;
  *   JYHIP_MODE_SPLIT_MV    decode Q8_0 matvecs of fewer than JYHIP_SPLIT_MV_ROWS rows with
- *                          each row's dot split across waves and the RMSNorm scale applied
- *                          after the dot (linearity); larger matrices keep the exact kernel,
- *                          which measured faster there (e.g. 4096 x 14336: 15.7 vs 18.9 us;
- *                          896 x 4864: 7.2 vs 5.1 us the other way);
+ *                          each row's dot split across waves; larger matrices keep the exact
+ *                          kernel's dot order, which measured faster there (e.g. 4096 x
+ *                          14336: 15.7 vs 18.9 us; 896 x 4864: 7.2 vs 5.1 us the other way);
+ *                          both apply the RMSNorm scale after the dot (linearity);
  *   JYHIP_MODE_MFMA_PREFILL Q8_0 prompt GEMMs (m > 1) on the matrix cores: each activation
  *                          row scaled by a power of two and split into fp16 high + low parts
  *                          (22 significant bits), int8 weights exact in fp16, one fp32 MFMA
@@ -183,7 +183,9 @@ JYHIP_API int jyhip_q8_set_mode(jyhip_q8mat* m, int mode);
  * *avg_us = mean kernel-to-kernel time per launch.  variant 0 is the plain
  * matvec; variant 1 is the decode step's gate/up launch of the same kernel
  * (RMSNorm over x, SwiGLU epilogue over interleaved row pairs); variants 2 and 3
- * are the same two launches of the split-dot kernel (JYHIP_MODE_SPLIT_MV). */
+ * are the same two launches of the split-dot kernel (JYHIP_MODE_SPLIT_MV); variant 4 is
+ * the gate/up launch of the first kernel with the RMSNorm applied after the dot, the form
+ * JYHIP_MODE_SPLIT_MV gives the matrices it leaves in the 32-lane order. */
 JYHIP_API int jyhip_q8_matvec_time(jyhip_q8mat* m, const float* x, int variant, int iters, double* avg_us);
 /* C[mr][rows] = A[mr][cols] W^T (row-major fp32) through the prompt GEMM of the
  * matrix's mode: the exact tiles, or with JYHIP_MODE_MFMA_PREFILL the matrix-core kernel

@@ -339,7 +339,8 @@ class Q8Matrix:
 
     def time(self, x, iters, variant=0):
         """Mean µs per launch over `iters` launches: variant 0 the plain matvec, 1 the decode
-        gate/up launch (RMSNorm + SwiGLU); 2 and 3 the same with the split-dot kernel."""
+        gate/up launch (RMSNorm + SwiGLU); 2 and 3 the same with the split-dot kernel; 4 the
+        gate/up launch of the first kernel with the RMSNorm applied after the dot."""
         x = np.ascontiguousarray(x, np.float32)
         us = C.c_double()
         _check(self._lib.jyhip_q8_matvec_time(self.h, _ptr(x), variant, iters, C.byref(us)))

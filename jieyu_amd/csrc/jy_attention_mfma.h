@@ -101,6 +101,7 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
     constexpr int KPI = 64 / PPK; // keys per V load instruction
     constexpr int NV = HD / 32;   // V loads per lane and step
     static_assert(2 * GT <= 16, "head columns");
+    static_assert(SPL_GMAX * HD / 16 <= NW * 64, "a prompt row's query pieces: one per thread");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, grp = lane >> 4;
@@ -159,11 +160,8 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
         }
     };
 
-    MslRegs<HD> cur;  // (all masked for a wave without keys)
-    load_k(cur, j0 + ST * wave);
-    load_vs(cur, j0 + ST * wave);
-
-    // q (and with the new position its k and v) quantised per head, as attn_slice does
+    // the query's loads go out first, then the first step's K / V / scale loads: waits are in
+    // issue order, so the quantisation below waits for the query only, with the keys in flight
     const int nitems = fused ? G + (holds_new ? 2 : 0) : 0;
     constexpr int PER = HD / 64;
     float qv[3][PER];
@@ -177,6 +175,20 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
             for (int c = 0; c < PER; c++) qv[t][c] = act_ld<COH>(src + lane + 64 * c);
         }
     }
+    // prompt rows: the row's quantised query heads of this group, as the packing pass left
+    // them (at most one 16-byte piece per thread), and their scales
+    int4 qp = make_int4(0, 0, 0, 0);
+    float qsp = 0.0f;
+    const size_t qrow = (size_t)(a.row0 + prow) * nh + (size_t)kvh * G;
+    if (!fused) {
+        if (tid < G * HD / 16) qp = reinterpret_cast<const int4*>(a.q8 + qrow * HD)[tid];
+        if (tid < G) qsp = a.qsc[qrow + tid];
+    }
+    MslRegs<HD> cur;  // (all masked for a wave without keys)
+    load_k(cur, j0 + ST * wave);
+    load_vs(cur, j0 + ST * wave);
+
+    // q (and with the new position its k and v) quantised per head, as attn_slice does
 #pragma unroll
     for (int t = 0; t < 3; t++) {
         const int i = wave + NW * t;
@@ -197,16 +209,13 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
             }
         }
     }
-    if (!fused) {  // the row's quantised query heads of this group, as the packing pass left them
-        const size_t qrow = (size_t)(a.row0 + prow) * nh + (size_t)kvh * G;
-        const int4* src = reinterpret_cast<const int4*>(a.q8 + qrow * HD);
-        for (int i = tid; i < G * HD / 16; i += NW * 64)
-            *reinterpret_cast<int4*>(&L.q8[i / (HD / 16)][16 * (i % (HD / 16))]) = src[i];
-        if (tid < G) L.qsc[tid] = a.qsc[qrow + tid];
+    if (!fused) {
+        if (tid < G * HD / 16) *reinterpret_cast<int4*>(&L.q8[tid / (HD / 16)][16 * (tid % (HD / 16))]) = qp;
+        if (tid < G) L.qsc[tid] = qsp;
     }
     for (int i = G * HD + tid; i < GT * HD; i += NW * 64) L.q8[i / HD][i % HD] = 0;
     if (tid < GT - G) L.qsc[G + tid] = 0.0f;
-    __syncthreads();
+    lds_barrier();  // (the key loads stay in flight)
     if (holds_new) {  // kv_pack_q8 of the new position, appended by the workgroup that holds it
         for (int d = tid; d < HD; d += NW * 64) {
             K[(size_t)pos * HD + d] = L.knew[d];

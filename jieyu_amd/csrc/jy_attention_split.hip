@@ -29,8 +29,10 @@ namespace jy {
 // P = hd / 16: 16-byte pieces per key row; GT = split_heads(query heads per kv head); NW
 // waves per workgroup.  One workgroup per (kv head, slice); with one slice (part ==
 // nullptr) the normalised output goes straight to a.out and no merge kernel follows.
-// (A form whose last slice workgroup of each kv head merged the slices measured slower than
-// the separate merge kernel: 8B decode after 1024 tokens 386 vs 427 tokens/s.)
+// (Two forms whose last slice workgroup of each kv head merged the slices measured slower
+// than the separate merge kernel: the partials' stores through the agent-coherent level,
+// the count and the merge's coherent loads are three serial memory round trips.  8B decode
+// after 1024 tokens: the VALU slice 386 vs 427 tokens/s; this slice 11.1 us vs 5.6 + 4.2.)
 template <int P, int GT, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4, 4))) void attn_split_kernel(
     AttnArgs a, int ns, float* __restrict__ part) {
@@ -46,10 +48,11 @@ __global__ __launch_bounds__(SPL_THREADS) __attribute__((amdgpu_waves_per_eu(4, 
     attn_slice_mfma<P, GT, 4, false>(a, 1, nullptr, blockIdx.x, 0, lds, a.nrows - 1 - (int)blockIdx.y);
 }
 
-// The merge for many slices: one workgroup per (query head, 32 output dims).  Every
-// workgroup of a head recomputes M and L from all live slices' (max, sum), loaded at once;
-// thread (d, group q) adds the weighted o_s of slices q, q+8, ... (four loads in flight),
-// and the 8 groups are added in order.
+// The merge for many slices: one workgroup per (query head, 32 output dims).  Every load
+// goes out first (thread (d, group q) holds o_s[d] of slices q, q+8, ..., q+248 in
+// registers, thread t the (max, sum) of slice t), so the merge costs one memory round trip;
+// then M and L from all live slices' (max, sum) and the weighted sum, the 8 groups added in
+// order.
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int ns, const float* __restrict__ part) {
     __shared__ float wsl[256], red[8][32], redl[4], redm[4];
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hd = a.hd, W = hd + 2;
@@ -58,6 +61,10 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int ns, c
     const int chunk = split_chunk(nk, ns);
     const int live = (nk + chunk - 1) / chunk;  // <= ns <= 256
     const float* p = part + (size_t)h * ns * W;
+    const int d = blockIdx.y * 32 + (tid & 31), q = tid >> 5;
+    float ov[32];
+#pragma unroll
+    for (int k = 0; k < 32; k++) ov[k] = q + 8 * k < live ? p[(size_t)(q + 8 * k) * W + d] : 0.0f;
     const float ms = tid < live ? p[(size_t)tid * W + hd] : -__builtin_inff();
     const float ls = tid < live ? p[(size_t)tid * W + hd + 1] : 0.0f;
     const float mw = wave_max64(ms);
@@ -70,18 +77,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int ns, c
     if (lane == 0) redl[wave] = lw;
     __syncthreads();
     const float L = (redl[0] + redl[1]) + (redl[2] + redl[3]);
-    const int d = blockIdx.y * 32 + (tid & 31), q = tid >> 5;
     float o = 0.0f;
-    int s = q;
-    for (; s + 24 < live; s += 32) {
-        const float o0 = p[(size_t)s * W + d], o1 = p[(size_t)(s + 8) * W + d];
-        const float o2 = p[(size_t)(s + 16) * W + d], o3 = p[(size_t)(s + 24) * W + d];
-        o = __builtin_fmaf(wsl[s], o0, o);
-        o = __builtin_fmaf(wsl[s + 8], o1, o);
-        o = __builtin_fmaf(wsl[s + 16], o2, o);
-        o = __builtin_fmaf(wsl[s + 24], o3, o);
-    }
-    for (; s < live; s += 8) o = __builtin_fmaf(wsl[s], p[(size_t)s * W + d], o);
+#pragma unroll
+    for (int k = 0; k < 32; k++) o = __builtin_fmaf(wsl[(q + 8 * k) & 255], ov[k], o);  // (0 past live)
     red[q][tid & 31] = o;
     __syncthreads();
     if (tid < 32) {

@@ -115,10 +115,11 @@ void launch_embed(const Q8Dev* q8, const float* f32, int hidden, const int* ids_
 void launch_rmsnorm(const float* X, float* Y, const float* w, int n, int rows, hipStream_t st);
 
 // y = W x for one token in the reference's 32-lane order; when norm_w != null the
-// kernel first applies RMSNorm (eps 1e-5) to x with those weights.  EPI_ARGMAX also
-// launches the one-workgroup pick over the per-workgroup maxima.
+// kernel first applies RMSNorm (eps 1e-5) to x with those weights, or with norm_linear
+// (the tolerance mode) scales each finished dot by the norm factor instead.  EPI_ARGMAX
+// also launches the one-workgroup pick over the per-workgroup maxima.
 void launch_matvec_q8(const Q8Dev& W, const float* x, const float* norm_w, float* out, Epi epi, const MvArgs& a,
-                      hipStream_t st);
+                      hipStream_t st, bool norm_linear = false);
 // the same y = W x with each row's dot split over waves in a free order (the tolerance
 // mode), RMSNorm applied after the dot by linearity; same epilogues
 void launch_matvec_q8_split(const Q8Dev& W, const float* x, const float* norm_w, float* out, Epi epi,

@@ -7,6 +7,11 @@
 
 namespace jy {
 
+// the RMSNorm a decode matvec applies to its input: none, the reference's prologue (the
+// normalised vector in LDS before the dot), or by linearity (x times the norm weights in
+// LDS, each finished dot times 1/sqrt(ss/K + eps): the tolerance mode)
+enum { MV_NORM_NONE = 0, MV_NORM_EXACT = 1, MV_NORM_LINEAR = 2 };
+
 // x in LDS, lane-pair major: element k sits at row (k & 31) >> 1 (the lane pair g that
 // reads it), column 2*(k >> 5) + (k & 1); XS = 2 * nbp + 4 floats per row
 __device__ __forceinline__ int xs_index(int k, int XS) {

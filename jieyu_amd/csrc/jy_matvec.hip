@@ -9,8 +9,11 @@
 // in-lane add.  Weights stream from HBM as 16 B per lane (1 KiB per wave per
 // chunk of 8 blocks) with eight chunks in flight; the activation vector sits in
 // LDS, lane-pair major.  Dequantisation is one v_fma_mix (q * fp16 scale, exact)
-// per weight.  With NORM the staged vector is RMS-normalised in LDS first (the
-// reference's rmsnorm), its weights prefetched while x is staged.
+// per weight.  With NORM == MV_NORM_EXACT the staged vector is RMS-normalised in LDS
+// first (the reference's rmsnorm), its weights prefetched while x is staged.  With
+// MV_NORM_LINEAR (the tolerance mode) the staged vector is x times the norm weights, the
+// sum of squares is taken in the same pass, and each finished dot is multiplied by
+// 1/sqrt(ss/K + eps) (RMSNorm by linearity): no step of the weight stream waits for it.
 #include <algorithm>
 
 #include "jy_matvec.h"
@@ -125,7 +128,7 @@ __device__ __forceinline__ float norm_chain(const float* pe, const float* po, in
 
 // one wave owns row groups wid, wid + TW, ... (TW = waves in the grid), `per` of
 // them; the chunk stream of consecutive row groups is pipelined without a gap.
-template <int EPI, bool NORM, int MV_U>
+template <int EPI, int NORM, int MV_U>
 __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __restrict__ x,
                                                         const float* __restrict__ nw, float* __restrict__ out,
                                                         MvArgs a, int per) {
@@ -133,6 +136,8 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
     // of the main loop aligned whatever static LDS the epilogue adds.
     extern __shared__ __align__(16) float xs[];
     __shared__ float red[18];
+    __shared__ float ssw[4];
+    constexpr bool EXN = NORM == MV_NORM_EXACT, LIN = NORM == MV_NORM_LINEAR;
     __shared__ float rowv[64];
     __shared__ int rowi[64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwv = blockDim.x >> 6;
@@ -184,6 +189,7 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
         const float4* x4 = reinterpret_cast<const float4*>(x);
         const float4* w4 = reinterpret_cast<const float4*>(nw);
         constexpr int SU = NORM ? 4 : 8;  // loads per thread per batch (x and w with NORM)
+        float ss = 0.0f;
         for (int b0 = 0; b0 < nv4; b0 += SU * blockDim.x) {
             float4 v[SU], wv[SU];
 #pragma unroll
@@ -194,24 +200,49 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
             }
             if (b0 == 0) {
                 load(wA, dA);
-                if (!NORM) load(wB, dB);
+                if (!EXN) load(wB, dB);
             }
 #pragma unroll
             for (int u = 0; u < SU; u++) {
                 const int i = b0 + tid + u * blockDim.x;
                 if (i < nv4) {
                     const int k = 4 * i;
-                    xs[xs_index(k, XS)] = v[u].x;
-                    xs[xs_index(k + 1, XS)] = v[u].y;
-                    xs[xs_index(k + 2, XS)] = v[u].z;
-                    xs[xs_index(k + 3, XS)] = v[u].w;
-                    if (NORM && i < nk4) reinterpret_cast<float4*>(nws)[i] = wv[u];
+                    float4 e = v[u];
+                    if (LIN) {
+                        ss = __builtin_fmaf(e.x, e.x, ss);
+                        ss = __builtin_fmaf(e.y, e.y, ss);
+                        ss = __builtin_fmaf(e.z, e.z, ss);
+                        ss = __builtin_fmaf(e.w, e.w, ss);
+                        e = make_float4(e.x * wv[u].x, e.y * wv[u].y, e.z * wv[u].z, e.w * wv[u].w);
+                    }
+                    xs[xs_index(k, XS)] = e.x;
+                    xs[xs_index(k + 1, XS)] = e.y;
+                    xs[xs_index(k + 2, XS)] = e.z;
+                    xs[xs_index(k + 3, XS)] = e.w;
+                    if (EXN && i < nk4) reinterpret_cast<float4*>(nws)[i] = wv[u];
                 }
             }
         }
+        if (LIN) {
+            ss += __shfl_xor(ss, 1);
+            ss += __shfl_xor(ss, 2);
+            ss += __shfl_xor(ss, 4);
+            ss += __shfl_xor(ss, 8);
+            ss += __shfl_xor(ss, 16);
+            ss += __shfl_xor(ss, 32);
+            if (lane == 0) ssw[wave] = ss;
+        }
     }
     lds_barrier();  // the weight prefetch stays in flight
-    if (NORM) {
+    float nscale = 1.0f;
+    bool nzero = false;
+    if (LIN) {
+        const float tot = (ssw[0] + ssw[1]) + (ssw[2] + ssw[3]);
+        const float den = tot / (float)K + 1e-5f;
+        nzero = !(den > 0.0f);
+        nscale = nzero ? 0.0f : 1.0f / sqrtf(den);
+    }
+    if (EXN) {
         // the second weight buffer, now that the vector is in: the weights are first
         // needed after the normalisation
         load(wB, dB);
@@ -324,7 +355,8 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
         a0 += dpp_f<0x4E>(a0);
         a1 += dpp_f<0x4E>(a1);
         const float t = a0 + a1;
-        const float y = t + dpp_f<0xB1>(t);
+        float y = t + dpp_f<0xB1>(t);
+        if (LIN) y = nzero ? 0.0f : y * nscale;
         const int row = rg * 4 + r;
         const bool own = active && g == 0 && row < W.rows;
         mv_epilogue<EPI>(y, row, own, r, W.rows, a, out, best_v, best_i);
@@ -412,11 +444,11 @@ int argmax_partials(int rows) {
     return std::max(grid, g2);
 }
 
-template <int EPI, bool NORM>
+template <int EPI, int NORM>
 static void mv_launch(const Q8Dev& W, const float* x, const float* nw, float* out, const MvArgs& a, hipStream_t st) {
     int grid, per;
-    mv_shape(W, NORM, &grid, &per);
-    const size_t lds = ((size_t)16 * (2 * W.nbp + 4) + (NORM ? (size_t)W.cols : 0)) * sizeof(float);
+    mv_shape(W, NORM != 0, &grid, &per);
+    const size_t lds = ((size_t)16 * (2 * W.nbp + 4) + (NORM == MV_NORM_EXACT ? (size_t)W.cols : 0)) * sizeof(float);
     if (W.U == 4)
         hipLaunchKernelGGL((matvec_q8_kernel<EPI, NORM, 4>), dim3(grid), dim3(256), lds, st, W, x, nw, out, a, per);
     else if (W.U == 2)
@@ -426,7 +458,7 @@ static void mv_launch(const Q8Dev& W, const float* x, const float* nw, float* ou
     if (EPI == EPI_ARGMAX) launch_argmax_finish(a, grid, st);
 }
 
-template <bool NORM>
+template <int NORM>
 static void mv_dispatch(const Q8Dev& W, const float* x, const float* nw, float* out, Epi epi, const MvArgs& a,
                         hipStream_t st) {
     switch (epi) {
@@ -440,11 +472,13 @@ static void mv_dispatch(const Q8Dev& W, const float* x, const float* nw, float* 
 }
 
 void launch_matvec_q8(const Q8Dev& W, const float* x, const float* norm_w, float* out, Epi epi, const MvArgs& a,
-                      hipStream_t st) {
-    if (norm_w)
-        mv_dispatch<true>(W, x, norm_w, out, epi, a, st);
+                      hipStream_t st, bool norm_linear) {
+    if (norm_w && norm_linear)
+        mv_dispatch<MV_NORM_LINEAR>(W, x, norm_w, out, epi, a, st);
+    else if (norm_w)
+        mv_dispatch<MV_NORM_EXACT>(W, x, norm_w, out, epi, a, st);
     else
-        mv_dispatch<false>(W, x, nullptr, out, epi, a, st);
+        mv_dispatch<MV_NORM_NONE>(W, x, nullptr, out, epi, a, st);
 }
 
 size_t matvec_lds_bytes(int cols, bool norm) {
@@ -453,7 +487,7 @@ size_t matvec_lds_bytes(int cols, bool norm) {
 }
 size_t matvec_lds_limit() { return 160 * 1024 - 2048; }
 
-template <int EPI, bool NORM>
+template <int EPI, int NORM>
 static hipError_t mv_attr() {
     hipError_t e = hipSuccess;
     for (const void* f : {reinterpret_cast<const void*>(&matvec_q8_kernel<EPI, NORM, 4>),
@@ -469,10 +503,12 @@ hipError_t matvec_init() {
     if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return e;
     if (cus > 0) g_cus = cus;
-    for (hipError_t r : {mv_attr<EPI_STORE, false>(), mv_attr<EPI_BIAS, false>(), mv_attr<EPI_RESID, false>(),
-                         mv_attr<EPI_SWIGLU, false>(), mv_attr<EPI_ROPE, false>(), mv_attr<EPI_ARGMAX, false>(),
-                         mv_attr<EPI_STORE, true>(), mv_attr<EPI_BIAS, true>(), mv_attr<EPI_RESID, true>(),
-                         mv_attr<EPI_SWIGLU, true>(), mv_attr<EPI_ROPE, true>(), mv_attr<EPI_ARGMAX, true>()})
+    for (hipError_t r : {mv_attr<EPI_STORE, 0>(), mv_attr<EPI_BIAS, 0>(), mv_attr<EPI_RESID, 0>(),
+                         mv_attr<EPI_SWIGLU, 0>(), mv_attr<EPI_ROPE, 0>(), mv_attr<EPI_ARGMAX, 0>(),
+                         mv_attr<EPI_STORE, 1>(), mv_attr<EPI_BIAS, 1>(), mv_attr<EPI_RESID, 1>(),
+                         mv_attr<EPI_SWIGLU, 1>(), mv_attr<EPI_ROPE, 1>(), mv_attr<EPI_ARGMAX, 1>(),
+                         mv_attr<EPI_STORE, 2>(), mv_attr<EPI_BIAS, 2>(), mv_attr<EPI_RESID, 2>(),
+                         mv_attr<EPI_SWIGLU, 2>(), mv_attr<EPI_ROPE, 2>(), mv_attr<EPI_ARGMAX, 2>()})
         if (r != hipSuccess && e == hipSuccess) e = r;
     return e;
 }

@@ -329,13 +329,15 @@ void ensure_part(jyhip_model* m, size_t n) {
     w.gen++;
 }
 
-// a decode Q8_0 matvec in the model's mode: the reference's 32-lane order, or the split dot
+// a decode Q8_0 matvec in the model's mode: the reference's 32-lane order, or the split dot;
+// with JYHIP_MODE_SPLIT_MV the larger matrices keep the 32-lane order with the RMSNorm
+// applied after the dot (linearity)
 void q8_matvec(const jyhip_model* m, const Q8Dev& W, const float* x, const float* norm_w, float* out, Epi epi,
                const MvArgs& a, hipStream_t st) {
     if ((m->mode & JYHIP_MODE_SPLIT_MV) && W.rows < JYHIP_SPLIT_MV_ROWS)
         launch_matvec_q8_split(W, x, norm_w, out, epi, a, st);
     else
-        launch_matvec_q8(W, x, norm_w, out, epi, a, st);
+        launch_matvec_q8(W, x, norm_w, out, epi, a, st, (m->mode & JYHIP_MODE_SPLIT_MV) != 0);
 }
 
 // the decode attention runs split across workgroups (flash-decoding)
@@ -1863,20 +1865,20 @@ JYHIP_API int jyhip_q8_gemm_time(jyhip_q8mat* q, int mr, const float* A, int ite
 
 JYHIP_API int jyhip_q8_matvec_time(jyhip_q8mat* q, const float* x, int variant, int iters, double* avg_us) {
     return guarded([&]() {
-        if (!q || !x || !avg_us || iters <= 0 || variant < 0 || variant > 3) fail("bad argument");
+        if (!q || !x || !avg_us || iters <= 0 || variant < 0 || variant > 4) fail("bad argument");
         const Q8Dev& d0 = q->copies[0];
-        if ((variant & 1) && d0.rows % 2) fail("the gate/up variant needs interleaved row pairs");
-        const bool split = variant >= 2;
+        if ((variant & 1 || variant == 4) && d0.rows % 2) fail("the gate/up variant needs interleaved row pairs");
+        const bool split = variant == 2 || variant == 3, lin = variant == 4;
         auto mv = [&](const Q8Dev& W, const float* nw, Epi epi) {
             if (split)
                 launch_matvec_q8_split(W, q->x, nw, q->y, epi, MvArgs(), q->stream);
             else
-                launch_matvec_q8(W, q->x, nw, q->y, epi, MvArgs(), q->stream);
+                launch_matvec_q8(W, q->x, nw, q->y, epi, MvArgs(), q->stream, lin);
         };
         CK(hipMemcpyAsync(q->x, x, sizeof(float) * d0.cols, hipMemcpyHostToDevice, q->stream));
         const float* nw = nullptr;
         Epi epi = EPI_STORE;
-        if (variant & 1) {  // decode's gate/up launch: RMSNorm (unit weights), SwiGLU epilogue
+        if (variant & 1 || lin) {  // decode's gate/up launch: RMSNorm (unit weights), SwiGLU epilogue
             if (!q->nw) {
                 std::vector<float> ones(d0.cols, 1.0f);
                 q->nw = dalloc<float>(d0.cols);
