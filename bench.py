@@ -40,8 +40,9 @@ METRIC = "batch-1 decode tokens/s (Q8, 8B shape) + achieved HBM GB/s vs peak"
 MODES = {"exact": 0, "fast": 7}
 SPLIT_MV_ROWS = 2048  # the fast mode's decode matvecs use the split-dot form below this many rows
 MODE_TEXT = {"exact": "bit-exact (reference arithmetic order)",
-             "fast": "fast: split-K (flash-decoding) attention, split-dot matvecs under 2048 rows, matrix-core "
-                     "(fp16 hi/lo MFMA) prompt GEMMs "
+             "fast": "fast: split-K (flash-decoding) attention with int8 / fp16 hi-lo MFMA slices, split-dot "
+                     "matvecs under 2048 rows and RMSNorm after the dot above, matrix-core (fp16 hi/lo MFMA) "
+                     "prompt GEMMs "
                      "(each layer within 1e-3 relative of the reference given the same input; deviations "
                      "compound over the stack through the int8 requantization of q/k/v; greedy ids identical "
                      "up to the first near tie)"}
@@ -88,7 +89,10 @@ def dominant_kernel_roofline(jy, d, mode, iters=64):
     """The decode step's gate/up launch (2F x hidden interleaved rows, RMSNorm, SwiGLU
     epilogue) in the benchmark's mode, timed in isolation with HIP events on its stream
     over enough copies to defeat the 256 MiB infinity cache."""
-    split = bool(MODES[mode] & 2) and 2 * d.intermediate < SPLIT_MV_ROWS  # the kernel the step uses
+    # the kernel the step uses: the split dot under SPLIT_MV_ROWS rows in the fast mode, else
+    # the 32-lane order, whose RMSNorm the fast mode applies after the dot
+    split = bool(MODES[mode] & 2) and 2 * d.intermediate < SPLIT_MV_ROWS
+    linear = bool(MODES[mode] & 2) and not split
     rows, cols = 2 * d.intermediate, d.hidden
     nbytes = q8b(rows, cols)
     copies = max(2, int(np.ceil(1.2e9 / nbytes)))
@@ -100,14 +104,15 @@ def dominant_kernel_roofline(jy, d, mode, iters=64):
     del x
     xin = np.random.default_rng(0).standard_normal(cols).astype(np.float32)
     m = jy.Q8Matrix(w, rows, cols, copies=copies)
-    us = m.time(xin, iters, variant=3 if split else 1)
+    us = m.time(xin, iters, variant=3 if split else 4 if linear else 1)
     m.close()
     algo = nbytes + 2 * cols * 4 + (rows // 2) * 4  # weights, x, norm weights, SwiGLU output
     ach = algo / (us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(),
-            "kernel": ("matvec_q8_split_kernel<EPI_SWIGLU, NORM>" if split else "matvec_q8_kernel<EPI_SWIGLU, NORM>")
-                      + " (gate/up, %d x %d)" % (rows, cols),
+            "kernel": ("matvec_q8_split_kernel<EPI_SWIGLU, NORM>" if split else
+                       "matvec_q8_kernel<EPI_SWIGLU, MV_NORM_LINEAR>" if linear else
+                       "matvec_q8_kernel<EPI_SWIGLU, MV_NORM_EXACT>") + " (gate/up, %d x %d)" % (rows, cols),
             "bytes_per_launch": algo, "avg_launch_us": round(us, 3), "launches": iters, "copies": copies}
 
 
