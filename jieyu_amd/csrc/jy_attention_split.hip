@@ -94,31 +94,46 @@ bool attn_split_supported(int nh, int nkv, int hd) {
     return nkv > 0 && nh % nkv == 0 && nh / nkv <= SPL_GMAX && (hd == 64 || hd == 128);
 }
 
-// slices of about MSL_SLICE_KEYS keys (one step per wave: a second step of a wave waits a
-// whole memory round trip, which measured slower than more workgroups and the merge
-// kernel: 16 waves x 64 keys per kv head at 1024 keys 14.1 us, 4 waves x 32 keys per slice
-// 7.0 us + 4.6 us merge)
-static constexpr int MSL_SLICE_KEYS = 128, MSL_NW = 4;
+// Slices: one 32-key step per wave.  Up to MSL_WIDE_KEYS keys (the most a launch may see),
+// workgroups of 4 waves over 128-key slices; beyond, 8 waves over 256-key slices (half the
+// slices for the merge to read: Qwen2.5-7B decode after 32768 positions 409 -> 418 tokens/s;
+// at Llama-3-8B's 1024 keys the 4-wave form is faster, 438 vs 434).  A second step of a
+// wave waits a whole memory round trip, which measured slower than more workgroups and the
+// merge kernel (16 waves x 64 keys per kv head at 1024 keys 14.1 us vs 7.0 + 4.6 us).
+static constexpr int MSL_WIDE_KEYS = 8192;
 
-int attn_split_slices(int keys) { return std::max(1, std::min(256, (keys + MSL_SLICE_KEYS - 1) / MSL_SLICE_KEYS)); }
+static int slice_keys(int max_keys) { return max_keys > MSL_WIDE_KEYS ? 256 : 128; }
+
+int attn_split_slices(int keys) {
+    const int sk = slice_keys(keys);
+    return std::max(1, std::min(256, (keys + sk - 1) / sk));
+}
 
 size_t attn_split_part_floats(int nh, int hd, int ns) { return (size_t)nh * ns * (hd + 2); }
 
-// the slices, then (more than one) the merge over (head, 32 dims)
-void launch_attention_split(const AttnArgs& a, float* part, int ns, hipStream_t st) {
-    const dim3 grid(a.nkv, ns), block(64 * MSL_NW);
-    auto k = attn_split_kernel<8, 8, MSL_NW>;
+template <int NW>
+static void split_launch(const AttnArgs& a, float* part, int ns, hipStream_t st) {
+    auto k = attn_split_kernel<8, 8, NW>;
     switch (split_heads(a.nh / a.nkv) * (a.hd == 64 ? -1 : 1)) {
-        case -1: k = attn_split_kernel<4, 1, MSL_NW>; break;
-        case -2: k = attn_split_kernel<4, 2, MSL_NW>; break;
-        case -4: k = attn_split_kernel<4, 4, MSL_NW>; break;
-        case -8: k = attn_split_kernel<4, 8, MSL_NW>; break;
-        case 1: k = attn_split_kernel<8, 1, MSL_NW>; break;
-        case 2: k = attn_split_kernel<8, 2, MSL_NW>; break;
-        case 4: k = attn_split_kernel<8, 4, MSL_NW>; break;
+        case -1: k = attn_split_kernel<4, 1, NW>; break;
+        case -2: k = attn_split_kernel<4, 2, NW>; break;
+        case -4: k = attn_split_kernel<4, 4, NW>; break;
+        case -8: k = attn_split_kernel<4, 8, NW>; break;
+        case 1: k = attn_split_kernel<8, 1, NW>; break;
+        case 2: k = attn_split_kernel<8, 2, NW>; break;
+        case 4: k = attn_split_kernel<8, 4, NW>; break;
         default: break;
     }
-    hipLaunchKernelGGL(k, grid, block, 0, st, a, ns, ns > 1 ? part : nullptr);
+    hipLaunchKernelGGL(k, dim3(a.nkv, ns), dim3(64 * NW), 0, st, a, ns, ns > 1 ? part : nullptr);
+}
+
+// the slices (the form by a.max_keys, the longest length the launch may see), then (more
+// than one) the merge over (head, 32 dims)
+void launch_attention_split(const AttnArgs& a, float* part, int ns, hipStream_t st) {
+    if (slice_keys(a.max_keys) > 128)
+        split_launch<8>(a, part, ns, st);
+    else
+        split_launch<4>(a, part, ns, st);
     if (ns > 1) hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nh, a.hd / 32), dim3(256), 0, st, a, ns, part);
 }
 
