@@ -10,14 +10,6 @@ namespace jy {
 
 static constexpr int SPL_THREADS = 256;  // one key per thread per tile
 static constexpr int SPL_GMAX = 8;       // query heads per kv head this form handles
-static constexpr int SPL_MIN_CHUNK = 16;
-
-// keys per slice for nk live keys over ns slices (a multiple of 16), and the slices used
-__host__ __device__ __forceinline__ int split_chunk(int nk, int ns) {
-    int c = (nk + ns - 1) / ns;
-    c = (c + SPL_MIN_CHUNK - 1) / SPL_MIN_CHUNK * SPL_MIN_CHUNK;
-    return c < SPL_MIN_CHUNK ? SPL_MIN_CHUNK : c;
-}
 
 // query heads per kv head as a kernel instance computes them: 1, 2, 4 or 8 (the heads
 // past the real count carry a zero query and are never written out)
@@ -33,9 +25,6 @@ __device__ __forceinline__ float wave_sum64(float v) {
     return (read_lane(v, 0) + read_lane(v, 16)) + (read_lane(v, 32) + read_lane(v, 48));
 }
 
-// e^x from the hardware exp2 (v_exp_f32): about 1 ulp plus the rounding of x*log2(e),
-// a relative error under 1e-6 for the |x| <= 20 that carry weight here
-__device__ __forceinline__ float exp_hw(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 
 // Sum of each group of LP adjacent lanes (LP 4 or 8) into the group's last lane, by DPP row
 // shifts within rows of 16 lanes (exact: integer adds)

@@ -162,6 +162,24 @@ __device__ __forceinline__ void act_st(float* p, float v) {
         *p = v;
 }
 
+// keys per slice of the split attention for nk live keys over ns slices (a multiple of 16)
+static constexpr int SPL_MIN_CHUNK = 16;
+__host__ __device__ __forceinline__ int split_chunk(int nk, int ns) {
+    int c = (nk + ns - 1) / ns;
+    c = (c + SPL_MIN_CHUNK - 1) / SPL_MIN_CHUNK * SPL_MIN_CHUNK;
+    return c < SPL_MIN_CHUNK ? SPL_MIN_CHUNK : c;
+}
+
+// e^x from the hardware exp2 (v_exp_f32): about 1 ulp plus the rounding of x*log2(e),
+// a relative error under 1e-6 for the |x| <= 20 that carry weight here
+__device__ __forceinline__ float exp_hw(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+#else
+    return x;  // host pass: never called
+#endif
+}
+
 // maximum over the 64 lanes of a wave, in every lane (fmaxf: order-independent for
 // the non-negative / finite values it is used on)
 __device__ __forceinline__ float wave_max64(float v) {

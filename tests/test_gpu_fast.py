@@ -44,11 +44,21 @@ MODELS = {
     "llama-hd128-g4": dict(name="llama3-8b", num_layers=2, hidden=2048, num_heads=16, num_kv_heads=4, head_dim=128,
                            intermediate=3072, vocab_size=4000),
 }
+# the other query heads per kv head the attention slices specialise on (1, 2 and a full 8;
+# the models above have 4 and 7): forward_cached only (per-layer tolerance)
+HEAD_GROUPS = {
+    "mha-hd64": dict(name="llama3-8b", num_layers=2, hidden=256, num_heads=4, num_kv_heads=4, head_dim=64,
+                     intermediate=768, vocab_size=1500),
+    "g2-hd128-bias": dict(name="qwen2.5-7b", num_layers=2, hidden=1024, num_heads=8, num_kv_heads=4, head_dim=128,
+                          intermediate=2048, vocab_size=2000),
+    "g8-hd128": dict(name="llama3-8b", num_layers=2, hidden=2048, num_heads=16, num_kv_heads=2, head_dim=128,
+                     intermediate=2048, vocab_size=2000),
+}
 
 
 def make(oracle_lib, key):
     from jieyu_amd.model import Synth, synth_config
-    spec = dict(MODELS[key])
+    spec = dict(MODELS[key] if key in MODELS else HEAD_GROUPS[key])
     name = spec.pop("name")
     return Synth(oracle_lib, synth_config(name, **spec))
 
@@ -134,7 +144,7 @@ MODES = {"SPLIT_ATTN": 1, "SPLIT_MV": 2, "MFMA_PREFILL": 4, "FAST": 7, "PERSIST"
 
 
 @pytest.mark.parametrize("mode_name", list(MODES))
-@pytest.mark.parametrize("key", list(MODELS))
+@pytest.mark.parametrize("key", list(MODELS) + list(HEAD_GROUPS))
 def test_forward_cached_within_tolerance(jy, oracle_lib, key, mode_name):
     """A prompt chunk then decode steps through forward_cached: every layer's output within
     1e-3 of the oracle's, the first layer's int8 K/V bytes equal to the oracle's."""
