@@ -59,8 +59,11 @@ JYHIP_API void jyhip_model_free(jyhip_model* model);
  * tolerance (per-layer fp32 hidden states within 1e-3 relative, identical greedy ids):
  *   JYHIP_MODE_SPLIT_ATTN  decode attention split across workgroups over the keys
  *                          (flash-decoding): exact int8 quantisation and int32 q.k, the
- *                          softmax sum and p.v accumulated per slice and merged; prompt
- *                          rows in the same arithmetic, one workgroup per kv head and row;
+ *                          softmax sum and p.v accumulated per slice and merged; up to
+ *                          1024 keys one kernel whose workgroups each take all the keys
+ *                          and 16 output dims (the sum and p.v per wave, merged in the
+ *                          workgroup); prompt rows in the same arithmetic, one workgroup
+ *                          per kv head and row;
  *   JYHIP_MODE_SPLIT_MV    decode Q8_0 matvecs of fewer than JYHIP_SPLIT_MV_ROWS rows with
  *                          each row's dot split across waves; larger matrices keep the exact
  *                          kernel's dot order, which measured faster there (e.g. 4096 x

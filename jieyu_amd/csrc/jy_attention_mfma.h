@@ -46,20 +46,22 @@ static constexpr int MSL_STEP = 32;  // keys per step of a wave
 // second 16 keys a further 64 bytes on, so that the 8 rows one 16-lane group reads together
 // for a p.v operand (keys 4g .. 4g+3 and 16+4g .. 16+4g+3) start in 8 distinct 16-byte
 // bank slots (every 128 bytes wrap the LDS banks) and a row's pieces follow at +16 each
-template <int HD>
+// (VW: the V bytes per key the workgroup holds, hd or one 16-dim tile; a 16-byte row needs
+// no padding for that, the 64 bytes after row 16 suffice)
+template <int VW>
 __host__ __device__ constexpr int msl_row(int r) {
-    return r * (HD + 16) + 64 * (r >> 4);
+    return r * (VW + (VW >= 64 ? 16 : 0)) + 64 * (r >> 4);
 }
-template <int HD>
+template <int VW>
 __host__ __device__ constexpr int msl_tile_bytes() {
-    return msl_row<HD>(MSL_STEP - 1) + HD;
+    return msl_row<VW>(MSL_STEP - 1) + VW;
 }
+__host__ __device__ constexpr int msl_max(int a, int b) { return a > b ? a : b; }
 
-template <int HD, int NW>
+template <int HD, int NW, int VW = HD>
 struct MslLds {
-    static constexpr int TB = (msl_tile_bytes<HD>() + 15) / 16 * 16;
-    static constexpr int OWS = HD + 4;  // a head's o row (padded: the 8 heads' rows on distinct banks)
-    static_assert(TB >= SPL_GMAX * OWS * 4, "a wave's o fits its tile");
+    static constexpr int OWS = VW + 4;  // a head's o row (padded: the 8 heads' rows on distinct banks)
+    static constexpr int TB = msl_max((msl_tile_bytes<VW>() + 15) / 16 * 16, SPL_GMAX * OWS * 4);
     union {
         int8_t vt[NW][TB];            // V rows of the wave's step (msl_row)
         float ow[NW][TB / 4];         // the wave's o per head column < GT: [c][dim]
@@ -76,12 +78,14 @@ struct MslLds {
 
 // the global loads of one step: the lane's K bytes of its key in each 16-key tile, its
 // pieces of the V rows, and one scale (lanes < 32: k scale of key l, others: v scale of
-// key l - 32)
-template <int HD>
+// key l - 32) as the raw bits of two loads, one of them out of range (zero).  The two are
+// combined where the step uses them: combined where they are loaded, the OR would be
+// placed at the loop's end and wait there for the loads of the steps after it.
+template <int HD, int NV>
 struct MslRegs {
     int4 k[2][HD / 64];
-    int4 v[HD / 32];
-    float s;
+    int4 v[NV];
+    unsigned ks, vs;
 };
 
 // x, or y where take
@@ -90,17 +94,25 @@ __device__ __forceinline__ int4 own_mix(int4 x, int4 y, bool take) {
     return make_int4((x.x & ~m) | (y.x & m), (x.y & ~m) | (y.y & m), (x.z & ~m) | (y.z & m), (x.w & ~m) | (y.w & m));
 }
 
-template <int P, int GT, int NW, bool COH>
+// DSP: the workgroup computes output dims VW dsl .. VW dsl + VW - 1 (VW = hd / DSP) of its
+// heads; with DSP > 1 every workgroup of a kv head runs the q.k and softmax of all its keys
+// (redundantly) and only its dims of p.v, so that one kernel covers the whole range without
+// a merge.  PF: steps of loads a wave keeps in flight (2: the next step's loads go out a
+// whole step ahead, for waves that take several steps).
+template <int P, int GT, int NW, bool COH, int DSP = 1, int PF = 1>
 __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float* __restrict__ part, int kvh, int s,
-                                                MslLds<P * 16, NW>& L, int prow = 0) {
+                                                MslLds<P * 16, NW, P * 16 / DSP>& L, int prow = 0, int dsl = 0) {
     constexpr int HD = P * 16, ST = MSL_STEP;
+    constexpr int VW = HD / DSP;  // V bytes per key this workgroup reads
     constexpr int DPL = HD / 4;   // K bytes per lane and key
     constexpr int KST = HD / 32;  // MFMA k-steps of q.k per tile
-    constexpr int DT = HD / 16;   // dim tiles of p.v
-    constexpr int PPK = HD / 16;  // 16-byte pieces per key row
+    constexpr int DT = VW / 16;   // dim tiles of p.v
+    constexpr int PPK = VW / 16;  // 16-byte pieces per key row
     constexpr int KPI = 64 / PPK; // keys per V load instruction
-    constexpr int NV = HD / 32;   // V loads per lane and step
+    constexpr int NV = msl_max(1, ST * PPK / 64);  // V loads per lane and step
+    constexpr bool VPART = KPI * NV > ST;          // lanes past the step's keys load no V
     static_assert(2 * GT <= 16, "head columns");
+    static_assert(VW % 16 == 0 && HD % VW == 0 && PF >= 1 && PF <= 3, "shape");
     static_assert(SPL_GMAX * HD / 16 <= NW * 64, "a prompt row's query pieces: one per thread");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -132,22 +144,22 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
     const __amdgpu_buffer_rsrc_t rks = __builtin_amdgcn_make_buffer_rsrc(KSc, (short)0, j1 * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t rvs = __builtin_amdgcn_make_buffer_rsrc(VSc, (short)0, j1 * 4, 0x00020000);
     constexpr int FAR = 0x7ffffff0;
-    auto load_vs = [&](MslRegs<HD>& r, int base) {
+    auto load_vs = [&](MslRegs<HD, NV>& r, int base) {
 #pragma unroll
         for (int u = 0; u < NV; u++) {
-            const int j = base + KPI * u + lane / PPK;
+            const int kr = KPI * u + lane / PPK, j = base + kr;
+            const bool skip = j == own || (VPART && kr >= ST);
             const i4_t x = __builtin_bit_cast(i4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                        rv, j == own ? FAR : j * HD + 16 * (lane % PPK), 0, 0));
+                                                        rv, skip ? FAR : j * HD + VW * dsl + 16 * (lane % PPK), 0, 0));
             r.v[u] = make_int4(x[0], x[1], x[2], x[3]);
         }
         const int j = base + (lane & 31);
         const int o = j == own ? FAR : 4 * j;
         // (b32 buffer loads return the raw bits)
-        const unsigned ks = __builtin_amdgcn_raw_buffer_load_b32(rks, lane < 32 ? o : FAR, 0, 0);
-        const unsigned vs = __builtin_amdgcn_raw_buffer_load_b32(rvs, lane < 32 ? FAR : o, 0, 0);
-        r.s = __builtin_bit_cast(float, ks | vs);  // one of the two is out of range: zero
+        r.ks = __builtin_amdgcn_raw_buffer_load_b32(rks, lane < 32 ? o : FAR, 0, 0);
+        r.vs = __builtin_amdgcn_raw_buffer_load_b32(rvs, lane < 32 ? FAR : o, 0, 0);
     };
-    auto load_k = [&](MslRegs<HD>& r, int base) {
+    auto load_k = [&](MslRegs<HD, NV>& r, int base) {
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             const int j = base + 16 * t + col;
@@ -184,9 +196,12 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
         if (tid < G * HD / 16) qp = reinterpret_cast<const int4*>(a.q8 + qrow * HD)[tid];
         if (tid < G) qsp = a.qsc[qrow + tid];
     }
-    MslRegs<HD> cur;  // (all masked for a wave without keys)
-    load_k(cur, j0 + ST * wave);
-    load_vs(cur, j0 + ST * wave);
+    MslRegs<HD, NV> rg[PF];  // (all masked for a wave without keys)
+#pragma unroll
+    for (int p = 0; p < PF; p++) {
+        load_k(rg[p], j0 + ST * (wave + NW * p));
+        load_vs(rg[p], j0 + ST * (wave + NW * p));
+    }
 
     // q (and with the new position its k and v) quantised per head, as attn_slice does
 #pragma unroll
@@ -216,7 +231,7 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
     for (int i = G * HD + tid; i < GT * HD; i += NW * 64) L.q8[i / HD][i % HD] = 0;
     if (tid < GT - G) L.qsc[G + tid] = 0.0f;
     lds_barrier();  // (the key loads stay in flight)
-    if (holds_new) {  // kv_pack_q8 of the new position, appended by the workgroup that holds it
+    if (holds_new && dsl == 0) {  // kv_pack_q8 of the new position, appended by the workgroup that holds it
         for (int d = tid; d < HD; d += NW * 64) {
             K[(size_t)pos * HD + d] = L.knew[d];
             V[(size_t)pos * HD + d] = L.vnew[d];
@@ -255,18 +270,21 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
     float pc = 8192.0f;
     bool first = true;
 
-    for (int base = j0 + ST * wave; base < j1; base += ST * NW) {
+    // one step of the wave: keys base .. base + 31, its loads in r; r then takes the loads of
+    // the step PF steps on
+    auto step = [&](MslRegs<HD, NV>& cur, const int base) {
         // stage the step: V pieces into the tile, the scales; in the one step that holds
         // the token's own key, that key from the workgroup's copy (substituted by bit masks:
         // a select between an LDS load and the registers would be turned into a load through
         // a selected pointer, forcing the registers to memory)
         const bool has_own = own >= base && own < base + ST;
-        float sv = cur.s;
+        float sv = __builtin_bit_cast(float, cur.ks | cur.vs);
         if (has_own) {
 #pragma unroll
             for (int u = 0; u < NV; u++) {
                 const int r = KPI * u + lane / PPK;
-                cur.v[u] = own_mix(cur.v[u], *reinterpret_cast<const int4*>(L.vnew + 16 * (lane % PPK)), base + r == own);
+                cur.v[u] = own_mix(cur.v[u], *reinterpret_cast<const int4*>(L.vnew + VW * dsl + 16 * (lane % PPK)),
+                                   base + r == own);
             }
             const int m = base + (lane & 31) == own ? -1 : 0;
             const int sn = __builtin_bit_cast(int, L.kvs_new[lane < 32 ? 0 : 1]);
@@ -282,9 +300,9 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
 #pragma unroll
         for (int u = 0; u < NV; u++) {
             const int r = KPI * u + lane / PPK;
-            *reinterpret_cast<int4*>(vt + msl_row<HD>(r) + 16 * (lane % PPK)) = cur.v[u];
+            if (!VPART || r < ST) *reinterpret_cast<int4*>(vt + msl_row<VW>(r) + 16 * (lane % PPK)) = cur.v[u];
         }
-        load_vs(cur, base + ST * NW);  // the next step's, independent of this one's math
+        load_vs(cur, base + ST * NW * PF);  // a later step's, independent of this one's math
 
         // the v scales' power of two (o rescaled when the largest v scale's exponent moves),
         // then the scales into LDS: k scales, and v scales times 2^c
@@ -320,7 +338,7 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
                 d[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ka, qa, d[t], 0, 0, 0);
             }
         }
-        load_k(cur, base + ST * NW);
+        load_k(cur, base + ST * NW * PF);
         float sc[2][4], vs[2][4];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
@@ -377,15 +395,27 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
 #pragma unroll
         for (int t = 0; t < DT; t++) {
             const i2_t vb = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-                (__attribute__((address_space(3))) i2_t*)(vt + msl_row<HD>(trk) + 16 * t + 8 * (col & 1)));
+                (__attribute__((address_space(3))) i2_t*)(vt + msl_row<VW>(trk) + 16 * t + 8 * (col & 1)));
             const h8_t va = q8_to_h8((uint32_t)vb.x, (uint32_t)vb.y);
             acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, acc[t], 0, 0, 0);
         }
+    };
+    // the wave's steps: PF at a time with no path that skips one (the compiler's wait counts
+    // merge over every path into the loop head: a path with fewer loads issued would make a
+    // step wait for the loads of the steps after it), then the remainder
+    const int nst = j1 - j0 > ST * wave ? (j1 - j0 - ST * wave + ST * NW - 1) / (ST * NW) : 0;
+    int k = 0;
+    for (; k + PF <= nst; k += PF) {
+#pragma unroll
+        for (int p = 0; p < PF; p++) step(rg[p], j0 + ST * (wave + NW * (k + p)));
     }
+#pragma unroll
+    for (int p = 0; p + 1 < PF; p++)
+        if (k + p < nst) step(rg[p], j0 + ST * (wave + NW * (k + p)));
 
     // the wave's totals: the sum over the 4 groups; o of head column c < GT plus its remainder
     // column c + GT, into the wave's tile as [c][dim] rows of OWS floats
-    constexpr int OWS = MslLds<HD, NW>::OWS;
+    constexpr int OWS = MslLds<HD, NW, VW>::OWS;
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
     float* ow = L.u.ow[wave];
@@ -404,28 +434,38 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
     __syncthreads();
 
     // merge of the waves (log2 units): M = max m_w, factors f_w = 2^(m_w - M) 2^-c_w,
-    // L = sum 2^(m_w - M) l_w, o = sum f_w o_w; M goes out in natural units
-    if (tid < G) {
-        float M = L.mw[0][tid];
-        for (int w = 1; w < NW; w++) M = fmaxf(M, L.mw[w][tid]);
-        float lsum = 0.0f;
-        for (int w = 0; w < NW; w++) {
-            const float f = __builtin_amdgcn_exp2f(L.mw[w][tid] - M);  // 0 for a wave without keys
-            lsum = __builtin_fmaf(f, L.lw[w][tid], lsum);
-            L.fw[w][tid] = f * L.cw[w];
+    // L = sum 2^(m_w - M) l_w, o = sum f_w o_w; M goes out in natural units.  Thread
+    // (head g, wave w) = (tid / NW, tid % NW) of the first two waves (G NW <= 128), the max
+    // and the sum over w as butterflies within groups of NW lanes.
+    static_assert(SPL_GMAX * NW <= 128 && 64 % NW == 0, "merge lanes");
+    if (tid < 128) {
+        const int w = tid % NW, g = tid / NW;
+        const bool ok = g < G;
+        const float mw = ok ? L.mw[w][g] : 0.0f;
+        float M = mw;
+#pragma unroll
+        for (int k = 1; k < NW; k <<= 1) M = fmaxf(M, __shfl_xor(M, k));
+        const float f = ok ? __builtin_amdgcn_exp2f(mw - M) : 0.0f;  // 0 for a wave without keys
+        float lsum = f * (ok ? L.lw[w][g] : 0.0f);
+#pragma unroll
+        for (int k = 1; k < NW; k <<= 1) lsum += __shfl_xor(lsum, k);
+        if (ok) {
+            L.fw[w][g] = f * L.cw[w];
+            if (w == 0) {
+                L.mg[g] = M * 0.6931471805599453f;
+                L.lg[g] = lsum;
+            }
         }
-        L.mg[tid] = M * 0.6931471805599453f;
-        L.lg[tid] = lsum;
     }
     __syncthreads();
     const int W = HD + 2;
-    for (int o = tid; o < G * HD; o += NW * 64) {
-        const int g = o / HD, dd = o - g * HD;
+    for (int o = tid; o < G * VW; o += NW * 64) {
+        const int g = o / VW, dd = o - g * VW;
         float t = 0.0f;
-#pragma unroll 4
+#pragma unroll
         for (int w = 0; w < NW; w++) t = __builtin_fmaf(L.fw[w][g], L.u.ow[w][g * OWS + dd], t);
         if (!part) {
-            a.out[((size_t)(a.row0 + prow) * nh + kvh * G + g) * HD + dd] = t / L.lg[g];
+            a.out[((size_t)(a.row0 + prow) * nh + kvh * G + g) * HD + VW * dsl + dd] = t / L.lg[g];
             continue;
         }
         float* out = part + ((size_t)(kvh * G + g) * ns + s) * W;

@@ -33,11 +33,23 @@ namespace jy {
 // than the separate merge kernel: the partials' stores through the agent-coherent level,
 // the count and the merge's coherent loads are three serial memory round trips.  8B decode
 // after 1024 tokens: the VALU slice 386 vs 427 tokens/s; this slice 11.1 us vs 5.6 + 4.2.)
+// waves per workgroup of the whole-range form (8 measured faster than 16 at 1024 keys, 10.3
+// vs 12.0 us, and alike at 512)
+static constexpr int WW = 8;
+
 template <int P, int GT, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4, 4))) void attn_split_kernel(
     AttnArgs a, int ns, float* __restrict__ part) {
     __shared__ MslLds<P * 16, NW> lds;
     attn_slice_mfma<P, GT, NW, false>(a, ns, part, blockIdx.x, blockIdx.y, lds);
+}
+
+// short ranges: one workgroup per (kv head, 16-dim tile of the output) over all the keys,
+// WW waves, two steps of loads in flight per wave; no merge kernel
+template <int P, int GT>
+__global__ __launch_bounds__(64 * WW) __attribute__((amdgpu_waves_per_eu(4, 4))) void attn_whole_kernel(AttnArgs a) {
+    __shared__ MslLds<P * 16, WW, 16> lds;
+    attn_slice_mfma<P, GT, WW, false, P, 2>(a, 1, nullptr, blockIdx.x, 0, lds, 0, blockIdx.y);
 }
 
 // prompt rows: one workgroup per (kv head, row), the row's whole key range as one slice,
@@ -135,6 +147,31 @@ void launch_attention_split(const AttnArgs& a, float* part, int ns, hipStream_t 
     else
         split_launch<4>(a, part, ns, st);
     if (ns > 1) hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nh, a.hd / 32), dim3(256), 0, st, a, ns, part);
+}
+
+// Up to this many keys a decode row takes the whole-range form (one launch, 64 workgroups at
+// Llama-3-8B's shape), beyond it the slices and the merge.  Every workgroup of a kv head
+// runs the q.k and softmax of all its keys, so the form's time grows with the keys about
+// twice as fast as the split form's (Llama-3-8B shape: 6.7 us at 512 keys, 10.3 at 1024,
+// 13.7 at 2048 vs 5.9 + 4.7 for the slices and merge at 1024); Qwen2.5-0.5B decode
+// after 512 positions 1340 -> 1405 tokens/s.
+static constexpr int ATT_WHOLE_KEYS = 1024;
+
+int att_whole_keys() { return ATT_WHOLE_KEYS; }
+
+void launch_attention_whole(const AttnArgs& a, hipStream_t st) {
+    auto k = attn_whole_kernel<8, 8>;
+    switch (split_heads(a.nh / a.nkv) * (a.hd == 64 ? -1 : 1)) {
+        case -1: k = attn_whole_kernel<4, 1>; break;
+        case -2: k = attn_whole_kernel<4, 2>; break;
+        case -4: k = attn_whole_kernel<4, 4>; break;
+        case -8: k = attn_whole_kernel<4, 8>; break;
+        case 1: k = attn_whole_kernel<8, 1>; break;
+        case 2: k = attn_whole_kernel<8, 2>; break;
+        case 4: k = attn_whole_kernel<8, 4>; break;
+        default: break;
+    }
+    hipLaunchKernelGGL(k, dim3(a.nkv, a.hd / 16), dim3(64 * WW), 0, st, a);
 }
 
 void launch_attention_prefill_split(const AttnArgs& a, hipStream_t st) {

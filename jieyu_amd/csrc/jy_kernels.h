@@ -190,6 +190,10 @@ bool attn_split_supported(int nh, int nkv, int hd);
 int attn_split_slices(int keys);
 size_t attn_split_part_floats(int nh, int hd, int ns);
 void launch_attention_split(const AttnArgs& a, float* part, int ns, hipStream_t st);
+// the same token row attending at most att_whole_keys() keys: one kernel, one workgroup per
+// (kv head, 16 output dims) over all the keys, output to a.out
+int att_whole_keys();
+void launch_attention_whole(const AttnArgs& a, hipStream_t st);
 // prompt rows in the same arithmetic (q8 / qsc from launch_rope_pack, keys in the cache,
 // a.nrows rows from a.row0): one workgroup per (kv head, row), output to a.out
 void launch_attention_prefill_split(const AttnArgs& a, hipStream_t st);

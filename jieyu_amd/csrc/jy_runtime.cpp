@@ -345,6 +345,10 @@ bool split_attention(const jyhip_model* m) {
     return (m->mode & JYHIP_MODE_SPLIT_ATTN) && m->wtype == JY_Q8_0 && attn_split_supported(m->nh, m->nkv, m->hd);
 }
 
+// the longest sequence whose decode step takes the short-context attention: the split mode's
+// whole-range kernel, or the exact mode's one-kernel form
+int short_keys(const jyhip_model* m) { return split_attention(m) ? att_whole_keys() : att_short_keys(); }
+
 // slice partials (floats) a decode step attending up to max_keys keys takes: the separate
 // kernels' slice count or the persistent kernel's, whichever is larger (either may run)
 size_t part_need(const jyhip_model* m, int max_keys) {
@@ -826,7 +830,9 @@ void run_decode_layers(jyhip_model* m, Workspace& w, const KVDev& kv, const int*
             q8_matvec(m, D.qkv, w.X, D.rms1, w.qkv, EPI_ROPE, qa, st);
             at.fused = true;
             at.qkv = w.qkv;
-            if (split_attention(m))
+            if (split_attention(m) && (state ? short_ctx : pos0 + 1 <= att_whole_keys()))
+                launch_attention_whole(at, st);
+            else if (split_attention(m))
                 launch_attention_split(at, w.part, attn_split_slices(max_keys), st);
             else
                 launch_attention(at, st);
@@ -1033,7 +1039,7 @@ void embed_rows(jyhip_model* m, int id0, const int* state, int seq, float* X) {
 }
 
 // one decode step: embed ids[len-1], layers, final norm, lm_head, greedy pick
-// short_ctx: the step will only be replayed at sequence lengths up to att_short_keys()
+// short_ctx: the step will only be replayed at sequence lengths up to short_keys(m)
 void decode_step(jyhip_model* m, const KVDev& kv, int max_keys, bool greedy, float rp, int prompt_len, int neos,
                  bool short_ctx) {
     Workspace& w = m->ws;
@@ -1099,7 +1105,7 @@ struct Session {
     unsigned rng = 12345u;
     jyhip_token_cb cb = nullptr;
     void* ud = nullptr;
-    // the decode step as a graph: [1] for sequence lengths up to att_short_keys() (one
+    // the decode step as a graph: [1] for sequence lengths up to short_keys(m) (one
     // attention kernel), [0] past it; each captured the first time a step call needs it
     hipGraphExec_t exec[2] = {nullptr, nullptr};
     unsigned exec_gen[2] = {0, 0};  // the workspace generation each graph was captured on
@@ -1246,7 +1252,7 @@ struct Session {
     }
 
     // the graph for a step over a sequence of `length` tokens (it attends `length` keys)
-    hipGraphExec_t graph_for(int length) const { return exec[length <= att_short_keys() ? 1 : 0]; }
+    hipGraphExec_t graph_for(int length) const { return exec[length <= short_keys(m) ? 1 : 0]; }
 
     // up to n more tokens; returns how many were produced
     int step(int n) {
@@ -1263,8 +1269,8 @@ struct Session {
                 exec[i] = nullptr;
             }
         // the steps run at lengths len .. len+n-1: capture what they need up front
-        if (len <= att_short_keys() && !exec[1]) capture(1);
-        if (len + n - 1 > att_short_keys() && !exec[0]) capture(0);
+        if (len <= short_keys(m) && !exec[1]) capture(1);
+        if (len + n - 1 > short_keys(m) && !exec[0]) capture(0);
         hipStream_t st = m->stream;
         CK(hipEventRecord(ev[2], st));
         int made = 0;

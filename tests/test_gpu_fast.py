@@ -217,9 +217,11 @@ def prefill_cache(oracle_lib, d, pre, max_seq, kv):
     return prefill_kv(oracle_lib, d, pre, max_seq, kv)
 
 
-# slices of 16 keys (40), one tile per slice (700 .. 20000), two tiles per slice past
-# 256 slices of 256 keys (70000)
-@pytest.mark.parametrize("pre", [40, 700, 3000, 20000, 70000])
+# the whole-range kernel up to 1024 keys (40 .. 1023: most of its 8 waves idle, one to
+# four steps per wave, the last step partial or full), the slices and the merge past it:
+# 128-key slices of 4 waves (3000, 5000), 256-key slices of 8 waves (20000), and past 256
+# such slices two steps for some waves (70000)
+@pytest.mark.parametrize("pre", [40, 700, 1023, 3000, 5000, 20000, 70000])
 def test_split_attention_long_context(jy, oracle_lib, pre):
     """Decode steps over a cache pre-filled with packed N(0,1) K/V: hidden states within
     tolerance, the appended K/V bytes of the first layer equal to the oracle's."""
@@ -253,7 +255,7 @@ def test_split_attention_long_context(jy, oracle_lib, pre):
 
 
 @pytest.mark.parametrize("mode_name", ["FAST", "PERSIST"])
-@pytest.mark.parametrize("pre,n_new", [(700, 24), (6000, 12)])
+@pytest.mark.parametrize("pre,n_new", [(700, 24), (1018, 12), (6000, 12)])
 def test_fast_resume_over_long_cache(jy, oracle_lib, pre, n_new, mode_name):
     """The graph-replayed decode step in MODE_FAST over a pre-filled cache: greedy ids equal
     the oracle driven token by token (embedding row, forward_cached, lm_head, first maximum)."""
