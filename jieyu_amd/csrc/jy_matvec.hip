@@ -425,13 +425,22 @@ void launch_argmax_finish(const MvArgs& a, int np, hipStream_t st) {
 static int g_cus = 256;
 
 // launch shape: 4 waves per workgroup, at most 4 workgroups per CU; each wave owns
-// `per` row groups so the prologue (staging, RMSNorm) is paid once per workgroup
-static void mv_shape(const Q8Dev& W, bool norm, int* grid, int* per) {
+// `per` row groups so the prologue (staging, RMSNorm) is paid once per workgroup.  With
+// two row groups per wave the grid is every slot (4 workgroups per CU) and the row groups
+// are strided over all its waves, so every CU gets the same share: sized to the row groups
+// instead, 28672 x 4096 took 896 workgroups, 4 on half the CUs and 3 on the others, and ran
+// 27.7 us against 26.2 (Llama-3-8B decode 436.5 -> 446.3 tokens/s).  With three or more
+// (Qwen2.5-7B's 37888-row gate/up, the lm_heads) the full grid measured slightly slower
+// (Qwen2.5-7B decode 412.9 vs 409.5, Qwen2.5-0.5B 1416.5 vs 1410.8): its extra workgroups
+// stage the vector again for less work each.
+static void mv_shape(const Q8Dev& W, bool exn, int* grid, int* per) {
     const int nwv = 4;
     const int groups = (W.rows + 3) / 4;
     const int max_waves = 4 * g_cus * nwv;
     *per = (groups + max_waves - 1) / max_waves;
     *grid = (groups + nwv * *per - 1) / (nwv * *per);
+    const size_t lds = ((size_t)16 * (2 * W.nbp + 4) + (exn ? (size_t)W.cols : 0)) * sizeof(float);
+    if (*per == 2 && 4 * lds <= matvec_lds_limit()) *grid = max_waves / nwv;
 }
 
 // workgroups of an lm_head launch (one partial maximum each), normalising or not
@@ -447,7 +456,7 @@ int argmax_partials(int rows) {
 template <int EPI, int NORM>
 static void mv_launch(const Q8Dev& W, const float* x, const float* nw, float* out, const MvArgs& a, hipStream_t st) {
     int grid, per;
-    mv_shape(W, NORM != 0, &grid, &per);
+    mv_shape(W, NORM == MV_NORM_EXACT, &grid, &per);
     const size_t lds = ((size_t)16 * (2 * W.nbp + 4) + (NORM == MV_NORM_EXACT ? (size_t)W.cols : 0)) * sizeof(float);
     if (W.U == 4)
         hipLaunchKernelGGL((matvec_q8_kernel<EPI, NORM, 4>), dim3(grid), dim3(256), lds, st, W, x, nw, out, a, per);
