@@ -44,11 +44,16 @@ MODELS = {
     "llama-hd128-g4": dict(name="llama3-8b", num_layers=2, hidden=2048, num_heads=16, num_kv_heads=4, head_dim=128,
                            intermediate=3072, vocab_size=4000),
 }
-# the other query heads per kv head the attention slices specialise on (1, 2 and a full 8;
-# the models above have 4 and 7): forward_cached only (per-layer tolerance)
+# the other query heads per kv head the attention slices specialise on (1, 2 and a full 8
+# at both head sizes; the models above have 4 and 7): forward_cached only (per-layer
+# tolerance)
 HEAD_GROUPS = {
     "mha-hd64": dict(name="llama3-8b", num_layers=2, hidden=256, num_heads=4, num_kv_heads=4, head_dim=64,
                      intermediate=768, vocab_size=1500),
+    "mha-hd128": dict(name="llama3-8b", num_layers=2, hidden=512, num_heads=4, num_kv_heads=4, head_dim=128,
+                      intermediate=1024, vocab_size=1500),
+    "g2-hd64": dict(name="qwen2.5-0.5b", num_layers=2, hidden=512, num_heads=8, num_kv_heads=4, head_dim=64,
+                    intermediate=1024, vocab_size=1500),
     "g2-hd128-bias": dict(name="qwen2.5-7b", num_layers=2, hidden=1024, num_heads=8, num_kv_heads=4, head_dim=128,
                           intermediate=2048, vocab_size=2000),
     "g8-hd128": dict(name="llama3-8b", num_layers=2, hidden=2048, num_heads=16, num_kv_heads=2, head_dim=128,
