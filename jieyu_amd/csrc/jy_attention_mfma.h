@@ -5,10 +5,10 @@
 // int32 q.k dot, score = (float)dot * ((ks * qsc) * (1/sqrtf(hd))), weights e^(score - max);
 // the softmax sum and the p.v accumulation are reordered and the weights carried at 22 bits.
 //
-// Work split.  A workgroup of NW waves (4 or 16) takes one (kv head, slice of keys); wave w
-// takes the slice's steps w, w+NW, ... of 32 keys and keeps its own running (max, sum, o)
-// per query head, with no workgroup barrier in the key loop; the waves' results are merged
-// through LDS at the end.
+// Work split.  A workgroup of NW waves (4 or 8) takes one (kv head, slice of keys), and
+// with DSP > 1 one tile of hd/DSP output dims over all the keys; wave w takes the slice's
+// steps w, w+NW, ... of 32 keys and keeps its own running (max, sum, o) per query head, with
+// no workgroup barrier in the key loop; the waves' results are merged through LDS at the end.
 //
 // One step of a wave (lane l: column c = l % 16, group g = l / 16):
 //  q.k  v_mfma_i32_16x16x32_i8 per 16-key tile and 32 dims, keys as the 16 rows (A: lane l

@@ -9,17 +9,18 @@
 // per slice of keys and are merged afterwards, so their fp32 rounding differs from the
 // reference's single ascending chains (a few ulp of the result).
 //
-// Two kernels per layer.
+// Two kernels per layer (the matrix-core slice of jy_attention_mfma.h in both):
 //  1. attn_split_kernel: one workgroup per (kv head, slice of keys).  It quantises the
-//     group's query heads, walks its keys in tiles of 256 (K and V rows in 16-byte pieces
-//     across adjacent lanes, V through LDS to the p.v stage), and keeps a running
-//     (max, sum, o[hd]) per query head of the group, rescaled per tile.  The workgroup whose slice holds the token's own
-//     position quantises its k and v, appends them to the cache and uses its own copy.
-//  2. attn_combine_kernel: one workgroup per query head merges the slices:
+//     group's query heads, walks its keys in 32-key steps per wave, and keeps a running
+//     (max, sum, o[hd]) per query head of the group.  The workgroup whose slice holds the
+//     token's own position appends its k and v to the cache; every workgroup uses its own
+//     copy of them.
+//  2. attn_combine_kernel: one workgroup per (query head, 32 dims) merges the slices:
 //     M = max m_s, L = sum l_s e^(m_s - M), o = sum o_s e^(m_s - M) / L.
 // Slices are a fixed count per launch (sized for the longest length a graph replay may
 // see); the keys per slice follow the live length on the device, so a replayed step
-// uses as many slices as that length needs.
+// uses as many slices as that length needs.  Up to ATT_WHOLE_KEYS keys one kernel instead:
+// attn_whole_kernel, one workgroup per (kv head, 16 output dims) over all the keys.
 #include <algorithm>
 
 #include "jy_attention_mfma.h"
