@@ -1,7 +1,7 @@
-"""CPU checkers for jieyu's decode path.  TEST INFRASTRUCTURE ONLY.
+"""CPU oracles for jieyu's decode path.  TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
-this package, and only as the checker / the timed CPU baseline.  The product
+this package, and only as the oracle / the timed CPU baseline.  The product
 (jieyu_amd, libjieyu_amd.so) never imports or links it.
 
   Oracle  -- oracle/_build/libjyoracle.so, the C restatement (jy_oracle.c)

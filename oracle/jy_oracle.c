@@ -1,7 +1,7 @@
 /*
  * jy_oracle.c — CPU oracle for jieyu's decode path.  TEST INFRASTRUCTURE ONLY
- * (the checker; never part of the product).  See jy_oracle.h for how it is
- * pinned.
+ * (what the GPU path is checked against; never part of the product).  See
+ * jy_oracle.h for how it is pinned.
  *
  * Built with -ffp-contract=off: every fused multiply-add below is an explicit
  * fmaf(), every other operation is rounded on its own, in the order the

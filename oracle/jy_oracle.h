@@ -1,7 +1,8 @@
 /*
  * jy_oracle.h — CPU oracle for jieyu's decode path.  TEST INFRASTRUCTURE:
  * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it,
- * as the checker.  The product (libjieyu_amd.so) never links or calls it.
+ * as the reference results the GPU path is checked against.  The product
+ * (libjieyu_amd.so) never links or calls it.
  *
  * A clean-room C restatement of the arithmetic of jieyu's default x86 path
  * (AVX2 + FMA, GCC -O3), operation for operation, so its results are
