@@ -32,20 +32,51 @@ __device__ __forceinline__ int xs_index(int k, int XS) {
 //   ARGMAX  out[row] = y, and the first maximum so far into (best_v, best_i)
 // With COH the activations are read and written through to the agent-coherent level
 // (act_ld / act_st), for a kernel whose workgroups hand them to each other.
+// The per-row operands an epilogue reads from memory (the bias; the residual; RoPE's cos
+// and sin at the token's position), loaded by mv_preload when the row group's weight stream
+// starts, so that the launch's tail waits for no memory round trip after the last chunk.
+struct MvPre {
+    float bias = 0.0f, resid = 0.0f, c = 0.0f, s = 0.0f;
+};
+
+template <int EPI, bool COH = false>
+__device__ __forceinline__ MvPre mv_preload(int row, bool own, int r, const MvArgs& a, const float* out) {
+    MvPre p;
+    if (EPI == EPI_BIAS || EPI == EPI_ROPE) {
+        if (a.aux && own) p.bias = a.aux[row];
+    }
+    if (EPI == EPI_RESID) {
+        if (own) p.resid = act_ld<COH>(out + row);
+    }
+    if (EPI == EPI_ROPE) {
+        if (own && !(r & 1) && row < (a.nh + a.nkv) * a.hd) {
+            const int hd = a.hd, half = hd >> 1;
+            const int m = (row - row / hd * hd) >> 1;
+            const int pos = a.state ? a.state[0] - 1 : a.pos0;
+            p.c = a.cos_t[(size_t)pos * half + m];
+            p.s = a.sin_t[(size_t)pos * half + m];
+        }
+    }
+    return p;
+}
+
+// pre: the row's operands from mv_preload, or nullptr to read them here
 template <int EPI, bool COH = false>
 __device__ __forceinline__ void mv_epilogue(float y, int row, bool own, int r, int rows, const MvArgs& a,
-                                            float* __restrict__ out, float& best_v, int& best_i) {
+                                            float* __restrict__ out, float& best_v, int& best_i,
+                                            const MvPre* pre = nullptr) {
+    const MvPre p = pre ? *pre : mv_preload<EPI, COH>(row, own, r, a, out);
     if (EPI == EPI_STORE) {
         if (own) act_st<COH>(out + row, y);
     } else if (EPI == EPI_BIAS) {
-        if (own) act_st<COH>(out + row, y + a.aux[row]);
+        if (own) act_st<COH>(out + row, y + p.bias);
     } else if (EPI == EPI_RESID) {
-        if (own) act_st<COH>(out + row, act_ld<COH>(out + row) + y);
+        if (own) act_st<COH>(out + row, p.resid + y);
     } else if (EPI == EPI_SWIGLU) {
         const float up = __shfl_xor(y, 16);
         if (own && !(r & 1) && row + 1 < rows) act_st<COH>(out + (row >> 1), silu_ref(y) * up);
     } else if (EPI == EPI_ROPE) {
-        const float yb = a.aux ? y + (own ? a.aux[row] : 0.0f) : y;
+        const float yb = a.aux ? y + (own ? p.bias : 0.0f) : y;
         const float partner = __shfl_xor(yb, 16);
         const int qk_rows = (a.nh + a.nkv) * a.hd;
         if (own) {
@@ -54,8 +85,7 @@ __device__ __forceinline__ void mv_epilogue(float y, int row, bool own, int r, i
             } else if (!(r & 1)) {
                 const int hd = a.hd, half = hd >> 1;
                 const int head = row / hd, m = (row - head * hd) >> 1;
-                const int pos = a.state ? a.state[0] - 1 : a.pos0;
-                const float c = a.cos_t[(size_t)pos * half + m], s = a.sin_t[(size_t)pos * half + m];
+                const float c = p.c, s = p.s;
                 const float y0 = __builtin_fmaf(yb, c, -(partner * s));
                 const float y1 = __builtin_fmaf(yb, s, partner * c);
                 int dst = m;

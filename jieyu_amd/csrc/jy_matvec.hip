@@ -330,6 +330,9 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
     for (int it = 0; it < per; it++) {
         const int rg = wid + it * TW;
         const bool active = rg < groups;
+        const int row = rg * 4 + r;
+        const bool own = active && g == 0 && row < W.rows;
+        const MvPre pre = mv_preload<EPI>(row, own, r, a, out);
         float a0 = 0.0f, a1 = 0.0f;
         for (int ch = 0; ch < nchp; ch += 2 * MV_U) {
             if (active) {
@@ -357,9 +360,7 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(Q8Dev W, const float* __
         const float t = a0 + a1;
         float y = t + dpp_f<0xB1>(t);
         if (LIN) y = nzero ? 0.0f : y * nscale;
-        const int row = rg * 4 + r;
-        const bool own = active && g == 0 && row < W.rows;
-        mv_epilogue<EPI>(y, row, own, r, W.rows, a, out, best_v, best_i);
+        mv_epilogue<EPI>(y, row, own, r, W.rows, a, out, best_v, best_i, &pre);
     }
 
     if (EPI == EPI_ARGMAX) mv_argmax_partial(best_v, best_i, g, r, wave, nwv, rowv, rowi, a);

@@ -151,6 +151,12 @@ __global__ __launch_bounds__(256) void matvec_q8_split_kernel(Q8Dev W, const flo
     int best_i = 0x7fffffff;
     float acc = 0.0f;
     int par = 0;
+    // the epilogue's per-row operands of a pass, requested when its stream starts
+    auto preload = [&](int p) {
+        const int rg = rg_of(p), row = rg * 4 + r;
+        return ks == 0 ? mv_preload<EPI>(row, rg < groups && g == 0 && row < W.rows, r, a, out) : MvPre();
+    };
+    MvPre pre = preload(0);
     // one finished row-group slice: fold the 16 lanes of each row, then the SK slices
     auto finish = [&](int p) {
         acc += dpp_f<0x128>(acc);  // l + 8
@@ -173,8 +179,9 @@ __global__ __launch_bounds__(256) void matvec_q8_split_kernel(Q8Dev W, const flo
             const int row = rg * 4 + r;
             const bool own = rg < groups && g == 0 && row < W.rows;
             if (NORM) y = nzero ? 0.0f : y * nscale;
-            mv_epilogue<EPI>(y, row, own, r, W.rows, a, out, best_v, best_i);
+            mv_epilogue<EPI>(y, row, own, r, W.rows, a, out, best_v, best_i, &pre);
         }
+        if (p + 1 < per) pre = preload(p + 1);
         acc = 0.0f;
     };
 
