@@ -119,14 +119,20 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
     const int col = lane & 15, grp = lane >> 4;
     const int nh = a.nh, nkv = a.nkv, G = nh / nkv;  // G <= GT
     const bool fused = a.fused;
-    const int pos = a.state ? a.state[0] - 1 : a.start_pos + a.row0 + prow;
-    const int nk = pos + 1;
+    // (the length as loaded, no arithmetic in the branch: the wait for it then falls at its
+    // first use, after the first loads)
+    const int nk = a.state ? a.state[0] : a.start_pos + a.row0 + prow + 1;
+    const int pos = nk - 1;
     const int chunk = split_chunk(nk, ns);
     const int j0 = s * chunk;
-    if (j0 >= nk) return false;  // whole workgroup: a slice past the live length
+    // a slice past the live length: the whole workgroup leaves (slice 0 always holds keys,
+    // and nothing before its first loads waits for the length)
+    if (s != 0 && j0 >= nk) return false;
     const int j1 = min(nk, j0 + chunk);
-    const bool holds_new = fused && j1 == nk;
-    const int own = fused ? pos : -1;  // the key taken from the workgroup's copy
+    const bool holds_new = fused && (ns == 1 || j1 == nk);  // (one slice ends at the token)
+    // the key taken from the workgroup's copy: only where it lies in the slice (a step of
+    // the slice before may reach past its end onto it, where it is masked like any other)
+    const int own = holds_new ? pos : -1;
     const size_t head = (size_t)a.layer * nkv + kvh;
     int8_t* K = a.kv.k + head * a.kv.max_seq * HD;
     int8_t* V = a.kv.v + head * a.kv.max_seq * HD;
@@ -137,36 +143,45 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
     // a step's global loads, in two parts so that each reuses the registers of the part of
     // the previous step already consumed: the V pieces and the scale (free once staged in
     // LDS), then the K bytes (free once the q.k MFMAs have read them).  Buffer loads whose
-    // range ends at the slice's last key: a key past it, and the token's own key (given an
-    // offset past every range), read as zeros without a branch.
-    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(K, (short)0, j1 * HD, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(V, (short)0, j1 * HD, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rks = __builtin_amdgcn_make_buffer_rsrc(KSc, (short)0, j1 * 4, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rvs = __builtin_amdgcn_make_buffer_rsrc(VSc, (short)0, j1 * 4, 0x00020000);
+    // range ends at the slice's last key (a key past it reads as zeros and costs no memory
+    // traffic), except the first steps of a whole range: their range is the cache's capacity,
+    // so that their addresses do not wait for the live length.  A key past the slice is
+    // masked in the step (no scale, no score), and the token's own key, read before it is
+    // appended, is replaced there by the workgroup's copy.  A piece past the step's keys
+    // gets an offset past every range (zeros).
+    struct Rs {
+        __amdgpu_buffer_rsrc_t k, v, ks, vs;
+    };
+    auto rsrc = [&](int keys) {
+        return Rs{__builtin_amdgcn_make_buffer_rsrc(K, (short)0, keys * HD, 0x00020000),
+                  __builtin_amdgcn_make_buffer_rsrc(V, (short)0, keys * HD, 0x00020000),
+                  __builtin_amdgcn_make_buffer_rsrc(KSc, (short)0, keys * 4, 0x00020000),
+                  __builtin_amdgcn_make_buffer_rsrc(VSc, (short)0, keys * 4, 0x00020000)};
+    };
+    const Rs rsl = rsrc(j1), rs0 = ns == 1 ? rsrc(a.kv.max_seq) : rsl;
     constexpr int FAR = 0x7ffffff0;
-    auto load_vs = [&](MslRegs<HD, NV>& r, int base) {
+    auto load_vs = [&](MslRegs<HD, NV>& r, int base, const Rs& R) {
 #pragma unroll
         for (int u = 0; u < NV; u++) {
             const int kr = KPI * u + lane / PPK, j = base + kr;
-            const bool skip = j == own || (VPART && kr >= ST);
+            const bool skip = VPART && kr >= ST;
             const i4_t x = __builtin_bit_cast(i4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                        rv, skip ? FAR : j * HD + VW * dsl + 16 * (lane % PPK), 0, 0));
+                                                        R.v, skip ? FAR : j * HD + VW * dsl + 16 * (lane % PPK), 0, 0));
             r.v[u] = make_int4(x[0], x[1], x[2], x[3]);
         }
-        const int j = base + (lane & 31);
-        const int o = j == own ? FAR : 4 * j;
+        const int o = 4 * (base + (lane & 31));
         // (b32 buffer loads return the raw bits)
-        r.ks = __builtin_amdgcn_raw_buffer_load_b32(rks, lane < 32 ? o : FAR, 0, 0);
-        r.vs = __builtin_amdgcn_raw_buffer_load_b32(rvs, lane < 32 ? FAR : o, 0, 0);
+        r.ks = __builtin_amdgcn_raw_buffer_load_b32(R.ks, lane < 32 ? o : FAR, 0, 0);
+        r.vs = __builtin_amdgcn_raw_buffer_load_b32(R.vs, lane < 32 ? FAR : o, 0, 0);
     };
-    auto load_k = [&](MslRegs<HD, NV>& r, int base) {
+    auto load_k = [&](MslRegs<HD, NV>& r, int base, const Rs& R) {
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             const int j = base + 16 * t + col;
 #pragma unroll
             for (int u = 0; u < HD / 64; u++) {
                 const i4_t x = __builtin_bit_cast(i4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                            rk, j == own ? FAR : j * HD + DPL * grp + 16 * u, 0, 0));
+                                                            R.k, j * HD + DPL * grp + 16 * u, 0, 0));
                 r.k[t][u] = make_int4(x[0], x[1], x[2], x[3]);
             }
         }
@@ -199,8 +214,8 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
     MslRegs<HD, NV> rg[PF];  // (all masked for a wave without keys)
 #pragma unroll
     for (int p = 0; p < PF; p++) {
-        load_k(rg[p], j0 + ST * (wave + NW * p));
-        load_vs(rg[p], j0 + ST * (wave + NW * p));
+        load_k(rg[p], j0 + ST * (wave + NW * p), rs0);
+        load_vs(rg[p], j0 + ST * (wave + NW * p), rs0);
     }
 
     // q (and with the new position its k and v) quantised per head, as attn_slice does
@@ -279,6 +294,7 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
         // a selected pointer, forcing the registers to memory)
         const bool has_own = own >= base && own < base + ST;
         float sv = __builtin_bit_cast(float, cur.ks | cur.vs);
+        if (base + ST > j1 && base + (lane & 31) >= j1) sv = 0.0f;  // a key past the slice
         if (has_own) {
 #pragma unroll
             for (int u = 0; u < NV; u++) {
@@ -302,7 +318,7 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
             const int r = KPI * u + lane / PPK;
             if (!VPART || r < ST) *reinterpret_cast<int4*>(vt + msl_row<VW>(r) + 16 * (lane % PPK)) = cur.v[u];
         }
-        load_vs(cur, base + ST * NW * PF);  // a later step's, independent of this one's math
+        load_vs(cur, base + ST * NW * PF, rsl);  // a later step's, independent of this one's math
 
         // the v scales' power of two (o rescaled when the largest v scale's exponent moves),
         // then the scales into LDS: k scales, and v scales times 2^c
@@ -338,7 +354,7 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
                 d[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ka, qa, d[t], 0, 0, 0);
             }
         }
-        load_k(cur, base + ST * NW * PF);
+        load_k(cur, base + ST * NW * PF, rsl);
         float sc[2][4], vs[2][4];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
