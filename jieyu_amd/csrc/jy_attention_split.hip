@@ -13,8 +13,8 @@
 //  1. attn_split_kernel: one workgroup per (kv head, slice of keys).  It quantises the
 //     group's query heads, walks its keys in 32-key steps per wave, and keeps a running
 //     (max, sum, o[hd]) per query head of the group.  The workgroup whose slice holds the
-//     token's own position appends its k and v to the cache; every workgroup uses its own
-//     copy of them.
+//     token's own position appends its k and v to the cache and takes them from its own
+//     copy, not from the cache row it is writing.
 //  2. attn_combine_kernel: one workgroup per (query head, 32 dims) merges the slices:
 //     M = max m_s, L = sum l_s e^(m_s - M), o = sum o_s e^(m_s - M) / L.
 // Slices are a fixed count per launch (sized for the longest length a graph replay may
