@@ -259,16 +259,20 @@ def test_split_attention_long_context(jy, oracle_lib, pre):
     s.close()
 
 
+# (1490, 12) in a 4096-position cache: the session's slices are sized for the capacity (32
+# of them), so at 1491..1502 keys each holds 48 and the last one 3..14: the slice before it
+# ends in a partial step whose keys past its end include the token's own (masked there;
+# only the last slice takes the token's key from its copy)
 @pytest.mark.parametrize("mode_name", ["FAST", "PERSIST"])
-@pytest.mark.parametrize("pre,n_new", [(700, 24), (1018, 12), (6000, 12)])
-def test_fast_resume_over_long_cache(jy, oracle_lib, pre, n_new, mode_name):
+@pytest.mark.parametrize("pre,n_new,cap", [(700, 24, 0), (1018, 12, 0), (1490, 12, 4096), (6000, 12, 0)])
+def test_fast_resume_over_long_cache(jy, oracle_lib, pre, n_new, cap, mode_name):
     """The graph-replayed decode step in MODE_FAST over a pre-filled cache: greedy ids equal
     the oracle driven token by token (embedding row, forward_cached, lm_head, first maximum)."""
-    say(f"MODE_FAST session resume over a {pre}-position cache")
+    say(f"MODE_FAST session resume over a {pre}-position cache (capacity {cap or pre + n_new + 8})")
     s = make(oracle_lib, "hd128")
     d = s.desc
     H, V, hd = d.hidden, d.vocab_size, d.head_dim
-    max_seq = pre + n_new + 8
+    max_seq = cap or pre + n_new + 8
     cos, sin = rope_tables(oracle_lib, max_seq, hd, d.rope_theta)
     g = jy.GpuModel(d, max_seq)
     g.mode = MODES[mode_name]
