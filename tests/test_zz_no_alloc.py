@@ -35,20 +35,25 @@ def small_model(oracle_lib, name, **kw):
     return Synth(oracle_lib, synth_config(name, **kw))
 
 
+# the tolerance mode as well: its split attention keeps the slices' partials in the
+# workspace, here the static array (both runs use the same kernels in the same order)
+@pytest.mark.parametrize("fast", [False, True])
 @pytest.mark.parametrize("spec", [
     dict(name="llama3-8b", num_layers=2, hidden=512, num_heads=8, num_kv_heads=2, head_dim=64, intermediate=1408,
          vocab_size=3000),
     dict(name="tiny-f32", num_layers=2, vocab_size=4000),
 ])
-def test_noalloc_matches_forward_cached(jy, oracle_lib, spec):
+def test_noalloc_matches_forward_cached(jy, oracle_lib, spec, fast):
     spec = dict(spec)
     name = spec.pop("name")
-    say(f"forward_cached_noalloc vs forward_cached ({name})")
+    say(f"forward_cached_noalloc vs forward_cached ({name}, {'fast' if fast else 'exact'} mode)")
     s = small_model(oracle_lib, name, **spec)
     d = s.desc
     L, H = d.num_layers, d.hidden
     max_seq = 40
     g = jy.GpuModel(d, max_seq)
+    if fast:
+        g.mode = jy.MODE_FAST
     kv_a, kv_b = g.kv(max_seq), g.kv(max_seq)
     rng = np.random.default_rng(11)
     start = 0
