@@ -218,6 +218,38 @@ def test_generate_fast_ids_match_oracle(jy, oracle_lib, key, mode_name):
     assert np.array_equal(ids, ref[:n]), f"gpu {ids[len(prompt):]} vs oracle {ref[len(prompt):n]}"
 
 
+@pytest.mark.parametrize("key", ["llama-like", "qwen-like"])
+def test_fast_penalty_and_eos(jy, oracle_lib, key):
+    """The tolerance mode with the repetition penalty applied on the device (greedy, rp 1.3)
+    and with an EOS id that ends the generation early: ids equal to the oracle's."""
+    say(f"fast mode: repetition penalty and EOS ({key})")
+    s = make(oracle_lib, key)
+    d = s.desc
+    prompt = np.arange(5, 14, dtype=np.int32)
+    max_seq = 64
+    cos, sin = rope_tables(oracle_lib, max_seq, d.head_dim, d.rope_theta)
+
+    def ref(max_new, rp=1.0, eos=None):
+        out = np.zeros(max_seq + 1, np.int32)
+        eos_a = None if eos is None else np.asarray(eos, np.int32)
+        n = oracle_lib.jyo_generate(C.byref(d), ptr(prompt), len(prompt), ptr(eos_a), 0 if eos is None else len(eos),
+                                    ptr(cos), ptr(sin), max_seq, max_new, 0.0, rp, ptr(out), None, None)
+        return out[:n].copy()
+
+    g = jy.GpuModel(d, max_seq)
+    g.mode = MODES["FAST"]
+    want = ref(20, rp=1.3)
+    ids, _ = g.generate(prompt, 20, repetition_penalty=1.3)
+    assert np.array_equal(ids, want), f"rp 1.3: gpu {ids[len(prompt):]} vs oracle {want[len(prompt):]}"
+    eos_tok = int(ref(30)[len(prompt) + 5])
+    want = ref(30, eos=[eos_tok])
+    ids, _ = g.generate(prompt, 30, eos=[eos_tok])
+    assert np.array_equal(ids, want), f"eos {eos_tok}: gpu {ids[len(prompt):]} vs oracle {want[len(prompt):]}"
+    assert len(want) < len(prompt) + 30
+    g.close()
+    s.close()
+
+
 def prefill_cache(oracle_lib, d, pre, max_seq, kv):
     return prefill_kv(oracle_lib, d, pre, max_seq, kv)
 
