@@ -103,7 +103,9 @@ __device__ __forceinline__ bool attn_slice(const AttnArgs& a, int ns, float* __r
     if (j0 >= nk) return false;  // whole workgroup: a slice past the live length
     const int j1 = min(nk, j0 + chunk);
     const bool holds_new = fused && j1 == nk;  // this slice ends at the token's own position
-    const int own = fused ? pos : -1;          // the key taken from the workgroup's copy
+    // the key taken from the workgroup's copy, only where it lies in the slice (a tile of the
+    // slice before may reach past its end onto it, where it is masked like any other)
+    const int own = holds_new ? pos : -1;
     const size_t head = (size_t)a.layer * nkv + kvh;
     int8_t* K = a.kv.k + head * a.kv.max_seq * HD;
     int8_t* V = a.kv.v + head * a.kv.max_seq * HD;
