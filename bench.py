@@ -225,11 +225,12 @@ def pack_kv_rows(x):
     return q, sc
 
 
-# (name, prompt tokens, new tokens, positions pre-filled in the cache before the prompt)
-OTHER_CONFIGS = (("tiny-f32", 16, 128, 0), ("qwen2.5-0.5b", 512, 256, 0), ("qwen2.5-7b", 1, 128, 32768))
+# (name, prompt tokens, new tokens, positions pre-filled in the cache before the prompt,
+#  reference CPU decode steps timed at the workload's positions: a bounded sample)
+OTHER_CONFIGS = (("tiny-f32", 16, 128, 0, 48), ("qwen2.5-0.5b", 512, 256, 0, 24), ("qwen2.5-7b", 1, 128, 32768, 6))
 
 
-def other_config(jy, name, prompt_len, n_new, prefilled, mode=0):
+def other_config(jy, name, prompt_len, n_new, prefilled, cpu_steps=0, mode=0):
     """Decode rate of one more model workload through the same session path.  With
     `prefilled` > 0 the cache first holds that many positions of N(0,1) K/V (one draw,
     packed like the cache's own rows, written to every layer), and the session resumes
@@ -282,9 +283,46 @@ def other_config(jy, name, prompt_len, n_new, prefilled, mode=0):
     if kv is not None:
         kv.close()
     g.close()
+    if cpu_steps:
+        # the reference's own decode step on the host at this workload's positions (outside
+        # every timed GPU region); the first step is untimed
+        t = time.time()
+        res["cpu_baseline"] = cpu_baseline(d, p0, cpu_steps + 1, (p0, p0 + steps - 1))
+        res["cpu_baseline"].pop("cpu", None)
+        log(f"  {name}: CPU baseline {res['cpu_baseline']['value']} tokens/s ({time.time() - t:.1f} s)")
     syn.close()
     log(f"  {name}: {res} (model built in {gen_s:.1f} s)")
     return res
+
+
+def attention_workload(name, pre, rows=10):
+    """A workload for counter profiles of the decode attention at long context: one layer
+    of `name` over a cache pre-filled to `pre` positions with one N(0,1) draw of K / V
+    (packed like the cache's own rows), `rows` fast-mode decode rows at position `pre`
+    by direct launches (forward_cached, no graph)."""
+    import jieyu_amd as jy
+    from jieyu_amd.model import Synth, synth_config
+    syn = Synth(jy.lib(), synth_config(name, num_layers=1, vocab_size=1000))
+    d = syn.desc
+    g = jy.GpuModel(d, pre + 64)
+    g.mode = MODES["fast"]
+    kv = g.kv(pre + 64)
+    nkv, hd = d.num_kv_heads, d.head_dim
+    f = np.zeros(pre * nkv * hd, np.float32)
+    jy.lib().jysyn_normal_fill(9, 1000, 1.0, ptr(f), f.size)
+    k8, ks = pack_kv_rows(f.reshape(pre, nkv, hd))
+    jy.lib().jysyn_normal_fill(9, 1001, 1.0, ptr(f), f.size)
+    v8, vs = pack_kv_rows(f.reshape(pre, nkv, hd))
+    del f
+    kv.write(0, 0, k8, ks, v8, vs)
+    x = np.random.default_rng(0).standard_normal((1, d.hidden)).astype(np.float32)
+    for _ in range(rows):
+        kv.set_len(pre)
+        g.forward_cached(kv, x, pre)
+    log(f"{name}: {rows} decode rows of one layer at position {pre} done")
+    kv.close()
+    g.close()
+    syn.close()
 
 
 def copy_calibration(mb):
@@ -401,6 +439,9 @@ def main():
                     help="steps then timed in the other mode, on the same session (0: skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="only run a plain device copy of MB MiB (rocprofv3 counter scaling) and exit")
+    ap.add_argument("--attention-workload", type=int, default=0, metavar="POSITIONS",
+                    help="only run a profiling workload and exit: one layer of --config over a cache "
+                         "pre-filled to POSITIONS, 10 fast-mode decode rows by direct launches")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this decode path is single-device (no sharding or collectives); "
@@ -409,6 +450,9 @@ def main():
 
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.attention_workload:
+        attention_workload(args.config, args.attention_workload)
         return
 
     import jieyu_amd as jy
@@ -497,7 +541,8 @@ def main():
     others = None
     if not args.no_other:
         log("other model workloads ...")
-        others = {name: other_config(jy, name, *rest, mode=MODES[args.mode]) for name, *rest in OTHER_CONFIGS}
+        others = {name: other_config(jy, name, pl, nn, pre, 0 if args.no_cpu else cs, mode=MODES[args.mode])
+                  for name, pl, nn, pre, cs in OTHER_CONFIGS}
 
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,

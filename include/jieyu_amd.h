@@ -123,7 +123,9 @@ JYHIP_API int jyhip_forward_cached(jyhip_model* model, jyhip_kv* kv, float* X, i
 
 /* jyhip_forward_cached (layer_out aside) without any device allocation.  It has no
  * counterpart in the reference: it is for callers that cannot allocate device memory
- * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * (tight serving loops, harnesses that forbid hipMalloc).  Like jyhip_forward_cached it
+ * copies X from and back to the host and waits for the model's stream, so it cannot be
+ * recorded into a caller's HIP graph: it allocates nothing, it is not capturable.
  * Same arguments, checks and results as jyhip_forward_cached with layer_out == NULL.
  * Its workspace is one static array of JYHIP_NOALLOC_SCRATCH_BYTES in each GPU's memory,
  * held until the process ends; a call whose rows and keys need more (a long prompt, a
@@ -169,6 +171,14 @@ JYHIP_API int jyhip_session_remaining(const jyhip_session* s);
 JYHIP_API int jyhip_session_len(const jyhip_session* s);
 JYHIP_API int jyhip_session_ids(const jyhip_session* s, int* out, int cap);
 JYHIP_API int jyhip_session_stats(jyhip_session* s, jyhip_stats* stats);
+/* Diagnostics of a session's captured decode graph `which` (0: the graph for lengths past
+ * the short-context threshold, 1: up to it); no counterpart in the reference.  Each graph is
+ * checked when it is captured (kernel nodes only, one dependency chain, launch shapes within
+ * the device's limits, every device buffer the step can address a live allocation on the
+ * model's device) and before each jyhip_session_step (no such buffer replaced since capture).
+ * Writes info[0] = nodes, info[1] = edges, info[2] = buffers checked; returns 1, 0 when that
+ * graph has not been captured, -1 on error (a failed check). */
+JYHIP_API int jyhip_session_graph_info(const jyhip_session* s, int which, long long* info);
 JYHIP_API void jyhip_session_end(jyhip_session* s);
 
 /* Isolated Q8_0 matvec (decode kernel): y[n] = W[n][:] . x for a [rows][cols/32]x34

@@ -78,6 +78,7 @@ def lib():
     _proto(L, "jyhip_forward_cached_noalloc", I, P, P, P, I, I)
     _proto(L, "jyhip_generate", I, P, P, P, I, P, I, I, I, F, F, P, TOKEN_CB, P, P, C.POINTER(Stats))
     _proto(L, "jyhip_session_begin", P, P, P, P, I, P, I, I, I, F, F)
+    _proto(L, "jyhip_session_graph_info", I, P, I, P)
     _proto(L, "jyhip_session_resume", P, P, P, P, I, P, I, I, I, F, F)
     _proto(L, "jyhip_session_step", I, P, I)
     _proto(L, "jyhip_session_remaining", I, P)
@@ -287,6 +288,13 @@ class Session:
         st = Stats()
         _check(self._lib.jyhip_session_stats(self.h, C.byref(st)))
         return st
+
+    def graph_info(self, which):
+        """(nodes, edges, buffers checked) of captured decode graph `which` (0: past the
+        short-context threshold, 1: up to it), None if not captured; raises on a failed check."""
+        info = (C.c_longlong * 3)()
+        r = _check(self._lib.jyhip_session_graph_info(self.h, which, info))
+        return tuple(info) if r == 1 else None
 
     def close(self):
         if self.h:

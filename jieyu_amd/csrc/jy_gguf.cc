@@ -957,7 +957,7 @@ vector<OutTensor> plan_tensors(const GFile& g, uint8_t out_dtype, bool quant, Gg
 // what would stop model.bf from being written, found before anything is: the entry
 // checks of bfile's writer (check_tensor_meta, bfile.h:258-273), then per tensor in output
 // order a source range past the end of the file or a type with no dequantization
-void check_tensors(const GFile& g, const vector<OutTensor>& ts) {
+void check_tensors(const GFile& g, const vector<OutTensor>& ts, int hd) {
     if (align64(64 + 104 * (uint64_t)ts.size()) > 0xFFFFFFFFull) throw runtime_error("bfile: 张量太多");
     for (const OutTensor& o : ts) {
         if (o.name.empty() || o.name.size() > 63) throw runtime_error("bfile: 张量名长度必须 1..63: " + o.name);
@@ -973,6 +973,16 @@ void check_tensors(const GFile& g, const vector<OutTensor>& ts) {
             throw runtime_error("bfile: 写张量失败: " + o.name);
         if (!o.raw && !dequant_known(o.src->type))
             throw runtime_error(string("gguf: 还没写这种量化的反量化 ") + gtype_name(o.src->type));
+    }
+    // perm_row reads source rows h * hd + k for k < hd of every head: the q / k rows (or a
+    // bias's elements) must be whole heads of an even head_dim, or it would read past the
+    // tensor.  jieyu's converter does not check this (gguf_convert.h:67-70 indexes blindly).
+    for (const OutTensor& o : ts) {
+        if (!o.pairs) continue;
+        const uint64_t n = o.src->shape.size() == 2 ? o.src->shape[1] : o.src->shape[0];
+        if (hd <= 0 || hd % 2 || n % (uint64_t)hd)
+            throw runtime_error("gguf: " + o.src->name + " 的行数不是偶数 head_dim(" + std::to_string(hd) +
+                                ") 的整数倍");
     }
 }
 
@@ -1047,7 +1057,7 @@ GgufResult gguf_convert(const std::string& src, const std::string& out_dir, uint
         for (size_t i = 0; i < skipped.size() && i < 6; i++) printf(" %s", skipped[i].c_str());
         printf(skipped.size() > 6 ? " ...\n" : "\n");
     }
-    check_tensors(g, tensors);
+    check_tensors(g, tensors, r.head_dim);
     const Meta* tokens = g.meta("tokenizer.ggml.tokens");
     if (!tokens || tokens->strs.empty()) throw runtime_error("gguf: 没有 tokenizer.ggml.tokens，抽不出词表");
     r.eos_id = (int)(g.meta("tokenizer.ggml.eos_token_id") ? g.meta("tokenizer.ggml.eos_token_id")->as_int(-1) : -1);

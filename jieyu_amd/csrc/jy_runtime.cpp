@@ -1089,6 +1089,123 @@ int host_pick(jyhip_model* m, std::vector<float>& logits, const std::vector<int>
     }
     return next;
 }
+// ---- captured decode graphs: what a replay addresses, checked on the host
+//
+// A replayed graph keeps the device addresses its kernels were captured with.  At capture
+// the graph is walked (kernel nodes only, one chain of dependencies as a single stream
+// records it, launch shapes within the device's limits), and every device buffer the decode
+// step can address is listed and checked to be a live device allocation on the model's
+// device.  Before each run of replays the list is compared with the buffers the model and
+// cache hold then, so a buffer replaced since capture (a grown workspace, a new cache) is
+// found on the host instead of being read on the device.
+
+// every device buffer a decode step of m over kv may address (a superset: unused ones too)
+std::vector<const void*> step_buffers(const jyhip_model* m, const KVDev& kv) {
+    std::vector<const void*> b;
+    auto add = [&](const void* p) {
+        if (p) b.push_back(p);
+    };
+    auto q8 = [&](const Q8Dev& q) {
+        add(q.qs);
+        add(q.d);
+    };
+    auto dw = [&](const DevW& w) {
+        add(w.dense);
+        q8(w.q8);
+        add(w.kq.nib);
+        add(w.kq.hi);
+        add(w.kq.hdr);
+        add(w.kq.dm);
+    };
+    const Workspace& w = m->ws;
+    for (const void* p : {(const void*)w.X, (const void*)w.xn, (const void*)w.qkv, (const void*)w.att,
+                          (const void*)w.g, (const void*)w.u, (const void*)w.h, (const void*)w.q8,
+                          (const void*)w.qsc, (const void*)w.scores, (const void*)w.part, (const void*)w.ah,
+                          (const void*)w.al, (const void*)w.aus})
+        add(p);
+    for (const void* p : {(const void*)m->cos_t, (const void*)m->sin_t, (const void*)m->embed_f32,
+                          (const void*)m->lm_f32, (const void*)m->final_rms, (const void*)m->logits,
+                          (const void*)m->ids, (const void*)m->state, (const void*)m->eos, (const void*)m->part_val,
+                          (const void*)m->part_idx, (const void*)m->pk_layers, (const void*)m->pk_flags,
+                          (const void*)m->pk_err})
+        add(p);
+    q8(m->embed_q8);
+    q8(m->lm_q8);
+    dw(m->embed_w);
+    dw(m->lm_w);
+    for (const DevLayer& D : m->layers) {
+        add(D.rms1);
+        add(D.rms2);
+        add(D.bqkv);
+        q8(D.qkv);
+        q8(D.o);
+        q8(D.gu);
+        q8(D.down);
+        for (const void* p : {(const void*)D.f_qkv, (const void*)D.f_o, (const void*)D.f_w1, (const void*)D.f_w3,
+                              (const void*)D.f_w2})
+            add(p);
+        for (const DevW& x : D.w) dw(x);
+    }
+    add(kv.k);
+    add(kv.v);
+    add(kv.ks);
+    add(kv.vs);
+    return b;
+}
+
+// what the walk of one captured graph found
+struct GraphCheck {
+    size_t nodes = 0, edges = 0, buffers = 0;
+};
+
+// the graph's shape and the buffers' liveness; throws with what is wrong
+GraphCheck check_graph(hipGraph_t graph, const jyhip_model* m, const std::vector<const void*>& bufs) {
+    GraphCheck r;
+    size_t n = 0;
+    CK(hipGraphGetNodes(graph, nullptr, &n));
+    std::vector<hipGraphNode_t> nodes(n);
+    if (n) CK(hipGraphGetNodes(graph, nodes.data(), &n));
+    size_t ne = 0;
+    CK(hipGraphGetEdges(graph, nullptr, nullptr, &ne));
+    size_t nroot = 0;
+    CK(hipGraphGetRootNodes(graph, nullptr, &nroot));
+    if (n == 0) fail("captured decode graph: no nodes");
+    if (ne != n - 1 || nroot != 1)
+        fail("captured decode graph: not one chain (" + std::to_string(n) + " nodes, " + std::to_string(ne) +
+             " edges, " + std::to_string(nroot) + " roots)");
+    for (size_t i = 0; i < n; i++) {
+        hipGraphNodeType t;
+        CK(hipGraphNodeGetType(nodes[i], &t));
+        if (t != hipGraphNodeTypeKernel)
+            fail("captured decode graph: node " + std::to_string(i) + " is not a kernel (type " + std::to_string((int)t) +
+                 ")");
+        hipKernelNodeParams kp{};
+        CK(hipGraphKernelNodeGetParams(nodes[i], &kp));
+        const size_t grid = (size_t)kp.gridDim.x * kp.gridDim.y * kp.gridDim.z;
+        const size_t block = (size_t)kp.blockDim.x * kp.blockDim.y * kp.blockDim.z;
+        if (!kp.func || grid == 0 || block == 0 || block > 1024 || kp.sharedMemBytes > 160u * 1024u ||
+            (!kp.kernelParams && !kp.extra))
+            fail("captured decode graph: kernel node " + std::to_string(i) + " has an invalid launch (grid " +
+                 std::to_string(grid) + ", block " + std::to_string(block) + ", LDS " +
+                 std::to_string(kp.sharedMemBytes) + ")");
+    }
+    for (const void* p : bufs) {
+        hipPointerAttribute_t a{};
+        const hipError_t e = hipPointerGetAttributes(&a, p);
+        if (e != hipSuccess || a.type != hipMemoryTypeDevice || a.device != m->device) {
+            (void)hipGetLastError();
+            char buf[64];
+            snprintf(buf, sizeof buf, "%p", p);
+            fail(std::string("captured decode graph: buffer ") + buf + " is not a live allocation on device " +
+                 std::to_string(m->device));
+        }
+    }
+    r.nodes = n;
+    r.edges = ne;
+    r.buffers = bufs.size();
+    return r;
+}
+
 // One generation (generate_cached, libs/model_libs/generate.h:9-89) driven step by
 // step: begin() runs the prompt and picks the first token, step(n) produces up to
 // n more.  Greedy decoding stays on the device (ids and the sequence length live
@@ -1110,6 +1227,8 @@ struct Session {
     hipGraphExec_t exec[2] = {nullptr, nullptr};
     unsigned exec_gen[2] = {0, 0};  // the workspace generation each graph was captured on
     int exec_mode[2] = {0, 0};      // the model's mode each graph was captured in
+    std::vector<const void*> exec_bufs[2];  // the buffers each graph may address, at capture
+    GraphCheck exec_check[2];
     hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
     double decode_ms = 0.0;
     int decoded = 0;
@@ -1244,11 +1363,28 @@ struct Session {
             throw;
         }
         CK(hipStreamEndCapture(st, &graph));
+        std::vector<const void*> bufs = step_buffers(m, kv->dev);
+        GraphCheck gc;
+        try {
+            gc = check_graph(graph, m, bufs);
+        } catch (...) {
+            (void)hipGraphDestroy(graph);
+            throw;
+        }
         const hipError_t ie = hipGraphInstantiate(&exec[which], graph, nullptr, nullptr, 0);
         (void)hipGraphDestroy(graph);
         ck(ie, "hipGraphInstantiate");
         exec_gen[which] = m->ws.gen;
         exec_mode[which] = m->mode;
+        exec_bufs[which] = std::move(bufs);
+        exec_check[which] = gc;
+    }
+
+    // the buffers graph `which` was captured with are the ones the model and cache hold now
+    void check_buffers(int which) const {
+        if (!exec[which]) return;
+        if (step_buffers(m, kv->dev) != exec_bufs[which])
+            fail("session: a buffer the captured decode graph addresses was replaced after capture");
     }
 
     // the graph for a step over a sequence of `length` tokens (it attends `length` keys)
@@ -1271,6 +1407,8 @@ struct Session {
         // the steps run at lengths len .. len+n-1: capture what they need up front
         if (len <= short_keys(m) && !exec[1]) capture(1);
         if (len + n - 1 > short_keys(m) && !exec[0]) capture(0);
+        check_buffers(0);
+        check_buffers(1);
         hipStream_t st = m->stream;
         CK(hipEventRecord(ev[2], st));
         int made = 0;
@@ -1692,6 +1830,19 @@ JYHIP_API int jyhip_session_ids(const jyhip_session* h, int* out, int cap) {
         if (cap < n) fail("output buffer too small");
         for (int i = 0; i < n; i++) out[i] = h->s.ids[i];
         return n;
+    }, -1);
+}
+
+JYHIP_API int jyhip_session_graph_info(const jyhip_session* h, int which, long long* info) {
+    return guarded([&]() {
+        if (!h || which < 0 || which > 1 || !info) fail("session_graph_info: bad arguments");
+        const Session& s = h->s;
+        if (!s.exec[which]) return 0;
+        s.check_buffers(which);
+        info[0] = (long long)s.exec_check[which].nodes;
+        info[1] = (long long)s.exec_check[which].edges;
+        info[2] = (long long)s.exec_check[which].buffers;
+        return 1;
     }, -1);
 }
 

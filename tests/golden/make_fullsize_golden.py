@@ -2,12 +2,28 @@
 from jieyu's own decode loop, compiled from the reference sources by oracle/Makefile
 (`make -C oracle ref` -> oracle/_ref/libjyref.so).
 
-    python tests/golden/make_fullsize_golden.py
+    python tests/golden/make_fullsize_golden.py [case ...]   # default: every case
+
+With case names only those are (re)written; the other cases already in the file stay.
 
 Models come from the repository's deterministic generator (include/jieyu_synth.h) with
 the benchmark configurations of jieyu_amd.model.CONFIGS; prompts are the first ids of
-the benchmark's prompt stream (jysyn_uniform_int_fill(seed, 99, 0, vocab - 1)).  Only
-the ids are committed.
+the benchmark's prompt stream (jysyn_uniform_int_fill(seed, 99, 0, vocab - 1)).
+
+Kinds of case:
+
+* "generate": the reference's own generate() (generate.h:90-112) writes the ids.  The
+  benchmark-length cases are also driven step by step through the reference's
+  forward_cached (forward.h:47-96) and its lm_head product (matmul_w), which must give the
+  same ids, and from that loop the file keeps, per generated token, the gap between the
+  largest and the second-largest logit over max|logit| (`rel_gap`): a fast-mode check uses
+  it to tell a near tie from a real error.  With `hidden` the last prompt row's state after
+  the final RMSNorm (the row the first token's logits come from) goes to fullsize_hidden.npz.
+* "resume": the cache first holds `prefilled` positions of N(0,1) K and V (one draw,
+  packed by the reference's kv_pack_q8, written to every layer: the long-context
+  benchmark's setup), then the prompt stream's id at `prefilled` is decoded greedily for
+  `max_new` tokens, one forward_cached row at a time (generate_cached's loop body,
+  generate.h:36-89, with the cache not restarted).
 """
 import ctypes as C
 import json
@@ -25,14 +41,23 @@ sys.path.insert(0, ROOT)
 import oracle  # noqa: E402
 from jieyu_amd.model import Synth, synth_config  # noqa: E402
 
-# name: (configuration, prompt tokens, new tokens, max_seq)
+# name: dict(kind, config, prompt_len, max_new, max_seq[, prefilled][, hidden][, driven])
 CASES = {
     # Llama-3-8B shape, Q8_0, seed 3: a 48-token prompt through the prompt GEMMs, 32 greedy tokens
-    "llama3-8b-full": ("llama3-8b", 48, 32, 96),
+    "llama3-8b-full": dict(kind="generate", config="llama3-8b", prompt_len=48, max_new=32, max_seq=96),
     # Qwen2.5-0.5B shape, Q8_0, tied head, biases: the benchmark's 512-token prompt, 64 greedy tokens
-    "qwen2.5-0.5b-full-512": ("qwen2.5-0.5b", 512, 64, 600),
+    "qwen2.5-0.5b-full-512": dict(kind="generate", config="qwen2.5-0.5b", prompt_len=512, max_new=64, max_seq=600),
     # Qwen2.5-7B shape, Q8_0, biases, theta 1e6: a 24-token prompt, 16 greedy tokens
-    "qwen2.5-7b-full": ("qwen2.5-7b", 24, 16, 48),
+    "qwen2.5-7b-full": dict(kind="generate", config="qwen2.5-7b", prompt_len=24, max_new=16, max_seq=48),
+    # the Llama-3-8B benchmark: 1024-token prompt, 512 greedy tokens, a 4096-position cache
+    "llama3-8b-bench": dict(kind="generate", config="llama3-8b", prompt_len=1024, max_new=512, max_seq=4096,
+                            hidden=True, driven=True),
+    # the Qwen2.5-0.5B benchmark: 512-token prompt, 256 greedy tokens
+    "qwen2.5-0.5b-bench": dict(kind="generate", config="qwen2.5-0.5b", prompt_len=512, max_new=256, max_seq=768,
+                               driven=True),
+    # the Qwen2.5-7B long-context benchmark: 128 greedy tokens after 32768 pre-filled positions
+    "qwen2.5-7b-32768": dict(kind="resume", config="qwen2.5-7b", prompt_len=1, max_new=128, max_seq=32768 + 136,
+                             prefilled=32768),
 }
 
 
@@ -40,35 +65,152 @@ def ptr(a):
     return None if a is None else a.ctypes.data_as(C.c_void_p)
 
 
+def rel_gap(lg):
+    """(largest - second largest logit) / max|logit|; the first maximum is the pick."""
+    i = int(np.argmax(lg))
+    rest = np.delete(lg, i)
+    return float((lg[i] - rest.max()) / max(float(np.abs(lg).max()), 1e-30))
+
+
+def embed(ref, d, tok, X):
+    ref.jyref_wmat_row(C.byref(d.embed), int(tok), d.hidden, ptr(X))
+
+
+def lm_head(ref, d, X):
+    logits = np.zeros(d.vocab_size, np.float32)
+    ref.jyref_matmul_w(C.byref(d.lm_head), 1, d.vocab_size, d.hidden, ptr(X), ptr(logits))
+    return logits
+
+
+def prefill_ref_kv(ref, olib, d, kvp, pre, max_seq):
+    """positions [0, pre) of every layer: one N(0,1) draw each for K and V (seeds 9 / 1000
+    and 9 / 1001), packed by the reference's kv_pack_q8."""
+    L, nkv, hd = d.num_layers, d.num_kv_heads, d.head_dim
+    packed = []
+    for sub in (1000, 1001):
+        f = np.zeros(pre * nkv * hd, np.float32)
+        olib.jysyn_normal_fill(9, sub, 1.0, ptr(f), f.size)
+        q = np.zeros(f.size, np.int8)
+        s = np.zeros(pre * nkv, np.float32)
+        ref.jyref_kv_pack(ptr(f), ptr(q), ptr(s), nkv, hd, pre)
+        packed.append((q.reshape(pre, nkv, hd), s.reshape(pre, nkv)))
+        del f
+    views = []
+    for fn, shape, ct in (("jyref_kv_k", (L, max_seq, nkv, hd), C.c_int8), ("jyref_kv_v", (L, max_seq, nkv, hd), C.c_int8),
+                          ("jyref_kv_ks", (L, max_seq, nkv), C.c_float), ("jyref_kv_vs", (L, max_seq, nkv), C.c_float)):
+        views.append(np.ctypeslib.as_array(C.cast(getattr(ref, fn)(kvp), C.POINTER(ct)), shape))
+    k, v, ks, vs = views
+    for l in range(L):
+        k[l, :pre] = packed[0][0]
+        ks[l, :pre] = packed[0][1]
+        v[l, :pre] = packed[1][0]
+        vs[l, :pre] = packed[1][1]
+    ref.jyref_kv_set_len(kvp, pre)
+
+
+def driven(ref, olib, d, prompt, start, n_new, max_seq, cos, sin, kvp, want_hidden=False):
+    """greedy ids, per-step rel_gap and (optionally) the last prompt row's final state from
+    forward_cached steps over the reference cache kvp, the prompt starting at `start`."""
+    H = d.hidden
+    n = len(prompt)
+    X = np.zeros((n, H), np.float32)
+    for i, t in enumerate(prompt):
+        embed(ref, d, t, X[i])
+    assert ref.jyref_forward_cached(C.byref(d), ptr(cos), ptr(sin), ptr(X), n, start, kvp, None) == 0
+    hidden = X[n - 1].copy() if want_hidden else None
+    ids, gaps = [], []
+    x = np.ascontiguousarray(X[n - 1:n])
+    pos = start + n
+    for i in range(n_new):
+        lg = lm_head(ref, d, x)
+        tok = int(np.argmax(lg))
+        ids.append(tok)
+        gaps.append(rel_gap(lg))
+        if i + 1 == n_new:
+            break
+        x = np.zeros((1, H), np.float32)
+        embed(ref, d, tok, x[0])
+        assert ref.jyref_forward_cached(C.byref(d), ptr(cos), ptr(sin), ptr(x), 1, pos, kvp, None) == 0
+        pos += 1
+        if i % 32 == 31:
+            print(f"    {i + 1} of {n_new} driven steps", flush=True)
+    return ids, gaps, hidden
+
+
+def run_case(ref, olib, name, cs):
+    cname, plen, new, max_seq = cs["config"], cs["prompt_len"], cs["max_new"], cs["max_seq"]
+    t0 = time.time()
+    cfg = synth_config(cname)
+    syn = Synth(olib, cfg)
+    d = syn.desc
+    pre = cs.get("prefilled", 0)
+    stream = np.zeros(pre + plen, np.int32)
+    olib.jysyn_uniform_int_fill(cfg.seed, 99, 0, d.vocab_size - 1, ptr(stream), len(stream))
+    prompt = stream[pre:]
+    c = np.zeros(max_seq * d.head_dim // 2, np.float32)
+    s = np.zeros_like(c)
+    ref.jyref_rope_table(max_seq, d.head_dim, d.rope_theta, ptr(c), ptr(s))
+    rec = dict(kind=cs["kind"], config=cname, prompt_len=plen, max_seq=max_seq, max_new=new)
+    hidden = None
+    if cs["kind"] == "generate":
+        ids = np.zeros(max_seq + 1, np.int32)
+        n = ref.jyref_generate(C.byref(d), ptr(prompt), plen, None, 0, ptr(c), ptr(s), max_seq, new, 0.0, 1.0,
+                               ptr(ids), None, None, 0)
+        rec["ids"] = ids[:n].tolist()
+        print(f"  {name}: generate gave {n - plen} tokens in {time.time() - t0:.1f} s", flush=True)
+        if cs.get("driven"):
+            kvp = ref.jyref_kv_create(d.num_layers, max_seq, d.num_kv_heads, d.head_dim)
+            got, gaps, hidden = driven(ref, olib, d, prompt, 0, new, max_seq, c, s, kvp, cs.get("hidden", False))
+            ref.jyref_kv_free(kvp)
+            assert got == rec["ids"][plen:], f"{name}: the driven loop's ids differ from generate()'s"
+            rec["rel_gap"] = [round(g, 7) for g in gaps]
+    else:
+        kvp = ref.jyref_kv_create(d.num_layers, max_seq, d.num_kv_heads, d.head_dim)
+        prefill_ref_kv(ref, olib, d, kvp, pre, max_seq)
+        got, gaps, _ = driven(ref, olib, d, prompt, pre, new, max_seq, c, s, kvp)
+        ref.jyref_kv_free(kvp)
+        rec["prefilled"] = pre
+        rec["ids"] = prompt.tolist() + got
+        rec["rel_gap"] = [round(g, 7) for g in gaps]
+    if "rel_gap" in rec:
+        g = np.array(rec["rel_gap"])
+        print(f"  {name}: smallest top-2 logit gap {g.min():.3g} of max|logit| at generated token {int(g.argmin())}",
+              flush=True)
+    syn.close()
+    print(f"{name}: {new} tokens in {time.time() - t0:.1f} s", flush=True)
+    return rec, hidden
+
+
 def main():
     if not oracle.ref_available():
         sys.exit("oracle/_ref/libjyref.so is missing: run `make -C oracle ref` where the reference tree exists")
+    names = sys.argv[1:] or list(CASES)
+    for n in names:
+        if n not in CASES:
+            sys.exit(f"unknown case {n}; cases: {', '.join(CASES)}")
     ref = oracle.load_ref()
     olib = oracle.load_oracle()
     isa = ref.jyref_init()
     meta = dict(reference_version=ref.jyref_version().decode(), isa_avx2=bool(isa & 1), isa_fma=bool(isa & 2),
                 isa_avxvnni=bool(isa & 4), libc=" ".join(platform.libc_ver()), machine=platform.machine(),
                 threads=os.environ.get("OMP_NUM_THREADS", str(os.cpu_count())))
+    path = os.path.join(HERE, "fullsize.json")
+    hpath = os.path.join(HERE, "fullsize_hidden.npz")
     out = {}
-    for name, (cname, plen, new, max_seq) in CASES.items():
-        t0 = time.time()
-        cfg = synth_config(cname)
-        syn = Synth(olib, cfg)
-        d = syn.desc
-        prompt = np.zeros(plen, np.int32)
-        olib.jysyn_uniform_int_fill(cfg.seed, 99, 0, d.vocab_size - 1, ptr(prompt), plen)
-        c = np.zeros(max_seq * d.head_dim // 2, np.float32)
-        s = np.zeros_like(c)
-        ref.jyref_rope_table(max_seq, d.head_dim, d.rope_theta, ptr(c), ptr(s))
-        ids = np.zeros(max_seq + 1, np.int32)
-        n = ref.jyref_generate(C.byref(d), ptr(prompt), plen, None, 0, ptr(c), ptr(s), max_seq, new, 0.0, 1.0,
-                               ptr(ids), None, None, 0)
-        out[name] = dict(config=cname, prompt_len=plen, max_seq=max_seq, max_new=new, ids=ids[:n].tolist())
-        syn.close()
-        print(f"{name}: {n - plen} tokens in {time.time() - t0:.1f} s", flush=True)
-    with open(os.path.join(HERE, "fullsize.json"), "w") as f:
-        json.dump(dict(meta=meta, cases=out), f, indent=1)
-    print("wrote", os.path.join(HERE, "fullsize.json"))
+    if os.path.exists(path):
+        with open(path) as f:
+            out = json.load(f)["cases"]
+    hid = dict(np.load(hpath)) if os.path.exists(hpath) else {}
+    for name in names:
+        rec, hidden = run_case(ref, olib, name, CASES[name])
+        out[name] = rec
+        if hidden is not None:
+            hid[name] = hidden
+        with open(path, "w") as f:  # after every case: a long run keeps what it finished
+            json.dump(dict(meta=meta, cases={k: out[k] for k in CASES if k in out}), f, indent=1)
+        if hid:
+            np.savez(hpath, **hid)
+    print("wrote", path)
 
 
 if __name__ == "__main__":

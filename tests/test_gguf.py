@@ -121,6 +121,21 @@ def test_perm_row_restores_adjacent_pairs(tmp_path):
     pytest.fail("q_proj not found")
 
 
+@pytest.mark.parametrize("hd", [24, 15])
+def test_pairs_need_whole_heads(tmp_path, hd):
+    """a key_length that does not split the q / k rows into whole heads of an even size is
+    refused before any file is written (the row permutation would read past the tensor)"""
+    import gguf_writer as G
+    g = GM.deepseek_f32()  # hidden 64: q / k have 64 rows
+    g.kv.append(("llama.attention.key_length", G.U32, hd, None))
+    src = g.write(str(tmp_path / "bad.gguf"))
+    out = str(tmp_path / "out")
+    rc, _, err = convert(src, out, "f32", True)
+    assert rc == -1
+    assert "head_dim" in err and "attn_q" in err
+    assert digest(out) == {}
+
+
 def test_reference_live(tmp_path):
     """the reference converter on the same GGUF bytes, compared file by file"""
     import oracle

@@ -75,6 +75,49 @@ def test_noalloc_matches_forward_cached(jy, oracle_lib, spec, fast):
     s.close()
 
 
+def device_free_bytes():
+    """hipMemGetInfo's free bytes on the current device (the HIP runtime the library uses)."""
+    hip = C.CDLL("libamdhip64.so")
+    free, total = C.c_size_t(0), C.c_size_t(0)
+    assert hip.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
+    return free.value
+
+
+@pytest.mark.parametrize("fast", [False, True])
+def test_noalloc_allocates_nothing(jy, oracle_lib, fast):
+    """After one warm-up call, repeated calls (prompt rows, then decode rows) leave the
+    device's free memory exactly where it was: no allocation and no growth of any pool."""
+    say(f"forward_cached_noalloc: device free memory across calls ({'fast' if fast else 'exact'} mode)")
+    s = small_model(oracle_lib, "llama3-8b", num_layers=2, hidden=512, num_heads=8, num_kv_heads=2, head_dim=64,
+                    intermediate=1408, vocab_size=3000)
+    d = s.desc
+    max_seq = 64
+    g = jy.GpuModel(d, max_seq)
+    if fast:
+        g.mode = jy.MODE_FAST
+    kv = g.kv(max_seq)
+    rng = np.random.default_rng(5)
+    xs = [rng.standard_normal((n, d.hidden)).astype(np.float32) for n in (12, 3, 1, 1, 1)]
+
+    def run_all():
+        start = 0
+        for X in xs:
+            Xn = X.copy()
+            rc = jy.lib().jyhip_forward_cached_noalloc(g.h, kv.h, ptr(Xn), Xn.shape[0], start)
+            assert rc == 0, jy.last_error()
+            start += Xn.shape[0]
+
+    run_all()  # warm-up: the first launches of each kernel
+    before = device_free_bytes()
+    for _ in range(3):
+        run_all()
+    after = device_free_bytes()
+    assert after == before, f"device free memory moved by {before - after} bytes across noalloc calls"
+    kv.close()
+    g.close()
+    s.close()
+
+
 def test_noalloc_rejects_oversize(jy, oracle_lib):
     """A call whose workspace would pass the static array's size is refused with an error
     that names the size; the library stays usable afterwards."""
