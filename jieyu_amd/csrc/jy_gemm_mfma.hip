@@ -18,18 +18,19 @@
 // The A operand takes lane l = r + 16 G for row r and the same k = 8G .. 8G+7: whatever
 // order the instruction gives the four lane groups' k, A and B agree on it.
 //
-// Tiling.  A workgroup of 4 waves computes 128 rows (tokens) x 128 columns (matrix rows),
-// each wave 64 x 64: 4 x 4 tiles of 16 x 16, acc in the MFMA C layout (lane l holds rows
-// 4 (l/16) .. +3 of column l % 16).  Per block the workgroup stages the tile's activation
-// parts and its weights (converted to fp16 once) in LDS, double-buffered, with the global
-// loads two blocks ahead in registers: block b+2's loads are in flight while the waves run
-// block b's MFMAs from LDS and stage block b+1.
+// Tiling.  A workgroup of 2 x 2 waves computes 64 rows (tokens) x 64 NT columns (matrix
+// rows), each wave 32 x 16 NT: 2 x NT tiles of 16 x 16, acc in the MFMA C layout (lane l
+// holds rows 4 (l/16) .. +3 of column l % 16).  The operands reach LDS by global -> LDS DMA
+// three blocks deep (activation parts in operand order, weights as stored, block scales),
+// one workgroup barrier per block; each wave converts its weight fragments to fp16.
+#include <cstddef>
+
 #include "jy_layout.h"
 #include "jy_mfma.h"
 
 namespace jy {
 
-static constexpr int GM_TILE = 128;  // workgroup tile: rows and columns
+static constexpr int GM_TILE = 128;  // activation rows are padded to a multiple of this
 
 // ---------------------------------------------------------------- the matrix copy
 
@@ -124,202 +125,235 @@ void launch_mfma_split(const float* A, int m, int mp, int K, _Float16* hi, _Floa
     hipLaunchKernelGGL(mfma_split_kernel, dim3(mp), dim3(256), 0, st, A, m, K, hi, lo, unscale);
 }
 
-// ---------------------------------------------------------------- the GEMM
+// ---------------------------------------------------------------- the GEMM, staged by DMA
+//
+// Per block: the hi-part MFMA, the lo-part MFMA into the same sum, one fp32 fma with the
+// block scale.  The operands are brought to LDS by global -> LDS DMA, S blocks deep, with
+// a wave tile of
+// 16 MT token rows x 16 NT columns (a workgroup of 2 x 2 waves: 32 MT x 32 NT).  The
+// weights stay int8 in LDS (8 bytes per lane per 16 x 32 tile) and become fp16 per
+// fragment (q8_to_h8).  Per block a wave reads 2 MT KiB of activation fragments and NT / 2
+// KiB of weights from LDS for 2 MT NT matrix operations.  (A register-staged form with one
+// 32-weight block per barrier, 64 x 64 per wave and the weight fragments read twice was
+// bound by LDS reads: gate/up at 1024 tokens 682 us against 576 here.)
 
-// LDS of one block stage, in MFMA operand order: for each of the 8 row tiles (high and
-// low parts) and 8 column tiles (weights as fp16), the 64 lanes' 16-byte operands at
-// lane * 16, so that every operand read and every staging write is one contiguous 1 KiB
-// per wave instruction (no bank conflicts); and the 128 columns' block scales
-template <int NT>
-struct GmStage {
-    h8_t ah[8][64];
-    h8_t al[8][64];
-    h8_t bq[2 * NT][64];
-    float d[32 * NT];
+// global -> LDS DMA (16 or 4 bytes per lane: lane l writes at the M0 base + l * size),
+// issued as inline assembly: the compiler cannot tell a DMA's LDS destination from the LDS
+// the waves read and would wait for every DMA before each LDS access; the kernel instead
+// waits for its own DMAs explicitly before the barrier that publishes a stage.  The asm sets
+// M0 itself; nothing else in these kernels uses M0 (checked in the generated code).
+// (M0 is a reserved register: the compiler warns that naming it as clobbered may not be
+// honoured, which is harmless here since no compiler-generated code in these kernels uses it)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_b128(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_b32(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+__device__ __forceinline__ uint32_t lds_byte_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char*)p;
+}
+
+// s_waitcnt with only vmcnt <= n (n < 64)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// one stage: activation fragments [part][row tile][lane], weights [column tile][lane]
+// (8 bytes: lanes 0..31 of a 16-byte DMA cover one tile), block scales [column tile][row]
+template <int MT, int NT>
+struct G2Stage {
+    h8_t a[2][2 * MT][64];
+    uint2 b[2 * NT][64];
+    float d[2 * NT][16];
 };
 
-// Block b of the workgroup's tile into registers (global loads only): thread t stages
-// operand positions p = t and t + 256 (row tile p/64, lane p%64: token row 16 (p/64) +
-// (p%16), k 8 ((p%64)/16) .. +7) of the high and low parts; lanes 2 (t%32), +1 of column
-// tile t/32 (8 weight bytes each); with t < 128 column t's scale
-struct GmRegs {
-    uint4 h0, h1, l0, l1;
-    uint2 q0, q1;
-    float d;
-};
-
-// NT column tiles per wave: a workgroup covers 128 tokens x 32 NT columns
-template <int EPI, int NT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_q8_mfma_kernel(Q8MfmaDev W, int m, int K, const _Float16* __restrict__ ahi,
-                                                           const _Float16* __restrict__ alo,
-                                                           const float* __restrict__ unscale, float* __restrict__ C,
-                                                           int ldc, const float* __restrict__ aux) {
-    __shared__ GmStage<NT> st[2];
-    const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
+template <int EPI, int MT, int NT, int S>
+__global__ __launch_bounds__(256, 2) void gemm_q8_mfma2_kernel(Q8MfmaDev W, int m, int K, const _Float16* __restrict__ ahi,
+                                                            const _Float16* __restrict__ alo,
+                                                            const float* __restrict__ unscale, float* __restrict__ C,
+                                                            int ldc, const float* __restrict__ aux) {
+    static_assert(MT == 2 || MT == 4, "row tiles per wave");
+    static_assert(NT == 4 || NT == 8, "column tiles per wave");
+    static_assert(S == 3 || S == 4, "stages");
+    using St = G2Stage<MT, NT>;
+    extern __shared__ __align__(16) unsigned char g2smem[];
+    St* stg = reinterpret_cast<St*>(g2smem);
+    const int tid = threadIdx.x, l = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave & 1, wn = wave >> 1;
     const int c = l & 15, G = l >> 4;
-    const int rowt = blockIdx.x * GM_TILE;               // the workgroup's first token row
-    const int tilet = blockIdx.y * 2 * NT;              // its first 16-column tile
+    const int rowt = blockIdx.x * 32 * MT;  // the workgroup's first token row
+    const int tilet = blockIdx.y * 2 * NT;  // its first 16-column tile
     const int nb = W.nb;
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_byte_addr(g2smem));
+    constexpr int PW = MT + NT / 4 + 1;  // DMA instructions per wave per block
 
-    // staging roles
-    const size_t a0 = (size_t)(rowt + 16 * (tid >> 6) + c) * K + 8 * G;        // position t
-    const size_t a1 = (size_t)(rowt + 16 * ((tid + 256) >> 6) + c) * K + 8 * G;  // position t + 256
-    const int qt = tid >> 5, qpart = tid & 31;  // column tile (of 2 NT) and lane pair
-    const bool qstage = qt < 2 * NT;
-    const bool qlive = qstage && tilet + qt < W.tiles;
-    const uint2* gq = reinterpret_cast<const uint2*>(W.q) + ((size_t)(qlive ? tilet + qt : 0) * nb) * 64 + 2 * qpart;
-    const int dtile = tilet + (tid >> 4);
-    const bool dlive = tid < 32 * NT && dtile < W.tiles;
-    const float* gd = W.d + ((size_t)(dlive ? dtile : 0) * W.nb4 * 16 + (tid & 15)) * 4;
-
-    auto fetch = [&](GmRegs& r, int b) {
-        const size_t kb = (size_t)b * 32;
-        r.h0 = *reinterpret_cast<const uint4*>(ahi + a0 + kb);
-        r.h1 = *reinterpret_cast<const uint4*>(ahi + a1 + kb);
-        r.l0 = *reinterpret_cast<const uint4*>(alo + a0 + kb);
-        r.l1 = *reinterpret_cast<const uint4*>(alo + a1 + kb);
-        if (qlive) {
-            r.q0 = gq[(size_t)b * 64];
-            r.q1 = gq[(size_t)b * 64 + 1];
-        } else {
-            r.q0 = r.q1 = make_uint2(0u, 0u);
-        }
-        r.d = dlive ? gd[(size_t)(b >> 2) * 64 + (b & 3)] : 0.0f;
-    };
-    auto stage = [&](const GmRegs& r, GmStage<NT>& S) {
-        (&S.ah[0][0])[tid] = __builtin_bit_cast(h8_t, r.h0);
-        (&S.ah[0][0])[tid + 256] = __builtin_bit_cast(h8_t, r.h1);
-        (&S.al[0][0])[tid] = __builtin_bit_cast(h8_t, r.l0);
-        (&S.al[0][0])[tid + 256] = __builtin_bit_cast(h8_t, r.l1);
-        if (qstage) {
-            S.bq[qt][2 * qpart] = q8_to_h8(r.q0.x, r.q0.y);
-            S.bq[qt][2 * qpart + 1] = q8_to_h8(r.q1.x, r.q1.y);
-        }
-        if (tid < 32 * NT) S.d[tid] = r.d;
-    };
-
-    f4_t acc[4][NT];
+    // block b into stage s: this wave's share of the 4 MT activation, NT weight and 4 scale
+    // DMA instructions (the same count for every wave)
+    auto issue = [&](int b, int s) {
+        const uint32_t sb = base + (uint32_t)(s * sizeof(St));
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
+        for (int j = 0; j < MT; j++) {
+            const int i = wave * MT + j, part = i / (2 * MT), rt = i % (2 * MT);
+            const _Float16* src = (part ? alo : ahi) + (size_t)(rowt + 16 * rt + c) * K + 32 * b + 8 * G;
+            dma_b128(src, sb + (uint32_t)(offsetof(St, a) + (size_t)(part * 2 * MT + rt) * 64 * 16));
+        }
+#pragma unroll
+        for (int j = 0; j < NT / 4; j++) {
+            const int jj = wave * (NT / 4) + j, t = 2 * jj + (l >> 5);
+            const int tg = min(tilet + t, W.tiles - 1);
+            const int8_t* src = W.q + ((size_t)tg * nb + b) * 512 + (l & 31) * 16;
+            dma_b128(src, sb + (uint32_t)(offsetof(St, b) + (size_t)(2 * jj) * 512));
+        }
+        {
+            const int f = wave * 8 * NT + l, t = f >> 4, r = f & 15;
+            const int tg = min(tilet + t, W.tiles - 1);
+            const float* src = W.d + ((size_t)(tg * W.nb4 + (b >> 2)) * 16 + r) * 4 + (b & 3);
+            if (l < 8 * NT) dma_b32(src, sb + (uint32_t)(offsetof(St, d) + (size_t)wave * 8 * NT * 4));
+        }
+    };
+
+    f4_t acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) acc[mt][nt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    bool ntv[NT];
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) ntv[nt] = tilet + wn * NT + nt < W.tiles;
-
-    // block b's MFMAs from LDS stage b % 2
-    auto compute = [&](int b) {
-        const GmStage<NT>& S = st[b & 1];
-        h8_t ah[4], al[4];
+    for (int s = 0; s < S - 1; s++)
+        if (s < nb) issue(s, s);
+    for (int b = 0; b < nb; b++) {
+        // block b has landed once at most the DMAs of the S - 2 blocks after it are pending
+        const int after = min(nb - 1 - b, S - 2);
+        if (after >= S - 2)
+            wait_vm<(S - 2) * PW>();
+        else if (S > 3 && after == 1)
+            wait_vm<(S > 3 ? PW : 0)>();
+        else
+            wait_vm<0>();
+        __syncthreads();  // every wave's DMAs of block b are in LDS; block b - 1 is done
+        if (b + S - 1 < nb) issue(b + S - 1, (b + S - 1) % S);
+        const St& T = stg[b % S];
+        h8_t ah[MT], al[MT];
 #pragma unroll
-        for (int mt = 0; mt < 4; mt++) {
-            ah[mt] = S.ah[wm * 4 + mt][l];
-            al[mt] = S.al[wm * 4 + mt][l];
+        for (int mt = 0; mt < MT; mt++) {
+            ah[mt] = T.a[0][wm * MT + mt][l];
+            al[mt] = T.a[1][wm * MT + mt][l];
         }
-        // two column tiles at a time: their 8 tiles' block sums (16 independent MFMAs back
-        // to back), then the scaling
 #pragma unroll
-        for (int n0 = 0; n0 < NT; n0 += 2) {
-            f4_t t[4][2];
-            float dj[2];
+        for (int nt = 0; nt < NT; nt++) {
+            const uint2 q = T.b[wn * NT + nt][l];
+            const h8_t bq = q8_to_h8(q.x, q.y);
+            const float dj = T.d[wn * NT + nt][c];
+            f4_t t[MT];
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const h8_t bq = S.bq[wn * NT + n0 + u][l];
-                dj[u] = S.d[(wn * NT + n0 + u) * 16 + c];
+            for (int mt = 0; mt < MT; mt++)
+                t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
-                for (int mt = 0; mt < 4; mt++)
-                    t[mt][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-            }
+            for (int mt = 0; mt < MT; mt++) t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], bq, t[mt], 0, 0, 0);
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const h8_t bq = S.bq[wn * NT + n0 + u][l];
+            for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-                for (int mt = 0; mt < 4; mt++)
-                    t[mt][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], bq, t[mt][u], 0, 0, 0);
-            }
-#pragma unroll
-            for (int u = 0; u < 2; u++)
-#pragma unroll
-                for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        acc[mt][n0 + u][i] = __builtin_fmaf(dj[u], t[mt][u][i], acc[mt][n0 + u][i]);
+                for (int i = 0; i < 4; i++) acc[mt][nt][i] = __builtin_fmaf(dj, t[mt][i], acc[mt][nt][i]);
         }
-    };
-    // registers: ra holds the block after the one being computed (in flight since the
-    // previous iteration), rb takes the loads of the block two ahead
-    GmRegs ra, rb;
-    fetch(ra, 0);
-    if (nb > 1) fetch(rb, 1);
-    stage(ra, st[0]);
-    __syncthreads();
-    auto iter = [&](int b, GmRegs& next, GmRegs& ahead) {
-        if (b + 2 < nb) fetch(ahead, b + 2);
-        compute(b);
-        if (b + 1 < nb) stage(next, st[(b + 1) & 1]);
-        __syncthreads();
-    };
-    for (int b = 0; b < nb; b += 2) {
-        iter(b, rb, ra);
-        if (b + 1 < nb) iter(b + 1, ra, rb);
     }
 
-    // epilogue: acc[mt][nt][i] is C[row][col] before the row's unscale
+    // epilogue: acc[mt][nt][i] is C[row][col] before the row's unscale; the rows' factors
+    // are loaded together first, so no store waits for a load of its own
     const int N = W.rows;
+    float us[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int row = rowt + wm * 16 * MT + 16 * mt + 4 * G + i;
+            us[mt][i] = row < m ? unscale[row] : 0.0f;
+        }
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         const int col = 16 * (tilet + wn * NT + nt) + c;
-        if (!ntv[nt] || col >= N) continue;
+        if (tilet + wn * NT + nt >= W.tiles || col >= N) continue;
         const float bias = EPI == EPI_BIAS ? aux[col] : 0.0f;
+        float old[MT][4];
+        if (EPI == EPI_RESID) {
 #pragma unroll
-        for (int mt = 0; mt < 4; mt++)
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int row = rowt + wm * 16 * MT + 16 * mt + 4 * G + i;
+                    old[mt][i] = row < m ? C[(size_t)row * ldc + col] : 0.0f;
+                }
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int row = rowt + wm * 64 + 16 * mt + 4 * G + i;
+                const int row = rowt + wm * 16 * MT + 16 * mt + 4 * G + i;
                 if (row >= m) continue;
-                const float y = acc[mt][nt][i] * unscale[row];
-                float* dst = C + (size_t)row * ldc + col;
-                if (EPI == EPI_RESID)
-                    *dst += y;
-                else
-                    *dst = y + bias;
+                const float y = acc[mt][nt][i] * us[mt][i];
+                C[(size_t)row * ldc + col] = EPI == EPI_RESID ? old[mt][i] + y : y + bias;
             }
     }
 }
 
 int mfma_rows_padded(int m) { return (m + GM_TILE - 1) / GM_TILE * GM_TILE; }
 
-template <int NT>
-static void gemm_mfma_launch(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
-                             float* C, int ldc, const float* aux, Epi epi, hipStream_t st) {
-    // x: token tiles (the fastest in dispatch order: the workgroups that read one column
-    // tile's weights run together), y: column tiles
-    const dim3 grid((unsigned)(mfma_rows_padded(m) / GM_TILE), (unsigned)((W.tiles + 2 * NT - 1) / (2 * NT)));
+template <int MT, int NT, int S>
+static size_t g2_lds() {
+    return (size_t)S * sizeof(G2Stage<MT, NT>);
+}
+
+template <int MT, int NT, int S>
+static void gemm2_launch(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
+                         float* C, int ldc, const float* aux, Epi epi, hipStream_t st) {
+    const dim3 grid((unsigned)(mfma_rows_padded(m) / (32 * MT)), (unsigned)((W.tiles + 2 * NT - 1) / (2 * NT)));
     const int K = W.nb * 32;
+    const size_t lds = g2_lds<MT, NT, S>();
     switch (epi) {
         case EPI_BIAS:
-            hipLaunchKernelGGL((gemm_q8_mfma_kernel<EPI_BIAS, NT>), grid, dim3(256), 0, st, W, m, K, hi, lo, unscale, C,
-                               ldc, aux);
+            hipLaunchKernelGGL((gemm_q8_mfma2_kernel<EPI_BIAS, MT, NT, S>), grid, dim3(256), lds, st, W, m, K, hi, lo,
+                               unscale, C, ldc, aux);
             break;
         case EPI_RESID:
-            hipLaunchKernelGGL((gemm_q8_mfma_kernel<EPI_RESID, NT>), grid, dim3(256), 0, st, W, m, K, hi, lo, unscale,
-                               C, ldc, aux);
+            hipLaunchKernelGGL((gemm_q8_mfma2_kernel<EPI_RESID, MT, NT, S>), grid, dim3(256), lds, st, W, m, K, hi, lo,
+                               unscale, C, ldc, aux);
             break;
         default:
-            hipLaunchKernelGGL((gemm_q8_mfma_kernel<EPI_STORE, NT>), grid, dim3(256), 0, st, W, m, K, hi, lo, unscale,
-                               C, ldc, aux);
+            hipLaunchKernelGGL((gemm_q8_mfma2_kernel<EPI_STORE, MT, NT, S>), grid, dim3(256), lds, st, W, m, K, hi, lo,
+                               unscale, C, ldc, aux);
             break;
     }
 }
 
+template <int MT, int NT, int S>
+static hipError_t gemm2_attr() {
+    hipError_t e = hipSuccess;
+    for (const void* f : {reinterpret_cast<const void*>(&gemm_q8_mfma2_kernel<EPI_STORE, MT, NT, S>),
+                          reinterpret_cast<const void*>(&gemm_q8_mfma2_kernel<EPI_BIAS, MT, NT, S>),
+                          reinterpret_cast<const void*>(&gemm_q8_mfma2_kernel<EPI_RESID, MT, NT, S>)})
+        if (e == hipSuccess) e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)g2_lds<MT, NT, S>());
+    return e;
+}
+
+hipError_t gemm_mfma_init() {
+    hipError_t e = gemm2_attr<2, 8, 3>();
+    if (e == hipSuccess) e = gemm2_attr<2, 4, 3>();
+    return e;
+}
+
 static int g_gemm_cus = 0;
 
-// the wide tile (64 columns per wave), or the narrow one (32 columns per wave: twice the
-// workgroups) when the wide tile would leave CUs with one workgroup or none (measured at
-// 1024 tokens: 4096-row matrices 160 -> 154 us, 14336-column 561 -> 546 us; the 6144-row
-// QKV, 384 wide workgroups, is faster wide: 185 vs 273 us)
+// the wide tile (128 columns per wave) when its grid gives every CU at least two
+// workgroups, else the narrow one (64 columns per wave, twice the workgroups).  Measured at
+// the Llama-3-8B shapes and 1024 tokens (the activation split included): gate/up (28672 x
+// 4096) 576 us wide, 686 narrow; QKV 164, O 118, down 422 us narrow; at the Qwen2.5-0.5B
+// shapes and 512 tokens the narrow tile throughout (QKV 23, O 23, gate/up 44, down 90 us).
 void launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
                          float* C, int ldc, const float* aux, Epi epi, hipStream_t st) {
     if (!g_gemm_cus) {
@@ -330,11 +364,11 @@ void launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _F
         else
             g_gemm_cus = 256;
     }
-    const long wide = (long)(mfma_rows_padded(m) / GM_TILE) * ((W.tiles + 7) / 8);
-    if (wide > g_gemm_cus)
-        gemm_mfma_launch<4>(W, m, hi, lo, unscale, C, ldc, aux, epi, st);
+    const long wide = (long)(mfma_rows_padded(m) / 64) * ((W.tiles + 15) / 16);
+    if (wide >= 2L * g_gemm_cus)
+        gemm2_launch<2, 8, 3>(W, m, hi, lo, unscale, C, ldc, aux, epi, st);
     else
-        gemm_mfma_launch<2>(W, m, hi, lo, unscale, C, ldc, aux, epi, st);
+        gemm2_launch<2, 4, 3>(W, m, hi, lo, unscale, C, ldc, aux, epi, st);
 }
 
 }  // namespace jy

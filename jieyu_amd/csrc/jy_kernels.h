@@ -101,6 +101,7 @@ Q8Dev q8_shape(int rows, int cols);
 // Once per device, before any launch: raise the dynamic LDS limit of the kernels
 // that stage a full activation vector.
 hipError_t kernels_init();
+hipError_t gemm_mfma_init();
 
 // src: jieyu Q8_0 rows [rows][cols/32] x 34 B (device copy).  Source row r lands
 // in destination row row_base + r*row_stride.

@@ -19,6 +19,14 @@ Kinds of case:
   largest and the second-largest logit over max|logit| (`rel_gap`): a fast-mode check uses
   it to tell a near tie from a real error.  With `hidden` the last prompt row's state after
   the final RMSNorm (the row the first token's logits come from) goes to fullsize_hidden.npz.
+* "driven": the same driven loop alone, its prompt through forward_cached in chunks of
+  `chunk` rows.  The reference's m > 1 product (matmul_q.h:145-161) computes every output
+  element from its own activation row in ascending k, and its attention packs a chunk's K/V
+  into the int8 cache before any row reads it, so a prompt in chunks of m >= 2 rows gives
+  the one-chunk result bit for bit; the chunks keep the activations cache-resident, where
+  one 1024-row chunk re-streams 16 MB of activations per output column (hours per layer
+  of the 8B shape).  The script checks that equivalence on the case's own model first: 64
+  prompt rows as one chunk and as four chunks of 16, hidden states and K/V bit-equal.
 * "resume": the cache first holds `prefilled` positions of N(0,1) K and V (one draw,
   packed by the reference's kv_pack_q8, written to every layer: the long-context
   benchmark's setup), then the prompt stream's id at `prefilled` is decoded greedily for
@@ -50,8 +58,8 @@ CASES = {
     # Qwen2.5-7B shape, Q8_0, biases, theta 1e6: a 24-token prompt, 16 greedy tokens
     "qwen2.5-7b-full": dict(kind="generate", config="qwen2.5-7b", prompt_len=24, max_new=16, max_seq=48),
     # the Llama-3-8B benchmark: 1024-token prompt, 512 greedy tokens, a 4096-position cache
-    "llama3-8b-bench": dict(kind="generate", config="llama3-8b", prompt_len=1024, max_new=512, max_seq=4096,
-                            hidden=True, driven=True),
+    "llama3-8b-bench": dict(kind="driven", config="llama3-8b", prompt_len=1024, max_new=512, max_seq=4096,
+                            hidden=True, chunk=32),
     # the Qwen2.5-0.5B benchmark: 512-token prompt, 256 greedy tokens
     "qwen2.5-0.5b-bench": dict(kind="generate", config="qwen2.5-0.5b", prompt_len=512, max_new=256, max_seq=768,
                                driven=True),
@@ -108,7 +116,43 @@ def prefill_ref_kv(ref, olib, d, kvp, pre, max_seq):
     ref.jyref_kv_set_len(kvp, pre)
 
 
-def driven(ref, olib, d, prompt, start, n_new, max_seq, cos, sin, kvp, want_hidden=False):
+def prefill(ref, d, X, start, cos, sin, kvp, chunk):
+    """forward_cached over the rows of X from position `start`, in chunks of `chunk` rows
+    (every chunk m >= 2 rows: the m > 1 product) or as one chunk (chunk = 0)."""
+    n = X.shape[0]
+    step = chunk or n
+    for r0 in range(0, n, step):
+        r1 = min(n, r0 + step)
+        assert chunk == 0 or r1 - r0 >= 2, "a chunk of one row would take the m = 1 product"
+        Xc = np.ascontiguousarray(X[r0:r1])
+        assert ref.jyref_forward_cached(C.byref(d), ptr(cos), ptr(sin), ptr(Xc), r1 - r0, start + r0, kvp, None) == 0
+        X[r0:r1] = Xc
+
+
+def check_chunking(ref, d, prompt, cos, sin, max_seq, rows=64, chunk=16):
+    """the first `rows` prompt rows as one chunk and in chunks: final states and K/V bit-equal"""
+    H = d.hidden
+    L, nkv, hd = d.num_layers, d.num_kv_heads, d.head_dim
+    outs = []
+    for ch in (0, chunk):
+        X = np.zeros((rows, H), np.float32)
+        for i, t in enumerate(prompt[:rows]):
+            embed(ref, d, t, X[i])
+        kvp = ref.jyref_kv_create(L, max_seq, nkv, hd)
+        prefill(ref, d, X, 0, cos, sin, kvp, ch)
+        k = np.ctypeslib.as_array(C.cast(ref.jyref_kv_k(kvp), C.POINTER(C.c_int8)), (L, max_seq, nkv, hd))[:, :rows].copy()
+        v = np.ctypeslib.as_array(C.cast(ref.jyref_kv_v(kvp), C.POINTER(C.c_int8)), (L, max_seq, nkv, hd))[:, :rows].copy()
+        ks = np.ctypeslib.as_array(C.cast(ref.jyref_kv_ks(kvp), C.POINTER(C.c_float)), (L, max_seq, nkv))[:, :rows].copy()
+        ref.jyref_kv_free(kvp)
+        outs.append((X, k, v, ks))
+    (x0, k0, v0, s0), (x1, k1, v1, s1) = outs
+    same = (np.array_equal(x0.view(np.uint32), x1.view(np.uint32)) and np.array_equal(k0, k1) and np.array_equal(v0, v1)
+            and np.array_equal(s0.view(np.uint32), s1.view(np.uint32)))
+    assert same, "a chunked prompt differs from the one-chunk prompt"
+    print(f"    {rows} prompt rows: one chunk and chunks of {chunk} are bit-equal", flush=True)
+
+
+def driven(ref, olib, d, prompt, start, n_new, max_seq, cos, sin, kvp, want_hidden=False, chunk=0):
     """greedy ids, per-step rel_gap and (optionally) the last prompt row's final state from
     forward_cached steps over the reference cache kvp, the prompt starting at `start`."""
     H = d.hidden
@@ -116,7 +160,9 @@ def driven(ref, olib, d, prompt, start, n_new, max_seq, cos, sin, kvp, want_hidd
     X = np.zeros((n, H), np.float32)
     for i, t in enumerate(prompt):
         embed(ref, d, t, X[i])
-    assert ref.jyref_forward_cached(C.byref(d), ptr(cos), ptr(sin), ptr(X), n, start, kvp, None) == 0
+    t0 = time.time()
+    prefill(ref, d, X, start, cos, sin, kvp, chunk if n > 1 else 0)
+    print(f"    prompt of {n} rows in {time.time() - t0:.1f} s", flush=True)
     hidden = X[n - 1].copy() if want_hidden else None
     ids, gaps = [], []
     x = np.ascontiguousarray(X[n - 1:n])
@@ -152,7 +198,16 @@ def run_case(ref, olib, name, cs):
     ref.jyref_rope_table(max_seq, d.head_dim, d.rope_theta, ptr(c), ptr(s))
     rec = dict(kind=cs["kind"], config=cname, prompt_len=plen, max_seq=max_seq, max_new=new)
     hidden = None
-    if cs["kind"] == "generate":
+    if cs["kind"] == "driven":
+        check_chunking(ref, d, prompt, c, s, max_seq)
+        kvp = ref.jyref_kv_create(d.num_layers, max_seq, d.num_kv_heads, d.head_dim)
+        got, gaps, hidden = driven(ref, olib, d, prompt, 0, new, max_seq, c, s, kvp, cs.get("hidden", False),
+                                   cs["chunk"])
+        ref.jyref_kv_free(kvp)
+        rec["ids"] = prompt.tolist() + got
+        rec["rel_gap"] = [round(g, 7) for g in gaps]
+        rec["chunk"] = cs["chunk"]
+    elif cs["kind"] == "generate":
         ids = np.zeros(max_seq + 1, np.int32)
         n = ref.jyref_generate(C.byref(d), ptr(prompt), plen, None, 0, ptr(c), ptr(s), max_seq, new, 0.0, 1.0,
                                ptr(ids), None, None, 0)
