@@ -1,30 +1,31 @@
 """The benchmark models at full size on the GPU, against the reference and the oracle.
 
-* Greedy ids of the Llama-3-8B, Qwen2.5-0.5B (its 512-token prompt, through the prompt
-  GEMM tiles) and Qwen2.5-7B shapes equal the ids jieyu's own decode loop produced for the
-  same seeded models and prompts (tests/golden/fullsize.json, written by
-  tests/golden/make_fullsize_golden.py from the compiled reference): in the exact mode
-  every id; in the fast mode every id up to a near tie.  At a tie the fast mode's logits of
-  that step (same prefix) must be within LOGIT_TOL * max|logit| (3e-2) of the exact ones, and the
-  exact-logit gap between the two picks no larger than twice their largest difference: the
-  flip is then what the measured rounding explains.  (These random-init models amplify a
-  change of rounding: GEMMs 5x closer to float64 than the reference's own fp32 sums still
-  move the logits by about 1e-3 of max|logit| after 32 layers.)  The ids after a tie follow
-  a different prefix and are not compared.
+* The benchmarks' own runs against jieyu's decode loop compiled from the reference sources
+  (tests/golden/fullsize.json, tests/golden/make_fullsize_golden.py): Llama-3-8B, the
+  1024-token prompt and 512 greedy tokens in a 4096-position cache; Qwen2.5-0.5B, the
+  512-token prompt and 256 tokens; Qwen2.5-7B, 128 tokens after a cache pre-filled to 32768
+  positions.  The exact mode must give every id.  The fast mode must give every id up to the
+  first divergence recorded in tests/golden/fast_ties.json (none where every id was equal),
+  and a divergence must be a near tie: the reference's own top-2 logit gap there at most twice
+  the fast logits' largest deviation from the exact ones at that step (same prefix), and that
+  deviation within LOGIT_TOL * max|logit| (2e-2; measured 6.4e-3 and 1.4e-2).  The ids after a tie
+  follow a different prefix and are not compared.  The Llama-3-8B prompt's last row after
+  the 1024-row prefill (the prompt GEMMs; on the matrix cores in the fast mode) against the
+  reference's: bit-equal in the exact mode, within HIDDEN_BENCH relative in the fast mode.
+* Shorter runs of the same three models against the reference (48 + 32, 512 + 64, 24 + 16
+  tokens), by the same rules with the exact-mode logits in place of the reference's gap.
+  (These random-init models amplify a change of rounding: per-layer deviations of ~1e-3
+  compound over the stack and the positions through the int8 requantization of q / k / v.)
 * Each layer on its own (the same input for the GPU's layer and the oracle's): a 16-row
   prompt and one decode row of Llama-3-8B through forward_cached, and at layers 0, 1, 15
   and 31 the oracle running that one layer on the GPU's input to it; bit-exact in the exact
-  mode, within 1e-3 relative in the fast mode.  (Over the whole stack the fast mode's
-  deviations compound: a change of rounding that moves a q / k / v value across an int8
-  rounding boundary moves that element by 1/127 of its head's range, so the random-init
-  8B model ends ~1e-2 from the exact run after 32 layers of 48 prompt rows.)
+  mode, within 1e-3 relative in the fast mode.
 * Decode steps at the benchmark positions through forward_cached: Llama-3-8B over a cache
   filled to 1024 positions, Qwen2.5-7B over 32768; per-layer hidden states bit-exact with
   the oracle in the exact mode, within 1e-3 relative (max|gpu - oracle| <= 1e-3 *
   max|oracle| per layer) in the fast mode.
-* Greedy decoding after the 32768-position cache (jyhip_session_resume) equals the oracle
-  driven token by token: every id in the exact mode, up to a near tie (as above, by the
-  oracle's logits) in the fast mode.
+* The benchmark sessions' captured decode graphs pass the host-side checks (kernel nodes in
+  one chain, every buffer they address live and unchanged) with the expected kernel count.
 The pre-filled caches hold packed N(0, 1) K and V, as the long-context benchmark sets up.
 """
 import ctypes as C
@@ -42,12 +43,16 @@ pytestmark = pytest.mark.gpu
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 TOL = 1e-3
-LOGIT_TOL = 3e-2  # the whole stack's compounded deviation (about 1e-2 of the hidden states after 32 layers)
-# benchmark-length runs: the fast logits' largest deviation from the exact ones at a
-# divergence step, as a fraction of max|logit|, and the last prompt row's relative error
-# after the whole stack
-LOGIT_BENCH = 1e-2
-HIDDEN_BENCH = 5e-2
+# The fast logits' largest deviation from the exact ones at a divergence step, as a fraction
+# of max|logit| (per-layer deviations of ~1e-3 compounded over 32 layers and the positions
+# through the int8 K/V): measured 6.41e-3 on the Llama-3-8B benchmark run (generated token
+# 112 after the 1024-token prompt) and 1.40e-2 on its 48-token run (generated token 24);
+# the bound leaves 1.4x over the larger.
+LOGIT_TOL = 2e-2
+LOGIT_BENCH = LOGIT_TOL
+# the last prompt row's relative error after the 32-layer, 1024-row fast prefill: measured
+# 4.19e-3
+HIDDEN_BENCH = 1e-2
 MODES = {"exact": 0, "fast": 7}
 
 
@@ -101,16 +106,24 @@ class Full:
         self.syn.close()
 
 
-def check_near_tie(got, want, n0, exact_logits, fast_logits=None):
+def check_near_tie(got, want, n0, exact_logits, fast_logits=None, name=None):
     """got (fast mode) against want (exact): equal, or equal up to index i where the step's
     fast logits (fast_logits(i), same prefix) are within LOGIT_TOL of the exact ones
     (exact_logits(i)) and the exact-logit gap of the two picks is within twice their largest
-    difference.  Without fast logits the gap is bounded by LOGIT_TOL * max|logit|."""
+    difference.  Without fast logits the gap is bounded by LOGIT_TOL * max|logit|.  With a
+    case name, i may not come before the tie recorded for it in fast_ties.json (and a case
+    recorded with every id equal may not diverge)."""
     if got == want:
         return
     assert len(got) == len(want), f"lengths {len(got)} vs {len(want)}"
     i = next(k for k in range(len(got)) if got[k] != want[k])
     assert i >= n0, f"prompt ids differ at {i}"
+    if name is not None:
+        ties = fast_ties()
+        assert not (name in ties and ties[name] is None), \
+            f"{name}: fast mode diverged at generated token {i - n0}; every id was equal when this case was recorded"
+        if ties.get(name) is not None:
+            assert i - n0 >= ties[name], f"{name}: diverged at {i - n0}, before the recorded tie at {ties[name]}"
     lg = exact_logits(i)
     assert int(np.argmax(lg)) == want[i]
     scale = float(np.abs(lg).max())
@@ -128,7 +141,7 @@ def check_near_tie(got, want, n0, exact_logits, fast_logits=None):
         assert gap <= LOGIT_TOL * scale, f"fast mode picked {got[i]} at {i}: gap {gap:.3g}"
 
 
-def check_generate(jy, olib, full, case):
+def check_generate(jy, olib, full, case, name=None):
     prompt = full.prompt(olib, case["prompt_len"])
     n0 = case["prompt_len"]
     assert prompt.tolist() == case["ids"][:n0]
@@ -147,7 +160,7 @@ def check_generate(jy, olib, full, case):
                 return lg
             return at
 
-        check_near_tie(ids.tolist(), case["ids"], n0, logits_in("exact"), logits_in(mode))
+        check_near_tie(ids.tolist(), case["ids"], n0, logits_in("exact"), logits_in(mode), name)
 
 
 def check_decode_layers(jy, olib, full, pre, steps):
@@ -234,13 +247,10 @@ def check_layers_alone(jy, olib, full, layers, rows=16):
 
 
 def fast_ties():
-    """The first fast-mode divergence found per benchmark-length case (generated-token
-    index), from the GPU runs that measured it; a later run may diverge there or later,
-    never earlier."""
-    p = os.path.join(HERE, "golden", "fast_ties.json")
-    if not os.path.exists(p):
-        return {}
-    with open(p) as f:
+    """The first fast-mode divergence measured per benchmark-length case (generated-token
+    index; None where every id was equal): a later run may diverge there or later, never
+    earlier, and a case recorded as equal may not diverge at all."""
+    with open(os.path.join(HERE, "golden", "fast_ties.json")) as f:
         return json.load(f)["ties"]
 
 
@@ -253,7 +263,10 @@ def check_bench_tie(name, k, case, exact_logits, fast_logits, pick):
     it must not come earlier than the recorded tie, the reference's own top-2 gap there must
     be small (rel_gap from the golden), the fast logits must be within LOGIT_BENCH of the
     exact ones, and the gap no larger than twice their largest difference."""
-    known = fast_ties().get(name)
+    ties = fast_ties()
+    assert not (name in ties and ties[name] is None), \
+        f"{name}: fast mode diverged at generated token {k}; every id was equal when this case was recorded"
+    known = ties.get(name)
     gap_rel = case["rel_gap"][k]
     lg, lf = exact_logits(), fast_logits()
     scale = float(np.abs(lg).max())
@@ -379,7 +392,7 @@ class TestLlama3_8B:
 
     def test_generate_matches_reference(self, jy, oracle_lib, full, golden):
         say("llama3-8b: greedy ids vs the reference")
-        check_generate(jy, oracle_lib, full, golden["llama3-8b-full"])
+        check_generate(jy, oracle_lib, full, golden["llama3-8b-full"], "llama3-8b-full")
 
     def test_layers_alone(self, jy, oracle_lib, full):
         say("llama3-8b: layers 0, 1, 15, 31 alone (16 prompt rows + 1 decode row) vs the oracle")
@@ -403,7 +416,7 @@ class TestQwen05B:
 
     def test_512_prompt_matches_reference(self, jy, oracle_lib, full, golden):
         say("qwen2.5-0.5b: 512-token prompt + 64 greedy tokens vs the reference")
-        check_generate(jy, oracle_lib, full, golden["qwen2.5-0.5b-full-512"])
+        check_generate(jy, oracle_lib, full, golden["qwen2.5-0.5b-full-512"], "qwen2.5-0.5b-full-512")
 
 
 class TestQwen7B:
@@ -417,7 +430,7 @@ class TestQwen7B:
 
     def test_generate_matches_reference(self, jy, oracle_lib, full, golden):
         say("qwen2.5-7b: greedy ids vs the reference")
-        check_generate(jy, oracle_lib, full, golden["qwen2.5-7b-full"])
+        check_generate(jy, oracle_lib, full, golden["qwen2.5-7b-full"], "qwen2.5-7b-full")
 
     def test_session_graph_checked(self, jy, oracle_lib, full):
         say("qwen2.5-7b: the long-context session's captured decode graph, host-side checks")
