@@ -89,14 +89,11 @@ void launch_mfma_repack(const Q8Dev& W, const Q8MfmaDev& M, hipStream_t st) {
 
 // ---------------------------------------------------------------- the activation split
 
-// one workgroup per row of the padded activations [mp][K]: rows past m are zero
-__global__ __launch_bounds__(256) void mfma_split_kernel(const float* __restrict__ A, int m, int K,
-                                                         _Float16* __restrict__ hi, _Float16* __restrict__ lo,
-                                                         float* __restrict__ unscale) {
-    __shared__ float red[4];
-    const int row = blockIdx.x, tid = threadIdx.x;
-    const float* a = A + (size_t)row * K;
-    const bool live = row < m;
+// one row of the padded activations (LDS or global, K values; `live` false: the row past m,
+// zero) into its fp16 high / low parts and its unscale, by a workgroup of 256 threads
+__device__ __forceinline__ void split_row(const float* a, bool live, int K, int row, _Float16* __restrict__ hi,
+                                          _Float16* __restrict__ lo, float* __restrict__ unscale, float* red) {
+    const int tid = threadIdx.x;
     float amax = 0.0f;
     if (live)
         for (int k = tid; k < K; k += 256) amax = fmaxf(amax, fabsf(a[k]));
@@ -118,6 +115,39 @@ __global__ __launch_bounds__(256) void mfma_split_kernel(const float* __restrict
         h[k] = vh;
         w[k] = (_Float16)(v - (float)vh);
     }
+}
+
+// one workgroup per row of the padded activations [mp][K]: rows past m are zero
+__global__ __launch_bounds__(256) void mfma_split_kernel(const float* __restrict__ A, int m, int K,
+                                                         _Float16* __restrict__ hi, _Float16* __restrict__ lo,
+                                                         float* __restrict__ unscale) {
+    __shared__ float red[4];
+    split_row(A + (size_t)blockIdx.x * K, (int)blockIdx.x < m, K, blockIdx.x, hi, lo, unscale, red);
+}
+
+// the same after the row's RMSNorm (block_rmsnorm, as rmsnorm_kernel computes it, in place in
+// LDS): one kernel and one pass over the row instead of two
+__global__ __launch_bounds__(256) void mfma_norm_split_kernel(const float* __restrict__ X, int m, int K,
+                                                              const float* __restrict__ nw, _Float16* __restrict__ hi,
+                                                              _Float16* __restrict__ lo,
+                                                              float* __restrict__ unscale) {
+    extern __shared__ __align__(16) float xr[];
+    __shared__ float red[18];
+    const bool live = (int)blockIdx.x < m;
+    if (live) {
+        const float* x = X + (size_t)blockIdx.x * K;
+        for (int i = threadIdx.x; i < K; i += 256) xr[i] = x[i];
+        __syncthreads();
+        block_rmsnorm(xr, K, nw, xr, red);
+        __syncthreads();
+    }
+    split_row(xr, live, K, blockIdx.x, hi, lo, unscale, red);
+}
+
+void launch_mfma_norm_split(const float* X, int m, int mp, int K, const float* nw, _Float16* hi, _Float16* lo,
+                            float* unscale, hipStream_t st) {
+    hipLaunchKernelGGL(mfma_norm_split_kernel, dim3(mp), dim3(256), (size_t)K * sizeof(float), st, X, m, K, nw, hi,
+                       lo, unscale);
 }
 
 void launch_mfma_split(const float* A, int m, int mp, int K, _Float16* hi, _Float16* lo, float* unscale,
@@ -275,6 +305,30 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_mfma2_kernel(Q8MfmaDev W, int 
             const int row = rowt + wm * 16 * MT + 16 * mt + 4 * G + i;
             us[mt][i] = row < m ? unscale[row] : 0.0f;
         }
+    if (EPI == EPI_SWIGLU) {
+        // the gate/up matrix's rows 2j, 2j+1 are gate_j, up_j: columns 2j and 2j+1 of C lie in
+        // lanes c and c + 1 of a tile; the even lane writes h[row][j] = silu(gate) * up with
+        // the reference's SiLU of element row * F + j of the m x F array (silu_mul_kernel)
+        const int F = N >> 1;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            if (tilet + wn * NT + nt >= W.tiles) continue;  // (uniform over the wave)
+            const int col = 16 * (tilet + wn * NT + nt) + c;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int row = rowt + wm * 16 * MT + 16 * mt + 4 * G + i;
+                    const float y = acc[mt][nt][i] * us[mt][i];
+                    const float up = __shfl_xor(y, 1);
+                    if (!(c & 1) && col + 1 < N && row < m) {
+                        const int j = col >> 1;
+                        C[(size_t)row * ldc + j] = silu_at(y, (size_t)row * F + j, (size_t)m * F) * up;
+                    }
+                }
+        }
+        return;
+    }
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         const int col = 16 * (tilet + wn * NT + nt) + c;
@@ -324,6 +378,10 @@ static void gemm2_launch(const Q8MfmaDev& W, int m, const _Float16* hi, const _F
             hipLaunchKernelGGL((gemm_q8_mfma2_kernel<EPI_RESID, MT, NT, S>), grid, dim3(256), lds, st, W, m, K, hi, lo,
                                unscale, C, ldc, aux);
             break;
+        case EPI_SWIGLU:
+            hipLaunchKernelGGL((gemm_q8_mfma2_kernel<EPI_SWIGLU, MT, NT, S>), grid, dim3(256), lds, st, W, m, K, hi, lo,
+                               unscale, C, ldc, aux);
+            break;
         default:
             hipLaunchKernelGGL((gemm_q8_mfma2_kernel<EPI_STORE, MT, NT, S>), grid, dim3(256), lds, st, W, m, K, hi, lo,
                                unscale, C, ldc, aux);
@@ -336,7 +394,8 @@ static hipError_t gemm2_attr() {
     hipError_t e = hipSuccess;
     for (const void* f : {reinterpret_cast<const void*>(&gemm_q8_mfma2_kernel<EPI_STORE, MT, NT, S>),
                           reinterpret_cast<const void*>(&gemm_q8_mfma2_kernel<EPI_BIAS, MT, NT, S>),
-                          reinterpret_cast<const void*>(&gemm_q8_mfma2_kernel<EPI_RESID, MT, NT, S>)})
+                          reinterpret_cast<const void*>(&gemm_q8_mfma2_kernel<EPI_RESID, MT, NT, S>),
+                          reinterpret_cast<const void*>(&gemm_q8_mfma2_kernel<EPI_SWIGLU, MT, NT, S>)})
         if (e == hipSuccess) e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)g2_lds<MT, NT, S>());
     return e;
 }

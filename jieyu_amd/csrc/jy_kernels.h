@@ -148,6 +148,9 @@ void launch_mfma_repack(const Q8Dev& W, const Q8MfmaDev& M, hipStream_t st);
 int mfma_rows_padded(int m);
 void launch_mfma_split(const float* A, int m, int mp, int K, _Float16* hi, _Float16* lo, float* unscale,
                        hipStream_t st);
+// the RMSNorm of X's rows (rmsnorm_kernel's arithmetic) and the split above in one kernel
+void launch_mfma_norm_split(const float* X, int m, int mp, int K, const float* nw, _Float16* hi, _Float16* lo,
+                            float* unscale, hipStream_t st);
 void launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
                          float* C, int ldc, const float* aux, Epi epi, hipStream_t st);
 void launch_gemm_f32(const float* B, int K, int N, int m, const float* A, float* C, const float* aux, Epi epi,

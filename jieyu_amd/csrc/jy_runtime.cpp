@@ -924,15 +924,23 @@ void run_prefill_layers(jyhip_model* m, Workspace& w, const KVDev& kv, int seq, 
             launch_gemm_q8(W, seq, A, Cm, aux, epi, st);
         }
     };
+    // matrix-core form of RMSNorm + GEMM: the norm and the activation split in one kernel
+    // (xn is not written); `ldc` the output row stride
+    auto norm_gemm_q8 = [&](const Q8MfmaDev& M, const float* nw, float* Cm, int ldc, const float* aux, Epi epi) {
+        launch_mfma_norm_split(w.X, seq, mp, H, nw, w.ah, w.al, w.aus, st);
+        launch_gemm_q8_mfma(M, seq, w.ah, w.al, w.aus, Cm, ldc, aux, epi, st);
+    };
     for (int l = 0; l < m->L; l++) {
         const DevLayer& D = m->layers[l];
-        launch_rmsnorm(w.X, w.xn, D.rms1, H, seq, st);
+        if (!mf) launch_rmsnorm(w.X, w.xn, D.rms1, H, seq, st);
         const Epi qkv_epi = D.bqkv ? EPI_BIAS : EPI_STORE;
         if (mixed) {
             const int qd = m->qd, kvd = m->kvd;
             launch_gemm(D.w[0], seq, w.xn, w.qkv, NQ, D.bqkv, qkv_epi, st);
             launch_gemm(D.w[1], seq, w.xn, w.qkv + qd, NQ, D.bqkv ? D.bqkv + qd : nullptr, qkv_epi, st);
             launch_gemm(D.w[2], seq, w.xn, w.qkv + qd + kvd, NQ, D.bqkv ? D.bqkv + qd + kvd : nullptr, qkv_epi, st);
+        } else if (mf) {
+            norm_gemm_q8(D.mqkv, D.rms1, w.qkv, D.qkv.rows, D.bqkv, qkv_epi);
         } else if (q8) {
             gemm_q8(D.qkv, D.mqkv, w.xn, w.qkv, D.bqkv, qkv_epi);
         } else {
@@ -958,12 +966,15 @@ void run_prefill_layers(jyhip_model* m, Workspace& w, const KVDev& kv, int seq, 
             gemm_q8(D.o, D.mo, w.att, w.X, nullptr, EPI_RESID);
         else
             launch_gemm_f32(D.f_o, m->qd, H, seq, w.att, w.X, nullptr, EPI_RESID, st);
-        launch_rmsnorm(w.X, w.xn, D.rms2, H, seq, st);
+        if (!mf) launch_rmsnorm(w.X, w.xn, D.rms2, H, seq, st);
         if (mixed) {
             launch_gemm(D.w[4], seq, w.xn, w.g, F, nullptr, EPI_STORE, st);
             launch_gemm(D.w[6], seq, w.xn, w.u, F, nullptr, EPI_STORE, st);
             launch_silu_mul(w.g, w.u, 0, seq, F, w.h, st);
             launch_gemm(D.w[5], seq, w.h, w.X, H, nullptr, EPI_RESID, st);
+        } else if (mf) {
+            norm_gemm_q8(D.mgu, D.rms2, w.h, F, nullptr, EPI_SWIGLU);  // h = silu(gate) * up, F wide
+            gemm_q8(D.down, D.mdown, w.h, w.X, nullptr, EPI_RESID);
         } else if (q8) {
             gemm_q8(D.gu, D.mgu, w.xn, w.g, nullptr, EPI_STORE);
             launch_silu_mul(w.g, nullptr, 1, seq, F, w.h, st);
