@@ -22,6 +22,9 @@
 // uses as many slices as that length needs.  Up to ATT_WHOLE_KEYS keys one kernel instead:
 // attn_whole_kernel, one workgroup per (kv head, 16 output dims) over all the keys.
 #include <algorithm>
+#include <mutex>
+#include <utility>
+#include <vector>
 
 #include "jy_attention_mfma.h"
 
@@ -124,8 +127,28 @@ int attn_split_slices(int keys) {
 
 size_t attn_split_part_floats(int nh, int hd, int ns) { return (size_t)nh * ns * (hd + 2); }
 
+// Workgroups of kernel k that the device holds at once (occupancy per CU times the CUs),
+// asked once per kernel.  The slice count is capped at that over the kv heads: a grid one
+// workgroup past it waits for a whole workgroup's time at the end (Qwen2.5-7B at 32769..32895
+// keys: 4 kv heads x 129 slices of 256 keys = 516 workgroups for 512 places).
+template <typename K>
+static int resident_wgs(K k, int threads) {
+    static std::mutex mu;
+    static std::vector<std::pair<const void*, int>> known;
+    std::lock_guard<std::mutex> g(mu);
+    for (const auto& e : known)
+        if (e.first == (const void*)k) return e.second;
+    int per_cu = 0, dev = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, threads, 0) != hipSuccess || hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 1 << 30;  // (no cap: the launch itself reports the device's error)
+    const int n = std::max(1, per_cu) * cus;
+    known.emplace_back((const void*)k, n);
+    return n;
+}
+
 template <int NW>
-static void split_launch(const AttnArgs& a, float* part, int ns, hipStream_t st) {
+static int split_launch(const AttnArgs& a, float* part, int ns, hipStream_t st) {
     auto k = attn_split_kernel<8, 8, NW>;
     switch (split_heads(a.nh / a.nkv) * (a.hd == 64 ? -1 : 1)) {
         case -1: k = attn_split_kernel<4, 1, NW>; break;
@@ -137,16 +160,15 @@ static void split_launch(const AttnArgs& a, float* part, int ns, hipStream_t st)
         case 4: k = attn_split_kernel<8, 4, NW>; break;
         default: break;
     }
+    ns = std::max(1, std::min(ns, resident_wgs(k, 64 * NW) / a.nkv));
     hipLaunchKernelGGL(k, dim3(a.nkv, ns), dim3(64 * NW), 0, st, a, ns, ns > 1 ? part : nullptr);
+    return ns;
 }
 
-// the slices (the form by a.max_keys, the longest length the launch may see), then (more
-// than one) the merge over (head, 32 dims)
+// the slices (the form by a.max_keys, the longest length the launch may see; at most ns, and
+// no more than the device holds at once), then (more than one) the merge over (head, 32 dims)
 void launch_attention_split(const AttnArgs& a, float* part, int ns, hipStream_t st) {
-    if (slice_keys(a.max_keys) > 128)
-        split_launch<8>(a, part, ns, st);
-    else
-        split_launch<4>(a, part, ns, st);
+    ns = slice_keys(a.max_keys) > 128 ? split_launch<8>(a, part, ns, st) : split_launch<4>(a, part, ns, st);
     if (ns > 1) hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nh, a.hd / 32), dim3(256), 0, st, a, ns, part);
 }
 
