@@ -23,6 +23,7 @@
 // holds rows 4 (l/16) .. +3 of column l % 16).  The operands reach LDS by global -> LDS DMA
 // three blocks deep (activation parts in operand order, weights as stored, block scales),
 // one workgroup barrier per block; each wave converts its weight fragments to fp16.
+#include <algorithm>
 #include <cstddef>
 
 #include "jy_layout.h"
@@ -221,6 +222,11 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_mfma2_kernel(Q8MfmaDev W, int 
     const int rowt = blockIdx.x * 32 * MT;  // the workgroup's first token row
     const int tilet = blockIdx.y * 2 * NT;  // its first 16-column tile
     const int nb = W.nb;
+    // the workgroup's K slice: blocks [b0, b1) of gridDim.z slices of nbz (all of them with
+    // one slice), its sums into C's slice z ([z][m][ldc]: the partials a sum kernel adds)
+    const int nbz = (nb + (int)gridDim.z - 1) / (int)gridDim.z;
+    const int b0 = (int)blockIdx.z * nbz, b1 = min(nb, b0 + nbz);
+    C += (size_t)blockIdx.z * m * ldc;
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_byte_addr(g2smem));
     constexpr int PW = MT + NT / 4 + 1;  // DMA instructions per wave per block
 
@@ -257,10 +263,10 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_mfma2_kernel(Q8MfmaDev W, int 
 
 #pragma unroll
     for (int s = 0; s < S - 1; s++)
-        if (s < nb) issue(s, s);
-    for (int b = 0; b < nb; b++) {
+        if (b0 + s < b1) issue(b0 + s, s);
+    for (int b = b0; b < b1; b++) {
         // block b has landed once at most the DMAs of the S - 2 blocks after it are pending
-        const int after = min(nb - 1 - b, S - 2);
+        const int after = min(b1 - 1 - b, S - 2);
         if (after >= S - 2)
             wait_vm<(S - 2) * PW>();
         else if (S > 3 && after == 1)
@@ -268,8 +274,8 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_mfma2_kernel(Q8MfmaDev W, int 
         else
             wait_vm<0>();
         __syncthreads();  // every wave's DMAs of block b are in LDS; block b - 1 is done
-        if (b + S - 1 < nb) issue(b + S - 1, (b + S - 1) % S);
-        const St& T = stg[b % S];
+        if (b + S - 1 < b1) issue(b + S - 1, (b - b0 + S - 1) % S);
+        const St& T = stg[(b - b0) % S];
         h8_t ah[MT], al[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
@@ -358,6 +364,40 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_mfma2_kernel(Q8MfmaDev W, int 
 
 int mfma_rows_padded(int m) { return (m + GM_TILE - 1) / GM_TILE * GM_TILE; }
 
+// ---------------------------------------------------------------- split over K
+//
+// A grid of fewer workgroups than CUs (the small matrices of a short prompt) leaves most of
+// the chip idle and each wave walking a long chain of blocks alone.  Such a GEMM runs as Z
+// slices of K (gridDim.z), each writing its partial sums [z][m][N] (plain stores), then
+// gemm_ksum_kernel adds the partials in slice order and applies the epilogue: the same
+// result for every run, whatever order the slices finish in.
+
+static constexpr int KSPLIT_MAX = 8;         // slices
+static constexpr int KSPLIT_MIN_BLOCKS = 8;  // 32-weight blocks per slice, at least
+
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_ksum_kernel(const float* __restrict__ P, int Z, int m, int N,
+                                                        float* __restrict__ C, int ldc, const float* __restrict__ aux) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t mn = (size_t)m * N;
+    if (i >= mn) return;
+    const int row = (int)(i / N), col = (int)(i - (size_t)row * N);
+    float v[KSPLIT_MAX];
+#pragma unroll
+    for (int z = 0; z < KSPLIT_MAX; z++) v[z] = z < Z ? P[(size_t)z * mn + i] : 0.0f;
+    float y = v[0];
+#pragma unroll
+    for (int z = 1; z < KSPLIT_MAX; z++)
+        if (z < Z) y += v[z];
+    float* c = C + (size_t)row * ldc + col;
+    if (EPI == EPI_RESID)
+        *c = *c + y;
+    else if (EPI == EPI_BIAS)
+        *c = y + aux[col];
+    else
+        *c = y;
+}
+
 template <int MT, int NT, int S>
 static size_t g2_lds() {
     return (size_t)S * sizeof(G2Stage<MT, NT>);
@@ -365,8 +405,9 @@ static size_t g2_lds() {
 
 template <int MT, int NT, int S>
 static void gemm2_launch(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
-                         float* C, int ldc, const float* aux, Epi epi, hipStream_t st) {
-    const dim3 grid((unsigned)(mfma_rows_padded(m) / (32 * MT)), (unsigned)((W.tiles + 2 * NT - 1) / (2 * NT)));
+                         float* C, int ldc, const float* aux, Epi epi, hipStream_t st, int Z = 1) {
+    const dim3 grid((unsigned)(mfma_rows_padded(m) / (32 * MT)), (unsigned)((W.tiles + 2 * NT - 1) / (2 * NT)),
+                    (unsigned)Z);
     const int K = W.nb * 32;
     const size_t lds = g2_lds<MT, NT, S>();
     switch (epi) {
@@ -408,13 +449,7 @@ hipError_t gemm_mfma_init() {
 
 static int g_gemm_cus = 0;
 
-// the wide tile (128 columns per wave) when its grid gives every CU at least two
-// workgroups, else the narrow one (64 columns per wave, twice the workgroups).  Measured at
-// the Llama-3-8B shapes and 1024 tokens (the activation split included): gate/up (28672 x
-// 4096) 576 us wide, 686 narrow; QKV 164, O 118, down 422 us narrow; at the Qwen2.5-0.5B
-// shapes and 512 tokens the narrow tile throughout (QKV 23, O 23, gate/up 44, down 90 us).
-void launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
-                         float* C, int ldc, const float* aux, Epi epi, hipStream_t st) {
+static int gemm_cus() {
     if (!g_gemm_cus) {
         int dev = 0, cus = 0;
         if (hipGetDevice(&dev) == hipSuccess &&
@@ -423,11 +458,63 @@ void launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _F
         else
             g_gemm_cus = 256;
     }
-    const long wide = (long)(mfma_rows_padded(m) / 64) * ((W.tiles + 15) / 16);
-    if (wide >= 2L * g_gemm_cus)
+    return g_gemm_cus;
+}
+
+// workgroups of the wide tile's grid (128 columns per wave)
+static long wide_wgs(const Q8MfmaDev& W, int m) { return (long)(mfma_rows_padded(m) / 64) * ((W.tiles + 15) / 16); }
+
+// K slices for C = A W^T over m rows: 1 unless the narrow tile's grid has fewer workgroups
+// than CUs; then up to two workgroups per CU, at most KSPLIT_MAX slices of at least
+// KSPLIT_MIN_BLOCKS blocks, none of them empty.  (The SwiGLU epilogue pairs columns and is
+// not split.)
+int gemm_q8_mfma_ksplit(const Q8MfmaDev& W, int m, Epi epi) {
+    const int cus = gemm_cus();
+    const long wgs = (long)(mfma_rows_padded(m) / 64) * ((W.tiles + 7) / 8);
+    if (epi == EPI_SWIGLU || wide_wgs(W, m) >= 2L * cus || wgs >= cus) return 1;
+    const int z = (int)std::min<long>(std::min<long>(KSPLIT_MAX, 2L * cus / std::max(1L, wgs)),
+                                      W.nb / KSPLIT_MIN_BLOCKS);
+    if (z < 2) return 1;
+    const int nbz = (W.nb + z - 1) / z;
+    return (W.nb + nbz - 1) / nbz;
+}
+
+size_t gemm_q8_mfma_kpart_floats(const Q8MfmaDev& W, int m, Epi epi) {
+    const int z = gemm_q8_mfma_ksplit(W, m, epi);
+    return z > 1 ? (size_t)z * m * W.rows : 0;
+}
+
+// the wide tile (128 columns per wave) when its grid gives every CU at least two
+// workgroups, else the narrow one (64 columns per wave, twice the workgroups), split over K
+// when even that grid leaves CUs idle and `kpart` holds the partials.  Measured at the
+// Llama-3-8B shapes and 1024 tokens (the activation split included): gate/up (28672 x
+// 4096) 576 us wide, 686 narrow; QKV 164, O 118, down 422 us narrow.
+void launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
+                         float* C, int ldc, const float* aux, Epi epi, hipStream_t st, float* kpart, size_t kpart_n) {
+    const int cus = gemm_cus();
+    if (wide_wgs(W, m) >= 2L * cus) {
         gemm2_launch<2, 8, 3>(W, m, hi, lo, unscale, C, ldc, aux, epi, st);
-    else
+        return;
+    }
+    const int Z = gemm_q8_mfma_ksplit(W, m, epi);
+    if (Z < 2 || !kpart || (size_t)Z * m * W.rows > kpart_n) {
         gemm2_launch<2, 4, 3>(W, m, hi, lo, unscale, C, ldc, aux, epi, st);
+        return;
+    }
+    gemm2_launch<2, 4, 3>(W, m, hi, lo, unscale, kpart, W.rows, nullptr, EPI_STORE, st, Z);
+    const size_t n = (size_t)m * W.rows;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    switch (epi) {
+        case EPI_BIAS:
+            hipLaunchKernelGGL(gemm_ksum_kernel<EPI_BIAS>, grid, dim3(256), 0, st, kpart, Z, m, W.rows, C, ldc, aux);
+            break;
+        case EPI_RESID:
+            hipLaunchKernelGGL(gemm_ksum_kernel<EPI_RESID>, grid, dim3(256), 0, st, kpart, Z, m, W.rows, C, ldc, aux);
+            break;
+        default:
+            hipLaunchKernelGGL(gemm_ksum_kernel<EPI_STORE>, grid, dim3(256), 0, st, kpart, Z, m, W.rows, C, ldc, aux);
+            break;
+    }
 }
 
 }  // namespace jy

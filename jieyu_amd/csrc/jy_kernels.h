@@ -151,8 +151,13 @@ void launch_mfma_split(const float* A, int m, int mp, int K, _Float16* hi, _Floa
 // the RMSNorm of X's rows (rmsnorm_kernel's arithmetic) and the split above in one kernel
 void launch_mfma_norm_split(const float* X, int m, int mp, int K, const float* nw, _Float16* hi, _Float16* lo,
                             float* unscale, hipStream_t st);
+// (kpart: kpart_n floats for the partial sums of a GEMM split over K, or nullptr: no split)
 void launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
-                         float* C, int ldc, const float* aux, Epi epi, hipStream_t st);
+                         float* C, int ldc, const float* aux, Epi epi, hipStream_t st, float* kpart = nullptr,
+                         size_t kpart_n = 0);
+// the K slices launch_gemm_q8_mfma takes for these rows, and the partial floats they need
+int gemm_q8_mfma_ksplit(const Q8MfmaDev& W, int m, Epi epi);
+size_t gemm_q8_mfma_kpart_floats(const Q8MfmaDev& W, int m, Epi epi);
 void launch_gemm_f32(const float* B, int K, int N, int m, const float* A, float* C, const float* aux, Epi epi,
                      hipStream_t st);
 // h[i][j] = silu(gu[i][2j]) * gu[i][2j+1]  (or silu(g) * u with separate buffers)

@@ -119,6 +119,8 @@ struct Workspace {
     float* aus = nullptr;
     size_t a_cap = 0;  // halves per part
     int a_rows = 0;    // rows of aus
+    float* kp = nullptr;  // partial sums of the matrix-core GEMMs split over K
+    size_t kp_n = 0;
     unsigned gen = 0;  // bumped whenever a buffer above is replaced: graphs captured before are stale
 };
 
@@ -241,6 +243,8 @@ void ensure_ws(jyhip_model* m, int rows) {
     w.aus = split.aus;
     w.a_cap = split.a_cap;
     w.a_rows = split.a_rows;
+    w.kp = split.kp;
+    w.kp_n = split.kp_n;
     const size_t r = (size_t)rows;
     w.X = dalloc<float>(r * m->H);
     w.xn = dalloc<float>(r * m->H);
@@ -282,6 +286,17 @@ void ensure_split(jyhip_model* m, size_t halves, int rows) {
     w.a_rows = rows;
 }
 
+// the partial sums of the matrix-core GEMMs split over K (floats)
+void ensure_kpart(jyhip_model* m, size_t n) {
+    Workspace& w = m->ws;
+    if (w.kp_n >= n) return;
+    dfree(w.kp);
+    w.kp = nullptr;
+    w.kp_n = 0;
+    w.kp = dalloc<float>(n, false);
+    w.kp_n = n;
+}
+
 // a matrix's copy for the matrix-core GEMM (allocation recorded in `owned`)
 Q8MfmaDev mfma_copy(std::vector<void*>& owned, const Q8Dev& W, hipStream_t st) {
     Q8MfmaDev M;
@@ -318,6 +333,15 @@ bool use_mfma(const jyhip_model* m) {
 }
 size_t mfma_split_halves(const jyhip_model* m, int seq) {
     return (size_t)mfma_rows_padded(seq) * std::max({m->H, m->qd, m->F});
+}
+// the partial floats a prompt pass of `seq` rows takes for its GEMMs split over K (every
+// layer has the same shapes)
+size_t mfma_kpart_need(const jyhip_model* m, int seq) {
+    if (m->layers.empty() || !m->mfma_built) return 0;
+    const DevLayer& D = m->layers[0];
+    return std::max({gemm_q8_mfma_kpart_floats(D.mqkv, seq, D.bqkv ? EPI_BIAS : EPI_STORE),
+                     gemm_q8_mfma_kpart_floats(D.mo, seq, EPI_RESID),
+                     gemm_q8_mfma_kpart_floats(D.mdown, seq, EPI_RESID)});
 }
 
 void ensure_part(jyhip_model* m, size_t n) {
@@ -762,7 +786,7 @@ void release(jyhip_model* m) {
     Workspace& w = m->ws;
     for (void* p : {(void*)w.X, (void*)w.xn, (void*)w.qkv, (void*)w.att, (void*)w.g, (void*)w.u, (void*)w.h,
                     (void*)w.q8, (void*)w.qsc, (void*)w.scores, (void*)w.part, (void*)w.ah, (void*)w.al,
-                    (void*)w.aus})
+                    (void*)w.aus, (void*)w.kp})
         dfree(p);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
@@ -916,10 +940,14 @@ void run_prefill_layers(jyhip_model* m, Workspace& w, const KVDev& kv, int seq, 
         if (&w != &m->ws) fail("prefill: the workspace has no room for the matrix-core split buffers");
         ensure_split(m, mfma_split_halves(m, seq), mp);
     }
+    if (mf && w.kp_n < mfma_kpart_need(m, seq)) {
+        if (&w != &m->ws) fail("prefill: the workspace has no room for the matrix-core partial sums");
+        ensure_kpart(m, mfma_kpart_need(m, seq));
+    }
     auto gemm_q8 = [&](const Q8Dev& W, const Q8MfmaDev& M, const float* A, float* Cm, const float* aux, Epi epi) {
         if (mf) {
             launch_mfma_split(A, seq, mp, W.cols, w.ah, w.al, w.aus, st);
-            launch_gemm_q8_mfma(M, seq, w.ah, w.al, w.aus, Cm, W.rows, aux, epi, st);
+            launch_gemm_q8_mfma(M, seq, w.ah, w.al, w.aus, Cm, W.rows, aux, epi, st, w.kp, w.kp_n);
         } else {
             launch_gemm_q8(W, seq, A, Cm, aux, epi, st);
         }
@@ -928,7 +956,7 @@ void run_prefill_layers(jyhip_model* m, Workspace& w, const KVDev& kv, int seq, 
     // (xn is not written); `ldc` the output row stride
     auto norm_gemm_q8 = [&](const Q8MfmaDev& M, const float* nw, float* Cm, int ldc, const float* aux, Epi epi) {
         launch_mfma_norm_split(w.X, seq, mp, H, nw, w.ah, w.al, w.aus, st);
-        launch_gemm_q8_mfma(M, seq, w.ah, w.al, w.aus, Cm, ldc, aux, epi, st);
+        launch_gemm_q8_mfma(M, seq, w.ah, w.al, w.aus, Cm, ldc, aux, epi, st, w.kp, w.kp_n);
     };
     for (int l = 0; l < m->L; l++) {
         const DevLayer& D = m->layers[l];
@@ -1535,6 +1563,8 @@ Workspace ws_view(const jyhip_model* m, int seq, int max_keys, size_t scores_n, 
         w.ah = (_Float16*)take(w.a_cap * 2);
         w.al = (_Float16*)take(w.a_cap * 2);
         w.aus = (float*)take((size_t)w.a_rows * 4);
+        w.kp_n = mfma_kpart_need(m, seq);
+        w.kp = (float*)take(w.kp_n * 4);
     }
     w.rows = seq;
     *bytes = off;
@@ -1956,40 +1986,51 @@ namespace {
 // C[mr][rows] = A[mr][cols] W^T for copy c in the matrix's mode, device buffers given;
 // the MFMA form splits A into hi / lo first
 void q8_gemm_launch(jyhip_q8mat* q, size_t c, int mr, const float* A, float* Cd, _Float16* hi, _Float16* lo,
-                    float* us) {
+                    float* us, float* kp, size_t kp_n) {
     const Q8Dev& d = q->copies[c];
     if (q->mode & JYHIP_MODE_MFMA_PREFILL) {
         launch_mfma_split(A, mr, mfma_rows_padded(mr), d.cols, hi, lo, us, q->stream);
-        launch_gemm_q8_mfma(q->mcopies[c], mr, hi, lo, us, Cd, d.rows, nullptr, EPI_STORE, q->stream);
+        launch_gemm_q8_mfma(q->mcopies[c], mr, hi, lo, us, Cd, d.rows, nullptr, EPI_STORE, q->stream, kp, kp_n);
     } else {
         launch_gemm_q8(d, mr, A, Cd, nullptr, EPI_STORE, q->stream);
     }
 }
 
-// run f(A_dev, C_dev, hi, lo, us) with device buffers for mr rows of A uploaded from host
+// the device buffers of a GEMM over mr rows: A, C, the activation split and the partial sums
+struct GemmBufs {
+    float *A = nullptr, *C = nullptr;
+    _Float16 *hi = nullptr, *lo = nullptr;
+    float* us = nullptr;
+    float* kp = nullptr;
+    size_t kp_n = 0;
+};
+
+// run f(bufs) with device buffers for mr rows of A uploaded from host
 template <class F>
 void with_gemm_buffers(jyhip_q8mat* q, int mr, const float* A, F&& f) {
     const Q8Dev& d = q->copies[0];
     const size_t mp = (size_t)mfma_rows_padded(mr);
-    float* Ad = nullptr;
-    float* Cd = nullptr;
-    uint16_t *hi = nullptr, *lo = nullptr;
-    float* us = nullptr;
+    GemmBufs b;
+    auto free_all = [&]() {
+        for (void* p : {(void*)b.A, (void*)b.C, (void*)b.hi, (void*)b.lo, (void*)b.us, (void*)b.kp}) dfree(p);
+    };
     try {
-        Ad = dalloc<float>((size_t)mr * d.cols, false);
-        Cd = dalloc<float>((size_t)mr * d.rows, false);
-        hi = dalloc<uint16_t>(mp * d.cols, false);
-        lo = dalloc<uint16_t>(mp * d.cols, false);
-        us = dalloc<float>(mp, false);
-        CK(hipMemcpyAsync(Ad, A, sizeof(float) * mr * d.cols, hipMemcpyHostToDevice, q->stream));
-        f(Ad, Cd, reinterpret_cast<_Float16*>(hi), reinterpret_cast<_Float16*>(lo), us);
+        b.A = dalloc<float>((size_t)mr * d.cols, false);
+        b.C = dalloc<float>((size_t)mr * d.rows, false);
+        b.hi = reinterpret_cast<_Float16*>(dalloc<uint16_t>(mp * d.cols, false));
+        b.lo = reinterpret_cast<_Float16*>(dalloc<uint16_t>(mp * d.cols, false));
+        b.us = dalloc<float>(mp, false);
+        if (!q->mcopies.empty()) b.kp_n = gemm_q8_mfma_kpart_floats(q->mcopies[0], mr, EPI_STORE);
+        if (b.kp_n) b.kp = dalloc<float>(b.kp_n, false);
+        CK(hipMemcpyAsync(b.A, A, sizeof(float) * mr * d.cols, hipMemcpyHostToDevice, q->stream));
+        f(b);
     } catch (...) {
         (void)hipStreamSynchronize(q->stream);
-        for (void* p : {(void*)Ad, (void*)Cd, (void*)hi, (void*)lo, (void*)us}) dfree(p);
+        free_all();
         throw;
     }
     (void)hipStreamSynchronize(q->stream);
-    for (void* p : {(void*)Ad, (void*)Cd, (void*)hi, (void*)lo, (void*)us}) dfree(p);
+    free_all();
 }
 }  // namespace
 
@@ -1998,10 +2039,10 @@ extern "C" {
 JYHIP_API int jyhip_q8_gemm(jyhip_q8mat* q, int mr, const float* A, float* Cout) {
     return guarded([&]() {
         if (!q || !A || !Cout || mr <= 0) fail("bad argument");
-        with_gemm_buffers(q, mr, A, [&](float* Ad, float* Cd, _Float16* hi, _Float16* lo, float* us) {
-            q8_gemm_launch(q, 0, mr, Ad, Cd, hi, lo, us);
+        with_gemm_buffers(q, mr, A, [&](const GemmBufs& b) {
+            q8_gemm_launch(q, 0, mr, b.A, b.C, b.hi, b.lo, b.us, b.kp, b.kp_n);
             CK(hipGetLastError());
-            CK(hipMemcpyAsync(Cout, Cd, sizeof(float) * mr * q->copies[0].rows, hipMemcpyDeviceToHost, q->stream));
+            CK(hipMemcpyAsync(Cout, b.C, sizeof(float) * mr * q->copies[0].rows, hipMemcpyDeviceToHost, q->stream));
             CK(hipStreamSynchronize(q->stream));
         });
         return 0;
@@ -2011,13 +2052,14 @@ JYHIP_API int jyhip_q8_gemm(jyhip_q8mat* q, int mr, const float* A, float* Cout)
 JYHIP_API int jyhip_q8_gemm_time(jyhip_q8mat* q, int mr, const float* A, int iters, double* avg_us) {
     return guarded([&]() {
         if (!q || !A || !avg_us || mr <= 0 || iters <= 0) fail("bad argument");
-        with_gemm_buffers(q, mr, A, [&](float* Ad, float* Cd, _Float16* hi, _Float16* lo, float* us) {
-            for (size_t c = 0; c < q->copies.size(); c++) q8_gemm_launch(q, c, mr, Ad, Cd, hi, lo, us);
+        with_gemm_buffers(q, mr, A, [&](const GemmBufs& g) {
+            for (size_t c = 0; c < q->copies.size(); c++) q8_gemm_launch(q, c, mr, g.A, g.C, g.hi, g.lo, g.us, g.kp, g.kp_n);
             hipEvent_t a, b;
             CK(hipEventCreate(&a));
             CK(hipEventCreate(&b));
             CK(hipEventRecord(a, q->stream));
-            for (int i = 0; i < iters; i++) q8_gemm_launch(q, (size_t)i % q->copies.size(), mr, Ad, Cd, hi, lo, us);
+            for (int i = 0; i < iters; i++)
+                q8_gemm_launch(q, (size_t)i % q->copies.size(), mr, g.A, g.C, g.hi, g.lo, g.us, g.kp, g.kp_n);
             CK(hipEventRecord(b, q->stream));
             CK(hipEventSynchronize(b));
             float ms = 0.0f;
