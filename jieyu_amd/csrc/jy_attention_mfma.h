@@ -98,8 +98,10 @@ __device__ __forceinline__ int4 own_mix(int4 x, int4 y, bool take) {
 // heads; with DSP > 1 every workgroup of a kv head runs the q.k and softmax of all its keys
 // (redundantly) and only its dims of p.v, so that one kernel covers the whole range without
 // a merge.  PF: steps of loads a wave keeps in flight (2: the next step's loads go out a
-// whole step ahead, for waves that take several steps).
-template <int P, int GT, int NW, bool COH, int DSP = 1, int PF = 1>
+// whole step ahead, for waves that take several steps).  RW (prompt rows only): the
+// workgroup takes rows prow - RW + 1 .. prow, RW x G query columns (column c: row c / G, head
+// c % G), each column's keys masked past its own row; rows below 0 are empty columns.
+template <int P, int GT, int NW, bool COH, int DSP = 1, int PF = 1, int RW = 1>
 __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float* __restrict__ part, int kvh, int s,
                                                 MslLds<P * 16, NW, P * 16 / DSP>& L, int prow = 0, int dsl = 0) {
     constexpr int HD = P * 16, ST = MSL_STEP;
@@ -118,6 +120,8 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int nh = a.nh, nkv = a.nkv, G = nh / nkv;  // G <= GT
+    const int Gc = RW * G;                           // query columns in use (<= GT)
+    static_assert(RW == 1 || RW == 2 || RW == 4 || RW == 8, "rows per workgroup");
     const bool fused = a.fused;
     // (the length as loaded, no arithmetic in the branch: the wait for it then falls at its
     // first use, after the first loads)
@@ -206,10 +210,20 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
     // them (at most one 16-byte piece per thread), and their scales
     int4 qp = make_int4(0, 0, 0, 0);
     float qsp = 0.0f;
-    const size_t qrow = (size_t)(a.row0 + prow) * nh + (size_t)kvh * G;
+    // a query column's row and its (row, head) index into q8 / qsc; -1: an empty column
+    auto qcol_at = [&](int cc) -> long {
+        const int rr = cc / G, r = prow - (RW - 1) + rr;
+        return r < 0 ? -1 : ((long)(a.row0 + r) * nh + (long)kvh * G + (cc - rr * G));
+    };
     if (!fused) {
-        if (tid < G * HD / 16) qp = reinterpret_cast<const int4*>(a.q8 + qrow * HD)[tid];
-        if (tid < G) qsp = a.qsc[qrow + tid];
+        if (tid < Gc * HD / 16) {
+            const long qi = qcol_at(tid / (HD / 16));
+            if (qi >= 0) qp = reinterpret_cast<const int4*>(a.q8 + (size_t)qi * HD)[tid % (HD / 16)];
+        }
+        if (tid < Gc) {
+            const long qi = qcol_at(tid);
+            if (qi >= 0) qsp = a.qsc[qi];
+        }
     }
     MslRegs<HD, NV> rg[PF];  // (all masked for a wave without keys)
 #pragma unroll
@@ -240,11 +254,11 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
         }
     }
     if (!fused) {
-        if (tid < G * HD / 16) *reinterpret_cast<int4*>(&L.q8[tid / (HD / 16)][16 * (tid % (HD / 16))]) = qp;
-        if (tid < G) L.qsc[tid] = qsp;
+        if (tid < Gc * HD / 16) *reinterpret_cast<int4*>(&L.q8[tid / (HD / 16)][16 * (tid % (HD / 16))]) = qp;
+        if (tid < Gc) L.qsc[tid] = qsp;
     }
-    for (int i = G * HD + tid; i < GT * HD; i += NW * 64) L.q8[i / HD][i % HD] = 0;
-    if (tid < GT - G) L.qsc[G + tid] = 0.0f;
+    for (int i = Gc * HD + tid; i < GT * HD; i += NW * 64) L.q8[i / HD][i % HD] = 0;
+    if (tid < GT - Gc) L.qsc[Gc + tid] = 0.0f;
     lds_barrier();  // (the key loads stay in flight)
     if (holds_new && dsl == 0) {  // kv_pack_q8 of the new position, appended by the workgroup that holds it
         for (int d = tid; d < HD; d += NW * 64) {
@@ -376,6 +390,14 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
                 for (int i = 0; i < 4; i++)
                     if (base + 16 * t + 4 * grp + i >= j1) sc[t][i] = -__builtin_inff();
         }
+        if (RW > 1 && base + ST > j1 - (RW - 1)) {  // the keys of the group's later rows
+            const int lim = j1 - (RW - 1 - qh / G);  // past the column's own row
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (base + 16 * t + 4 * grp + i >= lim) sc[t][i] = -__builtin_inff();
+        }
         // the step's maximum per head column; on a rise, the rescale of what came before
         float tm = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
                          fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
@@ -395,11 +417,13 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
         // weights: e for the sum; p = e * vs * 2^c, in fp16 (columns < GT) or its remainder
         h8_t pb;
         float esum = 0.0f;
+        // (with RW > 1 a column may have no key yet: its maximum is still -inf, its weights 0)
+        const float mref = (RW > 1 && m_run == -__builtin_inff()) ? 0.0f : m_run;
 #pragma unroll
         for (int t = 0; t < 2; t++) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float e = __builtin_amdgcn_exp2f(sc[t][i] - m_run);
+                const float e = __builtin_amdgcn_exp2f(sc[t][i] - mref);
                 esum += e;
                 const float p = e * vs[t][i];
                 const _Float16 hi = (_Float16)p;
@@ -456,7 +480,7 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
     static_assert(SPL_GMAX * NW <= 128 && 64 % NW == 0, "merge lanes");
     if (tid < 128) {
         const int w = tid % NW, g = tid / NW;
-        const bool ok = g < G;
+        const bool ok = g < Gc;
         const float mw = ok ? L.mw[w][g] : 0.0f;
         float M = mw;
 #pragma unroll
@@ -475,13 +499,14 @@ __device__ __forceinline__ bool attn_slice_mfma(const AttnArgs& a, int ns, float
     }
     __syncthreads();
     const int W = HD + 2;
-    for (int o = tid; o < G * VW; o += NW * 64) {
+    for (int o = tid; o < Gc * VW; o += NW * 64) {
         const int g = o / VW, dd = o - g * VW;
         float t = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; w++) t = __builtin_fmaf(L.fw[w][g], L.u.ow[w][g * OWS + dd], t);
         if (!part) {
-            a.out[((size_t)(a.row0 + prow) * nh + kvh * G + g) * HD + VW * dsl + dd] = t / L.lg[g];
+            const long qi = qcol_at(g);
+            if (qi >= 0) a.out[(size_t)qi * HD + VW * dsl + dd] = t / L.lg[g];
             continue;
         }
         float* out = part + ((size_t)(kvh * G + g) * ns + s) * W;

@@ -56,12 +56,15 @@ __global__ __launch_bounds__(64 * WW) __attribute__((amdgpu_waves_per_eu(4, 4)))
     attn_slice_mfma<P, GT, WW, false, P, 2>(a, 1, nullptr, blockIdx.x, 0, lds, 0, blockIdx.y);
 }
 
-// prompt rows: one workgroup per (kv head, row), the row's whole key range as one slice,
-// the normalised output straight to a.out; rows in descending order (the longest first)
-template <int P, int GT>
+// prompt rows: one workgroup per (kv head, R consecutive rows), the highest row's whole key
+// range as one slice, the other rows' later keys masked per query column; the normalised
+// output straight to a.out; row groups in descending order (the longest first).  R rows
+// fill the 8 query columns of the slice's matrix operations (R x the group's heads).
+template <int P, int R>
 __global__ __launch_bounds__(SPL_THREADS) __attribute__((amdgpu_waves_per_eu(4, 4))) void attn_prefill_kernel(AttnArgs a) {
     __shared__ MslLds<P * 16, 4> lds;
-    attn_slice_mfma<P, GT, 4, false>(a, 1, nullptr, blockIdx.x, 0, lds, a.nrows - 1 - (int)blockIdx.y);
+    attn_slice_mfma<P, SPL_GMAX, 4, false, 1, 1, R>(a, 1, nullptr, blockIdx.x, 0, lds,
+                                                    a.nrows - 1 - R * (int)blockIdx.y);
 }
 
 // The merge for many slices: one workgroup per (query head, 32 output dims).  Every load
@@ -197,17 +200,21 @@ void launch_attention_whole(const AttnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(k, dim3(a.nkv, a.hd / 16), dim3(64 * WW), 0, st, a);
 }
 
+// Rows per workgroup: as many as the 8 query columns hold (R = 8 / split_heads(G)).
+// Llama-3-8B shape (4 query heads per kv head), 1024 prompt rows: one row per workgroup
+// 108 us per layer, two rows [measured below].
 void launch_attention_prefill_split(const AttnArgs& a, hipStream_t st) {
-    const dim3 grid(a.nkv, a.nrows), block(SPL_THREADS);
-    auto k = attn_prefill_kernel<8, 8>;
-    switch (split_heads(a.nh / a.nkv) * (a.hd == 64 ? -1 : 1)) {
+    const int R = SPL_GMAX / split_heads(a.nh / a.nkv);
+    const dim3 grid(a.nkv, (a.nrows + R - 1) / R), block(SPL_THREADS);
+    auto k = attn_prefill_kernel<8, 1>;
+    switch (R * (a.hd == 64 ? -1 : 1)) {
         case -1: k = attn_prefill_kernel<4, 1>; break;
         case -2: k = attn_prefill_kernel<4, 2>; break;
         case -4: k = attn_prefill_kernel<4, 4>; break;
         case -8: k = attn_prefill_kernel<4, 8>; break;
-        case 1: k = attn_prefill_kernel<8, 1>; break;
         case 2: k = attn_prefill_kernel<8, 2>; break;
         case 4: k = attn_prefill_kernel<8, 4>; break;
+        case 8: k = attn_prefill_kernel<8, 8>; break;
         default: break;
     }
     hipLaunchKernelGGL(k, grid, block, 0, st, a);

@@ -33,6 +33,8 @@ namespace jy {
 
 static constexpr int GM_TILE = 128;  // activation rows are padded to a multiple of this
 
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+
 // ---------------------------------------------------------------- the matrix copy
 
 // one thread per (16-row tile t, block b, lane l): the 8 weights of row 16t + (l % 16),
@@ -145,15 +147,133 @@ __global__ __launch_bounds__(256) void mfma_norm_split_kernel(const float* __res
     split_row(xr, live, K, blockIdx.x, hi, lo, unscale, red);
 }
 
+// The same two kernels with the row in registers: NV float4s per thread (element
+// 4 (tid + 256 j) .. +3 in v[j]), one read of the row, 16-byte loads and 8-byte stores of
+// four halves; the same arithmetic element by element (K a multiple of 4, K <= 1024 NV).
+template <int NV>
+__device__ __forceinline__ void split_row4(const float4 (&v)[NV], int K, int row, _Float16* __restrict__ hi,
+                                           _Float16* __restrict__ lo, float* __restrict__ unscale, float* red) {
+    const int tid = threadIdx.x;
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; j++)
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+    amax = wave_max64(amax);
+    if ((tid & 63) == 0) red[tid >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int ex = 0;
+    if (amax > 0.0f) frexpf(amax, &ex);
+    const int s = amax > 0.0f ? min(max(14 - ex, -100), 100) : 0;
+    const float up = ldexpf(1.0f, s);
+    if (tid == 0) unscale[row] = ldexpf(1.0f, -s);
+    _Float16* h = hi + (size_t)row * K;
+    _Float16* w = lo + (size_t)row * K;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int k4 = tid + 256 * j;
+        if (4 * k4 >= K) break;
+        const float e[4] = {v[j].x * up, v[j].y * up, v[j].z * up, v[j].w * up};
+        h4_t vh, vl;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            vh[i] = (_Float16)e[i];
+            vl[i] = (_Float16)(e[i] - (float)vh[i]);
+        }
+        *reinterpret_cast<h4_t*>(h + 4 * k4) = vh;
+        *reinterpret_cast<h4_t*>(w + 4 * k4) = vl;
+    }
+}
+
+template <int NV>
+__global__ __launch_bounds__(256) void mfma_split4_kernel(const float* __restrict__ A, int m, int K,
+                                                          _Float16* __restrict__ hi, _Float16* __restrict__ lo,
+                                                          float* __restrict__ unscale) {
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    const bool live = row < m;
+    const float4* a4 = reinterpret_cast<const float4*>(A + (size_t)row * K);
+    float4 v[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int k4 = threadIdx.x + 256 * j;
+        v[j] = live && 4 * k4 < K ? a4[k4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    split_row4<NV>(v, K, row, hi, lo, unscale, red);
+}
+
+template <int NV>
+__global__ __launch_bounds__(256) void mfma_norm_split4_kernel(const float* __restrict__ X, int m, int K,
+                                                               const float* __restrict__ nw, _Float16* __restrict__ hi,
+                                                               _Float16* __restrict__ lo, float* __restrict__ unscale) {
+    extern __shared__ __align__(16) float xr[];
+    __shared__ float red[18];
+    const int row = blockIdx.x;
+    const bool live = row < m;
+    float4* x4 = reinterpret_cast<float4*>(xr);
+    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    // the norm weights go out first (they do not wait for the row), the row to registers
+    // and to LDS for the sum of squares in the reference's lane order
+    float4 w4[NV], v[NV];
+    const float4* n4 = reinterpret_cast<const float4*>(nw);
+    const float4* g4 = reinterpret_cast<const float4*>(X + (size_t)row * K);
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int k4 = threadIdx.x + 256 * j;
+        w4[j] = live && 4 * k4 < K ? n4[k4] : z4;
+        v[j] = live && 4 * k4 < K ? g4[k4] : z4;
+        if (live && 4 * k4 < K) x4[k4] = v[j];
+    }
+    if (live) {
+        __syncthreads();
+        block_rms_scale(xr, K, red);
+        // y = (x * scale) * w, as block_rmsnorm computes it
+        const float scale = red[16];
+        const bool zero = red[17] != 0.0f;
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            v[j].x = zero ? 0.0f : (v[j].x * scale) * w4[j].x;
+            v[j].y = zero ? 0.0f : (v[j].y * scale) * w4[j].y;
+            v[j].z = zero ? 0.0f : (v[j].z * scale) * w4[j].z;
+            v[j].w = zero ? 0.0f : (v[j].w * scale) * w4[j].w;
+        }
+        __syncthreads();  // (red is reused below)
+    }
+    split_row4<NV>(v, K, row, hi, lo, unscale, red);
+}
+
+// float4s per thread for a row of K (0: the scalar kernels: K not a multiple of 4 or past 16384)
+static int split_nv(int K) {
+    if (K % 4 || K > 16384) return 0;
+    const int n = (K + 1023) / 1024;
+    return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : n <= 8 ? 8 : 16;
+}
+
 void launch_mfma_norm_split(const float* X, int m, int mp, int K, const float* nw, _Float16* hi, _Float16* lo,
                             float* unscale, hipStream_t st) {
-    hipLaunchKernelGGL(mfma_norm_split_kernel, dim3(mp), dim3(256), (size_t)K * sizeof(float), st, X, m, K, nw, hi,
-                       lo, unscale);
+    const size_t lds = (size_t)K * sizeof(float);
+    switch (split_nv(K)) {
+        case 1: hipLaunchKernelGGL(mfma_norm_split4_kernel<1>, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale); break;
+        case 2: hipLaunchKernelGGL(mfma_norm_split4_kernel<2>, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale); break;
+        case 4: hipLaunchKernelGGL(mfma_norm_split4_kernel<4>, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale); break;
+        case 8: hipLaunchKernelGGL(mfma_norm_split4_kernel<8>, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale); break;
+        case 16: hipLaunchKernelGGL(mfma_norm_split4_kernel<16>, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale); break;
+        default:
+            hipLaunchKernelGGL(mfma_norm_split_kernel, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale);
+            break;
+    }
 }
 
 void launch_mfma_split(const float* A, int m, int mp, int K, _Float16* hi, _Float16* lo, float* unscale,
                        hipStream_t st) {
-    hipLaunchKernelGGL(mfma_split_kernel, dim3(mp), dim3(256), 0, st, A, m, K, hi, lo, unscale);
+    switch (split_nv(K)) {
+        case 1: hipLaunchKernelGGL(mfma_split4_kernel<1>, dim3(mp), dim3(256), 0, st, A, m, K, hi, lo, unscale); break;
+        case 2: hipLaunchKernelGGL(mfma_split4_kernel<2>, dim3(mp), dim3(256), 0, st, A, m, K, hi, lo, unscale); break;
+        case 4: hipLaunchKernelGGL(mfma_split4_kernel<4>, dim3(mp), dim3(256), 0, st, A, m, K, hi, lo, unscale); break;
+        case 8: hipLaunchKernelGGL(mfma_split4_kernel<8>, dim3(mp), dim3(256), 0, st, A, m, K, hi, lo, unscale); break;
+        case 16: hipLaunchKernelGGL(mfma_split4_kernel<16>, dim3(mp), dim3(256), 0, st, A, m, K, hi, lo, unscale); break;
+        default: hipLaunchKernelGGL(mfma_split_kernel, dim3(mp), dim3(256), 0, st, A, m, K, hi, lo, unscale); break;
+    }
 }
 
 // ---------------------------------------------------------------- the GEMM, staged by DMA
@@ -261,42 +381,124 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_mfma2_kernel(Q8MfmaDev W, int 
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) acc[mt][nt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-#pragma unroll
-    for (int s = 0; s < S - 1; s++)
-        if (b0 + s < b1) issue(b0 + s, s);
-    for (int b = b0; b < b1; b++) {
-        // block b has landed once at most the DMAs of the S - 2 blocks after it are pending
-        const int after = min(b1 - 1 - b, S - 2);
-        if (after >= S - 2)
-            wait_vm<(S - 2) * PW>();
-        else if (S > 3 && after == 1)
-            wait_vm<(S > 3 ? PW : 0)>();
-        else
-            wait_vm<0>();
-        __syncthreads();  // every wave's DMAs of block b are in LDS; block b - 1 is done
-        if (b + S - 1 < b1) issue(b + S - 1, (b - b0 + S - 1) % S);
-        const St& T = stg[(b - b0) % S];
-        h8_t ah[MT], al[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            ah[mt] = T.a[0][wm * MT + mt][l];
-            al[mt] = T.a[1][wm * MT + mt][l];
+    // The narrow tile (NT = 4) runs the block loop software-pipelined; the wide tile's
+    // registers do not hold a second set of fragments well (238 VGPRs: gate/up 594 -> 628 us),
+    // so it reads each block's fragments after its barrier.
+    if constexpr (NT == 4) {
+        // Software-pipelined over blocks: while the matrix cores work on block b from registers,
+        // the fragments of block b + 1 are read from LDS into the other register set.  S blocks
+        // are in LDS or in flight: block b + S goes into block b's stage once every wave has
+        // read block b (the barrier before block b + 1's reads).
+        struct Frag {
+            h8_t ah[MT], al[MT];
+            uint2 q[NT];
+            float dj[NT];
+        };
+        auto read_frag = [&](int b, Frag& f) {
+            const St& T = stg[(b - b0) % S];
+    #pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                f.ah[mt] = T.a[0][wm * MT + mt][l];
+                f.al[mt] = T.a[1][wm * MT + mt][l];
+            }
+    #pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                f.q[nt] = T.b[wn * NT + nt][l];
+                f.dj[nt] = T.d[wn * NT + nt][c];
+            }
+        };
+        // the wait for block b's DMAs when `later` blocks were issued after it
+        auto wait_block = [&](int later) {
+            if (later >= S - 1)
+                wait_vm<(S - 1) * PW>();
+            else if (later == S - 2)
+                wait_vm<(S - 2) * PW>();
+            else if (S > 3 && later == 1)
+                wait_vm<(S > 3 ? PW : 0)>();
+            else
+                wait_vm<0>();
+        };
+        auto compute = [&](const Frag& f) {
+    #pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const h8_t bq = q8_to_h8(f.q[nt].x, f.q[nt].y);
+                f4_t t[MT];
+    #pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+                    t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.ah[mt], bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    #pragma unroll
+                for (int mt = 0; mt < MT; mt++) t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.al[mt], bq, t[mt], 0, 0, 0);
+    #pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+    #pragma unroll
+                    for (int i = 0; i < 4; i++) acc[mt][nt][i] = __builtin_fmaf(f.dj[nt], t[mt][i], acc[mt][nt][i]);
+            }
+        };
+        // block b from cur; block b + 1 (if any) into nxt
+        auto step = [&](int b, const Frag& cur, Frag& nxt) {
+            if (b + 1 < b1) {
+                // issued after block b + 1 so far: blocks b + 2 .. min(b + S - 1, b1 - 1)
+                wait_block(min(S - 2, b1 - b - 2));
+                __syncthreads();  // block b + 1 is in LDS; every wave has read block b
+                if (b + S < b1) issue(b + S, (b - b0) % S);
+                read_frag(b + 1, nxt);
+            }
+            compute(cur);
+        };
+
+    #pragma unroll
+        for (int s = 0; s < S; s++)
+            if (b0 + s < b1) issue(b0 + s, s);
+        Frag fa, fb;
+        if (b0 < b1) {
+            wait_block(min(S - 1, b1 - b0 - 1));
+            __syncthreads();
+            read_frag(b0, fa);
         }
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const uint2 q = T.b[wn * NT + nt][l];
-            const h8_t bq = q8_to_h8(q.x, q.y);
-            const float dj = T.d[wn * NT + nt][c];
-            f4_t t[MT];
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-                t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], bq, t[mt], 0, 0, 0);
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[mt][nt][i] = __builtin_fmaf(dj, t[mt][i], acc[mt][nt][i]);
+        int b = b0;
+        for (; b + 1 < b1; b += 2) {
+            step(b, fa, fb);
+            step(b + 1, fb, fa);
+        }
+        if (b < b1) step(b, fa, fb);
+    } else {
+    #pragma unroll
+        for (int s = 0; s < S - 1; s++)
+            if (b0 + s < b1) issue(b0 + s, s);
+        for (int b = b0; b < b1; b++) {
+            // block b has landed once at most the DMAs of the S - 2 blocks after it are pending
+            const int after = min(b1 - 1 - b, S - 2);
+            if (after >= S - 2)
+                wait_vm<(S - 2) * PW>();
+            else if (S > 3 && after == 1)
+                wait_vm<(S > 3 ? PW : 0)>();
+            else
+                wait_vm<0>();
+            __syncthreads();  // every wave's DMAs of block b are in LDS; block b - 1 is done
+            if (b + S - 1 < b1) issue(b + S - 1, (b - b0 + S - 1) % S);
+            const St& T = stg[(b - b0) % S];
+            h8_t ah[MT], al[MT];
+    #pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                ah[mt] = T.a[0][wm * MT + mt][l];
+                al[mt] = T.a[1][wm * MT + mt][l];
+            }
+    #pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const uint2 q = T.b[wn * NT + nt][l];
+                const h8_t bq = q8_to_h8(q.x, q.y);
+                const float dj = T.d[wn * NT + nt][c];
+                f4_t t[MT];
+    #pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+                    t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    #pragma unroll
+                for (int mt = 0; mt < MT; mt++) t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], bq, t[mt], 0, 0, 0);
+    #pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+    #pragma unroll
+                    for (int i = 0; i < 4; i++) acc[mt][nt][i] = __builtin_fmaf(dj, t[mt][i], acc[mt][nt][i]);
+            }
         }
     }
 

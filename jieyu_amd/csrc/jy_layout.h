@@ -78,8 +78,9 @@ __device__ __forceinline__ float kq_elem(const KQDev& W, int R, int k) {
 // builds it (with t >= 4 the first four squares are rounded products added in
 // order, the rest fused), den = ss/n + eps, scale = 1/sqrtf(den),
 // y = (x*scale)*w.  red: 18 floats of shared memory.
-__device__ __forceinline__ void block_rmsnorm(const float* x, int n, const float* __restrict__ w,
-                                              float* __restrict__ y, float* red) {
+// The scale part: red[16] = 1/sqrtf(den), red[17] = 1 where den <= 0 (the row then
+// normalises to zeros); both visible to the whole workgroup on return.
+__device__ __forceinline__ void block_rms_scale(const float* x, int n, float* red) {
     const int t = threadIdx.x;
     const int n16 = n / 16 * 16;
     const bool rem8 = n16 + 8 <= n;
@@ -107,6 +108,12 @@ __device__ __forceinline__ void block_rmsnorm(const float* x, int n, const float
         red[16] = den <= 0.0f ? 0.0f : 1.0f / sqrtf(den);
     }
     __syncthreads();
+}
+
+__device__ __forceinline__ void block_rmsnorm(const float* x, int n, const float* __restrict__ w,
+                                              float* __restrict__ y, float* red) {
+    const int t = threadIdx.x;
+    block_rms_scale(x, n, red);
     const float scale = red[16];
     const bool zero = red[17] != 0.0f;
     for (int i = t; i < n; i += blockDim.x) y[i] = zero ? 0.0f : (x[i] * scale) * w[i];

@@ -1371,6 +1371,10 @@ struct Session {
         ensure_ws(m, seq);
         ensure_scores(m, scores_need(m, seq, max_keys));
         ensure_part(m, part_need(m, max_keys));
+        if (seq > 1 && use_mfma(m)) {  // (allocated here, before the prompt step is timed)
+            ensure_split(m, mfma_split_halves(m, seq), mfma_rows_padded(seq));
+            ensure_kpart(m, mfma_kpart_need(m, seq));
+        }
         m->owner = this;
         CK(hipMemcpyAsync(m->ids, prompt, sizeof(int) * plen, hipMemcpyHostToDevice, st));
         const int st0[4] = {plen, 0, 0, 0};
