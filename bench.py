@@ -358,6 +358,28 @@ def attention_workload(name, pre, rows=10):
     syn.close()
 
 
+def decode_workload(name, steps, pre=1024):
+    """A workload for kernel traces of the decode step without graph replays: the model's
+    fast-mode forward_cached over a `pre`-row prompt of N(0,1) activations, then `steps`
+    single-row decode steps at positions pre, pre+1, ..., each by direct launches (the same
+    kernels a session's graph replays, minus the embedding lookup, lm_head and pick)."""
+    import jieyu_amd as jy
+    from jieyu_amd.model import Synth, synth_config
+    syn = Synth(jy.lib(), synth_config(name))
+    d = syn.desc
+    g = jy.GpuModel(d, pre + steps + 8)
+    g.mode = MODES["fast"]
+    kv = g.kv(pre + steps + 8)
+    rng = np.random.default_rng(0)
+    g.forward_cached(kv, rng.standard_normal((pre, d.hidden)).astype(np.float32), 0)
+    for i in range(steps):
+        g.forward_cached(kv, rng.standard_normal((1, d.hidden)).astype(np.float32), pre + i)
+    log(f"{name}: {steps} decode rows after {pre} prompt rows done")
+    kv.close()
+    g.close()
+    syn.close()
+
+
 def copy_calibration(mb):
     """A plain device copy of known size for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE."""
     import torch
@@ -475,6 +497,9 @@ def main():
     ap.add_argument("--prefill-workload", type=int, default=0, metavar="TOKENS",
                     help="only run a profiling workload and exit: the --config model's fast-mode prompt pass "
                          "over TOKENS rows, 3 times by direct launches (forward_cached, no graph)")
+    ap.add_argument("--decode-workload", type=int, default=0, metavar="STEPS",
+                    help="only run a profiling workload and exit: the --config model's fast-mode decode rows "
+                         "after a --prompt-len prompt, STEPS of them by direct launches (forward_cached, no graph)")
     ap.add_argument("--attention-workload", type=int, default=0, metavar="POSITIONS",
                     help="only run a profiling workload and exit: one layer of --config over a cache "
                          "pre-filled to POSITIONS, 10 fast-mode decode rows by direct launches")
@@ -489,6 +514,9 @@ def main():
         return
     if args.attention_workload:
         attention_workload(args.config, args.attention_workload)
+        return
+    if args.decode_workload:
+        decode_workload(args.config, args.decode_workload, args.prompt_len)
         return
     if args.prefill_workload:
         prefill_workload(args.config, args.prefill_workload)
