@@ -396,12 +396,12 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_mfma2_kernel(Q8MfmaDev W, int 
         };
         auto read_frag = [&](int b, Frag& f) {
             const St& T = stg[(b - b0) % S];
-    #pragma unroll
+#pragma unroll
             for (int mt = 0; mt < MT; mt++) {
                 f.ah[mt] = T.a[0][wm * MT + mt][l];
                 f.al[mt] = T.a[1][wm * MT + mt][l];
             }
-    #pragma unroll
+#pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 f.q[nt] = T.b[wn * NT + nt][l];
                 f.dj[nt] = T.d[wn * NT + nt][c];
@@ -419,18 +419,18 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_mfma2_kernel(Q8MfmaDev W, int 
                 wait_vm<0>();
         };
         auto compute = [&](const Frag& f) {
-    #pragma unroll
+#pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 const h8_t bq = q8_to_h8(f.q[nt].x, f.q[nt].y);
                 f4_t t[MT];
-    #pragma unroll
+#pragma unroll
                 for (int mt = 0; mt < MT; mt++)
                     t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.ah[mt], bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-    #pragma unroll
+#pragma unroll
                 for (int mt = 0; mt < MT; mt++) t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.al[mt], bq, t[mt], 0, 0, 0);
-    #pragma unroll
+#pragma unroll
                 for (int mt = 0; mt < MT; mt++)
-    #pragma unroll
+#pragma unroll
                     for (int i = 0; i < 4; i++) acc[mt][nt][i] = __builtin_fmaf(f.dj[nt], t[mt][i], acc[mt][nt][i]);
             }
         };
@@ -446,7 +446,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_mfma2_kernel(Q8MfmaDev W, int 
             compute(cur);
         };
 
-    #pragma unroll
+#pragma unroll
         for (int s = 0; s < S; s++)
             if (b0 + s < b1) issue(b0 + s, s);
         Frag fa, fb;
@@ -462,7 +462,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_mfma2_kernel(Q8MfmaDev W, int 
         }
         if (b < b1) step(b, fa, fb);
     } else {
-    #pragma unroll
+#pragma unroll
         for (int s = 0; s < S - 1; s++)
             if (b0 + s < b1) issue(b0 + s, s);
         for (int b = b0; b < b1; b++) {
@@ -478,25 +478,25 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_mfma2_kernel(Q8MfmaDev W, int 
             if (b + S - 1 < b1) issue(b + S - 1, (b - b0 + S - 1) % S);
             const St& T = stg[(b - b0) % S];
             h8_t ah[MT], al[MT];
-    #pragma unroll
+#pragma unroll
             for (int mt = 0; mt < MT; mt++) {
                 ah[mt] = T.a[0][wm * MT + mt][l];
                 al[mt] = T.a[1][wm * MT + mt][l];
             }
-    #pragma unroll
+#pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 const uint2 q = T.b[wn * NT + nt][l];
                 const h8_t bq = q8_to_h8(q.x, q.y);
                 const float dj = T.d[wn * NT + nt][c];
                 f4_t t[MT];
-    #pragma unroll
+#pragma unroll
                 for (int mt = 0; mt < MT; mt++)
                     t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mt], bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-    #pragma unroll
+#pragma unroll
                 for (int mt = 0; mt < MT; mt++) t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[mt], bq, t[mt], 0, 0, 0);
-    #pragma unroll
+#pragma unroll
                 for (int mt = 0; mt < MT; mt++)
-    #pragma unroll
+#pragma unroll
                     for (int i = 0; i < 4; i++) acc[mt][nt][i] = __builtin_fmaf(dj, t[mt][i], acc[mt][nt][i]);
             }
         }
