@@ -1275,6 +1275,7 @@ hipError_t kernels_init() {
     if (e == hipSuccess) e = matvec_split_init();
     if (e == hipSuccess) e = persist_init();
     if (e == hipSuccess) e = gemm_mfma_init();
+    if (e == hipSuccess) e = rope_pack_init();
     if (e != hipSuccess) return e;
     return matvec_init();
 }

@@ -202,10 +202,14 @@ __global__ __launch_bounds__(256) void mfma_split4_kernel(const float* __restric
     split_row4<NV>(v, K, row, hi, lo, unscale, red);
 }
 
+// (kz > 1: X's rows first take the residual add of a GEMM split over K whose sum was
+// deferred, X += sum of the kz partials [kz][m][K] in slice order, written back to X: the
+// sum kernel's arithmetic)
 template <int NV>
-__global__ __launch_bounds__(256) void mfma_norm_split4_kernel(const float* __restrict__ X, int m, int K,
+__global__ __launch_bounds__(256) void mfma_norm_split4_kernel(float* __restrict__ X, int m, int K,
                                                                const float* __restrict__ nw, _Float16* __restrict__ hi,
-                                                               _Float16* __restrict__ lo, float* __restrict__ unscale) {
+                                                               _Float16* __restrict__ lo, float* __restrict__ unscale,
+                                                               const float* __restrict__ kp, int kz) {
     extern __shared__ __align__(16) float xr[];
     __shared__ float red[18];
     const int row = blockIdx.x;
@@ -222,6 +226,27 @@ __global__ __launch_bounds__(256) void mfma_norm_split4_kernel(const float* __re
         const int k4 = threadIdx.x + 256 * j;
         w4[j] = live && 4 * k4 < K ? n4[k4] : z4;
         v[j] = live && 4 * k4 < K ? g4[k4] : z4;
+    }
+    if (kz > 1 && live) {
+        const size_t mk4 = (size_t)m * K / 4;
+        const float4* p4 = reinterpret_cast<const float4*>(kp) + (size_t)row * K / 4;
+        float4* xw4 = reinterpret_cast<float4*>(X + (size_t)row * K);
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int k4 = threadIdx.x + 256 * j;
+            if (4 * k4 >= K) break;
+            float4 y = p4[k4];
+            for (int z = 1; z < kz; z++) {
+                const float4 t = p4[(size_t)z * mk4 + k4];
+                y = make_float4(y.x + t.x, y.y + t.y, y.z + t.z, y.w + t.w);
+            }
+            v[j] = make_float4(v[j].x + y.x, v[j].y + y.y, v[j].z + y.z, v[j].w + y.w);
+            xw4[k4] = v[j];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int k4 = threadIdx.x + 256 * j;
         if (live && 4 * k4 < K) x4[k4] = v[j];
     }
     if (live) {
@@ -249,16 +274,18 @@ static int split_nv(int K) {
     return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : n <= 8 ? 8 : 16;
 }
 
-void launch_mfma_norm_split(const float* X, int m, int mp, int K, const float* nw, _Float16* hi, _Float16* lo,
-                            float* unscale, hipStream_t st) {
+bool mfma_norm_split_takes_parts(int K) { return split_nv(K) != 0; }
+
+void launch_mfma_norm_split(float* X, int m, int mp, int K, const float* nw, _Float16* hi, _Float16* lo,
+                            float* unscale, hipStream_t st, const float* kp, int kz) {
     const size_t lds = (size_t)K * sizeof(float);
     switch (split_nv(K)) {
-        case 1: hipLaunchKernelGGL(mfma_norm_split4_kernel<1>, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale); break;
-        case 2: hipLaunchKernelGGL(mfma_norm_split4_kernel<2>, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale); break;
-        case 4: hipLaunchKernelGGL(mfma_norm_split4_kernel<4>, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale); break;
-        case 8: hipLaunchKernelGGL(mfma_norm_split4_kernel<8>, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale); break;
-        case 16: hipLaunchKernelGGL(mfma_norm_split4_kernel<16>, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale); break;
-        default:
+        case 1: hipLaunchKernelGGL(mfma_norm_split4_kernel<1>, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale, kp, kz); break;
+        case 2: hipLaunchKernelGGL(mfma_norm_split4_kernel<2>, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale, kp, kz); break;
+        case 4: hipLaunchKernelGGL(mfma_norm_split4_kernel<4>, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale, kp, kz); break;
+        case 8: hipLaunchKernelGGL(mfma_norm_split4_kernel<8>, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale, kp, kz); break;
+        case 16: hipLaunchKernelGGL(mfma_norm_split4_kernel<16>, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale, kp, kz); break;
+        default:  // (callers pass no partials here: mfma_norm_split_takes_parts)
             hipLaunchKernelGGL(mfma_norm_split_kernel, dim3(mp), dim3(256), lds, st, X, m, K, nw, hi, lo, unscale);
             break;
     }
@@ -691,19 +718,21 @@ size_t gemm_q8_mfma_kpart_floats(const Q8MfmaDev& W, int m, Epi epi) {
 // when even that grid leaves CUs idle and `kpart` holds the partials.  Measured at the
 // Llama-3-8B shapes and 1024 tokens (the activation split included): gate/up (28672 x
 // 4096) 576 us wide, 686 narrow; QKV 164, O 118, down 422 us narrow.
-void launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
-                         float* C, int ldc, const float* aux, Epi epi, hipStream_t st, float* kpart, size_t kpart_n) {
+int launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
+                        float* C, int ldc, const float* aux, Epi epi, hipStream_t st, float* kpart, size_t kpart_n,
+                        bool defer) {
     const int cus = gemm_cus();
     if (wide_wgs(W, m) >= 2L * cus) {
         gemm2_launch<2, 8, 3>(W, m, hi, lo, unscale, C, ldc, aux, epi, st);
-        return;
+        return 0;
     }
     const int Z = gemm_q8_mfma_ksplit(W, m, epi);
     if (Z < 2 || !kpart || (size_t)Z * m * W.rows > kpart_n) {
         gemm2_launch<2, 4, 3>(W, m, hi, lo, unscale, C, ldc, aux, epi, st);
-        return;
+        return 0;
     }
     gemm2_launch<2, 4, 3>(W, m, hi, lo, unscale, kpart, W.rows, nullptr, EPI_STORE, st, Z);
+    if (defer) return Z;
     const size_t n = (size_t)m * W.rows;
     const dim3 grid((unsigned)((n + 255) / 256));
     switch (epi) {
@@ -717,6 +746,18 @@ void launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _F
             hipLaunchKernelGGL(gemm_ksum_kernel<EPI_STORE>, grid, dim3(256), 0, st, kpart, Z, m, W.rows, C, ldc, aux);
             break;
     }
+    return 0;
+}
+
+void launch_gemm_ksum(const float* kpart, int Z, int m, int N, float* C, int ldc, const float* aux, Epi epi,
+                      hipStream_t st) {
+    const dim3 grid((unsigned)(((size_t)m * N + 255) / 256));
+    if (epi == EPI_RESID)
+        hipLaunchKernelGGL(gemm_ksum_kernel<EPI_RESID>, grid, dim3(256), 0, st, kpart, Z, m, N, C, ldc, aux);
+    else if (epi == EPI_BIAS)
+        hipLaunchKernelGGL(gemm_ksum_kernel<EPI_BIAS>, grid, dim3(256), 0, st, kpart, Z, m, N, C, ldc, aux);
+    else
+        hipLaunchKernelGGL(gemm_ksum_kernel<EPI_STORE>, grid, dim3(256), 0, st, kpart, Z, m, N, C, ldc, aux);
 }
 
 }  // namespace jy

@@ -148,13 +148,21 @@ void launch_mfma_repack(const Q8Dev& W, const Q8MfmaDev& M, hipStream_t st);
 int mfma_rows_padded(int m);
 void launch_mfma_split(const float* A, int m, int mp, int K, _Float16* hi, _Float16* lo, float* unscale,
                        hipStream_t st);
-// the RMSNorm of X's rows (rmsnorm_kernel's arithmetic) and the split above in one kernel
-void launch_mfma_norm_split(const float* X, int m, int mp, int K, const float* nw, _Float16* hi, _Float16* lo,
-                            float* unscale, hipStream_t st);
-// (kpart: kpart_n floats for the partial sums of a GEMM split over K, or nullptr: no split)
-void launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
-                         float* C, int ldc, const float* aux, Epi epi, hipStream_t st, float* kpart = nullptr,
-                         size_t kpart_n = 0);
+// the RMSNorm of X's rows (rmsnorm_kernel's arithmetic) and the split above in one kernel;
+// with kz > 1 (only where mfma_norm_split_takes_parts(K)) X += the kz partials in kp first
+// ([kz][m][K], a deferred residual GEMM split over K), written back to X
+bool mfma_norm_split_takes_parts(int K);
+void launch_mfma_norm_split(float* X, int m, int mp, int K, const float* nw, _Float16* hi, _Float16* lo,
+                            float* unscale, hipStream_t st, const float* kp = nullptr, int kz = 0);
+// (kpart: kpart_n floats for the partial sums of a GEMM split over K, or nullptr: no split.
+// With defer, a split GEMM leaves its sum to the caller: the return value is then the
+// number of partials in kpart ([Z][m][W.rows]), 0 when C holds the result)
+int launch_gemm_q8_mfma(const Q8MfmaDev& W, int m, const _Float16* hi, const _Float16* lo, const float* unscale,
+                        float* C, int ldc, const float* aux, Epi epi, hipStream_t st, float* kpart = nullptr,
+                        size_t kpart_n = 0, bool defer = false);
+// the deferred sum: C (+)= the Z partials [Z][m][N], with the epilogue
+void launch_gemm_ksum(const float* kpart, int Z, int m, int N, float* C, int ldc, const float* aux, Epi epi,
+                      hipStream_t st);
 // the K slices launch_gemm_q8_mfma takes for these rows, and the partial floats they need
 int gemm_q8_mfma_ksplit(const Q8MfmaDev& W, int m, Epi epi);
 size_t gemm_q8_mfma_kpart_floats(const Q8MfmaDev& W, int m, Epi epi);
@@ -164,11 +172,14 @@ void launch_gemm_f32(const float* B, int K, int N, int m, const float* A, float*
 void launch_silu_mul(const float* g, const float* u, int interleaved, int m, int F, float* h, hipStream_t st);
 
 // RoPE on q and k of every row, K/V int8 packing into the cache of `layer`, Q int8.
-// qkv: [seq][q_dim + 2*kv_dim].  Position start_pos + row, or state[0]-1 when
-// state != null (a one-row decode step).
-void launch_rope_pack(float* qkv, int seq, int start_pos, const int* state, int nh, int nkv, int hd,
+// qkv: [seq][q_dim + 2*kv_dim] (read only).  Position start_pos + row, or state[0]-1 when
+// state != null (a one-row decode step).  kz > 1: the rows are instead the sums of the kz
+// partials in kp ([kz][seq][q_dim + 2*kv_dim], launch_gemm_q8_mfma's deferred split), plus
+// bias when given.
+void launch_rope_pack(const float* qkv, int seq, int start_pos, const int* state, int nh, int nkv, int hd,
                       const float* cos_t, const float* sin_t, const KVDev& kv, int layer, int8_t* q8, float* qsc,
-                      hipStream_t st);
+                      hipStream_t st, const float* kp = nullptr, int kz = 0, const float* bias = nullptr);
+hipError_t rope_pack_init();
 
 struct AttnArgs {
     // fused (decode): q, k, v rows of the token from qkv (already roped); the kernel

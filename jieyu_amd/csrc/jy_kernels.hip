@@ -573,24 +573,42 @@ __device__ __forceinline__ float wave_max(float v) { return wave_max64(v); }
 // position pos; within every full group of 8 pairs the reference's store order puts
 // rotated pairs (4,5) in slots (2,3) and pairs (2,3) in slots (4,5)
 // (rope/x86/x86_classic.txt:23-29); remainder pairs stay in place.  Then K (after
-// RoPE) and V are packed into the cache and Q is quantised per head.
-__global__ __launch_bounds__(256) void rope_pack_kernel(float* __restrict__ qkv, int start_pos,
+// RoPE) and V are packed into the cache and Q is quantised per head.  The rotated q / k
+// go to LDS (sm) and are quantised from there; nothing is written back to qkv.  With
+// kz > 1 the row is first added up into LDS (raw) from the kz partial sums
+// [z][rows][width] a GEMM split over K left (in slice order, then the bias: the sum
+// kernel's arithmetic) and read from there instead of qkv.
+__global__ __launch_bounds__(256) void rope_pack_kernel(const float* __restrict__ qkv, int start_pos,
                                                         const int* __restrict__ state, int nh, int nkv, int hd,
                                                         const float* __restrict__ cos_t,
                                                         const float* __restrict__ sin_t, KVDev kv, int layer,
-                                                        int8_t* __restrict__ q8, float* __restrict__ qsc) {
+                                                        int8_t* __restrict__ q8, float* __restrict__ qsc,
+                                                        const float* __restrict__ kp, int kz, int rows,
+                                                        const float* __restrict__ bias) {
     extern __shared__ __align__(16) float sm[];
     const int row = blockIdx.x;
     const int pos = state ? state[0] - 1 : start_pos + row;
-    const int half = hd / 2, qd = nh * hd, kvd = nkv * hd;
-    float* base = qkv + (size_t)row * (qd + 2 * kvd);
+    const int half = hd / 2, qd = nh * hd, kvd = nkv * hd, width = qd + 2 * kvd;
+    float* raw = sm + (size_t)(nh + nkv) * hd;
+    const float* src_row = qkv + (size_t)row * width;
+    if (kz > 1) {
+        const size_t mn = (size_t)rows * width;
+        for (int e = threadIdx.x; e < width; e += blockDim.x) {
+            const size_t i = (size_t)row * width + e;
+            float y = kp[i];
+            for (int z = 1; z < kz; z++) y += kp[(size_t)z * mn + i];
+            raw[e] = bias ? y + bias[e] : y;
+        }
+        __syncthreads();
+        src_row = raw;
+    }
     const float* c = cos_t + (size_t)pos * half;
     const float* s = sin_t + (size_t)pos * half;
     const int npairs = (nh + nkv) * half;
     const int full = half / 8 * 8;
     for (int e = threadIdx.x; e < npairs; e += blockDim.x) {
         const int hh = e / half, m = e - hh * half;
-        const float* xh = base + (size_t)hh * hd;
+        const float* xh = src_row + (size_t)hh * hd;
         const float x0 = xh[2 * m], x1 = xh[2 * m + 1];
         const float cm = c[m], sn = s[m];
         const float y0 = __builtin_fmaf(x0, cm, -(x1 * sn));
@@ -604,11 +622,9 @@ __global__ __launch_bounds__(256) void rope_pack_kernel(float* __restrict__ qkv,
         sm[hh * hd + 2 * dst + 1] = y1;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < (nh + nkv) * hd; e += blockDim.x) base[e] = sm[e];
-    __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     for (int hh = wave; hh < nh + 2 * nkv; hh += nw) {
-        const float* src = base + (size_t)hh * hd;
+        const float* src = (hh < nh + nkv ? sm : src_row) + (size_t)hh * hd;  // q, k rotated; v as it is
         float amax = 0.0f;
         for (int d = lane; d < hd; d += 64) amax = fmaxf(amax, fabsf(src[d]));
         amax = wave_max(amax);
@@ -630,12 +646,17 @@ __global__ __launch_bounds__(256) void rope_pack_kernel(float* __restrict__ qkv,
     }
 }
 
-void launch_rope_pack(float* qkv, int seq, int start_pos, const int* state, int nh, int nkv, int hd,
+hipError_t rope_pack_init() {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&rope_pack_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               160 * 1024 - 2048);
+}
+
+void launch_rope_pack(const float* qkv, int seq, int start_pos, const int* state, int nh, int nkv, int hd,
                       const float* cos_t, const float* sin_t, const KVDev& kv, int layer, int8_t* q8, float* qsc,
-                      hipStream_t st) {
-    const size_t lds = (size_t)(nh + nkv) * hd * sizeof(float);
+                      hipStream_t st, const float* kp, int kz, const float* bias) {
+    const size_t lds = (size_t)(kz > 1 ? 2 * nh + 3 * nkv : nh + nkv) * hd * sizeof(float);
     hipLaunchKernelGGL(rope_pack_kernel, dim3(seq), dim3(256), lds, st, qkv, start_pos, state, nh, nkv, hd, cos_t,
-                       sin_t, kv, layer, q8, qsc);
+                       sin_t, kv, layer, q8, qsc, kp, kz, seq, bias);
 }
 
 // ---------------------------------------------------------------- greedy selection

@@ -944,38 +944,54 @@ void run_prefill_layers(jyhip_model* m, Workspace& w, const KVDev& kv, int seq, 
         if (&w != &m->ws) fail("prefill: the workspace has no room for the matrix-core partial sums");
         ensure_kpart(m, mfma_kpart_need(m, seq));
     }
-    auto gemm_q8 = [&](const Q8Dev& W, const Q8MfmaDev& M, const float* A, float* Cm, const float* aux, Epi epi) {
+    // A matrix-core GEMM split over K may leave its sum to the next kernel (`defer`): the
+    // QKV product's to rope_pack, a residual product's (O, down) to the next RMSNorm + split,
+    // which adds the partials into X.  pending_x counts the partials a residual product left
+    // in w.kp; resolve_x adds them where no such kernel follows (a layer's output copied out,
+    // the last layer).
+    const bool fuse_x = mf && mfma_norm_split_takes_parts(H);
+    int pending_x = 0;
+    auto resolve_x = [&]() {
+        if (pending_x > 1) launch_gemm_ksum(w.kp, pending_x, seq, H, w.X, H, nullptr, EPI_RESID, st);
+        pending_x = 0;
+    };
+    auto gemm_q8 = [&](const Q8Dev& W, const Q8MfmaDev& M, const float* A, float* Cm, const float* aux, Epi epi,
+                       bool defer = false) {
         if (mf) {
             launch_mfma_split(A, seq, mp, W.cols, w.ah, w.al, w.aus, st);
-            launch_gemm_q8_mfma(M, seq, w.ah, w.al, w.aus, Cm, W.rows, aux, epi, st, w.kp, w.kp_n);
-        } else {
-            launch_gemm_q8(W, seq, A, Cm, aux, epi, st);
+            return launch_gemm_q8_mfma(M, seq, w.ah, w.al, w.aus, Cm, W.rows, aux, epi, st, w.kp, w.kp_n, defer);
         }
+        launch_gemm_q8(W, seq, A, Cm, aux, epi, st);
+        return 0;
     };
     // matrix-core form of RMSNorm + GEMM: the norm and the activation split in one kernel
-    // (xn is not written); `ldc` the output row stride
-    auto norm_gemm_q8 = [&](const Q8MfmaDev& M, const float* nw, float* Cm, int ldc, const float* aux, Epi epi) {
-        launch_mfma_norm_split(w.X, seq, mp, H, nw, w.ah, w.al, w.aus, st);
-        launch_gemm_q8_mfma(M, seq, w.ah, w.al, w.aus, Cm, ldc, aux, epi, st, w.kp, w.kp_n);
+    // (xn is not written; X first takes the partials a residual product left); `ldc` the
+    // output row stride
+    auto norm_gemm_q8 = [&](const Q8MfmaDev& M, const float* nw, float* Cm, int ldc, const float* aux, Epi epi,
+                            bool defer = false) {
+        launch_mfma_norm_split(w.X, seq, mp, H, nw, w.ah, w.al, w.aus, st, w.kp, pending_x);
+        pending_x = 0;
+        return launch_gemm_q8_mfma(M, seq, w.ah, w.al, w.aus, Cm, ldc, aux, epi, st, w.kp, w.kp_n, defer);
     };
     for (int l = 0; l < m->L; l++) {
         const DevLayer& D = m->layers[l];
         if (!mf) launch_rmsnorm(w.X, w.xn, D.rms1, H, seq, st);
         const Epi qkv_epi = D.bqkv ? EPI_BIAS : EPI_STORE;
+        int pending_qkv = 0;  // partials of the QKV product, summed by rope_pack
         if (mixed) {
             const int qd = m->qd, kvd = m->kvd;
             launch_gemm(D.w[0], seq, w.xn, w.qkv, NQ, D.bqkv, qkv_epi, st);
             launch_gemm(D.w[1], seq, w.xn, w.qkv + qd, NQ, D.bqkv ? D.bqkv + qd : nullptr, qkv_epi, st);
             launch_gemm(D.w[2], seq, w.xn, w.qkv + qd + kvd, NQ, D.bqkv ? D.bqkv + qd + kvd : nullptr, qkv_epi, st);
         } else if (mf) {
-            norm_gemm_q8(D.mqkv, D.rms1, w.qkv, D.qkv.rows, D.bqkv, qkv_epi);
+            pending_qkv = norm_gemm_q8(D.mqkv, D.rms1, w.qkv, D.qkv.rows, D.bqkv, qkv_epi, true);
         } else if (q8) {
             gemm_q8(D.qkv, D.mqkv, w.xn, w.qkv, D.bqkv, qkv_epi);
         } else {
             launch_gemm_f32(D.f_qkv, H, NQ, seq, w.xn, w.qkv, D.bqkv, qkv_epi, st);
         }
         launch_rope_pack(w.qkv, seq, start_pos, nullptr, m->nh, m->nkv, m->hd, m->cos_t, m->sin_t, kv, l, w.q8,
-                         w.qsc, st);
+                         w.qsc, st, w.kp, pending_qkv, pending_qkv > 1 ? D.bqkv : nullptr);
         at.layer = l;
         if (split_rows) {
             at.row0 = 0;
@@ -991,7 +1007,7 @@ void run_prefill_layers(jyhip_model* m, Workspace& w, const KVDev& kv, int seq, 
         if (mixed)
             launch_gemm(D.w[3], seq, w.att, w.X, H, nullptr, EPI_RESID, st);
         else if (q8)
-            gemm_q8(D.o, D.mo, w.att, w.X, nullptr, EPI_RESID);
+            pending_x = gemm_q8(D.o, D.mo, w.att, w.X, nullptr, EPI_RESID, fuse_x);
         else
             launch_gemm_f32(D.f_o, m->qd, H, seq, w.att, w.X, nullptr, EPI_RESID, st);
         if (!mf) launch_rmsnorm(w.X, w.xn, D.rms2, H, seq, st);
@@ -1002,7 +1018,7 @@ void run_prefill_layers(jyhip_model* m, Workspace& w, const KVDev& kv, int seq, 
             launch_gemm(D.w[5], seq, w.h, w.X, H, nullptr, EPI_RESID, st);
         } else if (mf) {
             norm_gemm_q8(D.mgu, D.rms2, w.h, F, nullptr, EPI_SWIGLU);  // h = silu(gate) * up, F wide
-            gemm_q8(D.down, D.mdown, w.h, w.X, nullptr, EPI_RESID);
+            pending_x = gemm_q8(D.down, D.mdown, w.h, w.X, nullptr, EPI_RESID, fuse_x);
         } else if (q8) {
             gemm_q8(D.gu, D.mgu, w.xn, w.g, nullptr, EPI_STORE);
             launch_silu_mul(w.g, nullptr, 1, seq, F, w.h, st);
@@ -1014,11 +1030,13 @@ void run_prefill_layers(jyhip_model* m, Workspace& w, const KVDev& kv, int seq, 
             launch_gemm_f32(D.f_w2, F, H, seq, w.h, w.X, nullptr, EPI_RESID, st);
         }
         if (layer_out_host) {
+            resolve_x();
             CK(hipMemcpyAsync(layer_out_host + (size_t)l * seq * H, w.X, sizeof(float) * seq * H,
                               hipMemcpyDeviceToHost, st));
             CK(hipStreamSynchronize(st));
         }
     }
+    resolve_x();
     CK(hipGetLastError());
 }
 
