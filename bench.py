@@ -228,11 +228,19 @@ def pack_kv_rows(x):
     return q, sc
 
 
-def warm_prefill(g, prompt, max_seq):
+def warm_prefill(g, prompt, max_seq, timed=2):
     """One untimed prompt pass of the same length (a session of one token, closed): the
     first pass of a process also pays for first-touch work (fresh workspace and cache
-    allocations, code loaded on first launch) that the timed prefill should not carry."""
+    allocations, code loaded on first launch) that the timed prefill should not carry.
+    Then `timed` more such passes; their prefill times (ms) are returned, for the median
+    with the benchmark session's own."""
     g.session(prompt, 1, max_seq=max_seq).close()
+    out = []
+    for _ in range(timed):
+        s = g.session(prompt, 1, max_seq=max_seq)
+        out.append(s.stats().prefill_ms)
+        s.close()
+    return out
 
 
 # (name, prompt tokens, new tokens, positions pre-filled in the cache before the prompt,
@@ -270,10 +278,9 @@ def other_config(jy, name, prompt_len, n_new, prefilled, cpu_steps=0, mode=0):
         for layer in range(d.num_layers):
             kv.write(layer, 0, k8, ks, v8, vs)
         kv.set_len(prefilled)
-    if not prefilled:
-        warm_prefill(g, prompt, max_seq)
+    pre = warm_prefill(g, prompt, max_seq) if not prefilled else []
     sess = g.session(prompt, n_new, max_seq=max_seq, kv=kv, resume=bool(prefilled))
-    pre_ms = sess.stats().prefill_ms
+    pre_ms = float(np.median(pre + [sess.stats().prefill_ms]))  # (median of three passes)
     steps = n_new - 1
     t0 = time.perf_counter()
     made = sess.step(steps)
@@ -545,17 +552,18 @@ def main():
     total_new = 1 + W + K + (2 + K2 if K2 > 0 else 0)
     assert args.prompt_len + total_new <= args.max_seq
     log(f"prefill {args.prompt_len} tokens ...")
-    warm_prefill(g, prompt, args.max_seq)
+    pre = warm_prefill(g, prompt, args.max_seq)
     sess = g.session(prompt, total_new, max_seq=args.max_seq)
     st0 = sess.stats()
-    log(f"  prefill {st0.prefill_ms:.1f} ms; warmup {W} steps ...")
+    prefill_ms = float(np.median(pre + [st0.prefill_ms]))  # the median of three prompt passes
+    log(f"  prefill {st0.prefill_ms:.1f} ms (median of three {prefill_ms:.1f}); warmup {W} steps ...")
     sess.step(W)
     dec0 = sess.stats().decode_ms
     t0 = time.perf_counter()
     made = sess.step(K)
     t1 = time.perf_counter()
     st = sess.stats()
-    pre_mfma = prefill_mfma(d, args.prompt_len, st.prefill_ms, args.mode)  # while the descriptor is alive
+    pre_mfma = prefill_mfma(d, args.prompt_len, prefill_ms, args.mode)  # while the descriptor is alive
     ids = sess.ids()
     other_mode = None
     if K2 > 0:
@@ -623,7 +631,7 @@ def main():
                    "mode": MODE_TEXT[args.mode]},
         "hbm_gbs": round(hbm_gbs, 1), "hbm_frac": round(hbm_gbs / HBM_PEAK_GBS, 4),
         "bytes_per_token_avg": int(bytes_total / K), "device_ms_per_step": round(dev_ms / K, 4),
-        "prefill_ms": round(st.prefill_ms, 2), "prefill_tokens_s": round(args.prompt_len / (st.prefill_ms / 1e3), 1),
+        "prefill_ms": round(prefill_ms, 2), "prefill_tokens_s": round(args.prompt_len / (prefill_ms / 1e3), 1),
         "prefill_mfma": pre_mfma, "isolated_prompt_gemm": pgemm,
         "upload_s": round(st.upload_ms / 1e3, 2),
         "last_ids": ids[-8:].tolist(),
