@@ -361,3 +361,31 @@ def test_mode_switch_recaptures(jy, oracle_lib):
         g.mode = 64
     g.close()
     s.close()
+
+
+@pytest.mark.parametrize("key,seq", [("llama-like", 9), ("llama-like", 37), ("qwen-like", 64), ("hd128", 130)])
+def test_deferred_split_sums_bit_equal(jy, oracle_lib, key, seq):
+    """Prompt GEMMs whose small grids run split over K leave their sums to the next kernel
+    (rope_pack adds the QKV partials, the RMSNorm + split adds a residual product's into X).
+    A pass that copies every layer's output out adds them with the sum kernel instead, before
+    each copy: the final states and the K/V cache must be bit-identical either way, at prompt
+    lengths below, across and above the 128-row tile."""
+    say(f"deferred split-K sums {key} seq={seq}")
+    s = make(oracle_lib, key)
+    d = s.desc
+    L, H, nkv, hd = d.num_layers, d.hidden, d.num_kv_heads, d.head_dim
+    g = jy.GpuModel(d, seq + 8)
+    g.mode = MODES["FAST"]
+    X = np.random.default_rng(seq).standard_normal((seq, H)).astype(np.float32)
+    kv_a, kv_b = g.kv(seq + 8), g.kv(seq + 8)
+    ya = g.forward_cached(kv_a, X, 0)
+    yb, lo = g.forward_cached(kv_b, X, 0, layer_out=True)
+    assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32))
+    for layer in range(L):
+        a, b = kv_a.read(layer, 0, seq), kv_b.read(layer, 0, seq)
+        assert all(np.array_equal(np.asarray(u).view(np.uint8), np.asarray(v).view(np.uint8)) for u, v in zip(a, b))
+    assert np.all(np.isfinite(lo))
+    kv_a.close()
+    kv_b.close()
+    g.close()
+    s.close()
