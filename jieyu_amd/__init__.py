@@ -13,7 +13,8 @@ from .model import (CONFIGS, JY_F16, JY_F32, JY_Q4_K, JY_Q5_K, JY_Q6_K, JY_Q8_0,
                     SynthConfig, WMat, bind_synth, synth_config)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libjieyu_amd.so")
+# (JIEYU_AMD_LIB: another build of the library, e.g. the host-sanitized one)
+LIB_PATH = os.environ.get("JIEYU_AMD_LIB") or os.path.join(HERE, "libjieyu_amd.so")
 
 P = C.c_void_p
 I = C.c_int

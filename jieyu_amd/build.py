@@ -5,6 +5,13 @@
 Sources: csrc/*.hip and csrc/*.cpp through hipcc, csrc/*.c through gcc, and the
 host-only text layer csrc/*.cc through g++.  The library lands next to this
 file so it travels with the source tree.
+
+    python -m jieyu_amd.build --sanitize
+
+builds libjieyu_amd_asan.so instead: the host code (the runtime, the text layer)
+instrumented with AddressSanitizer and UBSan, device code unchanged, for the CPU
+tests (the loader takes it from JIEYU_AMD_LIB; the sanitizer runtime must be
+preloaded, see asan_runtime()).
 """
 import os
 import shutil
@@ -18,6 +25,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libjieyu_amd.so")
+LIB_ASAN = os.path.join(HERE, "libjieyu_amd_asan.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("JIEYU_AMD_ARCH", "gfx950")
@@ -42,8 +50,26 @@ def _run(cmd):
     return r.stdout
 
 
-def build(verbose=False, jobs=None):
+# host-side sanitizers: on hipcc lines each flag applies to the host compilation only
+SAN_FLAGS = ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer", "-g"]
+CLANGXX = os.path.join(os.path.dirname(os.path.realpath(HIPCC)), "..", "llvm", "bin", "clang++")
+
+
+def asan_runtime():
+    """The clang AddressSanitizer runtime the sanitized library links against (preload it:
+    LD_PRELOAD=<this> ASAN_OPTIONS=detect_leaks=0)."""
+    import glob
+    hits = sorted(glob.glob(os.path.join(os.path.dirname(CLANGXX), "..", "lib", "clang", "*", "lib", "linux",
+                                         "libclang_rt.asan-x86_64.so")))
+    if not hits:
+        raise RuntimeError("no clang AddressSanitizer runtime next to " + CLANGXX)
+    return os.path.realpath(hits[-1])
+
+
+def build(verbose=False, jobs=None, sanitize=False):
     srcs = sorted(os.listdir(CSRC))
+    lib_out = LIB_ASAN if sanitize else LIB
+    host_san = [y for f in SAN_FLAGS for y in ("-Xarch_host", f)] if sanitize else []
     tmp = tempfile.mkdtemp(prefix="jyamd_build_")
     try:
         objs, cmds = [], []
@@ -51,13 +77,15 @@ def build(verbose=False, jobs=None):
             path = os.path.join(CSRC, s)
             obj = os.path.join(tmp, s + ".o")
             if s.endswith((".hip", ".cpp")):
-                cmd = [HIPCC, *HIP_FLAGS, "-c", path, "-o", obj]
+                cmd = [HIPCC, *HIP_FLAGS, *host_san, "-c", path, "-o", obj]
                 if s.endswith(".cpp"):
                     cmd[1:1] = ["-x", "hip"]
             elif s.endswith(".c"):
                 cmd = ["gcc", *C_FLAGS, "-c", path, "-o", obj]
             elif s.endswith(".cc"):
-                cmd = ["g++", *CXX_FLAGS, "-c", path, "-o", obj]
+                # (clang++ with the sanitizers: one sanitizer runtime for the whole library)
+                cmd = [CLANGXX, *CXX_FLAGS, *SAN_FLAGS, "-c", path, "-o", obj] if sanitize else \
+                    ["g++", *CXX_FLAGS, "-c", path, "-o", obj]
             else:
                 continue
             if verbose:
@@ -69,13 +97,14 @@ def build(verbose=False, jobs=None):
         with ThreadPoolExecutor(max_workers=jobs) as ex:
             for f in [ex.submit(_run, c) for c in cmds]:
                 f.result()
-        out_tmp = LIB + ".tmp"
-        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out_tmp, *objs, "-lgomp", "-lm"])
-        os.replace(out_tmp, LIB)
+        out_tmp = lib_out + ".tmp"
+        rt = [asan_runtime()] if sanitize else []
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out_tmp, *objs, *rt, "-lgomp", "-lm"])
+        os.replace(out_tmp, lib_out)
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
-    return LIB
+    return lib_out
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, sanitize="--sanitize" in sys.argv))
