@@ -113,9 +113,16 @@ def dequant(w, rows, cols):
 # prompt GEMMs: ragged token counts (not multiples of the 128-row tile), rows not multiples of
 # 16, blocks not multiples of 4 (1184 = 37 blocks), the benchmark's 4096 x 4096 at 1024 tokens
 # (the narrow tile), and enough column tiles for the wide tile (1000 x 8200: 520 workgroups);
-# activation rows spread over 10^-3 .. 10^3 with one zero row
+# token counts either side of a workgroup's 64 rows and of the 128-row padding, on grids
+# split over K (1000 x 896: 3 slices; 2048 x 4096: up to 8), and either side of the narrow /
+# wide switch (8200 x 320 at 896 and 897 tokens: 896 and 1024 padded rows) and past it
+# (1025); activation rows spread over 10^-3 .. 10^3 with one zero row
 @pytest.mark.parametrize("m,rows,cols", [(2, 13, 96), (37, 300, 1184), (200, 517, 896), (130, 1000, 4864),
-                                         (1024, 4096, 4096), (1000, 8200, 320)])
+                                         (1024, 4096, 4096), (1000, 8200, 320),
+                                         (3, 1000, 896), (63, 1000, 896), (64, 1000, 896), (65, 1000, 896),
+                                         (127, 2048, 4096), (128, 2048, 4096), (129, 2048, 4096),
+                                         (257, 2048, 4096), (896, 8200, 320), (897, 8200, 320),
+                                         (1025, 8200, 320)])
 def test_mfma_gemm_within_tolerance(jy, oracle_lib, m, rows, cols):
     """The matrix-core prompt GEMM (fp16 high/low split of the activations, fp16 weights,
     fp32 block sums times the block scales) within 1e-5 of sum |a| |w| of the float64
