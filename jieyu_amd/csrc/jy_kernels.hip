@@ -646,6 +646,141 @@ __global__ __launch_bounds__(256) void rope_pack_kernel(const float* __restrict_
     }
 }
 
+// The same with the row in registers (NV float4s per thread, rows of at most 1024 NV floats):
+// the table entries and then every load of the row (or of its kz partial sums) go out at once,
+// the rotated q / k pairs go to their slots in LDS as float4s, the v heads beside them, and
+// each head is quantised from LDS with 2-byte stores.  Every value is computed as in
+// rope_pack_kernel (the same operations in the same order), so the bytes are the same.
+template <int NV>
+__global__ __launch_bounds__(256) void rope_pack4_kernel(const float* __restrict__ qkv, int start_pos,
+                                                         const int* __restrict__ state, int nh, int nkv, int hd,
+                                                         const float* __restrict__ cos_t,
+                                                         const float* __restrict__ sin_t, KVDev kv, int layer,
+                                                         int8_t* __restrict__ q8, float* __restrict__ qsc,
+                                                         const float* __restrict__ kp, int kz, int rows,
+                                                         const float* __restrict__ bias) {
+    extern __shared__ __align__(16) float sm[];  // the row after RoPE: q, k rotated, v as it is
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const int pos = state ? state[0] - 1 : start_pos + row;
+    const int half = hd / 2, width = (nh + 2 * nkv) * hd, w4 = width / 4, rot = (nh + nkv) * hd;
+    const int full = half / 8 * 8;
+    const float* c = cos_t + (size_t)pos * half;
+    const float* s = sin_t + (size_t)pos * half;
+    // head of element e (a shift where hd is a power of two: no integer division)
+    const int hsh = (hd & (hd - 1)) == 0 ? __builtin_ctz(hd) : -1;
+    auto head_of = [&](int e) { return hsh >= 0 ? e >> hsh : e / hd; };
+    // the table entries of the thread's pairs (m0, m0 + 1: m0 = (4 k4 mod hd) / 2, even)
+    float2 cm[NV], sn[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int e = 4 * (tid + 256 * j), m0 = (e - head_of(e) * hd) / 2;
+        const bool r = e < rot;
+        cm[j] = r ? *reinterpret_cast<const float2*>(c + m0) : make_float2(0.0f, 0.0f);
+        sn[j] = r ? *reinterpret_cast<const float2*>(s + m0) : make_float2(0.0f, 0.0f);
+    }
+    float4 v[NV];
+    if (kz > 1) {  // the sum kernel's order: the slices, then the bias
+        const size_t mn4 = (size_t)rows * w4;
+        const float4* p4 = reinterpret_cast<const float4*>(kp) + (size_t)row * w4;
+        const float4* b4 = reinterpret_cast<const float4*>(bias);
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int k4 = tid + 256 * j;
+            if (k4 >= w4) break;
+            float4 y = p4[k4];
+            for (int z = 1; z < kz; z++) {
+                const float4 t = p4[(size_t)z * mn4 + k4];
+                y = make_float4(y.x + t.x, y.y + t.y, y.z + t.z, y.w + t.w);
+            }
+            if (bias) {
+                const float4 b = b4[k4];
+                y = make_float4(y.x + b.x, y.y + b.y, y.z + b.z, y.w + b.w);
+            }
+            v[j] = y;
+        }
+    } else {
+        const float4* src4 = reinterpret_cast<const float4*>(qkv + (size_t)row * width);
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int k4 = tid + 256 * j;
+            v[j] = k4 < w4 ? src4[k4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int k4 = tid + 256 * j, e = 4 * k4;
+        if (k4 >= w4) break;
+        const float4 x = v[j];
+        if (e < rot) {
+            const int hh = head_of(e), m0 = (e - hh * hd) / 2;
+            float4 y;
+            y.x = __builtin_fmaf(x.x, cm[j].x, -(x.y * sn[j].x));
+            y.y = __builtin_fmaf(x.x, sn[j].x, x.y * cm[j].x);
+            y.z = __builtin_fmaf(x.z, cm[j].y, -(x.w * sn[j].y));
+            y.w = __builtin_fmaf(x.z, sn[j].y, x.w * cm[j].y);
+            int dst = m0;  // (pairs 2, 3 of a group of 8 to slots 4, 5 and back; m0 + 1 follows m0)
+            if (m0 < full) {
+                const int o = m0 & 7;
+                dst = m0 - o + (o == 2 ? 4 : o == 4 ? 2 : o);
+            }
+            *reinterpret_cast<float4*>(sm + hh * hd + 2 * dst) = y;
+        } else {
+            *reinterpret_cast<float4*>(sm + e) = x;
+        }
+    }
+    __syncthreads();
+    const int lane = tid & 63, wave = tid >> 6, nhead = nh + 2 * nkv;
+    // where head hh's bytes and scale go: q8 / qsc, or the K / V cache slot of this position
+    auto target = [&](int hh, int8_t*& dst, float*& sdst) {
+        if (hh < nh) {
+            dst = q8 + ((size_t)row * nh + hh) * hd;
+            sdst = qsc + (size_t)row * nh + hh;
+        } else {
+            const bool isv = hh >= nh + nkv;
+            const int kh = hh - nh - (isv ? nkv : 0);
+            const size_t slot = ((size_t)layer * nkv + kh) * kv.max_seq + pos;
+            dst = (isv ? kv.v : kv.k) + slot * hd;
+            sdst = (isv ? kv.vs : kv.ks) + slot;
+        }
+    };
+    const int lg = hd / 4;  // lanes per head at 4 values a lane
+    if (lg <= 64 && (lg & (lg - 1)) == 0) {
+        // 64 / lg heads per wave: the group's maximum by xor exchanges within the group
+        const int hpw = 64 / lg, gi = lane / lg, gl = lane - gi * lg;
+        for (int h0 = wave * hpw; h0 < nhead; h0 += 4 * hpw) {
+            const int hh = h0 + gi;
+            const bool on = hh < nhead;
+            const float4 x = on ? *reinterpret_cast<const float4*>(sm + (size_t)hh * hd + 4 * gl)
+                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float amax = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+            for (int o = 1; o < lg; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+            if (!on) continue;
+            const float inv = quant_inv(amax);
+            int8_t* dst;
+            float* sdst;
+            target(hh, dst, sdst);
+            const uint32_t b0 = (uint8_t)quant_i8(x.x, inv), b1 = (uint8_t)quant_i8(x.y, inv);
+            const uint32_t b2 = (uint8_t)quant_i8(x.z, inv), b3 = (uint8_t)quant_i8(x.w, inv);
+            *reinterpret_cast<uint32_t*>(dst + 4 * gl) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            if (gl == 0) *sdst = quant_scale(amax);
+        }
+        return;
+    }
+    // other head sizes: wave w quantises heads w, w + 4, ... (lane l values l, l + 64, ...)
+    for (int hh = wave; hh < nhead; hh += 4) {
+        const float* src = sm + (size_t)hh * hd;
+        float amax = 0.0f;
+        for (int d = lane; d < hd; d += 64) amax = fmaxf(amax, fabsf(src[d]));
+        amax = wave_max(amax);
+        const float inv = quant_inv(amax);
+        int8_t* dst;
+        float* sdst;
+        target(hh, dst, sdst);
+        for (int d = lane; d < hd; d += 64) dst[d] = quant_i8(src[d], inv);
+        if (lane == 0) *sdst = quant_scale(amax);
+    }
+}
+
 hipError_t rope_pack_init() {
     return hipFuncSetAttribute(reinterpret_cast<const void*>(&rope_pack_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                160 * 1024 - 2048);
@@ -654,9 +789,25 @@ hipError_t rope_pack_init() {
 void launch_rope_pack(const float* qkv, int seq, int start_pos, const int* state, int nh, int nkv, int hd,
                       const float* cos_t, const float* sin_t, const KVDev& kv, int layer, int8_t* q8, float* qsc,
                       hipStream_t st, const float* kp, int kz, const float* bias) {
-    const size_t lds = (size_t)(kz > 1 ? 2 * nh + 3 * nkv : nh + nkv) * hd * sizeof(float);
-    hipLaunchKernelGGL(rope_pack_kernel, dim3(seq), dim3(256), lds, st, qkv, start_pos, state, nh, nkv, hd, cos_t,
-                       sin_t, kv, layer, q8, qsc, kp, kz, seq, bias);
+    const int width = (nh + 2 * nkv) * hd;  // (hd is a multiple of 4)
+    const size_t lds4 = (size_t)width * sizeof(float);
+#define JY_ROPE4(NV)                                                                                                \
+    hipLaunchKernelGGL(rope_pack4_kernel<NV>, dim3(seq), dim3(256), lds4, st, qkv, start_pos, state, nh, nkv, hd, \
+                       cos_t, sin_t, kv, layer, q8, qsc, kp, kz, seq, bias)
+    if (width <= 1024)
+        JY_ROPE4(1);
+    else if (width <= 2048)
+        JY_ROPE4(2);
+    else if (width <= 4096)
+        JY_ROPE4(4);
+    else if (width <= 8192)
+        JY_ROPE4(8);
+    else {
+        const size_t lds = (size_t)(kz > 1 ? 2 * nh + 3 * nkv : nh + nkv) * hd * sizeof(float);
+        hipLaunchKernelGGL(rope_pack_kernel, dim3(seq), dim3(256), lds, st, qkv, start_pos, state, nh, nkv, hd, cos_t,
+                           sin_t, kv, layer, q8, qsc, kp, kz, seq, bias);
+    }
+#undef JY_ROPE4
 }
 
 // ---------------------------------------------------------------- greedy selection
