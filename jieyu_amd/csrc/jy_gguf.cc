@@ -110,6 +110,7 @@ uint64_t gtype_bytes(uint32_t t, uint64_t n) {
     const auto [be, bb] = gblock(t);
     if (!be) throw runtime_error(string("gguf: 不认识的量化类型 ") + gtype_name(t));
     if (n % be) throw runtime_error("gguf: 元素个数不是块的整数倍");
+    if (n / be > ~0ull / bb) throw runtime_error("gguf: 张量字节数溢出");  // (a corrupt shape)
     return n / be * bb;
 }
 
@@ -392,6 +393,12 @@ GFile gguf_open(const string& path) {
         t.n_elem = 1;
         for (uint32_t d = 0; d < nd; d++) {
             t.shape.push_back(r.u(8));
+            // model.bf keeps 32-bit dims, and a zero dim leaves the writer's loops over the
+            // others with nothing to bound them
+            if (t.shape.back() == 0 || t.shape.back() > 0xFFFFFFFFull)
+                throw runtime_error("gguf: 张量维度不对 " + t.name);
+            // (a corrupt shape whose element count wraps would pass every range check)
+            if (t.n_elem > ~0ull / t.shape.back()) throw runtime_error("gguf: 张量元素个数溢出 " + t.name);
             t.n_elem *= t.shape.back();
         }
         t.type = (uint32_t)r.u(4);
@@ -404,6 +411,8 @@ GFile gguf_open(const string& path) {
         if (a > 0) g.align = (uint64_t)a;
     }
     const uint64_t here = (uint64_t)f.tellg();
+    // (an alignment past the file's size would wrap the data offset: such a file has no data)
+    if (g.align > size) throw runtime_error("gguf: general.alignment 超出文件大小");
     g.data_off = (here + g.align - 1) / g.align * g.align;
     return g;
 }
@@ -440,6 +449,7 @@ uint16_t f2bf(float v) {  // converter.h:81-86: + 0x8000 unless inf / nan
 
 // float values in a model.bf dtype, little-endian, appended to `out`
 void encode_values(const float* v, size_t n, uint8_t dtype, vector<unsigned char>& out) {
+    if (n == 0) return;  // (a tensor with a zero dimension: nothing to append, and v may be null)
     const size_t at = out.size();
     if (dtype == BF_F32) {
         out.resize(at + n * 4);
@@ -968,8 +978,11 @@ void check_tensors(const GFile& g, const vector<OutTensor>& ts, int hd) {
         if (bf_tensor_bytes(o.dtype, elems) != o.bytes) throw runtime_error("bfile: shape 与数据长度不符: " + o.name);
     }
     for (const OutTensor& o : ts) {
+        // start = data_off + offset, formed only where it cannot wrap
+        if (g.data_off > g.file_size || o.src->offset > g.file_size - g.data_off)
+            throw runtime_error("bfile: 写张量失败: " + o.name);
         const uint64_t start = g.data_off + o.src->offset;
-        if (start > g.file_size || o.src->nbytes > g.file_size - start)
+        if (o.src->nbytes > g.file_size - start)
             throw runtime_error("bfile: 写张量失败: " + o.name);
         if (!o.raw && !dequant_known(o.src->type))
             throw runtime_error(string("gguf: 还没写这种量化的反量化 ") + gtype_name(o.src->type));

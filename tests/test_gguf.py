@@ -184,3 +184,95 @@ def test_bfile_writer_kquant_directory_binds(tmp_path):
     # an f16 tensor round-trips as dtype F16
     t = B.Tensor.f16("x", np.ones((2, 3), np.float16))
     assert t.dtype == B.F16 and len(t.data) == 12
+
+
+def _patch_tensor(raw, name, dims=None, offset=None):
+    """raw GGUF v3 bytes with tensor `name`'s dims and/or data offset replaced in its
+    tensor-info record (same dimension count, so the layout is unchanged)"""
+    import struct
+    key = struct.pack("<Q", len(name)) + name.encode()
+    at = raw.index(key) + len(key)
+    nd = struct.unpack_from("<I", raw, at)[0]
+    b = bytearray(raw)
+    if dims is not None:
+        assert len(dims) == nd
+        struct.pack_into("<" + "Q" * nd, b, at + 4, *dims)
+    if offset is not None:
+        struct.pack_into("<Q", b, at + 4 + 8 * nd + 4, offset)
+    return bytes(b)
+
+
+# corrupt tensor records and headers that once got past the range checks: a zero dim beside
+# a huge one (an endless panel loop), a dim past model.bf's 32 bits, a byte count that wraps
+# 64 bits, a data offset that wraps the start of the range, an alignment past the file
+@pytest.mark.parametrize("case,want", [("zero_dim", "维度不对"), ("dim_over_32bit", "维度不对"),
+                                       ("bytes_wrap", "字节数溢出"), ("offset_wraps", "写张量失败"),
+                                       ("align_past_file", "alignment")])
+def test_corrupt_records_fail_cleanly(tmp_path, case, want):
+    """each is refused with an error before any file is written"""
+    import gguf_writer as G
+    g = GM.deepseek_f32()
+    if case == "align_past_file":
+        g.kv.append(("general.alignment", G.U32, 1 << 31, None))
+    raw = g.bytes()
+    name = "blk.0.attn_output.weight"
+    if case == "zero_dim":
+        raw = _patch_tensor(raw, name, dims=(2 ** 63 + 64, 0))
+    elif case == "dim_over_32bit":
+        raw = _patch_tensor(raw, name, dims=(2 ** 32, 1))
+    elif case == "bytes_wrap":
+        raw = _patch_tensor(raw, name, dims=(2 ** 32 - 1, 2 ** 32 - 1))
+    elif case == "offset_wraps":
+        raw = _patch_tensor(raw, name, offset=2 ** 64 - 16)
+    src = str(tmp_path / "bad.gguf")
+    open(src, "wb").write(raw)
+    out = str(tmp_path / "out")
+    rc, _, err = convert(src, out, "f32", True)
+    assert rc == -1 and want in err, err
+    assert digest(out) == {}
+
+
+def _mutate(data, rng):
+    """one random corruption: a truncation, byte flips in the first 4 KiB or anywhere, or a
+    random 4- / 8-byte value (8-byte ones often edge values) at a header offset"""
+    b = bytearray(data)
+    kind = rng.randrange(5)
+    hdr = min(len(b), 4096)
+    if kind == 0:
+        return bytes(b[:rng.randrange(len(b))])
+    if kind == 1:
+        for _ in range(rng.randrange(1, 8)):
+            b[rng.randrange(hdr)] = rng.randrange(256)
+    elif kind == 2:
+        o = rng.randrange(0, max(1, hdr - 8)) & ~7
+        v = rng.choice([0, 1, 2 ** 31, 2 ** 32 - 1, 2 ** 63, 2 ** 64 - 1, rng.randrange(2 ** 64)])
+        b[o:o + 8] = v.to_bytes(8, "little")
+    elif kind == 3:
+        o = rng.randrange(0, max(1, hdr - 4))
+        b[o:o + 4] = rng.randrange(2 ** 32).to_bytes(4, "little")
+    else:
+        for _ in range(rng.randrange(1, 32)):
+            b[rng.randrange(len(b))] = rng.randrange(256)
+    return bytes(b)
+
+
+@pytest.mark.parametrize("model", list(GM.MODELS))
+def test_mutated_files_fail_cleanly(tmp_path, model):
+    """150 seeded random corruptions of each synthetic GGUF file: each converts or fails with
+    an error and writes nothing (a crash or a hang would end the test run).  The same sweep
+    at 3000 corruptions per file, against the host-sanitized library (ASan + UBSan), found
+    the cases of test_corrupt_records_fail_cleanly and now reports nothing."""
+    import random
+    import shutil
+    data = open(GM.MODELS[model]().write(str(tmp_path / "m.gguf")), "rb").read()
+    src, out = str(tmp_path / "f.gguf"), str(tmp_path / "out")
+    ok = 0
+    for seed in range(150):
+        open(src, "wb").write(_mutate(data, random.Random(seed)))
+        shutil.rmtree(out, ignore_errors=True)
+        rc, _, _ = convert(src, out, "f32", False)
+        if rc == 0:
+            ok += 1
+        else:
+            assert digest(out) == {}, f"seed {seed}: a failed conversion left files"
+    assert 0 < ok < 150
