@@ -276,3 +276,33 @@ def test_mutated_files_fail_cleanly(tmp_path, model):
         else:
             assert digest(out) == {}, f"seed {seed}: a failed conversion left files"
     assert 0 < ok < 150
+
+
+@pytest.mark.parametrize("target", ["model.bf", "model_info.json", "vocab.json", "merges.txt"])
+def test_mutated_model_directory(tmp_path, target):
+    """a converted model directory with one file corrupted (100 seeded corruptions): binding
+    it (model.bf, model_info.json) or loading its tokenizer (vocab.json, merges.txt) and
+    coding a few texts either works or raises.  The same sweep at 1000 corruptions per file,
+    against the host-sanitized library, reports nothing."""
+    import random
+    import shutil
+    base = str(tmp_path / "base")
+    api.gguf_convert(GM.MODELS["qwen-mixed"]().write(str(tmp_path / "m.gguf")), base, "f32", True)
+    files = {f: open(os.path.join(base, f), "rb").read() for f in os.listdir(base)}
+    d = str(tmp_path / "d")
+    for seed in range(100):
+        shutil.rmtree(d, ignore_errors=True)
+        os.makedirs(d)
+        for f, b in files.items():
+            open(os.path.join(d, f), "wb").write(b)
+        open(os.path.join(d, target), "wb").write(_mutate(files[target], random.Random(seed)))
+        try:
+            if target in ("model.bf", "model_info.json"):
+                api.model_bind(d)
+            else:
+                t = api.Tokenizer(os.path.join(d, "vocab.json"), os.path.join(d, "merges.txt"))
+                for text in ("hello world", "abé中文 <|x|> 123", ""):
+                    t.decode(t.encode(text) + [0, 1, 2, 10 ** 6, -5])
+                t.close()
+        except api.JieyuError:
+            pass
