@@ -1360,6 +1360,7 @@ struct Session {
             kv = kv_in;
             if (kv->dev.num_layers < m->L || kv->dev.max_seq < max_seq || kv->dev.nkv != m->nkv || kv->dev.hd != m->hd)
                 fail("generate: KV cache shape does not match the model");
+            if (kv->device != m->device) fail("generate: the KV cache is on another device than the model");
         } else {
             kv = jyhip_kv_create(m, max_seq);
             if (!kv) fail(g_err);
@@ -1532,6 +1533,7 @@ int forward_impl(jyhip_model* m, jyhip_kv* kv, float* X, int seq, int start_pos,
     if (!kv || !X) fail("forward: NULL kv or X");
     if (kv->dev.num_layers < m->L || kv->dev.nkv != m->nkv || kv->dev.hd != m->hd)
         fail("forward: KV cache shape does not match the model");  // forward.h:60-61
+    if (kv->device != m->device) fail("forward: the KV cache is on another device than the model");
     if (start_pos < 0) fail("forward: start_pos must not be negative");
     if (seq <= 0) fail("forward: seq must be positive");
     if ((size_t)start_pos + seq > (size_t)kv->dev.max_seq) fail("forward: KV cache capacity exceeded");
@@ -1599,6 +1601,7 @@ int forward_noalloc(jyhip_model* m, jyhip_kv* kv, float* X, int seq, int start_p
     if (!kv || !X) fail("forward: NULL kv or X");
     if (kv->dev.num_layers < m->L || kv->dev.nkv != m->nkv || kv->dev.hd != m->hd)
         fail("forward: KV cache shape does not match the model");
+    if (kv->device != m->device) fail("forward: the KV cache is on another device than the model");
     if (start_pos < 0) fail("forward: start_pos must not be negative");
     if (seq <= 0) fail("forward: seq must be positive");
     if ((size_t)start_pos + seq > (size_t)kv->dev.max_seq) fail("forward: KV cache capacity exceeded");
